@@ -1,0 +1,389 @@
+#!/usr/bin/env python3
+"""bench.py -- k-quant linear path on one MI355X.
+
+Headline ("C2"): Q4_K decode GEMV over the seven
+Llama-3-8B projections of one decoder layer at batch 1 --
+q 4096x4096, k 1024x4096, v 1024x4096, o 4096x4096, gate 14336x4096,
+up 14336x4096, down 4096x14336 (out x in).  One step = one pass over the
+seven GEMVs of one layer copy; steps rotate over --copies distinct layer
+copies (default 8 = 981 MB of quantized weights, beyond the 256 MB MALL) so
+weights stream from HBM.  value = quantized weight bytes per step x steps /
+wall time of the timed region, in GB/s; inputs are resident in HBM before
+timing starts.  Steps are replayed from HIP graphs (one graph per pass over
+all copies) so host launch overhead does not gate the GPU.
+
+The JSON line also carries:
+  roofline      the dominant kernel's algorithmic bytes / its own dispatch
+                duration (hipExtLaunchKernelGGL begin/end events), vs 8 TB/s
+  cpu_baseline  the reference CPU path (oracle restatement of
+                linear_out_by_in, scalar mode, 1 core since rows < 32) on one
+                layer copy, dequantized once outside the timing
+  extra         per-shape kernel times and secondary configs (C1, C3, C4)
+
+Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0          # MI355X datasheet HBM3E bandwidth
+BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16/fp16 MFMA
+Q4K, Q6K, Q8_0 = 12, 14, 8
+BLOCK = {Q4K: (256, 144), Q6K: (256, 210), Q8_0: (32, 34)}
+C2_PROJ = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
+           ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
+METRIC = "Q4_K dequant-GEMV GB/s (% of HBM peak) + prefill dequant-GEMM TFLOPS"
+
+
+def log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def wbytes(t: int, n: int, k: int) -> int:
+    e, b = BLOCK[t]
+    return n * (k // e) * b
+
+
+class Hip:
+    """Minimal hipEvent access (the events passed to okq_set_launch_events)."""
+
+    def __init__(self):
+        self.lib = ctypes.CDLL("libamdhip64.so")
+        self.lib.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+
+    def event(self) -> int:
+        e = ctypes.c_void_p()
+        assert self.lib.hipEventCreate(ctypes.byref(e)) == 0
+        return e.value
+
+    def elapsed_ms(self, a: int, b: int) -> float:
+        assert self.lib.hipEventSynchronize(b) == 0
+        ms = ctypes.c_float()
+        assert self.lib.hipEventElapsedTime(ctypes.byref(ms), a, b) == 0
+        return ms.value
+
+    def destroy(self, e: int) -> None:
+        self.lib.hipEventDestroy(e)
+
+
+class Ctx:
+    def __init__(self, torch, okq):
+        self.torch = torch
+        self.okq = okq
+        self.hip = Hip()
+        self.tmp = None
+
+    @property
+    def stream(self) -> int:
+        return self.torch.cuda.current_stream().cuda_stream
+
+    def quantized(self, t: int, n: int, k: int, seed: int, sigma: float = 0.02):
+        """Seeded N(0, sigma) weights quantized on the GPU (chunked through a
+        reusable f32 scratch tensor)."""
+        torch = self.torch
+        out = torch.empty(wbytes(t, n, k), dtype=torch.uint8, device="cuda")
+        e, b = BLOCK[t]
+        total = n * k
+        chunk = (1 << 26) // e * e
+        if self.tmp is None or self.tmp.numel() < chunk:
+            self.tmp = torch.empty(chunk, dtype=torch.float32, device="cuda")
+        done = 0
+        while done < total:
+            m = min(chunk, total - done)
+            self.okq.call("okq_fill_normal", seed, done, m, sigma, self.tmp.data_ptr(), self.stream)
+            self.okq.call("okq_quantize", t, self.tmp.data_ptr(), m, out.data_ptr() + done // e * b, self.stream)
+            done += m
+        return out
+
+    def normal(self, n: int, seed: int, sigma: float = 1.0):
+        x = self.torch.empty(n, dtype=self.torch.float32, device="cuda")
+        self.okq.call("okq_fill_normal", seed, 0, n, sigma, x.data_ptr(), self.stream)
+        return x
+
+    def gemv(self, t, x, k, w, n, y, entry="okq_gemv", rows=1):
+        self.okq.call(entry, x.data_ptr(), rows, k, t, w.data_ptr(), w.numel(), n, None, y.data_ptr(), self.stream)
+
+    def kernel_us(self, launch, reps: int) -> list:
+        """Per-launch dispatch duration (µs) of `reps` launches of launch(i)."""
+        evs = [(self.hip.event(), self.hip.event()) for _ in range(reps)]
+        try:
+            for i, (a, b) in enumerate(evs):
+                self.okq.call("okq_set_launch_events", a, b)
+                launch(i)
+        finally:
+            self.okq.call("okq_set_launch_events", None, None)
+        self.torch.cuda.synchronize()
+        us = [1000.0 * self.hip.elapsed_ms(a, b) for a, b in evs]
+        for a, b in evs:
+            self.hip.destroy(a)
+            self.hip.destroy(b)
+        return us
+
+
+def median(v):
+    s = sorted(v)
+    return s[len(s) // 2]
+
+
+def pct(v, p):
+    s = sorted(v)
+    return s[min(len(s) - 1, max(0, int(round(p / 100.0 * (len(s) - 1)))))]
+
+
+# ---------------------------------------------------------------------------
+# C2 headline
+# ---------------------------------------------------------------------------
+
+def run_c2(ctx: Ctx, args):
+    torch = ctx.torch
+    log(f"C2: generating {args.copies} Q4_K layer copies")
+    layers = []
+    for c in range(args.copies):
+        layers.append({name: ctx.quantized(Q4K, n, k, seed=10_000 + 100 * c + i)
+                       for i, (name, n, k) in enumerate(C2_PROJ)})
+    x4096 = ctx.normal(4096, 1)
+    x14336 = ctx.normal(14336, 2)
+    outs = {name: torch.empty(n, dtype=torch.float32, device="cuda") for name, n, _ in C2_PROJ}
+    step_bytes = sum(wbytes(Q4K, n, k) for _, n, k in C2_PROJ)
+
+    def step(c):
+        lay = layers[c % args.copies]
+        for name, n, k in C2_PROJ:
+            ctx.gemv(Q4K, x14336 if k == 14336 else x4096, k, lay[name], n, outs[name])
+
+    # warm up eagerly once (also compiles nothing: the library is prebuilt)
+    step(0)
+    torch.cuda.synchronize()
+    # one graph per pass over all copies + single-step graphs for remainders
+    g_all = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g_all):
+        for c in range(args.copies):
+            step(c)
+    g_one = []
+    for c in range(args.copies):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            step(c)
+        g_one.append(g)
+
+    def run_steps(nsteps, start=0):
+        i = start
+        while nsteps > 0:
+            if i % args.copies == 0 and nsteps >= args.copies:
+                g_all.replay()
+                i += args.copies
+                nsteps -= args.copies
+            else:
+                g_one[i % args.copies].replay()
+                i += 1
+                nsteps -= 1
+        return i
+
+    log(f"C2: warmup {args.warmup} steps, timing {args.steps} steps")
+    i = run_steps(args.warmup)
+    i = i - i % args.copies  # restart on a copy boundary
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    run_steps(args.steps, i)
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    sec = t1 - t0
+    gbs = step_bytes * args.steps / sec / 1e9
+
+    # per-projection kernel durations (dispatch begin/end), rotating copies
+    shapes = {}
+    for name, n, k in C2_PROJ:
+        x = x14336 if k == 14336 else x4096
+        us = ctx.kernel_us(lambda r, name=name, n=n, k=k, x=x: ctx.gemv(Q4K, x, k, layers[r % args.copies][name], n,
+                                                                           outs[name]), args.kernel_reps)
+        b = wbytes(Q4K, n, k)
+        med = median(us)
+        shapes[name] = {"n": n, "k": k, "weight_bytes": b, "us_median": round(med, 3),
+                        "us_p10": round(pct(us, 10), 3), "us_p90": round(pct(us, 90), 3),
+                        "us_mean": round(sum(us) / len(us), 3),
+                        "gbs": round(b / (sum(us) / len(us)) / 1e3, 1),
+                        "frac_hbm": round(b / (sum(us) / len(us)) / 1e3 / HBM_PEAK_GBS, 4)}
+    return {"gbs": gbs, "sec": sec, "step_bytes": step_bytes, "shapes": shapes, "layers": layers,
+            "x4096": x4096, "x14336": x14336}
+
+
+def roofline_from(shapes, step_share=None):
+    # dominant kernel: the C2 down projection (4096 x 14336, its own kernel
+    # instantiation, so rocprof's per-kernel average covers exactly it)
+    s = shapes["down"]
+    achieved = s["weight_bytes"] / s["us_mean"] / 1e3
+    return {"bound": "hbm", "kernel": "gemv_q4k_kernel<4> (C2 down 4096x14336 Q4_K)",
+            "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
+
+
+# ---------------------------------------------------------------------------
+# secondary configs
+# ---------------------------------------------------------------------------
+
+def run_c3(ctx: Ctx, args):
+    n, k = 128256, 4096
+    log("C3: Q6_K head 128256x4096")
+    w = ctx.quantized(Q6K, n, k, seed=31)
+    x = ctx.normal(k, 32)
+    y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
+    us = ctx.kernel_us(lambda r: ctx.gemv(Q6K, x, k, w, n, y), max(10, args.kernel_reps // 4))
+    b = wbytes(Q6K, n, k)
+    m = sum(us) / len(us)
+    del w
+    return {"shape": [n, k], "weight_bytes": b, "us_median": round(median(us), 2), "us_mean": round(m, 2),
+            "gbs": round(b / m / 1e3, 1), "frac_hbm": round(b / m / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def run_c1(ctx: Ctx, args):
+    n, k = 4096, 4096
+    log("C1: Q8_0 4096x4096 GEMV (GPU)")
+    copies = 32  # 570 MB rotated
+    ws = [ctx.quantized(Q8_0, n, k, seed=40 + c) for c in range(copies)]
+    x = ctx.normal(k, 41)
+    y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
+    us = ctx.kernel_us(lambda r: ctx.gemv(Q8_0, x, k, ws[r % copies], n, y), args.kernel_reps)
+    b = wbytes(Q8_0, n, k)
+    m = sum(us) / len(us)
+    return {"shape": [n, k], "weight_bytes": b, "us_median": round(median(us), 3), "us_mean": round(m, 3),
+            "gbs": round(b / m / 1e3, 1), "frac_hbm": round(b / m / 1e3 / HBM_PEAK_GBS, 4)}
+
+
+def run_c4(ctx: Ctx, args, c2):
+    """Q4_K prefill GEMM at M in {128, 512, 2048} with bf16 activations."""
+    torch = ctx.torch
+    res = {}
+    for m in (128, 512, 2048):
+        xf = ctx.normal(m * 14336, 50 + m)
+        xb = torch.empty(m * 14336, dtype=torch.int16, device="cuda")
+        ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
+        for name, n, k in C2_PROJ:
+            if name in ("k", "o", "up"):
+                continue  # same shapes as v, q, gate
+            y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+            lay = c2["layers"]
+            try:
+                us = ctx.kernel_us(lambda r: ctx.gemv(Q4K, xb, k, lay[r % len(lay)][name], n, y, entry="okq_gemm_bf16",
+                                                      rows=m), max(8, args.kernel_reps // 8))
+            except Exception as e:  # noqa: BLE001 -- report unsupported shapes instead of dying
+                res[f"M{m}_{name}"] = {"error": str(e)[:200]}
+                continue
+            t = sum(us) / len(us)
+            flops = 2.0 * m * n * k
+            res[f"M{m}_{name}"] = {"m": m, "n": n, "k": k, "us_mean": round(t, 2),
+                                   "tflops": round(flops / t / 1e6, 1),
+                                   "frac_bf16_peak": round(flops / t / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    return res
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (reference CPU path, oracle restatement)
+# ---------------------------------------------------------------------------
+
+def run_cpu_baseline(ctx: Ctx, c2, args):
+    import numpy as np
+    from oracle import oracle as O
+    orc = O.Oracle()
+    lay = c2["layers"][0]
+    log("cpu baseline: dequantizing one layer copy on the host (not timed)")
+    w = {name: orc.dequantize(O.Q4_K, lay[name].cpu().numpy(), n * k).reshape(n, k) for name, n, k in C2_PROJ}
+    x4096 = c2["x4096"].cpu().numpy()
+    x14336 = c2["x14336"].cpu().numpy()
+    # sanity: the GPU result of the last timed step equals the CPU path within tolerance
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        for name, n, k in C2_PROJ:
+            orc.linear(x14336 if k == 14336 else x4096, 1, k, w[name], n, None, O.MODE_SCALAR, 1)
+        passes += 1
+        if time.perf_counter() - t0 >= args.cpu_seconds:
+            break
+    sec = time.perf_counter() - t0
+    gbs = c2["step_bytes"] * passes / sec / 1e9
+    cpu = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"C2 layer copy 0 (7 Q4_K projections, {c2['step_bytes']} quantized bytes) dequantized to f32 "
+                      f"once (untimed); reference scalar linear_out_by_in, batch 1, serial (rows < 32); "
+                      f"{passes} passes in {sec:.2f} s on {cpu}",
+            "ms_per_step": round(1000.0 * sec / passes, 2)}
+
+
+# ---------------------------------------------------------------------------
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=400)
+    ap.add_argument("--warmup", type=int, default=40)
+    ap.add_argument("--copies", type=int, default=8)
+    ap.add_argument("--kernel-reps", type=int, default=200)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one MI355X only: this build has no multi-GPU path "
+              "(the sharding design is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from ocelotl_amd import okq
+    okq.call("okq_init", 0)
+    ctx = Ctx(torch, okq)
+
+    c2 = run_c2(ctx, args)
+    extra = {"c2_shapes": c2["shapes"]}
+    if not args.no_extra:
+        extra["c1_q8_0"] = run_c1(ctx, args)
+        extra["c3_q6_k_head"] = run_c3(ctx, args)
+        extra["c4_q4_k_gemm_bf16"] = run_c4(ctx, args, c2)
+    cpu = None if args.no_cpu else run_cpu_baseline(ctx, c2, args)
+
+    rec = {
+        "metric": METRIC,
+        "value": round(c2["gbs"], 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1000.0 * c2["sec"] / args.steps, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "q4_k weights x f32 activations (int8 dot4 -> i32, f32 scale/accumulate)",
+        "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K on the GPU, N(0,1) f32 activations",
+        "config": {"workload": "C2: Q4_K decode GEMV, one Llama-3-8B layer per step (q 4096x4096, k/v 1024x4096, "
+                               "o 4096x4096, gate/up 14336x4096, down 4096x14336), batch 1",
+                   "batch": 1, "layer_copies_rotated": args.copies,
+                   "weight_bytes_per_step": c2["step_bytes"],
+                   "frac_hbm_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4)},
+        "roofline": roofline_from(c2["shapes"]),
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

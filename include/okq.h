@@ -1,0 +1,163 @@
+/*
+ * okq.h -- C-ABI of libokq.so, the MI355X (gfx950) k-quant linear path.
+ *
+ * The library implements Ocelotl's quantized linear projection for the GGUF
+ * block formats Q8_0 (type id 8), Q4_K (12) and Q6_K (14) with hand-written
+ * HIP kernels: dequantize, a fused dequant-GEMV for decode and an MFMA
+ * dequant-GEMM for prefill.  Weights stay in the GGUF layout: tensor shape
+ * [ne0 = in_features, ne1 = out_features], each row one output feature made of
+ * in_features / block_elems consecutive blocks.
+ *
+ * Conventions (mirroring the reference's kernel contract):
+ *   - every entry point validates before launch and returns an okq_status; on
+ *     failure okq_last_error() holds a message, and nothing was launched
+ *     (crates/kernels/src/lib.rs:2443-2497, docs/design/kernels.md:96-99);
+ *   - `out` buffers are caller-allocated device memory (lib.rs:106-116);
+ *   - `stream` is a hipStream_t (NULL = the null stream); work is enqueued
+ *     asynchronously on it;
+ *   - results are deterministic: fixed reduction order, no float atomics.
+ * Thread safety: all entry points may be called from several host threads; the
+ * device used is the calling thread's current HIP device.
+ */
+#ifndef OKQ_H
+#define OKQ_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  OKQ_E_SHAPE / E_ARG map to OcelotlError::Kernel
+ * (crates/core/src/lib.rs:15-99, KernelError{backend:"hip-gfx950", message});
+ * OKQ_E_TYPE maps to OcelotlError::Unsupported (lib.rs:1662-1671). */
+typedef enum okq_status {
+    OKQ_OK = 0,
+    OKQ_E_SHAPE = 1,  /* lengths/shapes inconsistent, not block-aligned, or too large */
+    OKQ_E_TYPE = 2,   /* GGML tensor type not supported by this path */
+    OKQ_E_ALIGN = 3,  /* pointer misaligned for the kernel's vector loads */
+    OKQ_E_NODEV = 4,  /* no HIP device, or the device is not gfx950 */
+    OKQ_E_LAUNCH = 5, /* HIP runtime error at launch or copy */
+    OKQ_E_ARG = 6,    /* null pointer or invalid argument value */
+    OKQ_E_ALLOC = 7   /* device allocation failed */
+} okq_status;
+
+/* GGML tensor type ids, as GgmlTensorType::from_raw
+ * (crates/loader/src/gguf_inspect.rs:170-206). */
+enum {
+    OKQ_TYPE_F32 = 0,
+    OKQ_TYPE_F16 = 1,
+    OKQ_TYPE_Q8_0 = 8,
+    OKQ_TYPE_Q4_K = 12,
+    OKQ_TYPE_Q6_K = 14,
+    OKQ_TYPE_BF16 = 30
+};
+
+/* ---- identity and errors ---------------------------------------------- */
+
+/* Backend name, following the backend_id convention of
+ * crates/kernels/src/cubecl_backend.rs:2268-2272: "hip-gfx950". */
+const char *okq_backend_name(void);
+
+/* Copies the calling thread's last error message (NUL-terminated, truncated to
+ * len) and returns its full length. */
+size_t okq_last_error(char *buf, size_t len);
+
+/* ---- GGUF tensor layout (fills the byte_len = None gap of
+ *      GgmlTensorType::fixed_element_size, gguf_inspect.rs:208-219) ------- */
+
+/* Elements and bytes per block: Q8_0 32/34, Q4_K 256/144, Q6_K 256/210, and
+ * 1/4, 1/2, 1/2 for F32, F16, BF16.  OKQ_E_TYPE for anything else. */
+okq_status okq_type_info(uint32_t ggml_type, int64_t *block_elems, int64_t *block_bytes);
+
+/* Bytes of one row of ne0 elements; OKQ_E_SHAPE if ne0 is not a positive
+ * multiple of the block size. */
+okq_status okq_row_bytes(uint32_t ggml_type, int64_t ne0, int64_t *out_bytes);
+
+/* Byte length of a GGUF tensor with `n_dims` dims in ne order (shape[0] =
+ * ne0, contiguous).  Overflow is OKQ_E_SHAPE (gguf_inspect.rs:331-342). */
+okq_status okq_tensor_bytes(uint32_t ggml_type, const int64_t *shape, int n_dims, uint64_t *out_bytes);
+
+/* ---- device ------------------------------------------------------------ */
+
+/* Selects device `ordinal` for the calling thread and checks it is gfx950
+ * (Device::Gpu{ordinal}, crates/core/src/lib.rs:438-441). */
+okq_status okq_init(int ordinal);
+okq_status okq_device_count(int *count);
+okq_status okq_alloc(void **ptr, size_t bytes);
+okq_status okq_free(void *ptr);
+okq_status okq_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream);
+okq_status okq_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream);
+okq_status okq_sync(void *stream);
+
+/* ---- compute ----------------------------------------------------------- */
+
+/* dequantize(type, src_bytes, n_elems, out_f32): the reference defines no
+ * dequant signature; this follows the linear_out_by_in style
+ * (lib.rs:106-116).  n must be a multiple of the block size; src holds
+ * n / block_elems blocks.  Bit-exact with the CPU oracle (every product and
+ * difference rounded separately, fp16 decoded exactly as
+ * crates/loader/src/safetensors_values.rs:155-183). */
+okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float *dst, void *stream);
+
+/* Quantized counterpart of KernelBackend::linear_out_by_in
+ * (crates/kernels/src/lib.rs:106-116) and linear_d (:192-202):
+ *   out[r, o] = bias[o] + sum_k x[r, k] * W[o, k]
+ * x: [rows, in_features] f32 (device); w: GGUF blocks of an [out_features,
+ * in_features] tensor, w_bytes = out_features * row_bytes(in_features);
+ * bias: [out_features] f32 or NULL; out: [rows, out_features] f32.
+ * rows == 0 or out_features == 0 is a no-op.  Small `rows` run the fused
+ * dequant-GEMV, larger ones the MFMA dequant-GEMM. */
+okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
+                                  const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
+                                  float *out, void *stream);
+
+/* Same contract with bf16 activations x: [rows, in_features] (prefill,
+ * decoded exactly as safetensors_values.rs:115-123). */
+okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t in_features, uint32_t w_type,
+                                       const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
+                                       float *out, void *stream);
+
+/* Explicit-path variants of okq_linear_out_by_in_q (same arguments): the fused
+ * dequant-GEMV (one weight pass per activation row) and the MFMA dequant-GEMM.
+ * For benchmarks and tests that pin a path. */
+okq_status okq_gemv(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                    uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream);
+okq_status okq_gemm(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                    uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream);
+okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                         uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream);
+
+/* ---- instrumentation --------------------------------------------------- */
+
+/* The next compute kernel this thread launches through okq_dequantize,
+ * okq_linear_out_by_in_q*, okq_gemv or okq_gemm* records `start` and `stop`
+ * (hipEvent_t, created with timing enabled) at the begin and end of its
+ * dispatch (hipExtLaunchKernelGGL), so hipEventElapsedTime(start, stop) is
+ * that kernel's own duration.  One-shot: cleared by the launch; pass NULLs to
+ * clear.  Calls that split into several kernels time the first one.  No
+ * counterpart in the reference (its benchmarks time whole phases with
+ * Instant, src/main.rs:419-598). */
+okq_status okq_set_launch_events(void *start, void *stop);
+
+/* ---- data preparation -------------------------------------------------- */
+
+/* Quantize n f32 values (device) into GGUF blocks (device), on the GPU.  The
+ * reference has no quantizer; the algorithm is fixed by the CPU oracle and the
+ * bytes match it exactly. */
+okq_status okq_quantize(uint32_t ggml_type, const float *src, int64_t n, void *dst, void *stream);
+
+/* dst[i] = N(0, sigma) sample number (offset + i) of stream `seed`
+ * (SplitMix64 counter stream, Irwin-Hall of twelve 24-bit uniforms summed in
+ * integers): identical floats on CPU and GPU. */
+okq_status okq_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst, void *stream);
+
+/* f32 -> bf16, round to nearest even. */
+okq_status okq_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, void *stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OKQ_H */

@@ -1,0 +1,9 @@
+"""ocelotl_amd -- MI355X (gfx950) k-quant linear path for Ocelotl.
+
+Q8_0 / Q4_K / Q6_K GGUF weights, dequantized and contracted against
+activations by hand-written HIP kernels in ``libokq.so`` (C-ABI:
+``include/okq.h``).  ``ocelotl_amd.okq`` is the ctypes binding,
+``ocelotl_amd.backend`` the host mirror of the reference's KernelBackend
+linear surface, ``ocelotl_amd.gguf`` the GGUF tensor-payload loader.
+"""
+__all__ = ["okq", "backend", "build"]

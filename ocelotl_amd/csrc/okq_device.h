@@ -1,0 +1,102 @@
+// okq_device.h -- device-side helpers shared by the gfx950 kernels.
+//
+// GGUF block layouts (public GGUF spec; the reference stops at the type tag,
+// crates/loader/src/gguf_inspect.rs:170-219):
+//   Q8_0  34 B / 32 weights : f16 d | i8 qs[32]
+//   Q4_K 144 B / 256 weights: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
+//   Q6_K 210 B / 256 weights: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace okq {
+
+constexpr int kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
+constexpr int kQ8Bytes = 34, kQ4KBytes = 144, kQ6KBytes = 210;
+
+__device__ __forceinline__ float as_f32(uint32_t u) { return __uint_as_float(u); }
+__device__ __forceinline__ uint32_t as_u32(float f) { return __float_as_uint(f); }
+
+// Exact binary16 -> binary32 decode written with integer ops, matching
+// f16_bits_to_f32 (crates/loader/src/safetensors_values.rs:155-183) bit for
+// bit, NaN payloads included.  Subnormals: frac * 2^-24 is exact in f32.
+__device__ __forceinline__ float f16_bits_exact(uint32_t h) {
+  uint32_t sign = (h & 0x8000u) << 16;
+  uint32_t exp = (h >> 10) & 0x1fu;
+  uint32_t frac = h & 0x3ffu;
+  if (exp == 0x1f) return as_f32(sign | 0x7f800000u | (frac << 13));
+  if (exp != 0) return as_f32(sign | ((exp + 112u) << 23) | (frac << 13));
+  float v = __fmul_rn((float)frac, 5.9604644775390625e-08f);  // 2^-24
+  return as_f32(as_u32(v) | sign);
+}
+
+// Hardware conversion for the hot loops (exact for every non-NaN input).
+__device__ __forceinline__ float f16_bits_hw(uint32_t h) {
+  _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);
+  return (float)v;
+}
+
+// Realign a window of bytes that starts r (0 or 2) bytes into dword w0:
+// returns bytes [r, r+4) of (w1:w0).
+__device__ __forceinline__ uint32_t realign(uint32_t w1, uint32_t w0, uint32_t r) {
+  return __builtin_amdgcn_alignbyte(w1, w0, r);
+}
+
+// Signed 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
+__device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
+}
+
+// Wave-wide sum (64 lanes) with a fixed order: DPP within rows of 16, then
+// the four row sums combined with readlane.  Result is uniform.
+__device__ __forceinline__ float wave_sum(float v) {
+  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
+  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
+  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
+  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x140, 0xf, 0xf, false));  // row_mirror
+  float r0 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 0));
+  float r1 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 16));
+  float r2 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 32));
+  float r3 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 48));
+  return (r0 + r1) + (r2 + r3);
+}
+
+// Activation quantisation for the integer dot path.  A run of floats is
+// scaled by a power of two 2^-e chosen so that max|x| * 2^-e <= 32640, rounded
+// to an integer q and split as q = hi * 256 + lo with hi, lo in [-128, 127];
+// the weights' small integers then contract with hi and lo exactly through
+// v_dot4_i32_i8.  The scaling is exact (v_ldexp_f32); the only approximation
+// is the rounding of q, |error| <= 2^e / 2 <= max|x| * 2^-15.
+__device__ __forceinline__ int x_exp(float amax) {
+  int E = __builtin_amdgcn_frexp_expf(amax);    // amax = f * 2^E, f in [0.5, 1)
+  float f = __builtin_amdgcn_frexp_mantf(amax);
+  return (f > 0.99609375f) ? E - 14 : E - 15;
+}
+
+__device__ __forceinline__ void x_split(float v, int e, int &hi, int &lo) {
+  int q = (int)__builtin_rintf(ldexpf(v, -e));
+  hi = (q + 128) >> 8;
+  lo = q - (hi << 8);
+}
+
+// Pack four int8 lanes (low byte of each) into a dword, byte 0 first.
+__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
+  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
+         ((uint32_t)(d & 0xff) << 24);
+}
+
+// Q4_K 6-bit (scale, min) of sub-block j from the packed scale dwords
+// s0 = bytes 0..3, s1 = bytes 4..7, s2 = bytes 8..11 (GGUF spec).
+__device__ __forceinline__ void q4k_scale_min(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                              uint32_t &m) {
+  if (j < 4) {
+    sc = (s0 >> (8 * j)) & 63u;
+    m = (s1 >> (8 * j)) & 63u;
+  } else {
+    uint32_t jj = j - 4;
+    sc = ((s2 >> (8 * jj)) & 15u) | (((s0 >> (8 * jj + 6)) & 3u) << 4);
+    m = ((s2 >> (8 * jj + 4)) & 15u) | (((s1 >> (8 * jj + 6)) & 3u) << 4);
+  }
+}
+
+}  // namespace okq

@@ -1,0 +1,47 @@
+// okq_internal.h -- launcher declarations shared by the C-ABI layer and the
+// kernel translation units.  Every launcher assumes its arguments were
+// validated by okq_runtime.hip (shapes, alignment, 32-bit index ranges).
+#pragma once
+#include <hip/hip_ext.h>
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace okq {
+
+// Optional dispatch-timing events for the next launch (see
+// okq_set_launch_events).  take_launch_events() returns and clears them.
+struct LaunchEvents {
+  hipEvent_t start = nullptr, stop = nullptr;
+};
+LaunchEvents take_launch_events();
+
+// Launch `kernel` on s, recording the thread's pending timing events if any.
+template <typename... KArgs, typename... Args>
+inline void launch_timed(void (*kernel)(KArgs...), dim3 grid, dim3 block, unsigned shmem, hipStream_t s,
+                         Args... args) {
+  LaunchEvents ev = take_launch_events();
+  if (ev.start || ev.stop) {
+    hipExtLaunchKernelGGL(kernel, grid, block, shmem, s, ev.start, ev.stop, 0, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, shmem, s, args...);
+  }
+}
+
+hipError_t launch_dequantize(int type, const void *src, int64_t n, float *dst, hipStream_t s);
+hipError_t launch_quantize(int type, const float *src, int64_t n, void *dst, hipStream_t s);
+hipError_t launch_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst, hipStream_t s);
+hipError_t launch_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, hipStream_t s);
+
+// Fused dequant-GEMV for one activation row: y[o] = bias[o] + sum_k x[k] W[o,k].
+// cu_count sizes the persistent grid.
+hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
+                       int cu_count, hipStream_t s);
+
+// MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
+hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
+                       const float *bias, float *y, int cu_count, hipStream_t s);
+
+// True when launch_gemm supports this (type, K, N).
+bool gemm_supported(int type, int64_t K, int64_t N);
+
+}  // namespace okq

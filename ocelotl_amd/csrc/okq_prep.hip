@@ -1,0 +1,294 @@
+// okq_prep.hip -- bit-exact dequantize, quantize, seeded generator and
+// f32->bf16 kernels.  Compiled with -ffp-contract=off: every product and
+// difference is rounded on its own, in the order the GGUF spec writes it, so
+// results equal the CPU oracle bit for bit.
+#include "okq_device.h"
+#include "okq_internal.h"
+
+namespace okq {
+
+// ---------------------------------------------------------------------------
+// dequantize: one thread per output element (coalesced f32 stores; the block
+// bytes a wave touches are shared through the cache).
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
+  return (uint32_t)(*reinterpret_cast<const uint16_t *>(p));  // blocks are 2-byte aligned
+}
+
+__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ src, int64_t n,
+                                                           float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint8_t *blk = src + (i >> 5) * kQ8Bytes;
+  float d = f16_bits_exact(ld_u16(blk));
+  float q = (float)(int8_t)blk[2 + (i & 31)];
+  dst[i] = __fmul_rn(q, d);
+}
+
+__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src, int64_t n,
+                                                           float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint8_t *blk = src + (i >> 8) * kQ4KBytes;
+  uint32_t r = (uint32_t)(i & 255);
+  uint32_t c = r >> 6, hi = (r >> 5) & 1u, l = r & 31u;
+  uint32_t j = 2 * c + hi;
+  const uint32_t *w = reinterpret_cast<const uint32_t *>(blk);  // 144-byte blocks are 16-byte aligned
+  uint32_t sc, m;
+  q4k_scale_min(j, w[1], w[2], w[3], sc, m);
+  float d = f16_bits_exact(w[0] & 0xffffu);
+  float dmin = f16_bits_exact(w[0] >> 16);
+  uint32_t q = (blk[16 + 32 * c + l] >> (4 * hi)) & 15u;
+  float ds = __fmul_rn(d, (float)sc);
+  float dm = __fmul_rn(dmin, (float)m);
+  dst[i] = __fsub_rn(__fmul_rn(ds, (float)q), dm);
+}
+
+__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src, int64_t n,
+                                                           float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const uint8_t *blk = src + (i >> 8) * kQ6KBytes;
+  uint32_t r = (uint32_t)(i & 255);
+  uint32_t h = r >> 7, quarter = (r >> 5) & 3u, l = r & 31u;
+  uint32_t qlb = blk[64 * h + l + ((quarter & 1u) ? 32u : 0u)];
+  uint32_t lo4 = (qlb >> ((quarter & 2u) ? 4u : 0u)) & 15u;
+  uint32_t hi2 = (blk[128 + 32 * h + l] >> (2 * quarter)) & 3u;
+  int q = (int)(lo4 | (hi2 << 4)) - 32;
+  int sc = (int8_t)blk[192 + 8 * h + l / 16 + 2 * quarter];
+  float d = f16_bits_exact(ld_u16(blk + 208));
+  dst[i] = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+}
+
+// ---------------------------------------------------------------------------
+// Quantizers: one thread per block.  Step for step the algorithm of the CPU
+// oracle (comparisons written as a < b ? a : b, correctly rounded division,
+// round-to-nearest-even), so the bytes are identical.
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ float minf_(float a, float b) { return a < b ? a : b; }
+__device__ __forceinline__ float maxf_(float a, float b) { return a > b ? a : b; }
+__device__ __forceinline__ int clampi_(int v, int lo, int hi) { return v < lo ? lo : (v > hi ? hi : v); }
+__device__ __forceinline__ uint32_t f32_to_f16_bits(float f) {
+  return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f);  // v_cvt_f16_f32, round to nearest even
+}
+__device__ __forceinline__ void st_u16(uint8_t *p, uint32_t v) {
+  p[0] = (uint8_t)v;
+  p[1] = (uint8_t)(v >> 8);
+}
+
+__global__ __launch_bounds__(64) void quantize_q8_0_kernel(const float *__restrict__ x, int64_t nblocks,
+                                                            uint8_t *__restrict__ dst) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const float *xb = x + b * 32;
+  uint8_t *blk = dst + b * kQ8Bytes;
+  float amax = 0.0f;
+  for (int j = 0; j < 32; ++j) amax = maxf_(amax, fabsf(xb[j]));
+  float d = __fdiv_rn(amax, 127.0f);
+  float id = d != 0.0f ? __fdiv_rn(1.0f, d) : 0.0f;
+  st_u16(blk, f32_to_f16_bits(d));
+  for (int j = 0; j < 32; ++j) {
+    int q = (int)__builtin_rintf(__fmul_rn(xb[j], id));
+    blk[2 + j] = (uint8_t)(int8_t)clampi_(q, -127, 127);
+  }
+}
+
+__global__ __launch_bounds__(64) void quantize_q4_k_kernel(const float *__restrict__ x, int64_t nblocks,
+                                                            uint8_t *__restrict__ dst) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const float *xb = x + b * 256;
+  uint8_t *blk = dst + b * kQ4KBytes;
+  float scale[8], mmin[8];
+  float max_scale = 0.0f, max_min = 0.0f;
+  for (int s = 0; s < 8; ++s) {
+    float mn = xb[32 * s], mx = xb[32 * s];
+    for (int j = 1; j < 32; ++j) {
+      mn = minf_(mn, xb[32 * s + j]);
+      mx = maxf_(mx, xb[32 * s + j]);
+    }
+    mn = minf_(mn, 0.0f);
+    scale[s] = __fdiv_rn(__fsub_rn(mx, mn), 15.0f);
+    mmin[s] = -mn;
+    max_scale = maxf_(max_scale, scale[s]);
+    max_min = maxf_(max_min, mmin[s]);
+  }
+  float inv_scale = max_scale > 0.0f ? __fdiv_rn(63.0f, max_scale) : 0.0f;
+  float inv_min = max_min > 0.0f ? __fdiv_rn(63.0f, max_min) : 0.0f;
+  uint32_t ls[8], lm[8];
+  for (int s = 0; s < 8; ++s) {
+    ls[s] = (uint32_t)clampi_((int)__builtin_rintf(__fmul_rn(inv_scale, scale[s])), 0, 63);
+    lm[s] = (uint32_t)clampi_((int)__builtin_rintf(__fmul_rn(inv_min, mmin[s])), 0, 63);
+  }
+  uint32_t dh = f32_to_f16_bits(__fdiv_rn(max_scale, 63.0f));
+  uint32_t dminh = f32_to_f16_bits(__fdiv_rn(max_min, 63.0f));
+  st_u16(blk, dh);
+  st_u16(blk + 2, dminh);
+  uint32_t sc[12];
+  for (int j = 0; j < 4; ++j) {
+    sc[j] = ls[j] | ((ls[j + 4] >> 4) << 6);
+    sc[j + 4] = lm[j] | ((lm[j + 4] >> 4) << 6);
+    sc[j + 8] = (ls[j + 4] & 15u) | ((lm[j + 4] & 15u) << 4);
+  }
+  for (int j = 0; j < 12; ++j) blk[4 + j] = (uint8_t)sc[j];
+  float d16 = f16_bits_exact(dh), dmin16 = f16_bits_exact(dminh);
+  uint8_t *qs = blk + 16;
+  for (int c = 0; c < 4; ++c) {
+    float de0 = __fmul_rn(d16, (float)ls[2 * c]), me0 = __fmul_rn(dmin16, (float)lm[2 * c]);
+    float de1 = __fmul_rn(d16, (float)ls[2 * c + 1]), me1 = __fmul_rn(dmin16, (float)lm[2 * c + 1]);
+    for (int l = 0; l < 32; ++l) {
+      int q0 = 0, q1 = 0;
+      if (de0 != 0.0f) q0 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + l], me0), de0)), 0, 15);
+      if (de1 != 0.0f)
+        q1 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + 32 + l], me1), de1)), 0, 15);
+      qs[32 * c + l] = (uint8_t)(q0 | (q1 << 4));
+    }
+  }
+}
+
+__global__ __launch_bounds__(64) void quantize_q6_k_kernel(const float *__restrict__ x, int64_t nblocks,
+                                                            uint8_t *__restrict__ dst) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  const float *xb = x + b * 256;
+  uint8_t *blk = dst + b * kQ6KBytes;
+  float scale[16];
+  float max_scale = 0.0f, max_abs_scale = 0.0f;
+  for (int s = 0; s < 16; ++s) {
+    float mx = 0.0f, amax = 0.0f;
+    for (int j = 0; j < 16; ++j) {
+      float v = xb[16 * s + j];
+      float a = fabsf(v);
+      if (a > amax) {
+        amax = a;
+        mx = v;
+      }
+    }
+    scale[s] = __fdiv_rn(-mx, 32.0f);
+    float as = fabsf(scale[s]);
+    if (as > max_abs_scale) {
+      max_abs_scale = as;
+      max_scale = scale[s];
+    }
+  }
+  float iscale = max_scale != 0.0f ? __fdiv_rn(-128.0f, max_scale) : 0.0f;
+  float d = iscale != 0.0f ? __fdiv_rn(1.0f, iscale) : 0.0f;
+  uint32_t dh = f32_to_f16_bits(d);
+  float d16 = f16_bits_exact(dh);
+  int scs[16];
+  for (int s = 0; s < 16; ++s) scs[s] = clampi_((int)__builtin_rintf(__fmul_rn(iscale, scale[s])), -128, 127);
+  for (int h = 0; h < 2; ++h) {
+    for (int l = 0; l < 32; ++l) {
+      uint32_t L[4];
+      for (int qq = 0; qq < 4; ++qq) {
+        int e = 128 * h + 32 * qq + l;
+        int s = e >> 4;
+        float de = __fmul_rn(d16, (float)scs[s]);
+        int q = 0;
+        if (de != 0.0f) q = clampi_((int)__builtin_rintf(__fdiv_rn(xb[e], de)), -32, 31);
+        L[qq] = (uint32_t)(q + 32);
+      }
+      blk[64 * h + l] = (uint8_t)((L[0] & 15u) | ((L[2] & 15u) << 4));
+      blk[64 * h + 32 + l] = (uint8_t)((L[1] & 15u) | ((L[3] & 15u) << 4));
+      blk[128 + 32 * h + l] = (uint8_t)((L[0] >> 4) | ((L[1] >> 4) << 2) | ((L[2] >> 4) << 4) | ((L[3] >> 4) << 6));
+    }
+  }
+  for (int s = 0; s < 16; ++s) blk[192 + s] = (uint8_t)(int8_t)scs[s];
+  st_u16(blk + 208, dh);
+}
+
+// ---------------------------------------------------------------------------
+// Seeded N(0, sigma) and f32 -> bf16
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+  z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+  return z ^ (z >> 31);
+}
+
+__global__ __launch_bounds__(256) void fill_normal_kernel(uint64_t key, int64_t offset, int64_t n, float sigma,
+                                                          float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint64_t gi = (uint64_t)(offset + i);
+  int32_t s = 0;
+  for (int j = 0; j < 6; ++j) {
+    uint64_t z = mix64(key + (gi * 6u + (uint64_t)j + 1u) * 0x9E3779B97F4A7C15ull);
+    s += (int32_t)(z & 0xffffffu) + (int32_t)((z >> 32) & 0xffffffu);
+  }
+  s -= 6 * 0xffffff;
+  float u = __fmul_rn((float)s, 5.9604644775390625e-08f);
+  dst[i] = __fmul_rn(u, sigma);
+}
+
+__global__ __launch_bounds__(256) void f32_to_bf16_kernel(const float *__restrict__ src, int64_t n,
+                                                          uint16_t *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  uint32_t u = as_u32(src[i]);
+  if ((u & 0x7fffffffu) > 0x7f800000u) {
+    dst[i] = (uint16_t)((u >> 16) | 0x40u);
+    return;
+  }
+  u += 0x7fffu + ((u >> 16) & 1u);
+  dst[i] = (uint16_t)(u >> 16);
+}
+
+// ---------------------------------------------------------------------------
+// launchers
+// ---------------------------------------------------------------------------
+
+static inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n + threads - 1) / threads); }
+
+hipError_t launch_dequantize(int type, const void *src, int64_t n, float *dst, hipStream_t s) {
+  const uint8_t *p = static_cast<const uint8_t *>(src);
+  switch (type) {
+  case kQ8_0: launch_timed(dequant_q8_0_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  case kQ4_K: launch_timed(dequant_q4_k_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  case kQ6_K: launch_timed(dequant_q6_k_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_quantize(int type, const float *src, int64_t n, void *dst, hipStream_t s) {
+  uint8_t *p = static_cast<uint8_t *>(dst);
+  switch (type) {
+  case kQ8_0: {
+    int64_t nb = n / 32;
+    hipLaunchKernelGGL(quantize_q8_0_kernel, dim3(grid_for(nb, 64)), dim3(64), 0, s, src, nb, p);
+    break;
+  }
+  case kQ4_K: {
+    int64_t nb = n / 256;
+    hipLaunchKernelGGL(quantize_q4_k_kernel, dim3(grid_for(nb, 64)), dim3(64), 0, s, src, nb, p);
+    break;
+  }
+  case kQ6_K: {
+    int64_t nb = n / 256;
+    hipLaunchKernelGGL(quantize_q6_k_kernel, dim3(grid_for(nb, 64)), dim3(64), 0, s, src, nb, p);
+    break;
+  }
+  default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst, hipStream_t s) {
+  uint64_t key = seed;
+  key = (key ^ (key >> 30)) * 0xBF58476D1CE4E5B9ull;
+  key = (key ^ (key >> 27)) * 0x94D049BB133111EBull;
+  key = key ^ (key >> 31);
+  hipLaunchKernelGGL(fill_normal_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, key, offset, n, sigma, dst);
+  return hipGetLastError();
+}
+
+hipError_t launch_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, hipStream_t s) {
+  hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, src, n, dst);
+  return hipGetLastError();
+}
+
+}  // namespace okq

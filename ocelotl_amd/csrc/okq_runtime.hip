@@ -1,0 +1,398 @@
+// okq_runtime.hip -- the C-ABI of libokq.so (declared in include/okq.h).
+//
+// Every entry point validates its arguments before anything is launched and
+// maps failures to okq_status + a per-thread message, mirroring
+// validate_linear_out_by_in (crates/kernels/src/lib.rs:2443-2497) and the
+// error conventions of docs/design/kernels.md:96-99.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <mutex>
+#include <string>
+
+#include "../../include/okq.h"
+#include "okq_internal.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+thread_local okq::LaunchEvents g_launch_events;
+
+okq_status fail(okq_status st, const char *fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return st;
+}
+
+okq_status ok() { return OKQ_OK; }
+
+struct TypeInfo {
+  int64_t elems, bytes;
+  bool quantized;
+};
+
+bool type_info(uint32_t t, TypeInfo &ti) {
+  switch (t) {
+  case OKQ_TYPE_Q8_0: ti = {32, 34, true}; return true;
+  case OKQ_TYPE_Q4_K: ti = {256, 144, true}; return true;
+  case OKQ_TYPE_Q6_K: ti = {256, 210, true}; return true;
+  case OKQ_TYPE_F32: ti = {1, 4, false}; return true;
+  case OKQ_TYPE_F16: ti = {1, 2, false}; return true;
+  case OKQ_TYPE_BF16: ti = {1, 2, false}; return true;
+  default: return false;
+  }
+}
+
+const char *type_name(uint32_t t) {
+  switch (t) {
+  case OKQ_TYPE_Q8_0: return "Q8_0";
+  case OKQ_TYPE_Q4_K: return "Q4K";
+  case OKQ_TYPE_Q6_K: return "Q6K";
+  case OKQ_TYPE_F32: return "F32";
+  case OKQ_TYPE_F16: return "F16";
+  case OKQ_TYPE_BF16: return "BF16";
+  default: return "Unknown";
+  }
+}
+
+okq_status unsupported_type(uint32_t t, const char *what) {
+  return fail(OKQ_E_TYPE, "unsupported %s: tensor type %s (%u); supported: Q8_0, Q4K, Q6K", what, type_name(t),
+              t);
+}
+
+bool mul_ok(int64_t a, int64_t b, int64_t &out) {
+  if (a < 0 || b < 0) return false;
+  if (a != 0 && b > INT64_MAX / a) return false;
+  out = a * b;
+  return true;
+}
+
+// ---- device context ---------------------------------------------------------
+
+struct DevInfo {
+  bool probed = false;
+  bool ok = false;
+  int cu_count = 0;
+  char arch[64] = {0};
+};
+
+std::mutex g_dev_mutex;
+DevInfo g_dev[64];
+
+okq_status current_device(int &dev, DevInfo &info) {
+  if (hipGetDevice(&dev) != hipSuccess) return fail(OKQ_E_NODEV, "hip-gfx950: no HIP device available");
+  if (dev < 0 || dev >= 64) return fail(OKQ_E_NODEV, "hip-gfx950: device ordinal %d out of range", dev);
+  std::lock_guard<std::mutex> lock(g_dev_mutex);
+  DevInfo &d = g_dev[dev];
+  if (!d.probed) {
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, dev) != hipSuccess) return fail(OKQ_E_NODEV, "hip-gfx950: cannot query device %d", dev);
+    d.probed = true;
+    d.cu_count = prop.multiProcessorCount;
+    strncpy(d.arch, prop.gcnArchName, sizeof d.arch - 1);
+    d.ok = strncmp(prop.gcnArchName, "gfx950", 6) == 0;
+  }
+  info = d;
+  if (!d.ok) return fail(OKQ_E_NODEV, "hip-gfx950: device %d is %s, this library is built for gfx950", dev, d.arch);
+  return ok();
+}
+
+okq_status hip_status(hipError_t e, const char *what) {
+  if (e == hipSuccess) return ok();
+  return fail(OKQ_E_LAUNCH, "hip-gfx950: %s failed: %s", what, hipGetErrorString(e));
+}
+
+// ---- linear validation --------------------------------------------------------
+
+struct LinearArgs {
+  int64_t rows, K, N;
+  uint32_t type;
+  uint64_t w_bytes;
+};
+
+// Mirrors validate_linear_out_by_in: lengths first (weight bytes replace the
+// f32 weight length), then the block and 32-bit limits of the kernels.
+okq_status validate_linear(const void *x, const LinearArgs &a, const void *w, const void *out, bool x_bf16) {
+  TypeInfo ti;
+  if (!type_info(a.type, ti) || !ti.quantized) return unsupported_type(a.type, "linear_out_by_in weight");
+  if (a.rows < 0 || a.K < 0 || a.N < 0)
+    return fail(OKQ_E_SHAPE, "linear_out_by_in negative dimension rows=%lld in_features=%lld out_features=%lld",
+                (long long)a.rows, (long long)a.K, (long long)a.N);
+  if (a.K == 0 || a.K % ti.elems != 0)
+    return fail(OKQ_E_SHAPE, "linear_out_by_in in_features=%lld is not a positive multiple of the %s block size %lld",
+                (long long)a.K, type_name(a.type), (long long)ti.elems);
+  int64_t xe, oe, row_bytes, we;
+  if (!mul_ok(a.rows, a.K, xe)) return fail(OKQ_E_SHAPE, "linear_out_by_in x length rows*in_features overflows");
+  if (!mul_ok(a.rows, a.N, oe)) return fail(OKQ_E_SHAPE, "linear_out_by_in out length rows*out_features overflows");
+  row_bytes = a.K / ti.elems * ti.bytes;
+  if (!mul_ok(a.N, row_bytes, we)) return fail(OKQ_E_SHAPE, "linear_out_by_in weight byte length overflows");
+  if ((uint64_t)we != a.w_bytes)
+    return fail(OKQ_E_SHAPE,
+                "linear_out_by_in weight bytes=%llu does not match out_features*row_bytes(in_features)=%lld*%lld=%lld",
+                (unsigned long long)a.w_bytes, (long long)a.N, (long long)row_bytes, (long long)we);
+  if (a.N > INT32_MAX || a.K > INT32_MAX || a.rows > INT32_MAX)
+    return fail(OKQ_E_SHAPE, "linear_out_by_in dimension exceeds u32 launch limits");
+  if (a.rows == 0 || a.N == 0) return ok();
+  if (!x || !w || !out) return fail(OKQ_E_ARG, "linear_out_by_in null pointer (x=%p w=%p out=%p)", x, w, out);
+  const uintptr_t xa = reinterpret_cast<uintptr_t>(x);
+  if (xa & (x_bf16 ? 3u : 15u))
+    return fail(OKQ_E_ALIGN, "linear_out_by_in x must be %d-byte aligned", x_bf16 ? 4 : 16);
+  if (reinterpret_cast<uintptr_t>(w) & 3u) return fail(OKQ_E_ALIGN, "linear_out_by_in weight must be 4-byte aligned");
+  if (reinterpret_cast<uintptr_t>(out) & 3u) return fail(OKQ_E_ALIGN, "linear_out_by_in out must be 4-byte aligned");
+  return ok();
+}
+
+enum class Path { Auto, Gemv, Gemm };
+
+// Rows at or below this count run the GEMV once per row (each pass streams the
+// weights once); above it the MFMA GEMM reuses each dequantised tile across
+// the rows.
+constexpr int64_t kGemvMaxRows = 4;
+
+okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint32_t type, const void *w,
+                       uint64_t w_bytes, int64_t N, const float *bias, float *out, void *stream, Path path) {
+  LinearArgs a{rows, K, N, type, w_bytes};
+  okq_status st = validate_linear(x, a, w, out, x_bf16);
+  if (st != OKQ_OK) return st;
+  if (rows == 0 || N == 0) return ok();
+  int dev;
+  DevInfo info;
+  st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  bool use_gemm = false;
+  if (path == Path::Gemm) {
+    if (!okq::gemm_supported((int)type, K, N))
+      return fail(OKQ_E_SHAPE, "okq_gemm: shape in_features=%lld out_features=%lld not supported by the MFMA path",
+                  (long long)K, (long long)N);
+    use_gemm = true;
+  } else if (path == Path::Auto) {
+    use_gemm = (x_bf16 || rows > kGemvMaxRows) && okq::gemm_supported((int)type, K, N);
+  }
+  if (use_gemm) return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, info.cu_count, s), "gemm launch");
+  if (x_bf16) return fail(OKQ_E_SHAPE, "bf16 activations need the MFMA path, which does not support this shape");
+  const float *xf = static_cast<const float *>(x);
+  for (int64_t r = 0; r < rows; ++r) {
+    hipError_t e = okq::launch_gemv((int)type, xf + r * K, K, w, N, bias, out + r * N, info.cu_count, s);
+    if (e != hipSuccess) return hip_status(e, "gemv launch");
+  }
+  return ok();
+}
+
+}  // namespace
+
+namespace okq {
+LaunchEvents take_launch_events() {
+  LaunchEvents e = g_launch_events;
+  g_launch_events = LaunchEvents{};
+  return e;
+}
+}  // namespace okq
+
+extern "C" {
+
+okq_status okq_set_launch_events(void *start, void *stop) {
+  g_launch_events.start = static_cast<hipEvent_t>(start);
+  g_launch_events.stop = static_cast<hipEvent_t>(stop);
+  return ok();
+}
+
+const char *okq_backend_name(void) { return "hip-gfx950"; }
+
+size_t okq_last_error(char *buf, size_t len) {
+  if (buf && len) {
+    size_t n = g_last_error.size() < len - 1 ? g_last_error.size() : len - 1;
+    memcpy(buf, g_last_error.data(), n);
+    buf[n] = '\0';
+  }
+  return g_last_error.size();
+}
+
+okq_status okq_type_info(uint32_t ggml_type, int64_t *block_elems, int64_t *block_bytes) {
+  TypeInfo ti;
+  if (!type_info(ggml_type, ti)) return unsupported_type(ggml_type, "tensor type");
+  if (block_elems) *block_elems = ti.elems;
+  if (block_bytes) *block_bytes = ti.bytes;
+  return ok();
+}
+
+okq_status okq_row_bytes(uint32_t ggml_type, int64_t ne0, int64_t *out_bytes) {
+  TypeInfo ti;
+  if (!type_info(ggml_type, ti)) return unsupported_type(ggml_type, "tensor type");
+  if (!out_bytes) return fail(OKQ_E_ARG, "okq_row_bytes: out_bytes is null");
+  if (ne0 <= 0 || ne0 % ti.elems != 0)
+    return fail(OKQ_E_SHAPE, "row of %lld elements is not a positive multiple of the %s block size %lld",
+                (long long)ne0, type_name(ggml_type), (long long)ti.elems);
+  int64_t v;
+  if (!mul_ok(ne0 / ti.elems, ti.bytes, v)) return fail(OKQ_E_SHAPE, "row byte length overflows");
+  *out_bytes = v;
+  return ok();
+}
+
+okq_status okq_tensor_bytes(uint32_t ggml_type, const int64_t *shape, int n_dims, uint64_t *out_bytes) {
+  if (!shape || !out_bytes || n_dims <= 0 || n_dims > 8)
+    return fail(OKQ_E_ARG, "okq_tensor_bytes: need 1..8 dims and non-null pointers");
+  for (int i = 0; i < n_dims; ++i)
+    if (shape[i] <= 0) return fail(OKQ_E_SHAPE, "tensor has a non-positive dimension %lld", (long long)shape[i]);
+  int64_t row;
+  okq_status st = okq_row_bytes(ggml_type, shape[0], &row);
+  if (st != OKQ_OK) return st;
+  int64_t total = row;
+  for (int i = 1; i < n_dims; ++i)
+    if (!mul_ok(total, shape[i], total)) return fail(OKQ_E_SHAPE, "tensor byte length overflows");
+  *out_bytes = (uint64_t)total;
+  return ok();
+}
+
+okq_status okq_device_count(int *count) {
+  if (!count) return fail(OKQ_E_ARG, "okq_device_count: null pointer");
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return ok();
+}
+
+okq_status okq_init(int ordinal) {
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess || n == 0) return fail(OKQ_E_NODEV, "hip-gfx950: no HIP device available");
+  if (ordinal < 0 || ordinal >= n)
+    return fail(OKQ_E_NODEV, "hip-gfx950: device ordinal %d out of range (%d devices)", ordinal, n);
+  if (hipSetDevice(ordinal) != hipSuccess) return fail(OKQ_E_NODEV, "hip-gfx950: cannot select device %d", ordinal);
+  int dev;
+  DevInfo info;
+  return current_device(dev, info);
+}
+
+okq_status okq_alloc(void **ptr, size_t bytes) {
+  if (!ptr) return fail(OKQ_E_ARG, "okq_alloc: null pointer");
+  *ptr = nullptr;
+  if (bytes == 0) return ok();
+  if (hipMalloc(ptr, bytes) != hipSuccess) {
+    *ptr = nullptr;
+    return fail(OKQ_E_ALLOC, "hip-gfx950: hipMalloc of %zu bytes failed", bytes);
+  }
+  return ok();
+}
+
+okq_status okq_free(void *ptr) {
+  if (!ptr) return ok();
+  return hip_status(hipFree(ptr), "hipFree");
+}
+
+okq_status okq_memcpy_h2d(void *dst, const void *src, size_t bytes, void *stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(OKQ_E_ARG, "okq_memcpy_h2d: null pointer");
+  return hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, static_cast<hipStream_t>(stream)),
+                    "hipMemcpyAsync(H2D)");
+}
+
+okq_status okq_memcpy_d2h(void *dst, const void *src, size_t bytes, void *stream) {
+  if (bytes == 0) return ok();
+  if (!dst || !src) return fail(OKQ_E_ARG, "okq_memcpy_d2h: null pointer");
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  okq_status st = hip_status(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, s), "hipMemcpyAsync(D2H)");
+  if (st != OKQ_OK) return st;
+  return hip_status(hipStreamSynchronize(s), "hipStreamSynchronize");
+}
+
+okq_status okq_sync(void *stream) {
+  return hip_status(hipStreamSynchronize(static_cast<hipStream_t>(stream)), "hipStreamSynchronize");
+}
+
+okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float *dst, void *stream) {
+  TypeInfo ti;
+  if (!type_info(ggml_type, ti) || !ti.quantized) return unsupported_type(ggml_type, "dequantize");
+  if (n < 0 || n % ti.elems != 0)
+    return fail(OKQ_E_SHAPE, "dequantize n=%lld is not a multiple of the %s block size %lld", (long long)n,
+                type_name(ggml_type), (long long)ti.elems);
+  if (n == 0) return ok();
+  if (!src || !dst) return fail(OKQ_E_ARG, "dequantize null pointer");
+  if (ggml_type == OKQ_TYPE_Q4_K ? (reinterpret_cast<uintptr_t>(src) & 15u) : (reinterpret_cast<uintptr_t>(src) & 1u))
+    return fail(OKQ_E_ALIGN, "dequantize source must be %d-byte aligned", ggml_type == OKQ_TYPE_Q4_K ? 16 : 2);
+  if (reinterpret_cast<uintptr_t>(dst) & 3u) return fail(OKQ_E_ALIGN, "dequantize destination must be 4-byte aligned");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_dequantize((int)ggml_type, src, n, dst, static_cast<hipStream_t>(stream)),
+                    "dequantize launch");
+}
+
+okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                                  uint64_t w_bytes, int64_t out_features, const float *bias, float *out,
+                                  void *stream) {
+  return linear_impl(x, false, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Auto);
+}
+
+okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t in_features, uint32_t w_type,
+                                       const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
+                                       float *out, void *stream) {
+  return linear_impl(x, true, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Auto);
+}
+
+okq_status okq_gemv(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                    uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream) {
+  return linear_impl(x, false, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Gemv);
+}
+
+okq_status okq_gemm(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                    uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream) {
+  return linear_impl(x, false, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Gemm);
+}
+
+okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
+                         uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream) {
+  return linear_impl(x, true, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Gemm);
+}
+
+okq_status okq_quantize(uint32_t ggml_type, const float *src, int64_t n, void *dst, void *stream) {
+  TypeInfo ti;
+  if (!type_info(ggml_type, ti) || !ti.quantized) return unsupported_type(ggml_type, "quantize");
+  if (n < 0 || n % ti.elems != 0)
+    return fail(OKQ_E_SHAPE, "quantize n=%lld is not a multiple of the %s block size %lld", (long long)n,
+                type_name(ggml_type), (long long)ti.elems);
+  if (n == 0) return ok();
+  if (!src || !dst) return fail(OKQ_E_ARG, "quantize null pointer");
+  if (reinterpret_cast<uintptr_t>(src) & 3u) return fail(OKQ_E_ALIGN, "quantize source must be 4-byte aligned");
+  if (reinterpret_cast<uintptr_t>(dst) & 1u) return fail(OKQ_E_ALIGN, "quantize destination must be 2-byte aligned");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_quantize((int)ggml_type, src, n, dst, static_cast<hipStream_t>(stream)),
+                    "quantize launch");
+}
+
+okq_status okq_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst, void *stream) {
+  if (n < 0 || offset < 0) return fail(OKQ_E_SHAPE, "fill_normal: negative n or offset");
+  if (n == 0) return ok();
+  if (!dst) return fail(OKQ_E_ARG, "fill_normal: null destination");
+  if (reinterpret_cast<uintptr_t>(dst) & 3u) return fail(OKQ_E_ALIGN, "fill_normal destination must be 4-byte aligned");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_fill_normal(seed, offset, n, sigma, dst, static_cast<hipStream_t>(stream)),
+                    "fill_normal launch");
+}
+
+okq_status okq_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, void *stream) {
+  if (n < 0) return fail(OKQ_E_SHAPE, "f32_to_bf16: negative n");
+  if (n == 0) return ok();
+  if (!src || !dst) return fail(OKQ_E_ARG, "f32_to_bf16: null pointer");
+  if ((reinterpret_cast<uintptr_t>(src) & 3u) || (reinterpret_cast<uintptr_t>(dst) & 1u))
+    return fail(OKQ_E_ALIGN, "f32_to_bf16: misaligned pointer");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_f32_to_bf16(src, n, dst, static_cast<hipStream_t>(stream)), "f32_to_bf16 launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+"""Writes the golden fixtures under tests/golden/.
+
+* reference_kats.json -- known-answer vectors copied as data from the
+  reference's own tests: fp16 -> f32 (crates/loader/src/safetensors_values.rs:
+  316-351), bf16 -> f32 (:295-313), GGML type ids (gguf_inspect.rs:178-185)
+  and the GGUF fixture's ne-order shape and q4_k tag
+  (fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json).
+* oracle_vectors.json -- regression vectors produced by the CPU oracle:
+  the first values of the seeded generator and small quantized blocks with
+  their dequantized values.  These pin the oracle against later edits; the
+  oracle itself is pinned by the independent checks in tests/test_oracle_*.py.
+
+Run from the repo root: python tests/golden/make_golden.py
+"""
+import hashlib
+import json
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+from oracle import oracle as O  # noqa: E402
+
+
+def reference_kats():
+    return {
+        "source": {
+            "f16": "crates/loader/src/safetensors_values.rs:316-351",
+            "bf16": "crates/loader/src/safetensors_values.rs:295-313",
+            "type_ids": "crates/loader/src/gguf_inspect.rs:170-206",
+            "gguf_fixture": "fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json",
+        },
+        # (bits, expected f32 bit pattern); 0x7e00 decodes to a NaN
+        "f16": [[0x3C00, 0x3F800000], [0xC100, 0xC0200000], [0x0000, 0x00000000], [0x0400, 0x38800000],
+                [0x0001, 0x33800000], [0x7C00, 0x7F800000]],
+        "f16_nan": [0x7E00],
+        "bf16": [[0x3F80, 0x3F800000], [0xC020, 0xC0200000], [0x0000, 0x00000000], [0x7F80, 0x7F800000]],
+        "type_ids": {"F32": 0, "F16": 1, "Q8_0": 8, "Q4K": 12, "Q6K": 14, "BF16": 30},
+        "gguf_fixture_token_embd": {"name": "token_embd.weight", "shape": [2560, 262144], "tensor_type": "q4_k"},
+    }
+
+
+def oracle_vectors(o):
+    seeds = [0, 1, 0x5EED, 2**63 + 12345]
+    rng = {str(s): [float(v) for v in o.normal(s, 16, 1.0)] for s in seeds}
+    blocks = {}
+    for t, name in ((O.Q8_0, "Q8_0"), (O.Q4_K, "Q4_K"), (O.Q6_K, "Q6_K")):
+        x = o.normal(1000 + t, 512, 0.02)
+        q = o.quantize(t, x)
+        y = o.dequantize(t, q, 512)
+        big = o.quantize(t, o.normal(2000 + t, 4096 * 16, 0.02))
+        blocks[name] = {
+            "seed": 1000 + t, "n": 512, "sigma": 0.02,
+            "blocks_hex": q.tobytes().hex(),
+            "dequant_f32_bits": [int(v) for v in y.view(np.uint32)],
+            "sha256_4096x16_seed": 2000 + t,
+            "sha256_4096x16": hashlib.sha256(big.tobytes()).hexdigest(),
+        }
+    return {"generator": "SplitMix64 + Irwin-Hall(12), okr_normal_at", "normal_first16": rng, "blocks": blocks}
+
+
+if __name__ == "__main__":
+    O.build()
+    o = O.Oracle()
+    with open(os.path.join(HERE, "reference_kats.json"), "w") as f:
+        json.dump(reference_kats(), f, indent=1)
+    with open(os.path.join(HERE, "oracle_vectors.json"), "w") as f:
+        json.dump(oracle_vectors(o), f, indent=1)
+    print("wrote", os.listdir(HERE))

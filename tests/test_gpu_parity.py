@@ -1,0 +1,232 @@
+"""GPU parity of libokq.so against the CPU oracle (needs an MI355X).
+
+Bars: dequant/quantize/generator bit-exact; GEMV within the reference rule
+abs <= 1e-3 || rel <= 1e-3 per element (crates/kernels/src/lib.rs:2995-3002,
+BASELINE north_star tolerance), exact for the one-hot column probe.
+All calls go through the C-ABI (ctypes), device memory from torch.
+"""
+import numpy as np
+import pytest
+
+from oracle import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as _t
+    if not _t.cuda.is_available():
+        pytest.skip("no GPU")
+    return _t
+
+
+@pytest.fixture(scope="module")
+def okq(torch):
+    from ocelotl_amd import okq as _okq
+    _okq.call("okq_init", 0)
+    return _okq
+
+
+def _stream(torch):
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _dev(torch, a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _host(t):
+    return t.cpu().numpy()
+
+
+def _same_bits(a, b):
+    a = np.asarray(a, np.float32).reshape(-1)
+    b = np.asarray(b, np.float32).reshape(-1)
+    return (a.view(np.uint32) == b.view(np.uint32)) | (np.isnan(a) & np.isnan(b))
+
+
+def gpu_dequant(torch, okq, t, blocks, n):
+    src = _dev(torch, blocks)
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    okq.call("okq_dequantize", t, src.data_ptr(), n, out.data_ptr(), _stream(torch))
+    return _host(out)
+
+
+def gpu_linear(torch, okq, t, x, rows, k, wq, n, bias=None, entry="okq_linear_out_by_in_q"):
+    xd = _dev(torch, np.asarray(x, np.float32).reshape(-1))
+    wd = _dev(torch, wq)
+    bd = None if bias is None else _dev(torch, np.asarray(bias, np.float32))
+    out = torch.full((rows * n,), float("nan"), dtype=torch.float32, device="cuda")
+    okq.call(entry, xd.data_ptr(), rows, k, t, wd.data_ptr(), wq.size, n,
+             None if bd is None else bd.data_ptr(), out.data_ptr(), _stream(torch))
+    torch.cuda.synchronize()
+    return _host(out).reshape(rows, n)
+
+
+# ---------------------------------------------------------------------------
+# bit-exact data-path kernels
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_bit_exact_on_random_bytes(torch, okq, orc, t):
+    print(f"[gpu] dequant random bytes type={t}", flush=True)
+    rng = np.random.default_rng(10 + t)
+    nb = 8192
+    blocks = rng.integers(0, 256, nb * O.BLOCK_BYTES[t], dtype=np.uint8)
+    n = nb * O.BLOCK_ELEMS[t]
+    got = gpu_dequant(torch, okq, t, blocks, n)
+    want = orc.dequantize(t, blocks, n)
+    same = _same_bits(got, want)
+    assert same.all(), f"{(~same).sum()} mismatches, first at {np.argmax(~same)}"
+    finite = np.isfinite(want)
+    assert (got[finite].view(np.uint32) == want[finite].view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_dequant_bit_exact_on_quantized_normal(torch, okq, orc, t):
+    n = 4096 * 64
+    wq = orc.quantize(t, orc.normal(20 + t, n, 0.02))
+    got = gpu_dequant(torch, okq, t, wq, n)
+    assert (got.view(np.uint32) == orc.dequantize(t, wq, n).view(np.uint32)).all()
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gpu_quantizer_matches_oracle_bytes(torch, okq, orc, t):
+    print(f"[gpu] quantize type={t}", flush=True)
+    n = 256 * 2048
+    x = orc.normal(40 + t, n, 0.02)
+    # include exact zeros, a constant block and large values
+    x[:256] = 0.0
+    x[256:512] = 0.125
+    x[512:768] *= 1000.0
+    xd = _dev(torch, x)
+    out = torch.zeros(n // O.BLOCK_ELEMS[t] * O.BLOCK_BYTES[t], dtype=torch.uint8, device="cuda")
+    okq.call("okq_quantize", t, xd.data_ptr(), n, out.data_ptr(), _stream(torch))
+    got = _host(out)
+    want = orc.quantize(t, x)
+    bad = np.nonzero(got != want)[0]
+    assert bad.size == 0, f"{bad.size} bytes differ, first block {bad[0] // O.BLOCK_BYTES[t]}"
+
+
+def test_fill_normal_matches_oracle(torch, okq, orc):
+    n = 1 << 20
+    out = torch.empty(n, dtype=torch.float32, device="cuda")
+    okq.call("okq_fill_normal", 0x5EED, 12345, n, 0.02, out.data_ptr(), _stream(torch))
+    assert (_host(out).view(np.uint32) == orc.normal(0x5EED, n, 0.02, offset=12345).view(np.uint32)).all()
+
+
+def test_f32_to_bf16_matches_oracle(torch, okq, orc):
+    x = orc.normal(3, 1 << 18, 1.0) * np.float32(7.0)
+    xd = _dev(torch, x)
+    out = torch.empty(x.size, dtype=torch.int16, device="cuda")
+    okq.call("okq_f32_to_bf16", xd.data_ptr(), x.size, out.data_ptr(), _stream(torch))
+    assert (_host(out).view(np.uint16) == orc.f32_to_bf16(x)).all()
+
+
+# ---------------------------------------------------------------------------
+# GEMV parity
+# ---------------------------------------------------------------------------
+
+GEMV_SHAPES = {
+    O.Q4_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (3, 768), (64, 20480)],
+    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480)],
+    O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480)],
+}
+CASES = [(t, n, k) for t in TYPES for (n, k) in GEMV_SHAPES[t]]
+
+
+@pytest.mark.parametrize("t,n,k", CASES)
+def test_gemv_matches_reference_cpu_path(torch, okq, orc, t, n, k):
+    print(f"[gpu] gemv type={t} N={n} K={k}", flush=True)
+    wq = orc.quantize(t, orc.normal(1000 * t + n + k, n * k, 0.02))
+    x = orc.normal(7 * k + t, k, 1.0)
+    bias = orc.normal(99, n, 0.1)
+    got = gpu_linear(torch, okq, t, x, 1, k, wq, n, bias, entry="okq_gemv")
+    want = orc.linear_q(t, x, 1, k, wq, n, bias)
+    ok, idx, dmax, rmax = O.allclose_ref_rule(got, want, TOL)
+    assert ok, f"idx={idx} got={got.reshape(-1)[idx]} want={want.reshape(-1)[idx]} max_abs={dmax}"
+
+
+def test_q6k_head_gemv_matches_reference(torch, okq, orc):
+    """C3: the 128256 x 4096 Q6_K output head at batch 1."""
+    n, k = 128256, 4096
+    print(f"[gpu] gemv head N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q6_K, orc.normal(314, n * k, 0.02))
+    x = orc.normal(315, k, 1.0)
+    got = gpu_linear(torch, okq, O.Q6_K, x, 1, k, wq, n)
+    want = orc.linear_q(O.Q6_K, x, 1, k, wq, n)
+    ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, f"idx={idx} max_abs={dmax}"
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_one_hot_reproduces_dequantized_column_exactly(torch, okq, orc, t):
+    n, k = 96, 4096
+    wq = orc.quantize(t, orc.normal(50 + t, n * k, 0.02))
+    w = orc.dequantize(t, wq, n * k).reshape(n, k)
+    for j in (0, 1, 31, 32, 255, 256, 4095):
+        x = np.zeros(k, np.float32)
+        x[j] = 1.0
+        got = gpu_linear(torch, okq, t, x, 1, k, wq, n, entry="okq_gemv")[0]
+        assert (got == w[:, j]).all(), (t, j)
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_edge_inputs(torch, okq, orc, t):
+    n, k = 40, 1024
+    wq = orc.quantize(t, orc.normal(60 + t, n * k, 0.02))
+    bias = orc.normal(61, n, 1.0)
+    # zero activations give exactly the bias
+    got = gpu_linear(torch, okq, t, np.zeros(k, np.float32), 1, k, wq, n, bias)
+    assert (got[0] == bias).all()
+    # large and tiny magnitudes, mixed in one vector
+    x = orc.normal(62, k, 1.0)
+    x[:256] *= np.float32(1e4)
+    x[256:512] *= np.float32(1e-30)
+    got = gpu_linear(torch, okq, t, x, 1, k, wq, n)
+    want = orc.linear_q(t, x, 1, k, wq, n)
+    ok, idx, _, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, idx
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_small_batch_rows_and_determinism(torch, okq, orc, t):
+    n, k, rows = 300, 2048, 3
+    wq = orc.quantize(t, orc.normal(70 + t, n * k, 0.02))
+    x = orc.normal(71, rows * k, 1.0)
+    got = gpu_linear(torch, okq, t, x, rows, k, wq, n)
+    want = orc.linear_q(t, x, rows, k, wq, n)
+    ok, idx, _, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, idx
+    again = gpu_linear(torch, okq, t, x, rows, k, wq, n)
+    assert (got.view(np.uint32) == again.view(np.uint32)).all()
+
+
+def test_empty_inputs_are_noops(torch, okq):
+    out = torch.full((4,), 7.0, device="cuda")
+    okq.call("okq_linear_out_by_in_q", None, 0, 256, O.Q4_K, None, 144 * 4, 4, None, out.data_ptr(), None)
+    torch.cuda.synchronize()
+    assert (_host(out) == 7.0).all()
+
+
+def test_python_mirror_linear_d_and_host_slices(torch, orc):
+    from ocelotl_amd.backend import HipKernelBackend, GgmlTensorType, KernelError
+    be = HipKernelBackend(0)
+    assert be.name() == "hip-gfx950" and be.context().device.kind == "gpu"
+    n, k = 128, 512
+    wq = orc.quantize(O.Q4_K, orc.normal(80, n * k, 0.02))
+    w = be.upload_quantized(GgmlTensorType.Q4K, k, n, wq)
+    x = orc.normal(81, 2 * k)
+    b = orc.normal(82, n)
+    out = np.zeros(2 * n, np.float32)
+    be.linear_out_by_in(x, 2, k, w, n, b, out)
+    ok, idx, _, _ = O.allclose_ref_rule(out, orc.linear_q(O.Q4_K, x, 2, k, wq, n, b), TOL)
+    assert ok, idx
+    deq = be.dequantize(w).to_host_owned()
+    assert (deq.view(np.uint32) == orc.dequantize(O.Q4_K, wq, n * k).view(np.uint32)).all()
+    with pytest.raises(KernelError):
+        be.linear_d(be.upload(x), 2, k, w, n, None, be.alloc(2 * n - 1))
