@@ -263,10 +263,14 @@ def run_c1(ctx: Ctx, args):
 
 
 def run_c4(ctx: Ctx, args, c2):
-    """Q4_K prefill GEMM at M in {128, 512, 2048} with bf16 activations."""
+    """Q4_K prefill GEMM at M in {128, 512, 2048} with bf16 activations.
+    us_kernel: the MFMA kernel's own dispatch time; us_call: the whole entry
+    point (activation pre-pass + GEMM) timed with stream events."""
     torch = ctx.torch
     res = {}
+    lay = c2["layers"]
     for m in (128, 512, 2048):
+        log(f"C4: Q4_K GEMM M={m}")
         xf = ctx.normal(m * 14336, 50 + m)
         xb = torch.empty(m * 14336, dtype=torch.int16, device="cuda")
         ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
@@ -274,18 +278,27 @@ def run_c4(ctx: Ctx, args, c2):
             if name in ("k", "o", "up"):
                 continue  # same shapes as v, q, gate
             y = torch.empty(m * n, dtype=torch.float32, device="cuda")
-            lay = c2["layers"]
-            try:
-                us = ctx.kernel_us(lambda r: ctx.gemv(Q4K, xb, k, lay[r % len(lay)][name], n, y, entry="okq_gemm_bf16",
-                                                      rows=m), max(8, args.kernel_reps // 8))
-            except Exception as e:  # noqa: BLE001 -- report unsupported shapes instead of dying
-                res[f"M{m}_{name}"] = {"error": str(e)[:200]}
-                continue
+            reps = max(8, args.kernel_reps // 8)
+
+            def call(r, name=name, n=n, k=k, y=y):
+                ctx.gemv(Q4K, xb, k, lay[r % len(lay)][name], n, y, entry="okq_gemm_bf16", rows=m)
+
+            call(0)
+            us = ctx.kernel_us(call, reps)
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            e0.record()
+            for r in range(reps):
+                call(r)
+            e1.record()
+            torch.cuda.synchronize()
+            t_call = 1000.0 * e0.elapsed_time(e1) / reps
             t = sum(us) / len(us)
             flops = 2.0 * m * n * k
-            res[f"M{m}_{name}"] = {"m": m, "n": n, "k": k, "us_mean": round(t, 2),
+            res[f"M{m}_{name}"] = {"m": m, "n": n, "k": k, "us_kernel": round(t, 2), "us_call": round(t_call, 2),
                                    "tflops": round(flops / t / 1e6, 1),
-                                   "frac_bf16_peak": round(flops / t / 1e6 / BF16_PEAK_TFLOPS, 4)}
+                                   "frac_bf16_peak": round(flops / t / 1e6 / BF16_PEAK_TFLOPS, 4),
+                                   "tflops_call": round(flops / t_call / 1e6, 1)}
     return res
 
 
@@ -341,6 +354,7 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
+    ap.add_argument("--only", default="c1,c3,c4", help="secondary configs to run (comma list of c1,c3,c4)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -354,9 +368,12 @@ def main():
 
     c2 = run_c2(ctx, args)
     extra = {"c2_shapes": c2["shapes"]}
-    if not args.no_extra:
+    only = set(args.only.split(",")) if not args.no_extra else set()
+    if "c1" in only:
         extra["c1_q8_0"] = run_c1(ctx, args)
+    if "c3" in only:
         extra["c3_q6_k_head"] = run_c3(ctx, args)
+    if "c4" in only:
         extra["c4_q4_k_gemm_bf16"] = run_c4(ctx, args, c2)
     cpu = None if args.no_cpu else run_cpu_baseline(ctx, c2, args)
 

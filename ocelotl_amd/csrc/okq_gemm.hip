@@ -1,15 +1,442 @@
-// okq_gemm.hip -- MFMA dequant-GEMM for prefill (placeholder until the
-// MFMA kernels land; gemm_supported() reports no shape).
+// okq_gemm.hip -- MFMA dequant-GEMM for prefill: Y[M,N] = X[M,K] W[N,K]^T (+bias)
+//
+// Numerics (exact operands, f32 accumulation):
+//   * A = X as fp16.  bf16 -> fp16 is exact for 2^-17 <= |x| <= 65504 (bf16
+//     carries 8 significant bits); f32 activations are split into an fp16
+//     hi plane and an fp16 lo plane (x ~= hi + lo to ~2^-22) and contracted
+//     twice.
+//   * B = the integer part of the dequantised weight, exact in fp16:
+//       Q4_K: sc * q       (6-bit scale x 4-bit quant <= 945)
+//     The super-block scales d and dmin are applied in f32 to the per-super-
+//     block MFMA accumulators; the Q4_K min term  sum_s m_s * sum_{k in s} x_k
+//     is one extra K=16 MFMA per super-block on (xsum hi, xsum lo) x m.
+//   So every product inside an MFMA is exact and only f32 summation rounds.
+//
+// Layout / schedule (gfx950):
+//   * A pre-pass converts X once per call into a workspace: fp16 planes
+//     [M][K] and per-32 sums [M][K/32] as fp16 (hi, lo) pairs.
+//   * Workgroup tile 256 x 128 (8 waves) or 128 x 128 (4 waves) when 256-row
+//     tiles would leave CUs idle; each wave owns 64 x 64 = 2 x 2 MFMA 32x32x16
+//     tiles.  K advances in steps of one 64-weight Q4_K chunk through a
+//     software pipeline: raw loads two steps ahead in registers, the B
+//     dequantisation (GGUF blocks -> fp16 sc*q) of step i+1 overlapping the
+//     MFMAs of step i, double-buffered LDS, one barrier per step.
+//   * Tiles are ordered so consecutive tiles (the M-tiles of one N-tile) land
+//     on one XCD: workgroup b runs on XCD b % 8, so b is remapped to give each
+//     XCD a contiguous range of tiles and the weight tile is re-read from that
+//     XCD's L2.
+#include <type_traits>
+
 #include "okq_device.h"
 #include "okq_internal.h"
 
 namespace okq {
 
-bool gemm_supported(int, int64_t, int64_t) { return false; }
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f16x __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __amdgpu_buffer_rsrc_t Rsrc;
 
-hipError_t launch_gemm(int, const void *, bool, int64_t, int64_t, const void *, int64_t, const float *, float *, int,
-                       hipStream_t) {
-  return hipErrorNotSupported;
+// Buffer descriptor over [base, base + bytes), bytes < 2^32.  Loads past the
+// end return zeros: rows beyond M or N stage as zeros without branches.
+__device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 bload4(Rsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
+
+constexpr int kBN = 128;
+
+// ---------------------------------------------------------------------------
+// pre-pass: X -> fp16 planes + per-32 sums
+// ---------------------------------------------------------------------------
+template <bool kF32>
+__global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__ X, int M, int K,
+                                                        _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
+                                                        h2 *__restrict__ xsum) {
+  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-run per thread
+  const int runs = K / 32;
+  if (t >= (int64_t)M * runs) return;
+  const int64_t base = t * 32;  // element offset (row-major [M][K], runs never straddle rows)
+  float v[32];
+  if (kF32) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(X) + base);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 q = p[i];
+      v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+    }
+  } else {
+    const u32x4 *p = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(X) + base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 q = p[i];
+      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * i + 2 * j] = as_f32(w[j] << 16);
+        v[8 * i + 2 * j + 1] = as_f32(w[j] & 0xffff0000u);
+      }
+    }
+  }
+  float s = 0.0f;
+  h8 hv[4], lv[4];
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    s += v[i];
+    const _Float16 h = (_Float16)v[i];
+    hv[i / 8][i % 8] = h;
+    if (kF32) lv[i / 8][i % 8] = (_Float16)(v[i] - (float)h);
+  }
+  h8 *ph = reinterpret_cast<h8 *>(xhi + base);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) ph[i] = hv[i];
+  if (kF32) {
+    h8 *pl = reinterpret_cast<h8 *>(xlo + base);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pl[i] = lv[i];
+  }
+  const _Float16 sh = (_Float16)s;
+  h2 pair;
+  pair[0] = sh;
+  pair[1] = (_Float16)(s - (float)sh);
+  xsum[t] = pair;
+}
+
+// ---------------------------------------------------------------------------
+// Q4_K B staging
+// ---------------------------------------------------------------------------
+// 0x6400 | q is the fp16 value 1024 + q; (1024+q)*sc - 1024*sc = sc*q is one
+// fused fp16 FMA whose exact result (an integer <= 945) is representable.
+__device__ __forceinline__ h2 nib_pair(uint32_t spread, h2 sc2, h2 off2) {
+  return __builtin_elementwise_fma(__builtin_bit_cast(h2, spread), sc2, off2);
+}
+// Four nibbles (one per byte of n4) -> two fp16 pairs of sc*q, in byte order.
+// v_perm_b32 interleaves the bytes with the 0x64 exponent byte of 1024.
+__device__ __forceinline__ void nib4(uint32_t n4, h2 sc2, h2 off2, h2 &p0, h2 &p1) {
+  p0 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n4, 0x04010400u), sc2, off2);
+  p1 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n4, 0x04030402u), sc2, off2);
+}
+
+// ---------------------------------------------------------------------------
+// main kernel
+// ---------------------------------------------------------------------------
+constexpr int kKB = 64;         // K per pipeline step: one 64-weight Q4_K chunk
+constexpr int kLDB = kKB + 8;   // LDS row pitch in halves (spreads rows over banks)
+
+template <int BM, bool kLo>
+struct alignas(16) GemmSmem {
+  _Float16 A[2][BM][kLDB];
+  _Float16 Alo[2][kLo ? BM : 1][kLDB];
+  _Float16 B[2][kBN][kLDB];
+  _Float16 xs[2][BM][16];   // per super-block parity: xsum hi/lo of sub-blocks 0..7
+  _Float16 mn[2][kBN][16];  // per super-block parity: 6-bit mins, each twice
+  float d[2][kBN], dmin[2][kBN];
+};
+
+// Raw global data of one pipeline step for one thread.
+template <int BM, bool kLo>
+struct StepRegs {
+  u32x4 a[4], al[kLo ? 4 : 1];  // 32 activations (fp16) of one row
+  u32x4 xs;                     // 4 (hi, lo) xsum pairs (first chunk of a super-block)
+  u32x4 hd;                     // Q4_K header of the weight row's super-block
+  u32x4 q;                      // 16 (BM=128) or 8 (BM=256, in .x/.y) qs bytes
+};
+
+// BM x 128 workgroup tile, BM/32 waves arranged (BM/64) x 2, each 64 x 64.
+// Software pipeline over 64-wide K steps: raw loads run two steps ahead in
+// registers, the dequantisation of step i+1 overlaps the MFMAs of step i, LDS
+// is double buffered, one barrier per step.
+template <int BM, bool kLo>
+__global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__restrict__ xhi,
+                                                         const _Float16 *__restrict__ xlo,
+                                                         const h2 *__restrict__ xsum, const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ bias, float *__restrict__ Y, int M,
+                                                         int N, int K, int tiles_m, int tiles) {
+  constexpr int NT = BM * 2;       // threads
+  constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
+  constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
+  __shared__ GemmSmem<BM, kLo> sm;
+  // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
+  // contiguous range of tiles (consecutive tiles share an N-tile).
+  const int b = (int)blockIdx.x;
+  const int per_xcd = (tiles + 7) / 8;
+  const int tile = (b % 8) * per_xcd + b / 8;
+  if (tile >= tiles) return;
+  const int m0 = (tile % tiles_m) * BM;
+  const int n0 = (tile / tiles_m) * kBN;
+
+  const int tid = (int)threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int nsb = K / 256;
+  const int nsteps = 4 * nsb;
+  const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+
+  const int sr = tid >> 1, sp = tid & 1;        // A: row, 32-wide half
+  const int br = tid / TPR, bq = tid % TPR;     // B: weight row, byte window
+  const uint32_t K32 = (uint32_t)K;
+  const Rsrc rs_xh = make_rsrc(xhi, (uint32_t)((size_t)M * K * 2));
+  const Rsrc rs_xl = make_rsrc(kLo ? xlo : xhi, (uint32_t)((size_t)M * K * 2));
+  const Rsrc rs_xs = make_rsrc(xsum, (uint32_t)((size_t)M * (K / 32) * 4));
+  const Rsrc rs_w = make_rsrc(W, (uint32_t)((size_t)N * row_bytes));
+  // byte offsets of this thread's rows (past the end for rows >= M / >= N:
+  // the descriptors return zeros there)
+  const uint32_t a_row = (uint32_t)(m0 + sr) * K32 * 2u + 64u * (uint32_t)sp;
+  const uint32_t s_row = (uint32_t)(m0 + sr) * (K32 / 32u) * 4u + 16u * (uint32_t)sp;
+  const uint32_t w_row = (uint32_t)(n0 + br) * row_bytes;
+
+  // C = step & 3 is a compile-time constant at every call site, so the body
+  // is straight-line code (no divergent branches around the loads: the wait
+  // counters then only wait for the step actually consumed).  Steps past the
+  // end read inside the next row or past the descriptor (zeros); unused.
+  auto load = [&](StepRegs<BM, kLo> &r, int step, auto Cc) {
+    constexpr int c = decltype(Cc)::value;
+    const int sb = step >> 2;
+    const uint32_t ka = a_row + 2u * (uint32_t)(step * kKB);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.a[i] = bload4(rs_xh, ka + 16u * i);
+    if (kLo) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.al[i] = bload4(rs_xl, ka + 16u * i);
+    }
+    if constexpr (c == 0) r.xs = bload4(rs_xs, s_row + 32u * (uint32_t)sb);
+    const uint32_t blk = w_row + (uint32_t)sb * kQ4KBytes;
+    r.hd = bload4(rs_w, blk);
+    const uint32_t qo = blk + 16u + 32u * (uint32_t)c + (uint32_t)(QB * bq);
+    if (QB == 16) {
+      r.q = bload4(rs_w, qo);
+    } else {
+      const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs_w, qo, 0, 0);
+      r.q = u32x4{v.x, v.y, 0u, 0u};
+    }
+  };
+
+  auto stage = [&](const StepRegs<BM, kLo> &r, int step, int buf, auto Cc) {
+    constexpr int c = decltype(Cc)::value;
+    const int sbp = (step >> 2) & 1;
+    u32x4 *da = reinterpret_cast<u32x4 *>(&sm.A[buf][sr][32 * sp]);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) da[i] = r.a[i];
+    if (kLo) {
+      u32x4 *dl = reinterpret_cast<u32x4 *>(&sm.Alo[buf][sr][32 * sp]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) dl[i] = r.al[i];
+    }
+    if constexpr (c == 0) *reinterpret_cast<u32x4 *>(&sm.xs[sbp][sr][8 * sp]) = r.xs;
+    // low nibbles -> sub-block 2c (k = byte), high nibbles -> 2c+1 (k = 32 + byte)
+    uint32_t sc0, mv0, sc1, mv1;
+    q4k_scale_min(2 * c, r.hd.y, r.hd.z, r.hd.w, sc0, mv0);
+    q4k_scale_min(2 * c + 1, r.hd.y, r.hd.z, r.hd.w, sc1, mv1);
+    const _Float16 s0 = (_Float16)(float)sc0, s1 = (_Float16)(float)sc1;
+    const _Float16 o0 = (_Float16)(-1024.0f * (float)sc0), o1 = (_Float16)(-1024.0f * (float)sc1);
+    const h2 sc0v = {s0, s0}, sc1v = {s1, s1}, off0 = {o0, o0}, off1 = {o1, o1};
+    constexpr int NW = QB / 4;
+    const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    h2 lo[2 * NW], hi[2 * NW];
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      nib4(q[w] & 0x0F0F0F0Fu, sc0v, off0, lo[2 * w], lo[2 * w + 1]);
+      nib4((q[w] >> 4) & 0x0F0F0F0Fu, sc1v, off1, hi[2 * w], hi[2 * w + 1]);
+    }
+    u32x4 *dlo = reinterpret_cast<u32x4 *>(&sm.B[buf][br][QB * bq]);
+    u32x4 *dhi = reinterpret_cast<u32x4 *>(&sm.B[buf][br][32 + QB * bq]);
+#pragma unroll
+    for (int i = 0; i < NW / 2; ++i) {
+      dlo[i] = u32x4{__builtin_bit_cast(uint32_t, lo[4 * i]), __builtin_bit_cast(uint32_t, lo[4 * i + 1]),
+                     __builtin_bit_cast(uint32_t, lo[4 * i + 2]), __builtin_bit_cast(uint32_t, lo[4 * i + 3])};
+      dhi[i] = u32x4{__builtin_bit_cast(uint32_t, hi[4 * i]), __builtin_bit_cast(uint32_t, hi[4 * i + 1]),
+                     __builtin_bit_cast(uint32_t, hi[4 * i + 2]), __builtin_bit_cast(uint32_t, hi[4 * i + 3])};
+    }
+    if constexpr (c == 0) {
+      // every staging thread of the row loaded the same header: all of them
+      // store the same values (no branch, so no conservative wait counters)
+      sm.d[sbp][br] = f16_bits_hw(r.hd.x & 0xffffu);
+      sm.dmin[sbp][br] = f16_bits_hw(r.hd.x >> 16);
+      h8 m0v, m1v;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        uint32_t scj, mj;
+        q4k_scale_min((uint32_t)j, r.hd.y, r.hd.z, r.hd.w, scj, mj);
+        const _Float16 mh = (_Float16)(float)mj;
+        if (j < 4) {
+          m0v[2 * j] = mh;
+          m0v[2 * j + 1] = mh;
+        } else {
+          m1v[2 * (j - 4)] = mh;
+          m1v[2 * (j - 4) + 1] = mh;
+        }
+      }
+      *reinterpret_cast<h8 *>(&sm.mn[sbp][br][0]) = m0v;
+      *reinterpret_cast<h8 *>(&sm.mn[sbp][br][8]) = m1v;
+    }
+  };
+
+  f16x acc[2][2], accs[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int e = 0; e < 16; ++e) acc[i][j][e] = 0.0f;
+
+  // MFMA slice ks, lane group g = lane/32 covers k = 32g + 8ks + [0, 8) of the
+  // 64-wide step (the same k order as the direct-A kernel, so both kernels
+  // give bit-identical results for a row)
+  const int fr = lane & 31, fk = 8 * (lane >> 5), fk4 = 32 * (lane >> 5);
+  const f16x zero = {};
+
+  auto mma = [&](int buf, bool first) {
+#pragma unroll
+    for (int ks = 0; ks < kKB / 16; ++ks) {
+      h8 a[2], bv[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+        a[i] = *reinterpret_cast<const h8 *>(&sm.A[buf][wm * 64 + 32 * i + fr][fk4 + 8 * ks]);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        bv[j] = *reinterpret_cast<const h8 *>(&sm.B[buf][wn * 64 + 32 * j + fr][fk4 + 8 * ks]);
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+          accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv[j], (first && ks == 0) ? zero : accs[i][j],
+                                                              0, 0, 0);
+      if (kLo) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+          a[i] = *reinterpret_cast<const h8 *>(&sm.Alo[buf][wm * 64 + 32 * i + fr][fk4 + 8 * ks]);
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int j = 0; j < 2; ++j)
+            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv[j], accs[i][j], 0, 0, 0);
+      }
+    }
+  };
+
+  // end of a super-block: acc += d * accs - dmin * (xsum . m)
+  auto scale = [&](int sbp) {
+    h8 xa[2], mb[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) xa[i] = *reinterpret_cast<const h8 *>(&sm.xs[sbp][wm * 64 + 32 * i + fr][fk]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) mb[j] = *reinterpret_cast<const h8 *>(&sm.mn[sbp][wn * 64 + 32 * j + fr][fk]);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int nn = wn * 64 + 32 * j + fr;
+      const float dv = sm.d[sbp][nn], dm = -sm.dmin[sbp][nn];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) {
+        const f16x mins = __builtin_amdgcn_mfma_f32_32x32x16_f16(xa[i], mb[j], zero, 0, 0, 0);
+#pragma unroll
+        for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(dm, mins[e], fmaf(dv, accs[i][j][e], acc[i][j][e]));
+      }
+    }
+  };
+
+  // Pipeline over steps i = 4*sb + c: LDS buffer i&1 holds step i while the
+  // register set of step i+1 is staged into the other buffer and step i+2 is
+  // in flight.
+  using C0 = std::integral_constant<int, 0>;
+  using C1 = std::integral_constant<int, 1>;
+  using C2 = std::integral_constant<int, 2>;
+  using C3 = std::integral_constant<int, 3>;
+  StepRegs<BM, kLo> R0, R1;
+  load(R0, 0, C0{});
+  load(R1, 1, C1{});
+  stage(R0, 0, 0, C0{});
+  __syncthreads();
+  for (int sb = 0; sb < nsb; ++sb) {
+    const int i = 4 * sb;
+    load(R0, i + 2, C2{});
+    mma(0, true);
+    stage(R1, i + 1, 1, C1{});
+    __syncthreads();
+    load(R1, i + 3, C3{});
+    mma(1, false);
+    stage(R0, i + 2, 0, C2{});
+    __syncthreads();
+    load(R0, i + 4, C0{});
+    mma(0, false);
+    stage(R1, i + 3, 1, C3{});
+    __syncthreads();
+    load(R1, i + 5, C1{});
+    mma(1, false);
+    scale(sb & 1);
+    stage(R0, i + 4, 0, C0{});
+    __syncthreads();
+  }
+
+  // epilogue: C layout row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int col = n0 + wn * 64 + 32 * j + fr;
+    if (col >= N) continue;
+    const float bv = bias ? bias[col] : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        const int row = m0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+        if (row < M) Y[(size_t)row * N + col] = acc[i][j][e] + bv;
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
+  // 32-bit buffer offsets: activations (with a tile of padding rows) and weights
+  const int64_t a_bytes = (M + 256) * K * 2;
+  const int64_t w_bytes = (N + kBN) * (K / 256) * kQ4KBytes;
+  return type == kQ4_K && K % 256 == 0 && N >= 1 && M >= 1 && a_bytes < (int64_t)UINT32_MAX &&
+         w_bytes < (int64_t)UINT32_MAX;
+}
+
+size_t gemm_workspace_bytes(int64_t M, int64_t K, bool x_is_bf16) {
+  const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
+  const size_t sums = (size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16);
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  return up(plane) + (x_is_bf16 ? 0 : up(plane)) + up(sums);
+}
+
+hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
+                       const float *bias, float *y, void *workspace, int cu_count, hipStream_t s) {
+  if (type != kQ4_K) return hipErrorInvalidValue;
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
+  _Float16 *xhi = static_cast<_Float16 *>(workspace);
+  _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(static_cast<char *>(workspace) + up(plane));
+  h2 *xsum = reinterpret_cast<h2 *>(static_cast<char *>(workspace) + up(plane) + (x_is_bf16 ? 0 : up(plane)));
+  const int64_t runs = M * (K / 32);
+  const unsigned pg = (unsigned)((runs + 255) / 256);
+  if (x_is_bf16)
+    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(pg), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum);
+  else
+    hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(pg), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  // bf16 activations with M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x 64);
+  // otherwise 128 x 128 tiles (f32 activations need the second fp16 plane,
+  // which only fits the LDS budget at 128 rows).
+  (void)cu_count;
+  const uint8_t *W = static_cast<const uint8_t *>(w);
+  const int m = (int)M, n = (int)N, k = (int)K;
+  const int tiles_n = (int)((N + kBN - 1) / kBN);
+  const bool big = x_is_bf16 && M > 128;
+  const int bm = big ? 256 : 128;
+  const int tiles_m = (int)((M + bm - 1) / bm);
+  const int tiles = tiles_m * tiles_n;
+  const int per_xcd = (tiles + 7) / 8;
+  const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(bm * 2));
+  if (big) launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
+  else if (x_is_bf16) launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
+  else launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
+  return hipGetLastError();
 }
 
 }  // namespace okq

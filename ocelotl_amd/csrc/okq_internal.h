@@ -38,10 +38,13 @@ hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64
                        int cu_count, hipStream_t s);
 
 // MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
+// `workspace` holds gemm_workspace_bytes(M, K, x_is_bf16) bytes (256-aligned)
+// for the converted activations; it is reused by later calls on the stream.
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
-                       const float *bias, float *y, int cu_count, hipStream_t s);
+                       const float *bias, float *y, void *workspace, int cu_count, hipStream_t s);
+size_t gemm_workspace_bytes(int64_t M, int64_t K, bool x_is_bf16);
 
-// True when launch_gemm supports this (type, K, N).
-bool gemm_supported(int type, int64_t K, int64_t N);
+// True when launch_gemm supports this (type, M, K, N).
+bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);
 
 }  // namespace okq

@@ -9,8 +9,10 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <mutex>
 #include <string>
+#include <utility>
 
 #include "../../include/okq.h"
 #include "okq_internal.h"
@@ -148,6 +150,48 @@ okq_status validate_linear(const void *x, const LinearArgs &a, const void *w, co
   return ok();
 }
 
+// ---- GEMM workspace ----------------------------------------------------------
+// One buffer per (device, stream): work on one stream is ordered, so reuse is
+// safe; different streams never share.  Grows on demand; growing is refused
+// while the stream is being captured into a graph (allocation is not
+// capturable), so a caller that captures must run one call of at least the
+// same size on that stream first.
+struct Workspace {
+  void *ptr = nullptr;
+  size_t bytes = 0;
+};
+std::mutex g_ws_mutex;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out) {
+  std::lock_guard<std::mutex> lock(g_ws_mutex);
+  Workspace &w = g_ws[{dev, s}];
+  if (w.bytes >= bytes) {
+    *out = w.ptr;
+    return ok();
+  }
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(s, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+    return fail(OKQ_E_ALLOC,
+                "hip-gfx950: GEMM workspace of %zu bytes is not allocated for this stream and cannot be allocated "
+                "during graph capture; run one call of this size on the stream before capturing",
+                bytes);
+  if (w.ptr) {
+    if (hipStreamSynchronize(s) != hipSuccess || hipFree(w.ptr) != hipSuccess)
+      return fail(OKQ_E_LAUNCH, "hip-gfx950: cannot release the previous GEMM workspace");
+    w.ptr = nullptr;
+    w.bytes = 0;
+  }
+  const size_t want = bytes + bytes / 2;
+  if (hipMalloc(&w.ptr, want) != hipSuccess) {
+    w.ptr = nullptr;
+    return fail(OKQ_E_ALLOC, "hip-gfx950: hipMalloc of a %zu-byte GEMM workspace failed", want);
+  }
+  w.bytes = want;
+  *out = w.ptr;
+  return ok();
+}
+
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below this count run the GEMV once per row (each pass streams the
@@ -168,14 +212,19 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
   hipStream_t s = static_cast<hipStream_t>(stream);
   bool use_gemm = false;
   if (path == Path::Gemm) {
-    if (!okq::gemm_supported((int)type, K, N))
+    if (!okq::gemm_supported((int)type, rows, K, N))
       return fail(OKQ_E_SHAPE, "okq_gemm: shape in_features=%lld out_features=%lld not supported by the MFMA path",
                   (long long)K, (long long)N);
     use_gemm = true;
   } else if (path == Path::Auto) {
-    use_gemm = (x_bf16 || rows > kGemvMaxRows) && okq::gemm_supported((int)type, K, N);
+    use_gemm = (x_bf16 || rows > kGemvMaxRows) && okq::gemm_supported((int)type, rows, K, N);
   }
-  if (use_gemm) return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, info.cu_count, s), "gemm launch");
+  if (use_gemm) {
+    void *ws = nullptr;
+    st = get_workspace(dev, s, okq::gemm_workspace_bytes(rows, K, x_bf16), &ws);
+    if (st != OKQ_OK) return st;
+    return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, ws, info.cu_count, s), "gemm launch");
+  }
   if (x_bf16) return fail(OKQ_E_SHAPE, "bf16 activations need the MFMA path, which does not support this shape");
   const float *xf = static_cast<const float *>(x);
   for (int64_t r = 0; r < rows; ++r) {
