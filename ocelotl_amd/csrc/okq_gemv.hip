@@ -7,29 +7,39 @@
 //       Q4_K unit = (super-block, 64-weight chunk c) : 16 B header + 32 B qs
 //       Q6_K unit = (super-block, half h, 16-run u2) : 3 x 16 B of ql/qh + scales + d
 //       Q8_0 unit = a pair of 34-B blocks             : 68 B, dword aligned
-//     Lane l handles units l, l+64, ... (P per lane), so it always touches the
+//     A lane always handles the same unit position, so it always touches the
 //     same columns of x.
 //   * x is quantised once per workgroup, cooperatively, into LDS: each run of
 //     32 (Q4_K, Q8_0) or 16 (Q6_K) activations gets a power-of-two scale, is
-//     rounded to int16 and split into hi/lo int8 dwords, with the run's exact
-//     f32 sum alongside.  The weights' 4/6/8-bit integers contract with them
-//     through v_dot4_i32_i8; the partial sums are exact integers and the block
-//     scales are applied in f32.
+//     rounded to int16 and split into hi/lo int8 dwords, with the run's f32
+//     sum alongside (groups of 8 or 4 lanes, one float4 each, share the run's
+//     max and sum through DPP).  The weights' 4/6/8-bit integers contract with
+//     them through v_dot4_i32_i8; the partial sums are exact integers and the
+//     block scales are applied in f32.
 //   * A row of U = K/64 units is split over a team of T = ceil(U/64) waves,
 //     so every lane owns exactly one unit and keeps its activations in
-//     registers for all rows.  A workgroup holds G teams (G*T <= 16 waves) and
-//     walks batches of G*R rows; each wave issues the next batch's loads before
-//     computing the current one (register double buffer).  The first batch's
-//     loads are issued before the x prologue so their latency overlaps it.
+//     registers for all rows.  A workgroup holds G teams (G*T <= 16 waves).
+//   * Ordering is what makes it fast (measured with per-wave timestamps):
+//     vector loads complete in issue order per CU, so every wave first issues
+//     its x loads, a bare barrier queues all of them ahead of any weight load,
+//     and only then do the weight loads start.  Rows are swept step-major
+//     across the chip (one contiguous window of rows per step keeps the HBM
+//     channels evenly loaded); each wave keeps a ring of D rows in flight and
+//     computes a row as soon as it arrives.  Every load is unconditional:
+//     rows past the end address past the tensor and read zeros, because a
+//     branch around a load makes the compiler wait for all outstanding loads.
 //   * Weights are read with buffer loads against one descriptor spanning the
 //     tensor: 32-bit offsets (row offset + lane constant), immediate field
 //     offsets, and the hardware range check as a backstop.  2-byte-aligned
 //     Q6_K/Q8_0 blocks are read as dword-aligned windows and re-aligned with
 //     v_alignbyte_b32; no read leaves the weight tensor.
-//   * Row sums are reduced across the wave with DPP + readlane, then across
-//     the team's waves through LDS, both in a fixed order (deterministic).
+//   * Row sums are reduced across the wave with DPP + readlane, then (T > 1)
+//     across the team's waves through LDS once per chunk of steps, both in a
+//     fixed order (deterministic).
 #include "okq_device.h"
 #include "okq_internal.h"
+
+#include <algorithm>
 
 namespace okq {
 
@@ -61,40 +71,6 @@ struct XRec {
 };
 static_assert(sizeof(XRec) == 160, "XRec layout");
 
-// Quantise the run of NW*4 floats at xp; write limbs to hi/lo (LDS).
-template <int NW>
-__device__ __forceinline__ void quantize_run(const float *__restrict__ xp, uint32_t *hi, uint32_t *lo, float &sx,
-                                             float &sum) {
-  float v[4 * NW];
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    const float4 t = *reinterpret_cast<const float4 *>(xp + 4 * i);
-    v[4 * i] = t.x;
-    v[4 * i + 1] = t.y;
-    v[4 * i + 2] = t.z;
-    v[4 * i + 3] = t.w;
-  }
-  float amax = 0.0f, s = 0.0f;
-#pragma unroll
-  for (int i = 0; i < 4 * NW; ++i) {
-    amax = fmaxf(amax, fabsf(v[i]));
-    s += v[i];
-  }
-  const int e = x_exp(amax);
-  sx = ldexpf(1.0f, e);
-  sum = s;
-#pragma unroll
-  for (int i = 0; i < NW; ++i) {
-    int h0, l0, h1, l1, h2, l2, h3, l3;
-    x_split(v[4 * i], e, h0, l0);
-    x_split(v[4 * i + 1], e, h1, l1);
-    x_split(v[4 * i + 2], e, h2, l2);
-    x_split(v[4 * i + 3], e, h3, l3);
-    hi[i] = pack4(h0, h1, h2, h3);
-    lo[i] = pack4(l0, l1, l2, l3);
-  }
-}
-
 // 16 bytes starting at byte offset a (2-byte aligned, a & 3 == r) as four
 // dwords; reads [a - r, a - r + 16) and [a + 12 + r, a + 16 + r), both inside
 // [a - 2, a + 18).
@@ -119,7 +95,7 @@ struct FQ4K {
   struct Regs {
     u32x4a4 hd, qa, qb;
   };
-  static constexpr int kRows = 2;  // rows per batch (register budget)
+  static constexpr int kMaxDepth = 2;  // rows in flight per wave
   // lane constant: byte offset of the unit's block within a row
   __device__ static uint32_t unit_off(int u) { return (uint32_t)(u >> 2) * kQ4KBytes; }
   __device__ static void load(Regs &r, Rsrc rs, uint32_t blk, uint32_t lane) {
@@ -129,10 +105,10 @@ struct FQ4K {
     r.qb = ld4(rs, blk + 32 + 32 * c);
   }
   // run i = [32i, 32i+32): unit i/2, half i%2
-  __device__ static void prep(const float *x, int run, XRec *xr) {
-    XRec &rec = xr[run >> 1];
-    const int h = run & 1;
-    quantize_run<8>(x + 32 * run, rec.hi + 8 * h, rec.lo + 8 * h, rec.s[h], rec.t[h]);
+  __device__ static void xslot(int run, int &rec, int &word, int &slot) {
+    rec = run >> 1;
+    word = 8 * (run & 1);
+    slot = run & 1;
   }
   __device__ static float compute(const Regs &r, const XRec &x, uint32_t lane) {
     const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
@@ -188,7 +164,7 @@ struct FQ6K {
     uint32_t d;
     uint32_t r;
   };
-  static constexpr int kRows = 1;
+  static constexpr int kMaxDepth = 1;  // measured: deeper rings slow the long Q6_K streams
   __device__ static uint32_t unit_off(int u) { return (uint32_t)(u >> 2) * kQ6KBytes; }
   __device__ static void load(Regs &g, Rsrc rs, uint32_t B, uint32_t lane) {
     const uint32_t r = B & 3u;  // the tensor base is dword aligned
@@ -203,11 +179,12 @@ struct FQ6K {
     g.d = ld16(rs, B + 208);
   }
   // run j = [16j, 16j+16): super-block j/16; within it 16*(j%16) = 128h + 32qq + 16u2
-  __device__ static void prep(const float *x, int run, XRec *xr) {
+  __device__ static void xslot(int run, int &rec, int &word, int &slot) {
     const int sb = run >> 4, rr = run & 15;
     const int h = rr >> 3, qq = (rr & 7) >> 1, u2 = rr & 1;
-    XRec &rec = xr[4 * sb + 2 * h + u2];
-    quantize_run<4>(x + 16 * run, rec.hi + 4 * qq, rec.lo + 4 * qq, rec.s[qq], rec.t[qq]);
+    rec = 4 * sb + 2 * h + u2;
+    word = 4 * qq;
+    slot = qq;
   }
   __device__ static float compute(const Regs &g, const XRec &x, uint32_t lane) {
     uint32_t L[4], Lh[4], H[4];
@@ -256,7 +233,7 @@ struct FQ80 {
     u32x4a4 v0, v1, v2, v3;
     uint32_t v4;
   };
-  static constexpr int kRows = 1;
+  static constexpr int kMaxDepth = 2;
   __device__ static uint32_t unit_off(int u) { return (uint32_t)u * (2 * kQ8Bytes); }
   __device__ static void load(Regs &r, Rsrc rs, uint32_t pr, uint32_t) {
     r.v0 = ld4(rs, pr);
@@ -265,10 +242,10 @@ struct FQ80 {
     r.v3 = ld4(rs, pr + 48);
     r.v4 = ld1(rs, pr + 64);
   }
-  __device__ static void prep(const float *x, int run, XRec *xr) {
-    XRec &rec = xr[run >> 1];
-    const int h = run & 1;
-    quantize_run<8>(x + 32 * run, rec.hi + 8 * h, rec.lo + 8 * h, rec.s[h], rec.t[h]);
+  __device__ static void xslot(int run, int &rec, int &word, int &slot) {
+    rec = run >> 1;
+    word = 8 * (run & 1);
+    slot = run & 1;
   }
   __device__ static float compute(const Regs &r, const XRec &x, uint32_t) {
     const uint32_t w[17] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w, r.v2.x,
@@ -290,85 +267,168 @@ struct FQ80 {
 };
 
 // ---------------------------------------------------------------------------
+// activation prologue: lanes in groups of kRun/4 each hold one float4 of a
+// run; the group shares the run's max|x| and sum through DPP (fixed order),
+// then each lane writes one hi and one lo dword of the run's XRec.
+// ---------------------------------------------------------------------------
+template <int kCtl>
+__device__ __forceinline__ float dpp_f(float v) {
+  return as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), kCtl, 0xf, 0xf, false));
+}
+
+template <class F>
+__device__ __forceinline__ void quant_group(u32x4a4 raw, int f, int nf, XRec *xr) {
+  constexpr int GL = F::kRun / 4;  // lanes per run: 8 (runs of 32) or 4 (runs of 16)
+  const float v0 = as_f32(raw.x), v1 = as_f32(raw.y), v2 = as_f32(raw.z), v3 = as_f32(raw.w);
+  float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+  float t = (v0 + v1) + (v2 + v3);
+  a = fmaxf(a, dpp_f<0xB1>(a));  // quad_perm 1,0,3,2
+  t += dpp_f<0xB1>(t);
+  a = fmaxf(a, dpp_f<0x4E>(a));  // quad_perm 2,3,0,1
+  t += dpp_f<0x4E>(t);
+  if (GL == 8) {
+    a = fmaxf(a, dpp_f<0x141>(a));  // row_half_mirror: lane i <-> 7 - i within 8
+    t += dpp_f<0x141>(t);
+  }
+  if (f < nf) {
+    const int e = x_exp(a);
+    int h0, l0, h1, l1, h2, l2, h3, l3;
+    x_split(v0, e, h0, l0);
+    x_split(v1, e, h1, l1);
+    x_split(v2, e, h2, l2);
+    x_split(v3, e, h3, l3);
+    const int run = f / GL, i = f % GL;
+    int rec, word, slot;
+    F::xslot(run, rec, word, slot);
+    xr[rec].hi[word + i] = pack4(h0, h1, h2, h3);
+    xr[rec].lo[word + i] = pack4(l0, l1, l2, l3);
+    if (i == 0) {
+      xr[rec].s[slot] = ldexpf(1.0f, e);
+      xr[rec].t[slot] = t;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // the streaming kernel
 // ---------------------------------------------------------------------------
-template <class F>
+constexpr int kMaxXV = 4;        // float4s of x per thread (K <= 4 * 4 * 1024)
+constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
+
+// Rows are swept step-major across the chip: at step s, team g of workgroup
+// b (B workgroups of G teams) takes row (s * B + b) * G + g, so the whole grid
+// reads one contiguous window per step and HBM channels stay evenly loaded;
+// the launch picks G so that the steps divide the rows as evenly as
+// possible.  Each wave keeps the next D rows' loads in flight in a ring of
+// register sets and computes a row as soon as it has arrived.
+template <class F, int D, int XV>
 __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ W, uint32_t w_bytes,
                                                     const float *__restrict__ x, const float *__restrict__ bias,
-                                                    float *__restrict__ y, int N, int K, int T) {
-  constexpr int R = F::kRows;
+                                                    float *__restrict__ y, int N, int K, int T, int G) {
+  // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
+  // waves (g >= G) that only help quantise x.  D <= steps (chosen at launch).
   extern __shared__ __align__(16) unsigned char smem[];
   const int U = K >> 6;
   XRec *xr = reinterpret_cast<XRec *>(smem);
+  const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   const uint32_t lane = threadIdx.x & 63;
-  const int wave = (int)(threadIdx.x >> 6);
-  const int G = (int)(blockDim.x >> 6) / T;  // teams per workgroup
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: rows live in SGPRs
   const int g = wave / T, w = wave % T;
-  float *part = reinterpret_cast<float *>(smem + (size_t)U * sizeof(XRec));  // [2][G][R][T]
+  float *part = reinterpret_cast<float *>(smem + (size_t)U * sizeof(XRec));  // [kChunk][G][T] (T > 1)
   const int u = w * 64 + (int)lane;
-  const bool active = u < U;
+  const bool active = u < U && g < G;
   const uint32_t rb = (uint32_t)F::row_bytes(K);
   const uint32_t uoff = active ? F::unit_off(u) : 0u;
   const Rsrc rs = make_rsrc(W, w_bytes);
-  const int rows_per_batch = G * R;
+  const Rsrc rx = make_rsrc(x, (uint32_t)K * 4u);
+  const int window = (int)gridDim.x * G;         // rows per step
+  const int steps = (N + window - 1) / window;  // grid-uniform
+  const int end = N;
+  auto row_of = [&](int step) { return step * window + (int)blockIdx.x * G + g; };
+  // Byte offset of this lane's unit in `row`; rows outside the workgroup's
+  // range (and idle lanes) point at the end of the tensor, where buffer loads
+  // return zeros without touching memory, so every load is unconditional.
+  auto woff = [&](int row) -> uint32_t { return (active && row < end) ? (uint32_t)row * rb + uoff : w_bytes; };
+  // bias values are wave-uniform scalar loads, outside the vector-memory
+  // queue that the weight waits count
+  auto bload = [&](int row) -> float { return (bias != nullptr && row < end) ? bias[row] : 0.0f; };
 
-  typename F::Regs A[R], B[R];
-  int batch = (int)blockIdx.x;
-  const int row0 = batch * rows_per_batch + g * R;
-  if (active) {
+  // 1. activations first, XV float4s per thread (launch: XV * threads >= K/4;
+  //    loads past the end of x return zeros without a memory access).  The
+  //    CU serves vector loads in issue order, so the bare barrier below puts
+  //    every wave's x loads ahead of all weight loads: x arrives after one
+  //    cache round trip instead of behind the first rows of weights.
+  const int nf = K >> 2;
+  u32x4a4 xv[XV];
 #pragma unroll
-    for (int r = 0; r < R; ++r)
-      if (row0 + r < N) F::load(A[r], rs, (uint32_t)(row0 + r) * rb + uoff, lane);
+  for (int i = 0; i < XV; ++i) xv[i] = ld4(rx, 16u * (uint32_t)min(tid + i * nt, nf));
+  __builtin_amdgcn_s_barrier();
+
+  // 2. the first D rows of weights
+  typename F::Regs S[D];
+  float bs[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) {
+    F::load(S[j], rs, woff(row_of(j)), lane);
+    bs[j] = bload(row_of(j));
   }
 
-  // x prologue: one run per thread, cooperatively, into LDS
-  const int nruns = K / F::kRun;
-  for (int i = (int)threadIdx.x; i < nruns; i += (int)blockDim.x) F::prep(x, i, xr);
+  // 3. quantise x into LDS while the weights stream in
+#pragma unroll
+  for (int i = 0; i < XV; ++i) quant_group<F>(xv[i], tid + i * nt, nf, xr);
   __syncthreads();
-  XRec xreg;
+  if (g >= G) return;  // helper wave (T == 1: no barriers follow)
+  XRec xreg = {};
   if (active) xreg = xr[u];
 
-  int par = 0;
-  while (batch * rows_per_batch < N) {
-    const int nbatch = batch + (int)gridDim.x;
-    const int nrow0 = nbatch * rows_per_batch + g * R;
-    const int row = batch * rows_per_batch + g * R;
-    if (active && nbatch * rows_per_batch < N) {
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-        if (nrow0 + r < N) F::load(B[r], rs, (uint32_t)(nrow0 + r) * rb + uoff, lane);
+  // Teams of several waves (T > 1) park each row's per-wave sums in LDS and
+  // reduce them kChunk steps at a time, one barrier per chunk.
+  constexpr int kChunk = kPartChunk;
+  auto flush = [&](int step_end) {  // rows of steps [step_end - n, step_end), n = ((step_end - 1) % kChunk) + 1
+    __syncthreads();
+    const int first = (step_end - 1) / kChunk * kChunk;
+    if (w == 0 && lane < (uint32_t)(step_end - first)) {
+      const int st = first + (int)lane;
+      const int row = row_of(st);
+      if (row < end) {
+        const float *pp = part + ((size_t)(st % kChunk) * G + g) * T;
+        float t = 0.0f;
+        for (int q = 0; q < T; ++q) t += pp[q];
+        y[row] = t + (bias != nullptr ? bias[row] : 0.0f);
+      }
     }
-    float sum[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float acc = 0.0f;
-      if (active && row + r < N) acc = F::compute(A[r], xreg, lane);
-      sum[r] = wave_sum(acc);
-    }
+    __syncthreads();  // the slots are rewritten by the next chunk
+  };
+  auto finish = [&](const typename F::Regs &Q, float b, int step) {
+    const int row = row_of(step);
+    float acc = 0.0f;
+    if (active && row < end) acc = F::compute(Q, xreg, lane);
+    const float sum = wave_sum(acc);
     if (T == 1) {
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (row + r < N) y[row + r] = sum[r] + (bias ? bias[row + r] : 0.0f);
-      }
+      if (lane == 0 && row < end) y[row] = sum + b;
     } else {
-      float *pp = part + (size_t)par * G * R * T;
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) pp[(g * R + r) * T + w] = sum[r];
-      }
-      __syncthreads();
-      if (w == 0 && (int)lane < R && row + (int)lane < N) {
-        float s = 0.0f;
-        for (int t = 0; t < T; ++t) s += pp[(g * R + (int)lane) * T + t];
-        y[row + lane] = s + (bias ? bias[row + lane] : 0.0f);
-      }
-      par ^= 1;  // the next batch writes the other half; two barriers separate reuse
+      if (lane == 0) part[((size_t)(step % kChunk) * G + g) * T + w] = sum;
+      if ((step + 1) % kChunk == 0) flush(step + 1);
     }
+  };
+
+  // 4. stream: consume ring slot j, then refill it D steps ahead.  The loads
+  //    stay unconditional (control flow around loads makes the compiler wait
+  //    for all of them); the last pass may fetch up to D - 1 rows past the
+  //    range, which read zeros.  The final D rows are drained without loads.
+  int s0 = 0;
+  for (; s0 + D < steps; s0 += D) {
 #pragma unroll
-    for (int r = 0; r < R; ++r) A[r] = B[r];
-    batch = nbatch;
+    for (int j = 0; j < D; ++j) {
+      finish(S[j], bs[j], s0 + j);
+      F::load(S[j], rs, woff(row_of(s0 + j + D)), lane);
+      bs[j] = bload(row_of(s0 + j + D));
+    }
   }
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (s0 + j < steps) finish(S[j], bs[j], s0 + j);
+  if (T > 1 && steps % kChunk != 0) flush(steps);
 }
 
 // ---------------------------------------------------------------------------
@@ -423,6 +483,26 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(int type, const uint8
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
+// Ring depth: the format's maximum when every wave has that many rows to
+// stream, else 2 or 1 (a deeper ring than the row count would only issue
+// loads past the range).
+template <class F, int XV>
+void launch_depth(int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint8_t *W, uint32_t wb,
+                  const float *x, const float *bias, float *y, int n, int k, int T, int G) {
+  if (steps >= F::kMaxDepth)
+    launch_timed(gemv_kernel<F, F::kMaxDepth, XV>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T, G);
+  else
+    launch_timed(gemv_kernel<F, 1, XV>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T, G);
+}
+
+template <class F>
+void launch_xv(int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint8_t *W,
+               uint32_t wb, const float *x, const float *bias, float *y, int n, int k, int T, int G) {
+  if (xv <= 1) launch_depth<F, 1>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
+  else if (xv == 2) launch_depth<F, 2>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
+  else launch_depth<F, 4>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
+}
+
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s) {
   const uint8_t *W = static_cast<const uint8_t *>(w);
@@ -431,28 +511,37 @@ hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64
   const int T = (U + 63) / 64;  // waves per row team
   const size_t wbytes_total =
       (size_t)N * (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes : (K / 256) * (type == kQ4_K ? kQ4KBytes : kQ6KBytes));
-  bool fast = (K % 64 == 0) && T <= 16 && wbytes_total < 0xFFFFFFFFull;
+  bool fast = (K % 64 == 0) && K <= 4 * kMaxXV * 1024 && wbytes_total < 0xFFFFFFFFull;
   if (type == kQ4_K) fast = fast && (wa & 15u) == 0;
   else if (type == kQ6_K) fast = fast && (wa & 3u) == 0;
   else if (type == kQ8_0) fast = fast && (wa & 3u) == 0 && ((K / 32) % 2 == 0);
   else return hipErrorInvalidValue;
   if (fast) {
-    const int R = type == kQ4_K ? FQ4K::kRows : 1;
-    // teams per workgroup: cover the rows with about one workgroup per CU
+    // one workgroup per CU (fewer for short tensors); steps = rows per team
+    // at the largest team count, then the fewest teams that still finish in
+    // that many steps (so the last window is as full as possible)
+    int64_t blocks = std::min<int64_t>(cu_count, N);
     const int64_t max_g = 16 / T;
-    int64_t G = (N + (int64_t)cu_count * R - 1) / ((int64_t)cu_count * R);
-    if (G < 1) G = 1;
-    if (G > max_g) G = max_g;
-    const int64_t rows_per_batch = G * R;
-    int64_t blocks = (N + rows_per_batch - 1) / rows_per_batch;
-    if (blocks > cu_count) blocks = cu_count;
-    const dim3 grid((unsigned)blocks), block((unsigned)(64 * T * G));
-    const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * 2 * G * R * T : 0);
+    const int64_t steps0 = (N + blocks * max_g - 1) / (blocks * max_g);
+    const int64_t G = std::max<int64_t>(1, std::min<int64_t>(max_g, (N + blocks * steps0 - 1) / (blocks * steps0)));
+    blocks = std::min<int64_t>(blocks, (N + G * steps0 - 1) / (G * steps0));
+    const int64_t rows_per_wg = G * steps0;
+    // threads: the teams, plus helper waves (T == 1) so that each thread
+    // quantises at most kMaxXV float4s of x
+    int64_t threads = 64 * T * G;
+    if (T == 1) {
+      const int64_t want = ((K / 4 + kMaxXV - 1) / kMaxXV + 63) / 64 * 64;
+      threads = std::min<int64_t>(1024, std::max(threads, want));
+    }
+    const int xv = (int)((K / 4 + threads - 1) / threads);  // <= kMaxXV for K <= 16384
+    const dim3 grid((unsigned)blocks), block((unsigned)threads);
+    const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0);
     const uint32_t wb = (uint32_t)wbytes_total;
-    const int n = (int)N, k = (int)K;
-    if (type == kQ4_K) launch_timed(gemv_kernel<FQ4K>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T);
-    else if (type == kQ6_K) launch_timed(gemv_kernel<FQ6K>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T);
-    else launch_timed(gemv_kernel<FQ80>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T);
+    const int n = (int)N, k = (int)K, gg = (int)G;
+    const int64_t steps = (rows_per_wg + G - 1) / G;
+    if (type == kQ4_K) launch_xv<FQ4K>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
+    else if (type == kQ6_K) launch_xv<FQ6K>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
+    else launch_xv<FQ80>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
     return hipGetLastError();
   }
   int64_t blocks = (N + 3) / 4;
