@@ -13,14 +13,20 @@ timing starts.  Steps are replayed from HIP graphs (one graph per pass over
 all copies) so host launch overhead does not gate the GPU.
 
 The JSON line also carries:
-  roofline      the dominant kernel's algorithmic bytes / its own dispatch
-                duration (hipExtLaunchKernelGGL begin/end events), vs 8 TB/s
+  roofline      the dominant kernel (the gate/up GEMV, 14336x4096 Q4_K, two of
+                the seven launches and the largest share of the step): its
+                quantized weight bytes / its average launch duration, measured
+                with stream events around HIP-graph replays of back-to-back
+                launches over a >= 512 MB pool of weight replicas, vs 8 TB/s;
+                `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE
+                and WRITE_SIZE passes (profiles/gemv_q4k_gate_traffic.md)
   cpu_baseline  the reference CPU path (oracle restatement of
                 linear_out_by_in, scalar mode, 1 core since rows < 32) on one
                 layer copy, dequantized once outside the timing
   extra         per-shape kernel times and secondary configs (C1, C3, C4)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
+     python bench.py --probe gate|copy   (bare workload for counter passes)
 """
 from __future__ import annotations
 
@@ -115,6 +121,35 @@ class Ctx:
     def gemv(self, t, x, k, w, n, y, entry="okq_gemv", rows=1):
         self.okq.call(entry, x.data_ptr(), rows, k, t, w.data_ptr(), w.numel(), n, None, y.data_ptr(), self.stream)
 
+    def graph_us(self, launch, n: int, reps: int = 3) -> float:
+        """Average duration (µs) of one launch inside a HIP graph of n
+        back-to-back launch(i) calls, timed with events on the stream the graph
+        is replayed on."""
+        torch = self.torch
+        launch(0)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(n):
+                launch(i)
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        us = 1000.0 * e0.elapsed_time(e1) / (reps * n)
+        del g
+        return us
+
+    def replicas(self, w, min_bytes: int = 512 << 20):
+        """A pool of copies of w (>= min_bytes) so that rotating launches read
+        HBM rather than the 256 MB MALL; returns (pool, copies)."""
+        copies = max(2, -(-min_bytes // w.numel()))
+        return w.repeat(copies), copies
+
     def kernel_us(self, launch, reps: int) -> list:
         """Per-launch dispatch duration (µs) of `reps` launches of launch(i)."""
         evs = [(self.hip.event(), self.hip.event()) for _ in range(reps)]
@@ -202,31 +237,53 @@ def run_c2(ctx: Ctx, args):
     sec = t1 - t0
     gbs = step_bytes * args.steps / sec / 1e9
 
-    # per-projection kernel durations (dispatch begin/end), rotating copies
+    # per-projection launch durations: graphs of back-to-back launches over a
+    # >= 512 MB pool of replicas of layer copy 0's weights
     shapes = {}
     for name, n, k in C2_PROJ:
         x = x14336 if k == 14336 else x4096
-        us = ctx.kernel_us(lambda r, name=name, n=n, k=k, x=x: ctx.gemv(Q4K, x, k, layers[r % args.copies][name], n,
-                                                                           outs[name]), args.kernel_reps)
         b = wbytes(Q4K, n, k)
-        med = median(us)
-        shapes[name] = {"n": n, "k": k, "weight_bytes": b, "us_median": round(med, 3),
-                        "us_p10": round(pct(us, 10), 3), "us_p90": round(pct(us, 90), 3),
-                        "us_mean": round(sum(us) / len(us), 3),
-                        "gbs": round(b / (sum(us) / len(us)) / 1e3, 1),
-                        "frac_hbm": round(b / (sum(us) / len(us)) / 1e3 / HBM_PEAK_GBS, 4)}
+        pool, copies = ctx.replicas(layers[0][name])
+        y = outs[name]
+
+        def launch(i, pool=pool, copies=copies, b=b, n=n, k=k, x=x, y=y):
+            ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q4K, pool.data_ptr() + (i % copies) * b, b, n, None,
+                         y.data_ptr(), ctx.stream)
+
+        us = ctx.graph_us(launch, max(64, 2 * copies))
+        del pool
+        shapes[name] = {"n": n, "k": k, "weight_bytes": b, "us_mean": round(us, 3),
+                        "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
     return {"gbs": gbs, "sec": sec, "step_bytes": step_bytes, "shapes": shapes, "layers": layers,
             "x4096": x4096, "x14336": x14336}
 
 
-def roofline_from(shapes, step_share=None):
-    # dominant kernel: the C2 down projection (4096 x 14336, its own kernel
-    # instantiation, so rocprof's per-kernel average covers exactly it)
-    s = shapes["down"]
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel from the committed
+    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (line `traffic_bytes_per_launch:
+    N`), or None when no such measurement is committed."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            for line in f:
+                if line.strip().startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1].strip().split()[0])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
+def roofline_from(shapes):
+    # dominant kernel: the gate/up GEMV (14336 x 4096 Q4_K; gemv_kernel<FQ4K,
+    # 2, 2>, an instantiation no other C2 projection uses, so rocprof's
+    # per-kernel average covers exactly these launches)
+    s = shapes["gate"]
     achieved = s["weight_bytes"] / s["us_mean"] / 1e3
-    return {"bound": "hbm", "kernel": "gemv_q4k_kernel<4> (C2 down 4096x14336 Q4_K)",
+    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 2> (C2 gate/up, 14336x4096 Q4_K)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+            "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
 
 
@@ -240,26 +297,37 @@ def run_c3(ctx: Ctx, args):
     w = ctx.quantized(Q6K, n, k, seed=31)
     x = ctx.normal(k, 32)
     y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
-    us = ctx.kernel_us(lambda r: ctx.gemv(Q6K, x, k, w, n, y), max(10, args.kernel_reps // 4))
     b = wbytes(Q6K, n, k)
-    m = sum(us) / len(us)
+    pool, copies = ctx.replicas(w)
     del w
-    return {"shape": [n, k], "weight_bytes": b, "us_median": round(median(us), 2), "us_mean": round(m, 2),
-            "gbs": round(b / m / 1e3, 1), "frac_hbm": round(b / m / 1e3 / HBM_PEAK_GBS, 4)}
+
+    def launch(i):
+        ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q6K, pool.data_ptr() + (i % copies) * b, b, n, None,
+                     y.data_ptr(), ctx.stream)
+
+    us = ctx.graph_us(launch, 16)
+    del pool
+    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 2),
+            "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def run_c1(ctx: Ctx, args):
     n, k = 4096, 4096
     log("C1: Q8_0 4096x4096 GEMV (GPU)")
-    copies = 32  # 570 MB rotated
-    ws = [ctx.quantized(Q8_0, n, k, seed=40 + c) for c in range(copies)]
+    w = ctx.quantized(Q8_0, n, k, seed=40)
     x = ctx.normal(k, 41)
     y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
-    us = ctx.kernel_us(lambda r: ctx.gemv(Q8_0, x, k, ws[r % copies], n, y), args.kernel_reps)
     b = wbytes(Q8_0, n, k)
-    m = sum(us) / len(us)
-    return {"shape": [n, k], "weight_bytes": b, "us_median": round(median(us), 3), "us_mean": round(m, 3),
-            "gbs": round(b / m / 1e3, 1), "frac_hbm": round(b / m / 1e3 / HBM_PEAK_GBS, 4)}
+    pool, copies = ctx.replicas(w)
+
+    def launch(i):
+        ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q8_0, pool.data_ptr() + (i % copies) * b, b, n, None,
+                     y.data_ptr(), ctx.stream)
+
+    us = ctx.graph_us(launch, max(64, 2 * copies))
+    del pool
+    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 3),
+            "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def run_c4(ctx: Ctx, args, c2):
@@ -342,6 +410,28 @@ def run_cpu_baseline(ctx: Ctx, c2, args):
             "ms_per_step": round(1000.0 * sec / passes, 2)}
 
 
+def run_probe(ctx: Ctx, what: str):
+    """Bare workloads for `rocprofv3 --pmc` (one dispatch per launch, no graph)."""
+    torch = ctx.torch
+    if what == "gate":
+        n, k = 14336, 4096
+        b = wbytes(Q4K, n, k)
+        pool, copies = ctx.replicas(ctx.quantized(Q4K, n, k, seed=10_004))
+        x = ctx.normal(k, 1)
+        y = torch.empty(n, dtype=torch.float32, device="cuda")
+        for i in range(20):
+            ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q4K, pool.data_ptr() + (i % copies) * b, b, n, None,
+                         y.data_ptr(), ctx.stream)
+        log(f"probe gate: 20 launches, {b} weight bytes each")
+    else:
+        src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(20):
+            torch.mul(src, 1.0, out=dst)
+        log(f"probe copy: 20 launches, {src.numel() * 4} bytes read and written each")
+    torch.cuda.synchronize()
+
+
 # ---------------------------------------------------------------------------
 
 def main():
@@ -355,6 +445,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
     ap.add_argument("--only", default="c1,c3,c4", help="secondary configs to run (comma list of c1,c3,c4)")
+    ap.add_argument("--probe", choices=["gate", "copy"], default=None,
+                    help="run a bare workload for rocprofv3 counter passes and exit: 20 launches of the C2 gate GEMV "
+                         "over weight replicas, or 20 launches of a 256 MiB f32 elementwise copy (calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -365,6 +458,9 @@ def main():
     from ocelotl_amd import okq
     okq.call("okq_init", 0)
     ctx = Ctx(torch, okq)
+    if args.probe:
+        run_probe(ctx, args.probe)
+        return
 
     c2 = run_c2(ctx, args)
     extra = {"c2_shapes": c2["shapes"]}
