@@ -1,10 +1,11 @@
 // okq_gemm.hip -- MFMA dequant-GEMM for prefill: Y[M,N] = X[M,K] W[N,K]^T (+bias)
 //
 // Numerics (exact operands, f32 accumulation):
-//   * A = X as fp16.  bf16 -> fp16 is exact for 2^-17 <= |x| <= 65504 (bf16
-//     carries 8 significant bits); f32 activations are split into an fp16
-//     hi plane and an fp16 lo plane (x ~= hi + lo to ~2^-22) and contracted
-//     twice.
+//   * A = X as fp16 after a per-row power-of-two scale 2^-s (row max into
+//     [512, 1024), undone exactly in the epilogue).  A scaled bf16 value is
+//     exact in fp16 down to 2^-27 of its row's maximum (bf16 carries 8
+//     significant bits); f32 activations are split into an fp16 hi plane and
+//     an fp16 lo plane (x ~= hi + lo to ~2^-22 relative) and contracted twice.
 //   * B = the integer part of the dequantised weight, exact in fp16:
 //       Q4_K: sc * q       (6-bit scale x 4-bit quant <= 945)
 //     The super-block scales d and dmin are applied in f32 to the per-super-
@@ -13,8 +14,9 @@
 //   So every product inside an MFMA is exact and only f32 summation rounds.
 //
 // Layout / schedule (gfx950):
-//   * A pre-pass converts X once per call into a workspace: fp16 planes
-//     [M][K] and per-32 sums [M][K/32] as fp16 (hi, lo) pairs.
+//   * A pre-pass (one workgroup per row) converts X once per call into a
+//     workspace: fp16 planes [M][K], per-32 sums [M][K/32] as fp16 (hi, lo)
+//     pairs (<= 32768 after scaling) and the row scales 2^s [M].
 //   * Workgroup tile 256 x 128 (8 waves) or 128 x 128 (4 waves) when 256-row
 //     tiles would leave CUs idle; each wave owns 64 x 64 = 2 x 2 MFMA 32x32x16
 //     tiles.  K advances in steps of one 64-weight Q4_K chunk through a
@@ -49,59 +51,90 @@ __device__ __forceinline__ u32x4 bload4(Rsrc r, uint32_t off) { return __builtin
 constexpr int kBN = 128;
 
 // ---------------------------------------------------------------------------
-// pre-pass: X -> fp16 planes + per-32 sums
+// pre-pass: X -> fp16 planes + per-32 sums, one workgroup per row
 // ---------------------------------------------------------------------------
+// Row m is scaled by 2^-s_m (exact) so that its largest |x| lies in
+// [512, 1024): every fp16 value and every per-32 sum (<= 32768) is finite,
+// and a bf16 value is exact in fp16 down to 2^-27 of the row maximum.  The
+// GEMM epilogue multiplies the row's outputs by 2^s_m (rscale[m]), also exact.
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return as_f32(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return as_f32(w & 0xffff0000u); }
+
+template <bool kF32>
+__device__ __forceinline__ void load8(const void *X, int64_t base, float v[8]) {
+  if (kF32) {
+    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(X) + base);
+    const float4 a = p[0], b = p[1];
+    v[0] = a.x, v[1] = a.y, v[2] = a.z, v[3] = a.w, v[4] = b.x, v[5] = b.y, v[6] = b.z, v[7] = b.w;
+  } else {
+    const u32x4 q = *reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(X) + base);
+    v[0] = bf16_lo(q.x), v[1] = bf16_hi(q.x), v[2] = bf16_lo(q.y), v[3] = bf16_hi(q.y);
+    v[4] = bf16_lo(q.z), v[5] = bf16_hi(q.z), v[6] = bf16_lo(q.w), v[7] = bf16_hi(q.w);
+  }
+}
+
 template <bool kF32>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__ X, int M, int K,
                                                         _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
-                                                        h2 *__restrict__ xsum) {
-  const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;  // one 32-run per thread
-  const int runs = K / 32;
-  if (t >= (int64_t)M * runs) return;
-  const int64_t base = t * 32;  // element offset (row-major [M][K], runs never straddle rows)
-  float v[32];
-  if (kF32) {
-    const float4 *p = reinterpret_cast<const float4 *>(static_cast<const float *>(X) + base);
+                                                        h2 *__restrict__ xsum, float *__restrict__ rscale) {
+  __shared__ float red[4];
+  const int m = (int)blockIdx.x;
+  const int tid = (int)threadIdx.x;
+  const int chunks = K / 8;  // 8 activations per thread and pass; 4 consecutive threads = one 32-run
+  const int64_t row = (int64_t)m * K;
+  // pass 1: row max |x|
+  float amax = 0.0f;
+  for (int c = tid; c < chunks; c += 256) {
+    float v[8];
+    load8<kF32>(X, row + 8 * (int64_t)c, v);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  // 2^-s with amax * 2^-s in [512, 1024); zero, inf and NaN rows keep s = 0
+  const int s = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
+  if (tid == 0) rscale[m] = ldexpf(1.0f, s);
+  // pass 2: scaled fp16 planes and per-32 sums (fixed order: pairs within a
+  // thread, then the four threads of the run through DPP)
+  for (int c0 = 0; c0 < chunks; c0 += 256) {
+    const int c = c0 + tid;
+    const bool ok = c < chunks;  // chunks is a multiple of 32: runs never straddle the bound
+    float v[8];
+    if (ok) {
+      load8<kF32>(X, row + 8 * (int64_t)c, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v[i] = 0.0f;
+    }
+    h8 hv, lv;
+    float t = 0.0f;
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float4 q = p[i];
-      v[4 * i] = q.x, v[4 * i + 1] = q.y, v[4 * i + 2] = q.z, v[4 * i + 3] = q.w;
+      const float w = ldexpf(v[i], -s);
+      t += w;
+      const _Float16 h = (_Float16)w;
+      hv[i] = h;
+      lv[i] = (_Float16)(w - (float)h);
     }
-  } else {
-    const u32x4 *p = reinterpret_cast<const u32x4 *>(static_cast<const uint16_t *>(X) + base);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const u32x4 q = p[i];
-      const uint32_t w[4] = {q.x, q.y, q.z, q.w};
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        v[8 * i + 2 * j] = as_f32(w[j] << 16);
-        v[8 * i + 2 * j + 1] = as_f32(w[j] & 0xffff0000u);
+    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    if (ok) {
+      const int64_t base = row + 8 * (int64_t)c;
+      *reinterpret_cast<h8 *>(xhi + base) = hv;
+      if (kF32) *reinterpret_cast<h8 *>(xlo + base) = lv;
+      if ((tid & 3) == 0) {
+        const _Float16 sh = (_Float16)t;
+        h2 pair;
+        pair[0] = sh;
+        pair[1] = (_Float16)(t - (float)sh);
+        xsum[(int64_t)m * (K / 32) + c / 4] = pair;
       }
     }
   }
-  float s = 0.0f;
-  h8 hv[4], lv[4];
-#pragma unroll
-  for (int i = 0; i < 32; ++i) {
-    s += v[i];
-    const _Float16 h = (_Float16)v[i];
-    hv[i / 8][i % 8] = h;
-    if (kF32) lv[i / 8][i % 8] = (_Float16)(v[i] - (float)h);
-  }
-  h8 *ph = reinterpret_cast<h8 *>(xhi + base);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) ph[i] = hv[i];
-  if (kF32) {
-    h8 *pl = reinterpret_cast<h8 *>(xlo + base);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) pl[i] = lv[i];
-  }
-  const _Float16 sh = (_Float16)s;
-  h2 pair;
-  pair[0] = sh;
-  pair[1] = (_Float16)(s - (float)sh);
-  xsum[t] = pair;
 }
 
 // ---------------------------------------------------------------------------
@@ -151,9 +184,10 @@ struct StepRegs {
 template <int BM, bool kLo>
 __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__restrict__ xhi,
                                                          const _Float16 *__restrict__ xlo,
-                                                         const h2 *__restrict__ xsum, const uint8_t *__restrict__ W,
-                                                         const float *__restrict__ bias, float *__restrict__ Y, int M,
-                                                         int N, int K, int tiles_m, int tiles) {
+                                                         const h2 *__restrict__ xsum, const float *__restrict__ rscale,
+                                                         const uint8_t *__restrict__ W, const float *__restrict__ bias,
+                                                         float *__restrict__ Y, int M, int N, int K, int tiles_m,
+                                                         int tiles) {
   constexpr int NT = BM * 2;       // threads
   constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
   constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
@@ -369,7 +403,16 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
     __syncthreads();
   }
 
-  // epilogue: C layout row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32
+  // epilogue: C layout row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32;
+  // undo the pre-pass's per-row power-of-two scale (exact)
+  float rs[2][16];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      const int row = m0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+      rs[i][e] = row < M ? rscale[row] : 0.0f;
+    }
 #pragma unroll
   for (int j = 0; j < 2; ++j) {
     const int col = n0 + wn * 64 + 32 * j + fr;
@@ -380,7 +423,7 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = m0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-        if (row < M) Y[(size_t)row * N + col] = acc[i][j][e] + bv;
+        if (row < M) Y[(size_t)row * N + col] = acc[i][j][e] * rs[i][e] + bv;
       }
     }
   }
@@ -401,7 +444,7 @@ size_t gemm_workspace_bytes(int64_t M, int64_t K, bool x_is_bf16) {
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
   const size_t sums = (size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  return up(plane) + (x_is_bf16 ? 0 : up(plane)) + up(sums);
+  return up(plane) + (x_is_bf16 ? 0 : up(plane)) + up(sums) + up((size_t)M * sizeof(float));
 }
 
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
@@ -411,13 +454,15 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
   _Float16 *xhi = static_cast<_Float16 *>(workspace);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(static_cast<char *>(workspace) + up(plane));
-  h2 *xsum = reinterpret_cast<h2 *>(static_cast<char *>(workspace) + up(plane) + (x_is_bf16 ? 0 : up(plane)));
-  const int64_t runs = M * (K / 32);
-  const unsigned pg = (unsigned)((runs + 255) / 256);
+  char *sums_at = static_cast<char *>(workspace) + up(plane) + (x_is_bf16 ? 0 : up(plane));
+  h2 *xsum = reinterpret_cast<h2 *>(sums_at);
+  float *rscale = reinterpret_cast<float *>(sums_at + up((size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16)));
   if (x_is_bf16)
-    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3(pg), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum);
+    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum,
+                       rscale);
   else
-    hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3(pg), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum);
+    hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum,
+                       rscale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   // bf16 activations with M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x 64);
@@ -433,9 +478,9 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(bm * 2));
-  if (big) launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
-  else if (x_is_bf16) launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
-  else launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, W, bias, y, m, n, k, tiles_m, tiles);
+  if (big) launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
+  else if (x_is_bf16) launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
+  else launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
   return hipGetLastError();
 }
 

@@ -117,3 +117,59 @@ def test_gemm_is_deterministic_and_row_independent(torch, okq, orc):
     # a row computed alone equals the same row inside the big batch
     one = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb.reshape(rows, k)[137:138].reshape(-1), 1, k, wq, n)
     assert (one[0].view(np.uint32) == a[137].view(np.uint32)).all()
+
+
+def q4k_parts(orc, wq, n, k):
+    """|d*sc*q| and |dmin*m| per weight: dequantizing with every 4-bit quant
+    zeroed leaves exactly -dmin*m (Q4_K qs are bytes 16..143 of a block)."""
+    w = orc.dequantize(O.Q4_K, wq, n * k).reshape(n, k)
+    z = wq.reshape(-1, 144).copy()
+    z[:, 16:] = 0
+    w0 = orc.dequantize(O.Q4_K, z.reshape(-1), n * k).reshape(n, k)
+    return np.abs(w.astype(np.float64) - w0), np.abs(w0.astype(np.float64))
+
+
+def test_gemm_wide_dynamic_range_rows(torch, okq, orc):
+    """Activations far outside fp16's range: the pre-pass's per-row
+    power-of-two scale keeps every operand finite.
+      rows 0-2: N(0,1) plus outlier channels (a 32-run of 3000 summing to
+                96000 > 65504, -2500 every 7th channel, a single 60000);
+      rows 3-4: row 0 times 2^40 and 2^-60 -- outputs must equal row 0's times
+                the same power of two, bit for bit (the scale is undone
+                exactly);
+      row 5:    zeros -> exactly zero;
+      row 6:    N(0,1) times 1e6.
+    Outliers make outputs the small difference of large sums, where any f32
+    evaluation order (the reference's included) rounds at the scale of the
+    sums; the GEMM contracts x with d*sc*q and with dmin*m separately, so rows
+    0-2 and 6 are held to 1e-3 |want| + 2^-20 sum_k |x_k| (|d sc q_k| +
+    |dmin m_k|) -- far below what a wrong term, index or scale produces."""
+    rows, n, k = 7, 256, 1024
+    wq = orc.quantize(O.Q4_K, orc.normal(91, n * k, 0.02))
+    pa, pb = q4k_parts(orc, wq, n, k)
+    x = orc.normal(92, rows * k, 1.0).reshape(rows, k)
+    x[0, 64:96] = 3000.0
+    x[1, ::7] = -2500.0
+    x[2, 5] = 60000.0
+    x[3] = x[0] * np.float32(2.0 ** 40)
+    x[4] = x[0] * np.float32(2.0 ** -60)
+    x[5] = 0.0
+    x[6] *= np.float32(1e6)
+    for entry, xin in (("okq_gemm_bf16", "bf16"), ("okq_gemm", "f32")):
+        if xin == "bf16":
+            xb = orc.f32_to_bf16(x.reshape(-1))
+            x32 = orc.bf16_to_f32(xb).reshape(rows, k)
+            got = run(torch, okq, entry, O.Q4_K, xb, rows, k, wq, n)
+        else:
+            x32 = x
+            got = run(torch, okq, entry, O.Q4_K, x.reshape(-1), rows, k, wq, n)
+        assert np.isfinite(got).all(), entry
+        want = orc.linear_q(O.Q4_K, x32.reshape(-1), rows, k, wq, n, None, O.MODE_SCALAR, 1)
+        for r in (0, 1, 2, 6):
+            ax = np.abs(x32[r].astype(np.float64))
+            bound = 1e-3 * np.abs(want[r]) + 2.0 ** -20 * (pa @ ax + pb @ ax)
+            err = np.abs(got[r].astype(np.float64) - want[r])
+            assert (err <= bound).all(), (entry, r, float((err / bound).max()))
+        assert (got[3] == got[0] * np.float32(2.0 ** 40)).all(), entry
+        assert (got[4] == got[0] * np.float32(2.0 ** -60)).all(), entry
+        assert (got[5] == 0.0).all(), entry
