@@ -62,15 +62,18 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Activation quantisation for the integer dot path.  A run of floats is
-// scaled by a power of two 2^-e chosen so that max|x| * 2^-e <= 32640, rounded
-// to an integer q and split as q = hi * 256 + lo with hi, lo in [-128, 127];
-// the weights' small integers then contract with hi and lo exactly through
+// scaled by a power of two 2^-e chosen so that max|x| * 2^-e <= 0.99 * 2^15 =
+// 32440.3, rounded to an integer q and split as q = hi * 256 + lo with hi, lo
+// in [-128, 127] (hi = (q + 128) >> 8 stays <= 127 only while q <= 32639, so
+// run maxima whose mantissa f exceeds 0.99 take the next exponent: a bf16
+// maximum with f = 255/256 would otherwise give q = 32640 and hi = 128); the
+// weights' small integers then contract with hi and lo exactly through
 // v_dot4_i32_i8.  The scaling is exact (v_ldexp_f32); the only approximation
 // is the rounding of q, |error| <= 2^e / 2 <= max|x| * 2^-15.
 __device__ __forceinline__ int x_exp(float amax) {
   int E = __builtin_amdgcn_frexp_expf(amax);    // amax = f * 2^E, f in [0.5, 1)
   float f = __builtin_amdgcn_frexp_mantf(amax);
-  return (f > 0.99609375f) ? E - 14 : E - 15;
+  return (f > 0.99f) ? E - 14 : E - 15;
 }
 
 __device__ __forceinline__ void x_split(float v, int e, int &hi, int &lo) {

@@ -31,6 +31,7 @@ hipError_t launch_dequantize(int type, const void *src, int64_t n, float *dst, h
 hipError_t launch_quantize(int type, const float *src, int64_t n, void *dst, hipStream_t s);
 hipError_t launch_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst, hipStream_t s);
 hipError_t launch_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, hipStream_t s);
+hipError_t launch_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, hipStream_t s);
 
 // Fused dequant-GEMV for one activation row: y[o] = bias[o] + sum_k x[k] W[o,k].
 // cu_count sizes the persistent grid.

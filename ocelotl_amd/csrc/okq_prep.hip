@@ -286,6 +286,20 @@ hipError_t launch_fill_normal(uint64_t seed, int64_t offset, int64_t n, float si
   return hipGetLastError();
 }
 
+// bf16 -> f32 is exact: the bf16 bits are the high half of the f32
+// (crates/loader/src/safetensors_values.rs:115-123).
+__global__ __launch_bounds__(256) void bf16_to_f32_kernel(const uint16_t *__restrict__ src, int64_t n,
+                                                          float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = as_f32((uint32_t)src[i] << 16);
+}
+
+hipError_t launch_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, hipStream_t s) {
+  hipLaunchKernelGGL(bf16_to_f32_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, src, n, dst);
+  return hipGetLastError();
+}
+
 hipError_t launch_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, hipStream_t s) {
   hipLaunchKernelGGL(f32_to_bf16_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, src, n, dst);
   return hipGetLastError();

@@ -225,8 +225,16 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
     if (st != OKQ_OK) return st;
     return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, ws, info.cu_count, s), "gemm launch");
   }
-  if (x_bf16) return fail(OKQ_E_SHAPE, "bf16 activations need the MFMA path, which does not support this shape");
+  // GEMV path: bf16 activations are widened to f32 on the device first (exact)
   const float *xf = static_cast<const float *>(x);
+  if (x_bf16) {
+    void *ws = nullptr;
+    st = get_workspace(dev, s, (size_t)rows * (size_t)K * sizeof(float), &ws);
+    if (st != OKQ_OK) return st;
+    hipError_t e = okq::launch_bf16_to_f32(static_cast<const uint16_t *>(x), rows * K, static_cast<float *>(ws), s);
+    if (e != hipSuccess) return hip_status(e, "bf16 widening launch");
+    xf = static_cast<const float *>(ws);
+  }
   for (int64_t r = 0; r < rows; ++r) {
     hipError_t e = okq::launch_gemv((int)type, xf + r * K, K, w, N, bias, out + r * N, info.cu_count, s);
     if (e != hipSuccess) return hip_status(e, "gemv launch");

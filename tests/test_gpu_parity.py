@@ -243,3 +243,53 @@ def test_python_mirror_linear_d_and_host_slices(torch, orc):
     assert (deq.view(np.uint32) == orc.dequantize(O.Q4_K, wq, n * k).view(np.uint32)).all()
     with pytest.raises(KernelError):
         be.linear_d(be.upload(x), 2, k, w, n, None, be.alloc(2 * n - 1))
+
+
+@pytest.mark.parametrize("t,rows,n,k", [(O.Q6_K, 1, 1024, 4096), (O.Q6_K, 6, 300, 1024), (O.Q8_0, 1, 1024, 4096),
+                                        (O.Q8_0, 5, 130, 800)])
+def test_bf16_activations_on_the_gemv_path(torch, okq, orc, t, rows, n, k):
+    """okq_linear_out_by_in_q_bf16 for formats without an MFMA path: the bf16
+    activations are widened to f32 on the device (exactly, as
+    safetensors_values.rs:115-123) and run through the GEMV."""
+    print(f"[gpu] bf16 linear type={t} rows={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(t, orc.normal(2000 + t + n, n * k, 0.02))
+    xb = orc.f32_to_bf16(orc.normal(2001 + rows, rows * k, 1.0))
+    x32 = orc.bf16_to_f32(xb)
+    bias = orc.normal(2002, n, 0.1)
+    xd = _dev(torch, xb.view(np.int16))
+    wd = _dev(torch, wq)
+    bd = _dev(torch, bias)
+    out = torch.full((rows * n,), float("nan"), dtype=torch.float32, device="cuda")
+    okq.call("okq_linear_out_by_in_q_bf16", xd.data_ptr(), rows, k, t, wd.data_ptr(), wq.size, n, bd.data_ptr(),
+             out.data_ptr(), _stream(torch))
+    torch.cuda.synchronize()
+    got = _host(out).reshape(rows, n)
+    # same result as the f32 entry point on the decoded activations, bit for bit
+    ref32 = gpu_linear(torch, okq, t, x32, rows, k, wq, n, bias)
+    assert _same_bits(got, ref32).all()
+    want = orc.linear_q(t, x32, rows, k, wq, n, bias)
+    ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, f"idx={idx} got={got.reshape(-1)[idx]} want={want.reshape(-1)[idx]} max_abs={dmax}"
+
+
+@pytest.mark.parametrize("t", TYPES)
+def test_gemv_run_max_at_the_limb_boundary(torch, okq, orc, t):
+    """Every activation run's maximum has mantissa 255/256 (1.9921875 * 2^j,
+    exactly representable in bf16): the run's integer scale must leave the
+    high int8 limb in range (q + 128) >> 8 <= 127, here and at the largest
+    mantissa below 255/256."""
+    n, k = 96, 1024
+    wq = orc.quantize(t, orc.normal(3000 + t, n * k, 0.02))
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal(k) * 0.3).astype(np.float32)
+    run = 16 if t == O.Q6_K else 32
+    edge = np.float32(1.9921875)
+    below = np.nextafter(np.float32(0.99), np.float32(1)) * np.float32(2.0)
+    for r in range(k // run):
+        scale = np.float32(2.0 ** (r % 7 - 3))
+        sign = np.float32(-1.0 if r % 2 else 1.0)
+        x[r * run + (r % run)] = sign * (edge if r % 3 else below) * scale
+    got = gpu_linear(torch, okq, t, x, 1, k, wq, n, entry="okq_gemv")
+    want = orc.linear_q(t, x, 1, k, wq, n, None)
+    ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, f"idx={idx} got={got.reshape(-1)[idx]} want={want.reshape(-1)[idx]} max_abs={dmax}"
