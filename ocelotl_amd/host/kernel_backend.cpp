@@ -1,0 +1,263 @@
+// kernel_backend.cpp -- the C++ mirror of the kernel boundary over libokq.so.
+// Validation order and messages follow validate_linear_out_by_in
+// (crates/kernels/src/lib.rs:2443-2497); every check happens before a launch.
+#include "kernel_backend.hpp"
+
+#include <cstdio>
+#include <cstring>
+
+#include "okq.h"
+
+namespace ocelotl {
+
+namespace {
+
+constexpr const char *kBackend = "hip-gfx950";
+
+const std::vector<std::string> &quantized_names() {
+  static const std::vector<std::string> v = {"Q8_0", "Q4K", "Q6K"};
+  return v;
+}
+
+bool is_quantized(GgmlTensorType t) {
+  return t == GgmlTensorType::Q8_0 || t == GgmlTensorType::Q4K || t == GgmlTensorType::Q6K;
+}
+
+std::string last_error() {
+  char buf[512];
+  const size_t n = okq_last_error(buf, sizeof buf);
+  (void)n;
+  return std::string(buf);
+}
+
+// okq_status -> the reference's error kinds: OKQ_E_TYPE is a type this path
+// does not execute (Unsupported), OKQ_E_NODEV is the require_gpu error
+// (lib.rs:1662-1671), everything else is a KernelError with the library's
+// message.
+OcelotlError status_error(okq_status st, std::optional<uint32_t> type_id) {
+  if (st == OKQ_E_TYPE) {
+    std::optional<std::string> req;
+    if (type_id) req = std::to_string(*type_id);
+    return OcelotlError::unsupported("quantized_tensor_type", req, quantized_names());
+  }
+  if (st == OKQ_E_NODEV) return OcelotlError::unsupported("gpu_backend", std::string("gfx950"), {});
+  return OcelotlError::kernel(kBackend, last_error());
+}
+
+Result<void> check(okq_status st, std::optional<uint32_t> type_id = std::nullopt) {
+  if (st == OKQ_OK) return {};
+  return status_error(st, type_id);
+}
+
+OcelotlError kernel_err(const std::string &message) { return OcelotlError::kernel(kBackend, message); }
+
+std::string len_mismatch(const char *what, size_t got, const char *expr, size_t a, size_t b) {
+  char buf[256];
+  std::snprintf(buf, sizeof buf, "linear_out_by_in %s=%zu does not match %s=%zu*%zu=%zu", what, got, expr, a, b,
+                a * b);
+  return buf;
+}
+
+}  // namespace
+
+// ---- errors ------------------------------------------------------------------
+
+OcelotlError OcelotlError::kernel(std::string backend, std::string message) {
+  return OcelotlError(KernelError{std::move(backend), std::move(message)});
+}
+
+OcelotlError OcelotlError::unsupported(std::string feature, std::optional<std::string> requested,
+                                       std::vector<std::string> supported) {
+  return OcelotlError(UnsupportedError{std::move(feature), std::move(requested), std::move(supported)});
+}
+
+std::string OcelotlError::to_string() const {
+  if (const KernelError *k = as_kernel()) return "kernel error on backend `" + k->backend + "`: " + k->message;
+  const UnsupportedError *u = as_unsupported();
+  std::string s = "unsupported feature `" + u->feature + "`";
+  if (u->requested) s += " (requested `" + *u->requested + "`)";
+  s += ": supported = [";
+  for (size_t i = 0; i < u->supported.size(); ++i) s += (i ? ", " : "") + u->supported[i];
+  return s + "]";
+}
+
+// ---- layout --------------------------------------------------------------------
+
+Result<std::pair<int64_t, int64_t>> block_info(GgmlTensorType type) {
+  int64_t e = 0, b = 0;
+  const okq_status st = okq_type_info((uint32_t)type, &e, &b);
+  if (st != OKQ_OK) return status_error(st, (uint32_t)type);
+  return std::make_pair(e, b);
+}
+
+Result<uint64_t> tensor_byte_len(GgmlTensorType type, const std::vector<int64_t> &shape_ne) {
+  uint64_t out = 0;
+  const okq_status st = okq_tensor_bytes((uint32_t)type, shape_ne.data(), (int)shape_ne.size(), &out);
+  if (st != OKQ_OK) return status_error(st, (uint32_t)type);
+  return out;
+}
+
+// ---- buffers -------------------------------------------------------------------
+
+struct DeviceAllocation {
+  void *ptr = nullptr;
+  ~DeviceAllocation() {
+    if (ptr) (void)okq_free(ptr);
+  }
+};
+
+namespace {
+Result<std::shared_ptr<DeviceAllocation>> device_alloc(size_t bytes) {
+  auto a = std::make_shared<DeviceAllocation>();
+  if (bytes > 0) {
+    const okq_status st = okq_alloc(&a->ptr, bytes);
+    if (st != OKQ_OK) return status_error(st, std::nullopt);
+  }
+  return a;
+}
+}  // namespace
+
+float *DeviceTensor::device_ptr() const { return static_cast<float *>(buf_->ptr); }
+
+Result<std::vector<float>> DeviceTensor::to_host_owned() const {
+  std::vector<float> v(len_);
+  if (len_ == 0) return v;
+  Result<void> r = check(okq_memcpy_d2h(v.data(), buf_->ptr, len_ * sizeof(float), stream_));
+  if (r.is_err()) return r.error();
+  r = check(okq_sync(stream_));
+  if (r.is_err()) return r.error();
+  return v;
+}
+
+Result<void> DeviceTensor::write_from_host_slice(const float *src, size_t len) const {
+  if (len != len_) {
+    return kernel_err("write_from_host_slice length " + std::to_string(len) + " does not match tensor length " +
+                      std::to_string(len_));
+  }
+  if (len == 0) return {};
+  Result<void> r = check(okq_memcpy_h2d(buf_->ptr, src, len * sizeof(float), stream_));
+  if (r.is_err()) return r;
+  return check(okq_sync(stream_));  // the host slice may be reused on return
+}
+
+const void *QuantizedWeight::device_ptr() const { return buf_->ptr; }
+
+// ---- backend -------------------------------------------------------------------
+
+Result<HipKernelBackend> HipKernelBackend::create(int ordinal) {
+  Result<void> r = check(okq_init(ordinal));
+  if (r.is_err()) return r.error();
+  return HipKernelBackend(ordinal);
+}
+
+const char *HipKernelBackend::name() const { return okq_backend_name(); }
+
+Result<DeviceTensor> HipKernelBackend::alloc(size_t len) const {
+  auto a = device_alloc(len * sizeof(float));
+  if (a.is_err()) return a.error();
+  DeviceTensor t(a.value(), len, stream_);
+  if (len > 0) {  // zero-filled, like the trait's default (lib.rs:177-181)
+    const std::vector<float> zeros(len, 0.0f);
+    Result<void> r = t.write_from_host_slice(zeros.data(), len);
+    if (r.is_err()) return r.error();
+  }
+  return t;
+}
+
+Result<DeviceTensor> HipKernelBackend::upload(const float *host, size_t len) const {
+  auto a = device_alloc(len * sizeof(float));
+  if (a.is_err()) return a.error();
+  DeviceTensor t(a.value(), len, stream_);
+  Result<void> r = t.write_from_host_slice(host, len);
+  if (r.is_err()) return r.error();
+  return t;
+}
+
+Result<QuantizedWeight> HipKernelBackend::upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1,
+                                                           const uint8_t *blocks, size_t len) const {
+  if (!is_quantized(type))
+    return OcelotlError::unsupported("quantized_tensor_type", std::to_string((uint32_t)type), quantized_names());
+  auto want = tensor_byte_len(type, {(int64_t)ne0, (int64_t)ne1});
+  if (want.is_err()) return want.error();
+  if (len != want.value()) {
+    return kernel_err("quantized weight has " + std::to_string(len) + " bytes, shape [" + std::to_string(ne0) + ", " +
+                      std::to_string(ne1) + "] needs " + std::to_string(want.value()));
+  }
+  auto a = device_alloc(len);
+  if (a.is_err()) return a.error();
+  if (len > 0) {
+    Result<void> r = check(okq_memcpy_h2d(a.value()->ptr, blocks, len, stream_));
+    if (r.is_err()) return r.error();
+    r = check(okq_sync(stream_));
+    if (r.is_err()) return r.error();
+  }
+  return QuantizedWeight(type, ne0, ne1, len, a.value());
+}
+
+Result<DeviceTensor> HipKernelBackend::dequantize(const QuantizedWeight &weight) const {
+  const size_t n = weight.ne0() * weight.ne1();
+  auto a = device_alloc(n * sizeof(float));
+  if (a.is_err()) return a.error();
+  DeviceTensor t(a.value(), n, stream_);
+  Result<void> r = check(okq_dequantize((uint32_t)weight.tensor_type(), weight.device_ptr(), (int64_t)n,
+                                        t.device_ptr(), stream_),
+                         (uint32_t)weight.tensor_type());
+  if (r.is_err()) return r.error();
+  return t;
+}
+
+Result<void> HipKernelBackend::synchronize() const { return check(okq_sync(stream_)); }
+
+Result<void> HipKernelBackend::linear_d(const DeviceTensor &x, size_t rows, size_t in_features,
+                                        const QuantizedWeight &weight, size_t out_features, const DeviceTensor *bias,
+                                        const DeviceTensor &out) const {
+  if (weight.ne0() != in_features || weight.ne1() != out_features) {
+    return kernel_err("linear_d weight shape [" + std::to_string(weight.ne0()) + ", " + std::to_string(weight.ne1()) +
+                      "] does not match in_features=" + std::to_string(in_features) +
+                      " out_features=" + std::to_string(out_features));
+  }
+  if (x.len() != rows * in_features) return kernel_err(len_mismatch("x.len()", x.len(), "rows*in_features", rows, in_features));
+  if (bias && bias->len() != out_features) {
+    return kernel_err("linear_out_by_in bias.len()=" + std::to_string(bias->len()) +
+                      " does not match out_features=" + std::to_string(out_features));
+  }
+  if (out.len() != rows * out_features)
+    return kernel_err(len_mismatch("out.len()", out.len(), "rows*out_features", rows, out_features));
+  return check(okq_linear_out_by_in_q(x.device_ptr(), (int64_t)rows, (int64_t)in_features,
+                                      (uint32_t)weight.tensor_type(), weight.device_ptr(), weight.byte_len(),
+                                      (int64_t)out_features, bias ? bias->device_ptr() : nullptr, out.device_ptr(),
+                                      stream_),
+               (uint32_t)weight.tensor_type());
+}
+
+// Host slices: the trait default's bounce (lib.rs:193-217) -- upload x and
+// bias, run on the device, read `out` back.
+Result<void> HipKernelBackend::linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
+                                                const QuantizedWeight &weight, size_t out_features, const float *bias,
+                                                size_t bias_len, float *out, size_t out_len) const {
+  if (x_len != rows * in_features) return kernel_err(len_mismatch("x.len()", x_len, "rows*in_features", rows, in_features));
+  if (bias && bias_len != out_features) {
+    return kernel_err("linear_out_by_in bias.len()=" + std::to_string(bias_len) +
+                      " does not match out_features=" + std::to_string(out_features));
+  }
+  if (out_len != rows * out_features)
+    return kernel_err(len_mismatch("out.len()", out_len, "rows*out_features", rows, out_features));
+  auto xd = upload(x, x_len);
+  if (xd.is_err()) return xd.error();
+  std::optional<DeviceTensor> bd;
+  if (bias) {
+    auto b = upload(bias, bias_len);
+    if (b.is_err()) return b.error();
+    bd = b.value();
+  }
+  auto od = alloc(out_len);
+  if (od.is_err()) return od.error();
+  Result<void> r = linear_d(xd.value(), rows, in_features, weight, out_features, bd ? &*bd : nullptr, od.value());
+  if (r.is_err()) return r;
+  auto host = od.value().to_host_owned();
+  if (host.is_err()) return host.error();
+  if (out_len) std::memcpy(out, host.value().data(), out_len * sizeof(float));
+  return {};
+}
+
+}  // namespace ocelotl

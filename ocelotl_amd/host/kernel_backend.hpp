@@ -1,0 +1,226 @@
+// kernel_backend.hpp -- C++ host-side mirror of Ocelotl's kernel dispatch
+// boundary for the k-quant linear path, layered on the C-ABI of libokq.so.
+//
+// The reference is Rust: the trait KernelBackend (crates/kernels/src/lib.rs:
+// 84-495), the f32 DeviceTensor (crates/kernels/src/tensor.rs:45-268) and the
+// error types OcelotlError / KernelError / UnsupportedError
+// (crates/core/src/lib.rs:15-99).  This header restates the part of that
+// surface the quantized linear needs, with the same names, argument order and
+// error behaviour, in C++17:
+//   * Result<T> stands for ocelotl_core::Result<T>: a value or an
+//     OcelotlError, never an exception;
+//   * slices (&[f32]) are (pointer, length) pairs and are length-checked
+//     before anything is launched, like validate_linear_out_by_in
+//     (lib.rs:2443-2497);
+//   * the quantized weight takes the place of the f32 weight_out_by_in
+//     (lib.rs:106-116) as raw GGUF blocks of shape [ne0 = in, ne1 = out].
+// Only functions of okq.h are used: device memory comes from okq_alloc, work
+// is queued on the backend's stream (a hipStream_t passed as void*).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <memory>
+#include <optional>
+#include <string>
+#include <utility>
+#include <variant>
+#include <vector>
+
+namespace ocelotl {
+
+// ---- errors (crates/core/src/lib.rs) -------------------------------------
+
+// KernelError{backend, message} (core lib.rs:63-66).
+struct KernelError {
+  std::string backend;
+  std::string message;
+};
+
+// UnsupportedError{feature, requested, supported} (core lib.rs:47-51).
+struct UnsupportedError {
+  std::string feature;
+  std::optional<std::string> requested;
+  std::vector<std::string> supported;
+};
+
+// The two OcelotlError variants this path produces (core lib.rs:15-26).
+class OcelotlError {
+ public:
+  enum class Kind { Kernel, Unsupported };
+
+  static OcelotlError kernel(std::string backend, std::string message);
+  static OcelotlError unsupported(std::string feature, std::optional<std::string> requested,
+                                  std::vector<std::string> supported);
+
+  Kind kind() const { return std::holds_alternative<KernelError>(v_) ? Kind::Kernel : Kind::Unsupported; }
+  const KernelError *as_kernel() const { return std::get_if<KernelError>(&v_); }
+  const UnsupportedError *as_unsupported() const { return std::get_if<UnsupportedError>(&v_); }
+  // Display text in the reference's format ("kernel error on backend `b`: m").
+  std::string to_string() const;
+
+ private:
+  explicit OcelotlError(std::variant<KernelError, UnsupportedError> v) : v_(std::move(v)) {}
+  std::variant<KernelError, UnsupportedError> v_;
+};
+
+// ocelotl_core::Result<T>.
+template <class T>
+class [[nodiscard]] Result {
+ public:
+  Result(T value) : v_(std::move(value)) {}                  // NOLINT: Ok(value)
+  Result(OcelotlError error) : v_(std::move(error)) {}       // NOLINT: Err(error)
+  bool is_ok() const { return v_.index() == 0; }
+  bool is_err() const { return v_.index() == 1; }
+  T &value() { return std::get<0>(v_); }
+  const T &value() const { return std::get<0>(v_); }
+  const OcelotlError &error() const { return std::get<1>(v_); }
+
+ private:
+  std::variant<T, OcelotlError> v_;
+};
+
+template <>
+class [[nodiscard]] Result<void> {
+ public:
+  Result() = default;                                        // Ok(())
+  Result(OcelotlError error) : e_(std::move(error)) {}       // NOLINT: Err(error)
+  bool is_ok() const { return !e_.has_value(); }
+  bool is_err() const { return e_.has_value(); }
+  const OcelotlError &error() const { return *e_; }
+
+ private:
+  std::optional<OcelotlError> e_;
+};
+
+// ---- device, types ---------------------------------------------------------
+
+// Device::Cpu | Device::Gpu{ordinal} (core lib.rs:438-441).
+struct Device {
+  enum class Kind { Cpu, Gpu } kind;
+  int ordinal;
+  static Device gpu(int ordinal) { return Device{Kind::Gpu, ordinal}; }
+};
+
+struct KernelContext {
+  Device device;
+};
+
+// Raw GGML tensor type ids (crates/loader/src/gguf_inspect.rs:170-206): the
+// quantized types this path executes plus the unquantized float types.
+enum class GgmlTensorType : uint32_t { F32 = 0, F16 = 1, Q8_0 = 8, Q4K = 12, Q6K = 14, BF16 = 30 };
+
+// (elements, bytes) per block: the byte_len that GgmlTensorType::
+// fixed_element_size leaves as None for quantized types (gguf_inspect.rs:208-219).
+Result<std::pair<int64_t, int64_t>> block_info(GgmlTensorType type);
+// Byte length of a GGUF tensor from its ne-order shape (gguf_inspect.rs:331-342).
+Result<uint64_t> tensor_byte_len(GgmlTensorType type, const std::vector<int64_t> &shape_ne);
+
+// ---- buffers (crates/kernels/src/tensor.rs) --------------------------------
+
+struct DeviceAllocation;  // okq_alloc'd bytes, freed with the last owner
+
+// f32 device-resident tensor (the Device residency of tensor.rs:87-268).
+// Copies share the buffer, as DeviceTensor's Arc does.
+class DeviceTensor {
+ public:
+  size_t len() const { return len_; }
+  bool is_empty() const { return len_ == 0; }
+  float *device_ptr() const;
+  // tensor.rs:204-222 and :224-245.
+  Result<std::vector<float>> to_host_owned() const;
+  Result<void> write_from_host_slice(const float *src, size_t len) const;
+
+ private:
+  friend class HipKernelBackend;
+  DeviceTensor(std::shared_ptr<DeviceAllocation> buf, size_t len, void *stream)
+      : buf_(std::move(buf)), len_(len), stream_(stream) {}
+  std::shared_ptr<DeviceAllocation> buf_;
+  size_t len_;
+  void *stream_;
+};
+
+// A GGUF weight tensor resident on the device in its file layout:
+// [ne0 = in_features, ne1 = out_features], rows of consecutive blocks
+// (gguf_inspect.rs:118-130).
+class QuantizedWeight {
+ public:
+  GgmlTensorType tensor_type() const { return type_; }
+  size_t ne0() const { return ne0_; }
+  size_t ne1() const { return ne1_; }
+  size_t in_features() const { return ne0_; }
+  size_t out_features() const { return ne1_; }
+  uint64_t byte_len() const { return bytes_; }
+  const void *device_ptr() const;
+
+ private:
+  friend class HipKernelBackend;
+  QuantizedWeight(GgmlTensorType t, size_t ne0, size_t ne1, uint64_t bytes, std::shared_ptr<DeviceAllocation> buf)
+      : type_(t), ne0_(ne0), ne1_(ne1), bytes_(bytes), buf_(std::move(buf)) {}
+  GgmlTensorType type_;
+  size_t ne0_, ne1_;
+  uint64_t bytes_;
+  std::shared_ptr<DeviceAllocation> buf_;
+};
+
+// ---- the backend (crates/kernels/src/lib.rs:84-495) ------------------------
+
+// The slice of KernelBackend the quantized linear touches.
+class KernelBackend {
+ public:
+  virtual ~KernelBackend() = default;
+  virtual const char *name() const = 0;
+  virtual const KernelContext &context() const = 0;
+  // lib.rs:171-181
+  virtual Result<DeviceTensor> upload(const float *host, size_t len) const = 0;
+  virtual Result<DeviceTensor> alloc(size_t len) const = 0;
+  // linear_out_by_in over host slices (lib.rs:106-116) with a quantized
+  // weight: out[r, o] = bias[o] + sum_k x[r, k] * W[o, k].  `bias` may be
+  // null (bias_len 0).
+  virtual Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
+                                        const QuantizedWeight &weight, size_t out_features, const float *bias,
+                                        size_t bias_len, float *out, size_t out_len) const = 0;
+  // linear_d over device-resident tensors (lib.rs:186-217); `out` is
+  // caller-supplied and written in place.
+  virtual Result<void> linear_d(const DeviceTensor &x, size_t rows, size_t in_features, const QuantizedWeight &weight,
+                                size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const = 0;
+};
+
+// The gfx950 backend: name() == "hip-gfx950" (the backend_id convention of
+// crates/kernels/src/cubecl_backend.rs:2268-2272).
+class HipKernelBackend final : public KernelBackend {
+ public:
+  // okq_init(ordinal); a missing or non-gfx950 device is
+  // Unsupported{feature: "gpu_backend"} (require_gpu, lib.rs:1662-1671).
+  static Result<HipKernelBackend> create(int ordinal);
+
+  const char *name() const override;
+  const KernelContext &context() const override { return ctx_; }
+  Result<DeviceTensor> upload(const float *host, size_t len) const override;
+  Result<DeviceTensor> alloc(size_t len) const override;
+  Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
+                                const QuantizedWeight &weight, size_t out_features, const float *bias, size_t bias_len,
+                                float *out, size_t out_len) const override;
+  Result<void> linear_d(const DeviceTensor &x, size_t rows, size_t in_features, const QuantizedWeight &weight,
+                        size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const override;
+
+  // Uploads raw GGUF blocks after checking their byte length against the
+  // shape; only Q8_0 / Q4_K / Q6_K are accepted (Unsupported otherwise).
+  Result<QuantizedWeight> upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1, const uint8_t *blocks,
+                                           size_t len) const;
+  // The weight dequantized to f32 (bit-exact with the CPU definition).
+  Result<DeviceTensor> dequantize(const QuantizedWeight &weight) const;
+  // Waits for the backend's stream.
+  Result<void> synchronize() const;
+
+  // Work is queued on this hipStream_t (null = the null stream).
+  void set_stream(void *stream) { stream_ = stream; }
+  void *stream() const { return stream_; }
+
+ private:
+  explicit HipKernelBackend(int ordinal) : ctx_{Device::gpu(ordinal)} {}
+  KernelContext ctx_;
+  void *stream_ = nullptr;
+};
+
+}  // namespace ocelotl

@@ -1,0 +1,296 @@
+// test_kernel_backend.cpp -- tests of the C++ mirror of the kernel boundary
+// (ocelotl_amd/host/kernel_backend.hpp), written the way the reference tests
+// its backends (crates/kernels/src/lib.rs:2809-3070, :3339-3430;
+// cubecl_backend.rs:2538-2737): same inputs to the reference CPU path and to
+// the backend, compared with the reference rule abs <= tol || rel <= tol.
+//
+// The CPU path is the oracle (oracle/liboracle.so, linked by this test only).
+// Usage: test_kernel_backend cpu|gpu   (cpu: needs no GPU; gpu: an MI355X)
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <functional>
+#include <string>
+#include <vector>
+
+#include "kernel_backend.hpp"
+
+extern "C" {
+// oracle/kquant_oracle.c
+void okr_fill_normal(uint64_t seed, int64_t offset, int64_t n, float sigma, float *dst);
+int okr_quantize(int type, const float *x, int64_t n, uint8_t *dst);
+int okr_dequantize(int type, const uint8_t *src, int64_t n, float *dst);
+int okr_linear_q(int type, int mode, int threads, const float *x, int64_t rows, int64_t in_f, const uint8_t *wq,
+                 int64_t out_f, const float *bias, float *out);
+int64_t okr_block_elems(int type);
+int64_t okr_block_bytes(int type);
+}
+
+using namespace ocelotl;
+
+namespace {
+
+struct Failure {
+  std::string what;
+};
+
+#define CHECK(cond, msg)                                                                     \
+  do {                                                                                       \
+    if (!(cond)) throw Failure{std::string(msg) + "  [" #cond "] line " + std::to_string(__LINE__)}; \
+  } while (0)
+
+template <class T>
+T ok(Result<T> r, const char *what) {
+  if (r.is_err()) throw Failure{std::string(what) + ": " + r.error().to_string()};
+  return std::move(r.value());
+}
+void ok(Result<void> r, const char *what) {
+  if (r.is_err()) throw Failure{std::string(what) + ": " + r.error().to_string()};
+}
+
+constexpr int kScalarMode = 0;  // oracle: linear_out_by_in_compute (lib.rs:1974-2123)
+
+std::vector<float> normal(uint64_t seed, size_t n, float sigma) {
+  std::vector<float> v(n);
+  okr_fill_normal(seed, 0, (int64_t)n, sigma, v.data());
+  return v;
+}
+
+std::vector<uint8_t> quantize(GgmlTensorType t, const std::vector<float> &w) {
+  const int64_t blocks = (int64_t)w.size() / okr_block_elems((int)t);
+  std::vector<uint8_t> q((size_t)(blocks * okr_block_bytes((int)t)));
+  CHECK(okr_quantize((int)t, w.data(), (int64_t)w.size(), q.data()) == 0, "oracle quantize");
+  return q;
+}
+
+std::vector<float> reference(GgmlTensorType t, const std::vector<float> &x, size_t rows, size_t in, const std::vector<uint8_t> &wq,
+                             size_t out_f, const float *bias) {
+  std::vector<float> y(rows * out_f);
+  CHECK(okr_linear_q((int)t, kScalarMode, 1, x.data(), (int64_t)rows, (int64_t)in, wq.data(), (int64_t)out_f, bias,
+                     y.data()) == 0,
+        "oracle linear");
+  return y;
+}
+
+// The reference's comparison (lib.rs:2995-3002): per element abs <= tol or rel <= tol.
+void assert_close(const std::vector<float> &got, const std::vector<float> &want, double tol, const char *what) {
+  CHECK(got.size() == want.size(), what);
+  for (size_t i = 0; i < got.size(); ++i) {
+    const double g = got[i], w = want[i];
+    const double abs = std::fabs(g - w), rel = abs / std::max(std::fabs(w), 1e-30);
+    if (!(abs <= tol || rel <= tol)) {
+      char buf[200];
+      std::snprintf(buf, sizeof buf, "%s: element %zu got %.9g want %.9g", what, i, g, w);
+      throw Failure{buf};
+    }
+  }
+}
+
+bool same_bits(const std::vector<float> &a, const std::vector<float> &b) {
+  return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
+}
+
+const GgmlTensorType kTypes[] = {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q6K};
+
+// ---- tests that need no GPU ---------------------------------------------------
+
+void block_info_matches_gguf_block_sizes() {
+  struct Case { GgmlTensorType t; int64_t e, b; };
+  for (Case c : {Case{GgmlTensorType::Q8_0, 32, 34}, Case{GgmlTensorType::Q4K, 256, 144},
+                 Case{GgmlTensorType::Q6K, 256, 210}, Case{GgmlTensorType::F32, 1, 4},
+                 Case{GgmlTensorType::F16, 1, 2}, Case{GgmlTensorType::BF16, 1, 2}}) {
+    auto info = ok(block_info(c.t), "block_info");
+    CHECK(info.first == c.e && info.second == c.b, "block sizes");
+  }
+  auto q4_0 = block_info((GgmlTensorType)2);  // Q4_0: named by the loader, not executed here
+  CHECK(q4_0.is_err(), "Q4_0 must be unsupported");
+  CHECK(q4_0.error().kind() == OcelotlError::Kind::Unsupported, "Q4_0 error kind");
+  CHECK(q4_0.error().as_unsupported()->feature == "quantized_tensor_type", "Q4_0 feature");
+}
+
+void tensor_byte_len_of_the_gemma4_fixture_tensor() {
+  // fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json: token_embd.weight [2560, 262144] q4_k
+  const uint64_t b = ok(tensor_byte_len(GgmlTensorType::Q4K, {2560, 262144}), "byte len");
+  CHECK(b == 262144ull * (2560 / 256) * 144, "q4_k byte length");
+  auto bad = tensor_byte_len(GgmlTensorType::Q4K, {100, 2});  // rows not block aligned
+  CHECK(bad.is_err() && bad.error().kind() == OcelotlError::Kind::Kernel, "unaligned rows rejected");
+}
+
+void error_display_matches_the_reference_format() {
+  CHECK(OcelotlError::kernel("hip-gfx950", "boom").to_string() == "kernel error on backend `hip-gfx950`: boom",
+        "KernelError display");
+  CHECK(OcelotlError::unsupported("gpu_backend", std::string("gpu"), {"cpu"}).to_string() ==
+            "unsupported feature `gpu_backend` (requested `gpu`): supported = [cpu]",
+        "UnsupportedError display");
+  CHECK(OcelotlError::unsupported("x", std::nullopt, {"a", "b"}).to_string() ==
+            "unsupported feature `x`: supported = [a, b]",
+        "UnsupportedError display without request");
+}
+
+void create_without_a_gfx950_device_is_unsupported() {
+  auto be = HipKernelBackend::create(0);
+  if (be.is_ok()) {
+    std::printf("         (a gfx950 device is present: nothing to check)\n");
+    return;
+  }
+  CHECK(be.error().kind() == OcelotlError::Kind::Unsupported, "require_gpu kind");
+  CHECK(be.error().as_unsupported()->feature == "gpu_backend", "require_gpu feature");
+}
+
+// ---- GPU tests ----------------------------------------------------------------------
+
+HipKernelBackend backend() { return ok(HipKernelBackend::create(0), "create"); }
+
+void backend_identity() {
+  HipKernelBackend be = backend();
+  CHECK(std::string(be.name()) == "hip-gfx950", "name");
+  CHECK(be.context().device.kind == Device::Kind::Gpu && be.context().device.ordinal == 0, "context");
+}
+
+void linear_d_matches_reference_cpu_path() {
+  HipKernelBackend be = backend();
+  struct Shape { size_t rows, out_f, in; };
+  for (GgmlTensorType t : kTypes) {
+    for (Shape s : {Shape{1, 300, 1024}, Shape{3, 257, 2048}, Shape{6, 64, 4096}, Shape{40, 96, 512}}) {
+      const auto wq = quantize(t, normal(100 + (int)t + s.in, s.out_f * s.in, 0.02f));
+      const auto x = normal(200 + s.rows, s.rows * s.in, 1.0f);
+      const auto bias = normal(300, s.out_f, 0.1f);
+      QuantizedWeight w = ok(be.upload_quantized(t, s.in, s.out_f, wq.data(), wq.size()), "upload_quantized");
+      DeviceTensor xd = ok(be.upload(x.data(), x.size()), "upload x");
+      DeviceTensor bd = ok(be.upload(bias.data(), bias.size()), "upload bias");
+      DeviceTensor od = ok(be.alloc(s.rows * s.out_f), "alloc out");
+      ok(be.linear_d(xd, s.rows, s.in, w, s.out_f, &bd, od), "linear_d");
+      const auto got = ok(od.to_host_owned(), "readback");
+      assert_close(got, reference(t, x, s.rows, s.in, wq, s.out_f, bias.data()), 1e-3, "linear_d vs reference");
+    }
+  }
+}
+
+void linear_out_by_in_host_slices_match_linear_d_bit_for_bit() {
+  HipKernelBackend be = backend();
+  const size_t rows = 2, in = 2048, out_f = 130;
+  for (GgmlTensorType t : kTypes) {
+    const auto wq = quantize(t, normal(400 + (int)t, out_f * in, 0.02f));
+    const auto x = normal(401, rows * in, 1.0f);
+    QuantizedWeight w = ok(be.upload_quantized(t, in, out_f, wq.data(), wq.size()), "upload_quantized");
+    std::vector<float> host_out(rows * out_f, NAN);
+    ok(be.linear_out_by_in(x.data(), x.size(), rows, in, w, out_f, nullptr, 0, host_out.data(), host_out.size()),
+       "linear_out_by_in");
+    DeviceTensor xd = ok(be.upload(x.data(), x.size()), "upload");
+    DeviceTensor od = ok(be.alloc(rows * out_f), "alloc");
+    ok(be.linear_d(xd, rows, in, w, out_f, nullptr, od), "linear_d");
+    CHECK(same_bits(host_out, ok(od.to_host_owned(), "readback")), "host-slice and device paths agree");
+  }
+}
+
+void linear_d_rejects_mismatched_lengths_before_launch() {
+  HipKernelBackend be = backend();
+  const size_t in = 256, out_f = 8;
+  const auto wq = quantize(GgmlTensorType::Q4K, normal(500, out_f * in, 0.02f));
+  QuantizedWeight w = ok(be.upload_quantized(GgmlTensorType::Q4K, in, out_f, wq.data(), wq.size()), "upload");
+  std::vector<float> sentinel(2 * out_f, 7.0f);
+  DeviceTensor od = ok(be.upload(sentinel.data(), sentinel.size()), "out");
+  DeviceTensor x_short = ok(be.alloc(2 * in - 1), "x");
+  auto r = be.linear_d(x_short, 2, in, w, out_f, nullptr, od);
+  CHECK(r.is_err() && r.error().kind() == OcelotlError::Kind::Kernel, "short x is a KernelError");
+  CHECK(r.error().as_kernel()->backend == "hip-gfx950", "backend named");
+  CHECK(r.error().as_kernel()->message == "linear_out_by_in x.len()=511 does not match rows*in_features=2*256=512",
+        "message: " + r.error().as_kernel()->message);
+  DeviceTensor x = ok(be.alloc(2 * in), "x");
+  DeviceTensor bias_bad = ok(be.alloc(out_f + 1), "bias");
+  CHECK(be.linear_d(x, 2, in, w, out_f, &bias_bad, od).is_err(), "bias length");
+  DeviceTensor od_short = ok(be.alloc(2 * out_f - 1), "out");
+  CHECK(be.linear_d(x, 2, in, w, out_f, nullptr, od_short).is_err(), "out length");
+  CHECK(be.linear_d(x, 2, in, w, out_f + 1, nullptr, od).is_err(), "weight shape");
+  CHECK(same_bits(ok(od.to_host_owned(), "readback"), sentinel), "nothing was launched");
+}
+
+void upload_quantized_validates_type_and_byte_length() {
+  HipKernelBackend be = backend();
+  std::vector<uint8_t> bytes(144 * 4, 0);
+  CHECK(be.upload_quantized(GgmlTensorType::Q4K, 256, 4, bytes.data(), bytes.size()).is_ok(), "exact length");
+  auto short_len = be.upload_quantized(GgmlTensorType::Q4K, 256, 4, bytes.data(), bytes.size() - 1);
+  CHECK(short_len.is_err() && short_len.error().kind() == OcelotlError::Kind::Kernel, "wrong length");
+  auto f32 = be.upload_quantized(GgmlTensorType::F32, 256, 4, bytes.data(), bytes.size());
+  CHECK(f32.is_err() && f32.error().kind() == OcelotlError::Kind::Unsupported, "unquantized type");
+}
+
+void dequantize_is_bit_exact_with_the_cpu_definition() {
+  HipKernelBackend be = backend();
+  for (GgmlTensorType t : kTypes) {
+    const size_t in = 1024, out_f = 33;
+    const auto wq = quantize(t, normal(600 + (int)t, out_f * in, 0.02f));
+    QuantizedWeight w = ok(be.upload_quantized(t, in, out_f, wq.data(), wq.size()), "upload");
+    const auto got = ok(ok(be.dequantize(w), "dequantize").to_host_owned(), "readback");
+    std::vector<float> want(out_f * in);
+    CHECK(okr_dequantize((int)t, wq.data(), (int64_t)want.size(), want.data()) == 0, "oracle dequant");
+    CHECK(same_bits(got, want), "dequant bits");
+  }
+}
+
+void linear_d_one_hot_column_is_exact() {
+  // x = e_j reproduces column j of the dequantized weight exactly
+  HipKernelBackend be = backend();
+  for (GgmlTensorType t : kTypes) {
+    const size_t in = 512, out_f = 40;
+    const auto wq = quantize(t, normal(700 + (int)t, out_f * in, 0.02f));
+    std::vector<float> wdeq(out_f * in);
+    CHECK(okr_dequantize((int)t, wq.data(), (int64_t)wdeq.size(), wdeq.data()) == 0, "oracle dequant");
+    QuantizedWeight w = ok(be.upload_quantized(t, in, out_f, wq.data(), wq.size()), "upload");
+    for (size_t j : {size_t(0), size_t(31), size_t(257), in - 1}) {
+      std::vector<float> x(in, 0.0f);
+      x[j] = 1.0f;
+      DeviceTensor xd = ok(be.upload(x.data(), in), "x");
+      DeviceTensor od = ok(be.alloc(out_f), "out");
+      ok(be.linear_d(xd, 1, in, w, out_f, nullptr, od), "linear_d");
+      const auto got = ok(od.to_host_owned(), "readback");
+      for (size_t o = 0; o < out_f; ++o) CHECK(got[o] == wdeq[o * in + j], "one-hot column");
+    }
+  }
+}
+
+struct Test {
+  const char *name;
+  std::function<void()> fn;
+};
+
+}  // namespace
+
+int main(int argc, char **argv) {
+  const std::string suite = argc > 1 ? argv[1] : "cpu";
+  std::vector<Test> tests;
+  if (suite == "cpu") {
+    tests = {{"block_info_matches_gguf_block_sizes", block_info_matches_gguf_block_sizes},
+             {"tensor_byte_len_of_the_gemma4_fixture_tensor", tensor_byte_len_of_the_gemma4_fixture_tensor},
+             {"error_display_matches_the_reference_format", error_display_matches_the_reference_format},
+             {"create_without_a_gfx950_device_is_unsupported", create_without_a_gfx950_device_is_unsupported}};
+  } else if (suite == "gpu") {
+    tests = {{"backend_identity", backend_identity},
+             {"linear_d_matches_reference_cpu_path", linear_d_matches_reference_cpu_path},
+             {"linear_out_by_in_host_slices_match_linear_d_bit_for_bit",
+              linear_out_by_in_host_slices_match_linear_d_bit_for_bit},
+             {"linear_d_rejects_mismatched_lengths_before_launch", linear_d_rejects_mismatched_lengths_before_launch},
+             {"upload_quantized_validates_type_and_byte_length", upload_quantized_validates_type_and_byte_length},
+             {"dequantize_is_bit_exact_with_the_cpu_definition", dequantize_is_bit_exact_with_the_cpu_definition},
+             {"linear_d_one_hot_column_is_exact", linear_d_one_hot_column_is_exact}};
+  } else {
+    std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
+    return 2;
+  }
+  int failed = 0;
+  for (const Test &t : tests) {
+    std::printf("[ RUN  ] %s\n", t.name);
+    std::fflush(stdout);
+    try {
+      t.fn();
+      std::printf("[  OK  ] %s\n", t.name);
+    } catch (const Failure &f) {
+      ++failed;
+      std::printf("[ FAIL ] %s: %s\n", t.name, f.what.c_str());
+    }
+    std::fflush(stdout);
+  }
+  std::printf("%zu tests, %d failed\n", tests.size(), failed);
+  return failed ? 1 : 0;
+}
