@@ -129,6 +129,22 @@ okq_status okq_gemm(const float *x, int64_t rows, int64_t in_features, uint32_t 
 okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
                          uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream);
 
+/* Several quantized linears that read the same activations, in one pass over
+ * their weights:  out[i][r, o] = bias[i][o] + sum_k x[r, k] * W_i[o, k]  for
+ * i < count (1..4), every W_i of type w_type with in_features columns and
+ * out_features[i] rows (w_bytes[i] bytes).  The decode GEMV streams the
+ * matrices' concatenated rows in one launch per activation row, quantizing x
+ * once.  `bias` may be NULL (no bias anywhere) or hold NULL entries.  Each
+ * matrix is validated like okq_gemv before anything launches; results equal
+ * okq_gemv's on each matrix bit for bit.  No counterpart in the reference,
+ * whose callers compute such groups one projection at a time: the gate/up
+ * pair of mlp_gated_silu (crates/kernels/src/lib.rs:150-162,
+ * crates/kernels/src/mlp.rs:139-250) and the q/k/v projections of one
+ * normalized hidden state. */
+okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
+                          const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
+                          const float *const *bias, float *const *out, void *stream);
+
 /* ---- instrumentation --------------------------------------------------- */
 
 /* The next compute kernel this thread launches through okq_dequantize,

@@ -312,6 +312,17 @@ __device__ __forceinline__ void quant_group(u32x4a4 raw, int f, int nf, XRec *xr
 // ---------------------------------------------------------------------------
 // the streaming kernel
 // ---------------------------------------------------------------------------
+// Matrices 1..3 of a multi-matrix launch (matrix 0 travels in the kernel's
+// own arguments): rows [start[i], start[i+1]) belong to matrix i + 1;
+// start[i] = INT_MAX for unused entries.
+struct GemvMore {
+  const uint8_t *w[kGemvMaxProblems - 1];
+  const float *bias[kGemvMaxProblems - 1];
+  float *y[kGemvMaxProblems - 1];
+  uint32_t bytes[kGemvMaxProblems - 1];
+  int start[kGemvMaxProblems - 1];
+};
+
 constexpr int kMaxXV = 4;        // float4s of x per thread (K <= 4 * 4 * 1024)
 constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
 
@@ -321,10 +332,15 @@ constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
 // the launch picks G so that the steps divide the rows as evenly as
 // possible.  Each wave keeps the next D rows' loads in flight in a ring of
 // register sets and computes a row as soon as it has arrived.
-template <class F, int D, int XV>
+//
+// One launch may serve several weight matrices of one format and in_features
+// that share the activation row (q/k/v, gate/up): their rows are numbered
+// consecutively and every row finds its matrix, bias and output through
+// wave-uniform scalar selects.
+template <class F, int D, int XV, bool kMulti>
 __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ W, uint32_t w_bytes,
                                                     const float *__restrict__ x, const float *__restrict__ bias,
-                                                    float *__restrict__ y, int N, int K, int T, int G) {
+                                                    float *__restrict__ y, int N, int K, int T, int G, GemvMore M) {
   // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
   // waves (g >= G) that only help quantise x.  D <= steps (chosen at launch).
   extern __shared__ __align__(16) unsigned char smem[];
@@ -339,19 +355,52 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   const bool active = u < U && g < G;
   const uint32_t rb = (uint32_t)F::row_bytes(K);
   const uint32_t uoff = active ? F::unit_off(u) : 0u;
-  const Rsrc rs = make_rsrc(W, w_bytes);
   const Rsrc rx = make_rsrc(x, (uint32_t)K * 4u);
   const int window = (int)gridDim.x * G;         // rows per step
   const int steps = (N + window - 1) / window;  // grid-uniform
   const int end = N;
   auto row_of = [&](int step) { return step * window + (int)blockIdx.x * G + g; };
-  // Byte offset of this lane's unit in `row`; rows outside the workgroup's
-  // range (and idle lanes) point at the end of the tensor, where buffer loads
-  // return zeros without touching memory, so every load is unconditional.
-  auto woff = [&](int row) -> uint32_t { return (active && row < end) ? (uint32_t)row * rb + uoff : w_bytes; };
+  // Matrix selection: single-matrix launches (kMulti = false) never touch M,
+  // so their argument fetch is one small block; multi-matrix launches read
+  // every field of M once with constant indices (runtime indexing would make
+  // each row's lookup a dependent kernel-argument load ahead of the weight
+  // loads) and rows pick their matrix with scalar selects.
+  const int st1 = kMulti ? M.start[0] : INT32_MAX, st2 = kMulti ? M.start[1] : INT32_MAX;
+  const int st3 = kMulti ? M.start[2] : INT32_MAX;
+  const Rsrc rs0 = make_rsrc(W, w_bytes);
+  const Rsrc rs1 = make_rsrc(kMulti ? M.w[0] : nullptr, kMulti ? M.bytes[0] : 0u);
+  const Rsrc rs2 = make_rsrc(kMulti ? M.w[1] : nullptr, kMulti ? M.bytes[1] : 0u);
+  const Rsrc rs3 = make_rsrc(kMulti ? M.w[2] : nullptr, kMulti ? M.bytes[2] : 0u);
+  // the matrix of a row (rows past the end map to the last one)
+  auto prob = [&](int row) {
+    return kMulti ? (int)(row >= st1) + (int)(row >= st2) + (int)(row >= st3) : 0;
+  };
+  auto first_row = [&](int p) { return p == 0 ? 0 : p == 1 ? st1 : p == 2 ? st2 : st3; };
+  auto rsrc = [&](int p) { return p == 0 ? rs0 : p == 1 ? rs1 : p == 2 ? rs2 : rs3; };
+  auto bytes_of = [&](int p) {
+    return p == 0 ? w_bytes : p == 1 ? M.bytes[0] : p == 2 ? M.bytes[1] : M.bytes[2];
+  };
+  auto bias_of = [&](int p) { return p == 0 ? bias : p == 1 ? M.bias[0] : p == 2 ? M.bias[1] : M.bias[2]; };
+  auto y_of = [&](int p) { return p == 0 ? y : p == 1 ? M.y[0] : p == 2 ? M.y[1] : M.y[2]; };
+  // Byte offset of this lane's unit in `row`; rows past the end (and idle
+  // lanes) point at the end of their tensor, where buffer loads return zeros
+  // without touching memory, so every load is unconditional.
+  auto wload = [&](typename F::Regs &R, int row) {
+    const int p = prob(row);
+    const uint32_t off = (active && row < end) ? (uint32_t)(row - first_row(p)) * rb + uoff : bytes_of(p);
+    F::load(R, rsrc(p), off, lane);
+  };
   // bias values are wave-uniform scalar loads, outside the vector-memory
   // queue that the weight waits count
-  auto bload = [&](int row) -> float { return (bias != nullptr && row < end) ? bias[row] : 0.0f; };
+  auto bload = [&](int row) -> float {
+    const int p = prob(row);
+    const float *b = bias_of(p);
+    return (b != nullptr && row < end) ? b[row - first_row(p)] : 0.0f;
+  };
+  auto store = [&](int row, float v) {
+    const int p = prob(row);
+    y_of(p)[row - first_row(p)] = v;
+  };
 
   // 1. activations first, XV float4s per thread (launch: XV * threads >= K/4;
   //    loads past the end of x return zeros without a memory access).  The
@@ -369,7 +418,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   float bs[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) {
-    F::load(S[j], rs, woff(row_of(j)), lane);
+    wload(S[j], row_of(j));
     bs[j] = bload(row_of(j));
   }
 
@@ -394,7 +443,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
         const float *pp = part + ((size_t)(st % kChunk) * G + g) * T;
         float t = 0.0f;
         for (int q = 0; q < T; ++q) t += pp[q];
-        y[row] = t + (bias != nullptr ? bias[row] : 0.0f);
+        const int p = prob(row);
+        const float *b = bias_of(p);
+        store(row, t + (b != nullptr ? b[row - first_row(p)] : 0.0f));
       }
     }
     __syncthreads();  // the slots are rewritten by the next chunk
@@ -405,7 +456,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     if (active && row < end) acc = F::compute(Q, xreg, lane);
     const float sum = wave_sum(acc);
     if (T == 1) {
-      if (lane == 0 && row < end) y[row] = sum + b;
+      if (lane == 0 && row < end) store(row, sum + b);
     } else {
       if (lane == 0) part[((size_t)(step % kChunk) * G + g) * T + w] = sum;
       if ((step + 1) % kChunk == 0) flush(step + 1);
@@ -421,7 +472,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
 #pragma unroll
     for (int j = 0; j < D; ++j) {
       finish(S[j], bs[j], s0 + j);
-      F::load(S[j], rs, woff(row_of(s0 + j + D)), lane);
+      wload(S[j], row_of(s0 + j + D));
       bs[j] = bload(row_of(s0 + j + D));
     }
   }
@@ -484,74 +535,156 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(int type, const uint8
 // launcher
 // ---------------------------------------------------------------------------
 // Ring depth: the format's maximum when every wave has that many rows to
-// stream, else 2 or 1 (a deeper ring than the row count would only issue
-// loads past the range).
-template <class F, int XV>
-void launch_depth(int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint8_t *W, uint32_t wb,
-                  const float *x, const float *bias, float *y, int n, int k, int T, int G) {
-  if (steps >= F::kMaxDepth)
-    launch_timed(gemv_kernel<F, F::kMaxDepth, XV>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T, G);
+// stream, else 1 (a deeper ring than the row count would only issue loads
+// past the range).
+// The matrices of one launch: matrix 0 in the kernel arguments, the rest in M.
+struct GemvLaunch {
+  const uint8_t *w;
+  uint32_t bytes;
+  const float *bias;
+  float *y;
+  int rows;  // total over all matrices
+  bool multi;
+  GemvMore M;
+};
+
+template <class F, int D, int XV>
+void launch_multi(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
+                  int G) {
+  if (L.multi)
+    launch_timed(gemv_kernel<F, D, XV, true>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y, L.rows, k,
+                 T, G, L.M);
   else
-    launch_timed(gemv_kernel<F, 1, XV>, grid, block, (unsigned)lds, s, W, wb, x, bias, y, n, k, T, G);
+    launch_timed(gemv_kernel<F, D, XV, false>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y, L.rows,
+                 k, T, G, L.M);
+}
+
+template <class F, int XV>
+void launch_depth(int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
+                  const float *x, int k, int T, int G) {
+  if (steps >= F::kMaxDepth) launch_multi<F, F::kMaxDepth, XV>(grid, block, lds, s, L, x, k, T, G);
+  else launch_multi<F, 1, XV>(grid, block, lds, s, L, x, k, T, G);
 }
 
 template <class F>
-void launch_xv(int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const uint8_t *W,
-               uint32_t wb, const float *x, const float *bias, float *y, int n, int k, int T, int G) {
-  if (xv <= 1) launch_depth<F, 1>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
-  else if (xv == 2) launch_depth<F, 2>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
-  else launch_depth<F, 4>(steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, G);
+void launch_xv(int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
+               const float *x, int k, int T, int G) {
+  if (xv <= 1) launch_depth<F, 1>(steps, grid, block, lds, s, L, x, k, T, G);
+  else if (xv == 2) launch_depth<F, 2>(steps, grid, block, lds, s, L, x, k, T, G);
+  else launch_depth<F, 4>(steps, grid, block, lds, s, L, x, k, T, G);
+}
+
+namespace {
+
+size_t row_bytes_of(int type, int64_t K) {
+  return (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes : (K / 256) * (type == kQ4_K ? kQ4KBytes : kQ6KBytes));
+}
+
+// Conditions of the streaming kernel for one matrix: aligned base, a 32-bit
+// tensor size, and K within the x prologue's reach.
+bool fast_ok(int type, int64_t K, const void *w, int64_t N) {
+  const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
+  const size_t bytes = (size_t)N * row_bytes_of(type, K);
+  bool fast = (K % 64 == 0) && K <= 4 * kMaxXV * 1024 && bytes < 0xFFFFFFFFull;
+  if (type == kQ4_K) fast = fast && (wa & 15u) == 0;
+  else if (type == kQ6_K) fast = fast && (wa & 3u) == 0;
+  else fast = fast && (wa & 3u) == 0 && ((K / 32) % 2 == 0);
+  return fast;
+}
+
+hipError_t launch_generic(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
+                          int cu_count, hipStream_t s) {
+  int64_t blocks = (N + 3) / 4;
+  if (blocks > (int64_t)cu_count * 4) blocks = (int64_t)cu_count * 4;
+  if (blocks < 1) blocks = 1;
+  launch_timed(gemv_generic_kernel, dim3((unsigned)blocks), dim3(256), 0u, s, type, static_cast<const uint8_t *>(w),
+               x, bias, y, (int)N, (int)K, row_bytes_of(type, K));
+  return hipGetLastError();
+}
+
+// One streaming launch over the concatenated rows of P (all matrices pass
+// fast_ok).
+hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &P, int cu_count, hipStream_t s) {
+  const int64_t N = P.rows;
+  const int U = (int)(K / 64);
+  const int T = (U + 63) / 64;  // waves per row team
+  // one workgroup per CU (fewer for short tensors); steps = rows per team at
+  // the largest team count, then the fewest teams that still finish in that
+  // many steps (so the last window is as full as possible)
+  int64_t blocks = std::min<int64_t>(cu_count, N);
+  const int64_t max_g = 16 / T;
+  const int64_t steps0 = (N + blocks * max_g - 1) / (blocks * max_g);
+  int64_t G = std::max<int64_t>(1, std::min<int64_t>(max_g, (N + blocks * steps0 - 1) / (blocks * steps0)));
+  // Every thread quantises at most kMaxXV float4s of x: with T == 1 extra
+  // helper waves cover x, with teams (T > 1) extra teams do (teams without
+  // rows stream nothing; K <= 16384 keeps this within 16 waves).
+  const int64_t x_threads = (K / 4 + kMaxXV - 1) / kMaxXV;
+  if (T > 1) G = std::max<int64_t>(G, (x_threads + 64 * T - 1) / (64 * T));
+  blocks = std::min<int64_t>(blocks, (N + G * steps0 - 1) / (G * steps0));
+  int64_t threads = 64 * T * G;
+  if (T == 1) threads = std::min<int64_t>(1024, std::max(threads, (x_threads + 63) / 64 * 64));
+  const int xv = (int)((K / 4 + threads - 1) / threads);
+  if (xv > kMaxXV || threads > 1024) return hipErrorInvalidConfiguration;  // excluded by fast_ok's K bound
+  const dim3 grid((unsigned)blocks), block((unsigned)threads);
+  const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0);
+  const int k = (int)K, gg = (int)G;
+  if (type == kQ4_K) launch_xv<FQ4K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  else if (type == kQ6_K) launch_xv<FQ6K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  else launch_xv<FQ80>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
+                             const int64_t *N, const float *const *bias, float *const *y, int cu_count,
+                             hipStream_t s) {
+  if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
+  if (count < 1 || count > kGemvMaxProblems) return hipErrorInvalidValue;
+  GemvLaunch P{};
+  int64_t total = 0;
+  bool fast = true;
+  for (int i = 0; i < count; ++i) {
+    fast = fast && fast_ok(type, K, w[i], N[i]);
+    total += N[i];
+  }
+  fast = fast && total < (int64_t)INT32_MAX;
+  if (!fast) {  // matrix by matrix, each on its own best path
+    for (int i = 0; i < count; ++i) {
+      if (N[i] == 0) continue;
+      hipError_t e = fast_ok(type, K, w[i], N[i]) ? launch_gemv_multi(type, x, K, 1, &w[i], &N[i], &bias[i], &y[i],
+                                                                       cu_count, s)
+                                                  : launch_generic(type, x, K, w[i], N[i], bias[i], y[i], cu_count, s);
+      if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+  P.w = static_cast<const uint8_t *>(w[0]);
+  P.bytes = (uint32_t)((size_t)N[0] * row_bytes_of(type, K));
+  P.bias = bias[0];
+  P.y = y[0];
+  P.multi = count > 1;
+  int64_t start = N[0];
+  for (int i = 1; i < kGemvMaxProblems; ++i) {
+    if (i < count) {
+      P.M.w[i - 1] = static_cast<const uint8_t *>(w[i]);
+      P.M.bytes[i - 1] = (uint32_t)((size_t)N[i] * row_bytes_of(type, K));
+      P.M.bias[i - 1] = bias[i];
+      P.M.y[i - 1] = y[i];
+      P.M.start[i - 1] = (int)start;
+      start += N[i];
+    } else {
+      P.M.start[i - 1] = INT32_MAX;
+    }
+  }
+  P.rows = (int)total;
+  if (total == 0) return hipSuccess;
+  return launch_stream(type, x, K, P, cu_count, s);
 }
 
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s) {
-  const uint8_t *W = static_cast<const uint8_t *>(w);
-  const uintptr_t wa = reinterpret_cast<uintptr_t>(W);
-  const int U = (int)(K / 64);
-  const int T = (U + 63) / 64;  // waves per row team
-  const size_t wbytes_total =
-      (size_t)N * (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes : (K / 256) * (type == kQ4_K ? kQ4KBytes : kQ6KBytes));
-  bool fast = (K % 64 == 0) && K <= 4 * kMaxXV * 1024 && wbytes_total < 0xFFFFFFFFull;
-  if (type == kQ4_K) fast = fast && (wa & 15u) == 0;
-  else if (type == kQ6_K) fast = fast && (wa & 3u) == 0;
-  else if (type == kQ8_0) fast = fast && (wa & 3u) == 0 && ((K / 32) % 2 == 0);
-  else return hipErrorInvalidValue;
-  if (fast) {
-    // one workgroup per CU (fewer for short tensors); steps = rows per team
-    // at the largest team count, then the fewest teams that still finish in
-    // that many steps (so the last window is as full as possible)
-    int64_t blocks = std::min<int64_t>(cu_count, N);
-    const int64_t max_g = 16 / T;
-    const int64_t steps0 = (N + blocks * max_g - 1) / (blocks * max_g);
-    const int64_t G = std::max<int64_t>(1, std::min<int64_t>(max_g, (N + blocks * steps0 - 1) / (blocks * steps0)));
-    blocks = std::min<int64_t>(blocks, (N + G * steps0 - 1) / (G * steps0));
-    const int64_t rows_per_wg = G * steps0;
-    // threads: the teams, plus helper waves (T == 1) so that each thread
-    // quantises at most kMaxXV float4s of x
-    int64_t threads = 64 * T * G;
-    if (T == 1) {
-      const int64_t want = ((K / 4 + kMaxXV - 1) / kMaxXV + 63) / 64 * 64;
-      threads = std::min<int64_t>(1024, std::max(threads, want));
-    }
-    const int xv = (int)((K / 4 + threads - 1) / threads);  // <= kMaxXV for K <= 16384
-    const dim3 grid((unsigned)blocks), block((unsigned)threads);
-    const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0);
-    const uint32_t wb = (uint32_t)wbytes_total;
-    const int n = (int)N, k = (int)K, gg = (int)G;
-    const int64_t steps = (rows_per_wg + G - 1) / G;
-    if (type == kQ4_K) launch_xv<FQ4K>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
-    else if (type == kQ6_K) launch_xv<FQ6K>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
-    else launch_xv<FQ80>(xv, steps, grid, block, lds, s, W, wb, x, bias, y, n, k, T, gg);
-    return hipGetLastError();
-  }
-  int64_t blocks = (N + 3) / 4;
-  if (blocks > (int64_t)cu_count * 4) blocks = (int64_t)cu_count * 4;
-  if (blocks < 1) blocks = 1;
-  const size_t row_bytes =
-      (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes : (K / 256) * (type == kQ4_K ? kQ4KBytes : kQ6KBytes));
-  launch_timed(gemv_generic_kernel, dim3((unsigned)blocks), dim3(256), 0u, s, type, W, x, bias, y, (int)N, (int)K,
-               row_bytes);
-  return hipGetLastError();
+  return launch_gemv_multi(type, x, K, 1, &w, &N, &bias, &y, cu_count, s);
 }
 
 }  // namespace okq

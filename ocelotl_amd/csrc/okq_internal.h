@@ -37,6 +37,13 @@ hipError_t launch_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, hipStr
 // cu_count sizes the persistent grid.
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s);
+// Several matrices of one format and K against the same activation row in
+// one launch (row-concatenated); matrices the streaming kernel cannot take
+// run on their own.  count <= kGemvMaxProblems.
+constexpr int kGemvMaxProblems = 4;
+hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
+                             const int64_t *N, const float *const *bias, float *const *y, int cu_count,
+                             hipStream_t s);
 
 // MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
 // `workspace` holds gemm_workspace_bytes(M, K, x_is_bf16) bytes (256-aligned)

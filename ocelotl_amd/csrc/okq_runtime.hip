@@ -393,6 +393,42 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
   return linear_impl(x, true, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Auto);
 }
 
+okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
+                          const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
+                          const float *const *bias, float *const *out, void *stream) {
+  if (count < 1 || count > okq::kGemvMaxProblems)
+    return fail(OKQ_E_ARG, "gemv_multi count=%d must be between 1 and %d", count, okq::kGemvMaxProblems);
+  if (!w || !w_bytes || !out_features || !out) return fail(OKQ_E_ARG, "gemv_multi null argument array");
+  // every matrix is validated like a single linear before anything launches
+  bool any = false;
+  for (int i = 0; i < count; ++i) {
+    LinearArgs a{rows, in_features, out_features[i], w_type, w_bytes[i]};
+    okq_status st = validate_linear(x, a, w[i], out[i], false);
+    if (st != OKQ_OK) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
+      return fail(st, "gemv_multi matrix %d: %s", i, msg);
+    }
+    any = any || (rows > 0 && out_features[i] > 0);
+  }
+  if (!any) return ok();
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
+  const float *const *b = bias ? bias : nobias;
+  for (int64_t r = 0; r < rows; ++r) {
+    float *o[okq::kGemvMaxProblems];
+    for (int i = 0; i < count; ++i) o[i] = out[i] + r * out_features[i];
+    hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * in_features, in_features, count, w, out_features, b, o,
+                                          info.cu_count, s);
+    if (e != hipSuccess) return hip_status(e, "gemv_multi launch");
+  }
+  return ok();
+}
+
 okq_status okq_gemv(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
                     uint64_t w_bytes, int64_t out_features, const float *bias, float *out, void *stream) {
   return linear_impl(x, false, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Gemv);

@@ -132,9 +132,11 @@ def test_f32_to_bf16_matches_oracle(torch, okq, orc):
 # ---------------------------------------------------------------------------
 
 GEMV_SHAPES = {
-    O.Q4_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (3, 768), (64, 20480)],
-    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480)],
-    O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480)],
+    # few rows with long K (teams of waves per row, x covered by extra teams) included
+    O.Q4_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (3, 768), (64, 20480),
+             (300, 14336), (17, 8192), (2, 16384)],
+    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480), (33, 12288)],
+    O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480), (5, 14336)],
 }
 CASES = [(t, n, k) for t in TYPES for (n, k) in GEMV_SHAPES[t]]
 
@@ -293,3 +295,67 @@ def test_gemv_run_max_at_the_limb_boundary(torch, okq, orc, t):
     want = orc.linear_q(t, x, 1, k, wq, n, None)
     ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
     assert ok, f"idx={idx} got={got.reshape(-1)[idx]} want={want.reshape(-1)[idx]} max_abs={dmax}"
+
+
+MULTI_CASES = [
+    (O.Q4_K, 1, 4096, [4096, 1024, 1024]),   # q/k/v of a Llama-3-8B layer
+    (O.Q4_K, 1, 4096, [14336, 14336]),       # gate/up
+    (O.Q4_K, 3, 14336, [300, 17]),           # K > 4096: teams of waves
+    (O.Q6_K, 2, 1024, [33, 300, 5, 64]),
+    (O.Q8_0, 1, 4096, [1024, 4096]),
+]
+
+
+@pytest.mark.parametrize("t,rows,k,ns", MULTI_CASES)
+def test_gemv_multi_equals_single_gemvs_bit_for_bit(torch, okq, orc, t, rows, k, ns):
+    """okq_gemv_multi streams several matrices sharing x in one launch; every
+    output must equal okq_gemv on its matrix alone, bit for bit, and the
+    reference CPU path within the rule."""
+    import ctypes
+    print(f"[gpu] gemv_multi type={t} rows={rows} K={k} N={ns}", flush=True)
+    wqs = [orc.quantize(t, orc.normal(4000 + 17 * i + t, n * k, 0.02)) for i, n in enumerate(ns)]
+    biases = [orc.normal(4100 + i, n, 0.1) if i % 2 == 0 else None for i, n in enumerate(ns)]
+    x = orc.normal(4200 + rows, rows * k, 1.0)
+    xd = _dev(torch, x)
+    wds = [_dev(torch, wq) for wq in wqs]
+    bds = [None if b is None else _dev(torch, b) for b in biases]
+    outs = [torch.full((rows * n,), float("nan"), dtype=torch.float32, device="cuda") for n in ns]
+    c = len(ns)
+    arr = lambda ty, vals: (ty * c)(*vals)
+    okq.call("okq_gemv_multi", xd.data_ptr(), rows, k, t, c,
+             arr(ctypes.c_void_p, [w.data_ptr() for w in wds]),
+             arr(ctypes.c_uint64, [wq.size for wq in wqs]),
+             arr(ctypes.c_int64, ns),
+             arr(ctypes.c_void_p, [None if b is None else b.data_ptr() for b in bds]),
+             arr(ctypes.c_void_p, [o.data_ptr() for o in outs]), _stream(torch))
+    torch.cuda.synchronize()
+    for i, n in enumerate(ns):
+        got = _host(outs[i]).reshape(rows, n)
+        single = gpu_linear(torch, okq, t, x, rows, k, wqs[i], n, biases[i], entry="okq_gemv")
+        assert _same_bits(got, single).all(), f"matrix {i}"
+        want = orc.linear_q(t, x, rows, k, wqs[i], n, biases[i])
+        ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+        assert ok, f"matrix {i} idx={idx} max_abs={dmax}"
+
+
+def test_gemv_multi_validates_every_matrix_before_launch(torch, okq, orc):
+    import ctypes
+    k, ns = 256, [8, 8]
+    wq = orc.quantize(O.Q4_K, orc.normal(4300, 8 * k, 0.02))
+    wd = _dev(torch, wq)
+    xd = _dev(torch, orc.normal(4301, k, 1.0))
+    o0 = torch.full((8,), 7.0, device="cuda")
+    o1 = torch.full((8,), 7.0, device="cuda")
+    ptrs = (ctypes.c_void_p * 2)(wd.data_ptr(), wd.data_ptr())
+    nn = (ctypes.c_int64 * 2)(*ns)
+    outs = (ctypes.c_void_p * 2)(o0.data_ptr(), o1.data_ptr())
+    with pytest.raises(okq.OkqStatusError) as e:
+        okq.call("okq_gemv_multi", xd.data_ptr(), 1, k, O.Q4_K, 2, ptrs, (ctypes.c_uint64 * 2)(wq.size, wq.size - 1),
+                 nn, None, outs, _stream(torch))
+    assert e.value.status == okq.E_SHAPE and "matrix 1" in e.value.message
+    with pytest.raises(okq.OkqStatusError) as e:
+        okq.call("okq_gemv_multi", xd.data_ptr(), 1, k, O.Q4_K, 5, ptrs, (ctypes.c_uint64 * 2)(wq.size, wq.size),
+                 nn, None, outs, _stream(torch))
+    assert e.value.status == okq.E_ARG
+    torch.cuda.synchronize()
+    assert (o0.cpu().numpy() == 7.0).all() and (o1.cpu().numpy() == 7.0).all()
