@@ -5,28 +5,33 @@ Headline ("C2"): Q4_K decode GEMV over the seven
 Llama-3-8B projections of one decoder layer at batch 1 --
 q 4096x4096, k 1024x4096, v 1024x4096, o 4096x4096, gate 14336x4096,
 up 14336x4096, down 4096x14336 (out x in).  One step = one pass over the
-seven GEMVs of one layer copy; steps rotate over --copies distinct layer
-copies (default 8 = 981 MB of quantized weights, beyond the 256 MB MALL) so
-weights stream from HBM.  value = quantized weight bytes per step x steps /
-wall time of the timed region, in GB/s; inputs are resident in HBM before
-timing starts.  Steps are replayed from HIP graphs (one graph per pass over
-all copies) so host launch overhead does not gate the GPU.
+seven projections of one layer copy, issued as an inference engine issues
+them: q+k+v in one launch and gate+up in one launch (each group reads the same
+activations; okq_gemv_multi), then o and down, which read activations produced
+in between -- 4 launches.  Steps rotate over --copies distinct layer copies
+(default 8 = 981 MB of quantized weights, beyond the 256 MB MALL) so weights
+stream from HBM.  value = quantized weight bytes per step x steps / wall time of
+the timed region, in GB/s; inputs are resident in HBM before timing starts.
+Steps are replayed from HIP graphs so host launch overhead does not gate the
+GPU.  The same steps as seven single-projection launches are reported in
+extra.c2_sequential.
 
 The JSON line also carries:
-  roofline      the dominant kernel (the gate/up GEMV, 14336x4096 Q4_K, two of
-                the seven launches and the largest share of the step): its
-                quantized weight bytes / its average launch duration, measured
-                with stream events around HIP-graph replays of back-to-back
-                launches over a >= 512 MB pool of weight replicas, vs 8 TB/s;
-                `traffic` is the HBM bytes per launch from rocprofv3 FETCH_SIZE
-                and WRITE_SIZE passes (profiles/gemv_q4k_gate_traffic.md)
+  roofline      the dominant kernel (the gate+up launch, 2 x 14336x4096 Q4_K,
+                54% of the step's bytes): its quantized weight bytes / its
+                average launch duration, measured with stream events around
+                HIP-graph replays of back-to-back launches over >= 512 MB of
+                weight replicas per matrix, vs 8 TB/s; `traffic` is the HBM
+                bytes per launch from rocprofv3 FETCH_SIZE and WRITE_SIZE passes
+                (profiles/gemv_q4k_gate_up_traffic.md)
   cpu_baseline  the reference CPU path (oracle restatement of
                 linear_out_by_in, scalar mode, 1 core since rows < 32) on one
                 layer copy, dequantized once outside the timing
-  extra         per-shape kernel times and secondary configs (C1, C3, C4)
+  extra         per-launch and per-projection times, the 7-launch step, and
+                the secondary configs (C1, C3, C4)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate|copy   (bare workload for counter passes)
+     python bench.py --probe gate_up|copy   (bare workload for counter passes)
 """
 from __future__ import annotations
 
@@ -181,27 +186,35 @@ def pct(v, p):
 # C2 headline
 # ---------------------------------------------------------------------------
 
-def run_c2(ctx: Ctx, args):
+# The launches of one decoder layer's projections as an inference engine
+# issues them: projections that read the same activations share a launch
+# (okq_gemv_multi); o and down read activations produced in between.
+C2_GROUPS = [("qkv", ["q", "k", "v"]), ("o", ["o"]), ("gate_up", ["gate", "up"]), ("down", ["down"])]
+C2_SHAPE = {name: (n, k) for name, n, k in C2_PROJ}
+
+
+def launch_group(ctx, names, ws, x, outs):
+    """One launch over the matrices `names` (weights ws[name]) against x."""
+    n0, k = C2_SHAPE[names[0]]
+    if len(names) == 1:
+        w = ws[names[0]]
+        ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q4K, w.data_ptr(), w.numel(), n0, None,
+                     outs[names[0]].data_ptr(), ctx.stream)
+        return
+    c = len(names)
+    ctx.okq.call("okq_gemv_multi", x.data_ptr(), 1, k, Q4K, c,
+                 (ctypes.c_void_p * c)(*[ws[m].data_ptr() for m in names]),
+                 (ctypes.c_uint64 * c)(*[ws[m].numel() for m in names]),
+                 (ctypes.c_int64 * c)(*[C2_SHAPE[m][0] for m in names]), None,
+                 (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), ctx.stream)
+
+
+def time_steps(ctx, args, step):
+    """Wall time of args.steps steps replayed from HIP graphs (one graph per
+    pass over all layer copies, single-step graphs for the remainder)."""
     torch = ctx.torch
-    log(f"C2: generating {args.copies} Q4_K layer copies")
-    layers = []
-    for c in range(args.copies):
-        layers.append({name: ctx.quantized(Q4K, n, k, seed=10_000 + 100 * c + i)
-                       for i, (name, n, k) in enumerate(C2_PROJ)})
-    x4096 = ctx.normal(4096, 1)
-    x14336 = ctx.normal(14336, 2)
-    outs = {name: torch.empty(n, dtype=torch.float32, device="cuda") for name, n, _ in C2_PROJ}
-    step_bytes = sum(wbytes(Q4K, n, k) for _, n, k in C2_PROJ)
-
-    def step(c):
-        lay = layers[c % args.copies]
-        for name, n, k in C2_PROJ:
-            ctx.gemv(Q4K, x14336 if k == 14336 else x4096, k, lay[name], n, outs[name])
-
-    # warm up eagerly once (also compiles nothing: the library is prebuilt)
     step(0)
     torch.cuda.synchronize()
-    # one graph per pass over all copies + single-step graphs for remainders
     g_all = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g_all):
         for c in range(args.copies):
@@ -226,39 +239,75 @@ def run_c2(ctx: Ctx, args):
                 nsteps -= 1
         return i
 
-    log(f"C2: warmup {args.warmup} steps, timing {args.steps} steps")
     i = run_steps(args.warmup)
     i = i - i % args.copies  # restart on a copy boundary
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     run_steps(args.steps, i)
     torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    sec = t1 - t0
-    gbs = step_bytes * args.steps / sec / 1e9
+    return time.perf_counter() - t0
 
-    # per-projection launch durations: graphs of back-to-back launches over a
-    # >= 512 MB pool of replicas of layer copy 0's weights
-    shapes = {}
-    for name, n, k in C2_PROJ:
-        x = x14336 if k == 14336 else x4096
-        b = wbytes(Q4K, n, k)
-        pool, copies = ctx.replicas(layers[0][name])
-        y = outs[name]
 
-        def launch(i, pool=pool, copies=copies, b=b, n=n, k=k, x=x, y=y):
-            ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q4K, pool.data_ptr() + (i % copies) * b, b, n, None,
-                         y.data_ptr(), ctx.stream)
+def run_c2(ctx: Ctx, args):
+    torch = ctx.torch
+    log(f"C2: generating {args.copies} Q4_K layer copies")
+    layers = []
+    for c in range(args.copies):
+        layers.append({name: ctx.quantized(Q4K, n, k, seed=10_000 + 100 * c + i)
+                       for i, (name, n, k) in enumerate(C2_PROJ)})
+    x4096 = ctx.normal(4096, 1)
+    x14336 = ctx.normal(14336, 2)
+    outs = {name: torch.empty(n, dtype=torch.float32, device="cuda") for name, n, _ in C2_PROJ}
+    step_bytes = sum(wbytes(Q4K, n, k) for _, n, k in C2_PROJ)
+
+    def xin(names):
+        return x14336 if C2_SHAPE[names[0]][1] == 14336 else x4096
+
+    def step_fused(c):
+        lay = layers[c % args.copies]
+        for _, names in C2_GROUPS:
+            launch_group(ctx, names, lay, xin(names), outs)
+
+    def step_seq(c):
+        lay = layers[c % args.copies]
+        for name, n, k in C2_PROJ:
+            ctx.gemv(Q4K, xin([name]), k, lay[name], n, outs[name])
+
+    log(f"C2: warmup {args.warmup} steps, timing {args.steps} steps (4 launches per layer)")
+    sec = time_steps(ctx, args, step_fused)
+    log(f"C2: the same steps as 7 single-projection launches")
+    sec_seq = time_steps(ctx, args, step_seq)
+
+    # per-launch durations: graphs of back-to-back launches, each launch on the
+    # next replica of the group's weights (>= 512 MB of replicas per matrix)
+    def group_time(names):
+        pools = {m: ctx.replicas(layers[0][m]) for m in names}
+        copies = min(cp for _, cp in pools.values())
+        x = xin(names)
+
+        def launch(i):
+            ws = {}
+            for m in names:
+                pool, _ = pools[m]
+                b = wbytes(Q4K, *C2_SHAPE[m])
+                ws[m] = pool.narrow(0, (i % copies) * b, b)
+            launch_group(ctx, names, ws, x, outs)
 
         us = ctx.graph_us(launch, max(64, 2 * copies))
-        del pool
-        shapes[name] = {"n": n, "k": k, "weight_bytes": b, "us_mean": round(us, 3),
-                        "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
-    return {"gbs": gbs, "sec": sec, "step_bytes": step_bytes, "shapes": shapes, "layers": layers,
+        b = sum(wbytes(Q4K, *C2_SHAPE[m]) for m in names)
+        del pools
+        return {"matrices": names, "weight_bytes": b, "us_mean": round(us, 3), "gbs": round(b / us / 1e3, 1),
+                "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
+
+    launches = {g: group_time(names) for g, names in C2_GROUPS}
+    shapes = {name: group_time([name]) for name, _, _ in C2_PROJ}
+    return {"gbs": step_bytes * args.steps / sec / 1e9, "sec": sec,
+            "gbs_sequential": step_bytes * args.steps / sec_seq / 1e9, "sec_sequential": sec_seq,
+            "step_bytes": step_bytes, "launches": launches, "shapes": shapes, "layers": layers,
             "x4096": x4096, "x14336": x14336}
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_traffic.md")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
 
 
 def measured_traffic():
@@ -275,13 +324,14 @@ def measured_traffic():
     return None
 
 
-def roofline_from(shapes):
-    # dominant kernel: the gate/up GEMV (14336 x 4096 Q4_K; gemv_kernel<FQ4K,
-    # 2, 2>, an instantiation no other C2 projection uses, so rocprof's
-    # per-kernel average covers exactly these launches)
-    s = shapes["gate"]
+def roofline_from(launches):
+    # dominant kernel: the gate+up launch (two 14336 x 4096 Q4_K matrices, 54%
+    # of the step's bytes; gemv_kernel<FQ4K, 2, 1, true>, an instantiation no
+    # other launch of the step uses, so rocprof's per-kernel average covers
+    # exactly these launches)
+    s = launches["gate_up"]
     achieved = s["weight_bytes"] / s["us_mean"] / 1e3
-    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 2> (C2 gate/up, 14336x4096 Q4_K)",
+    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 1, true> (C2 gate+up, 2 x 14336x4096 Q4_K)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
@@ -413,16 +463,17 @@ def run_cpu_baseline(ctx: Ctx, c2, args):
 def run_probe(ctx: Ctx, what: str):
     """Bare workloads for `rocprofv3 --pmc` (one dispatch per launch, no graph)."""
     torch = ctx.torch
-    if what == "gate":
-        n, k = 14336, 4096
-        b = wbytes(Q4K, n, k)
-        pool, copies = ctx.replicas(ctx.quantized(Q4K, n, k, seed=10_004))
-        x = ctx.normal(k, 1)
-        y = torch.empty(n, dtype=torch.float32, device="cuda")
+    if what == "gate_up":
+        names = ["gate", "up"]
+        ws = {m: ctx.quantized(Q4K, *C2_SHAPE[m], seed=10_004 + i) for i, m in enumerate(names)}
+        pools = {m: ctx.replicas(ws[m]) for m in names}
+        copies = min(cp for _, cp in pools.values())
+        x = ctx.normal(4096, 1)
+        outs = {m: torch.empty(C2_SHAPE[m][0], dtype=torch.float32, device="cuda") for m in names}
+        b = wbytes(Q4K, *C2_SHAPE["gate"])
         for i in range(20):
-            ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q4K, pool.data_ptr() + (i % copies) * b, b, n, None,
-                         y.data_ptr(), ctx.stream)
-        log(f"probe gate: 20 launches, {b} weight bytes each")
+            launch_group(ctx, names, {m: pools[m][0].narrow(0, (i % copies) * b, b) for m in names}, x, outs)
+        log(f"probe gate_up: 20 launches, {2 * b} weight bytes each")
     else:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -445,9 +496,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
     ap.add_argument("--only", default="c1,c3,c4", help="secondary configs to run (comma list of c1,c3,c4)")
-    ap.add_argument("--probe", choices=["gate", "copy"], default=None,
-                    help="run a bare workload for rocprofv3 counter passes and exit: 20 launches of the C2 gate GEMV "
-                         "over weight replicas, or 20 launches of a 256 MiB f32 elementwise copy (calibration)")
+    ap.add_argument("--probe", choices=["gate_up", "copy"], default=None,
+                    help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
+                         "weight replicas, or 20 launches of a 256 MiB f32 elementwise copy (calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -463,7 +514,11 @@ def main():
         return
 
     c2 = run_c2(ctx, args)
-    extra = {"c2_shapes": c2["shapes"]}
+    extra = {"c2_launches": c2["launches"], "c2_shapes": c2["shapes"],
+             "c2_sequential": {"what": "the same step as 7 single-projection launches",
+                               "gbs": round(c2["gbs_sequential"], 1),
+                               "ms_per_step": round(1000.0 * c2["sec_sequential"] / args.steps, 5),
+                               "frac_hbm_peak": round(c2["gbs_sequential"] / HBM_PEAK_GBS, 4)}}
     only = set(args.only.split(",")) if not args.no_extra else set()
     if "c1" in only:
         extra["c1_q8_0"] = run_c1(ctx, args)
@@ -487,11 +542,12 @@ def main():
         "dtype": "q4_k weights x f32 activations (int8 dot4 -> i32, f32 scale/accumulate)",
         "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K on the GPU, N(0,1) f32 activations",
         "config": {"workload": "C2: Q4_K decode GEMV, one Llama-3-8B layer per step (q 4096x4096, k/v 1024x4096, "
-                               "o 4096x4096, gate/up 14336x4096, down 4096x14336), batch 1",
+                               "o 4096x4096, gate/up 14336x4096, down 4096x14336), batch 1, as 4 launches: "
+                               "q+k+v and gate+up each in one okq_gemv_multi launch (they share x), o, down",
                    "batch": 1, "layer_copies_rotated": args.copies,
                    "weight_bytes_per_step": c2["step_bytes"],
                    "frac_hbm_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4)},
-        "roofline": roofline_from(c2["shapes"]),
+        "roofline": roofline_from(c2["launches"]),
         "cpu_baseline": cpu,
         "extra": extra,
     }
