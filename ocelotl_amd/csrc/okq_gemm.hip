@@ -27,6 +27,7 @@
 //     on one XCD: workgroup b runs on XCD b % 8, so b is remapped to give each
 //     XCD a contiguous range of tiles and the weight tile is re-read from that
 //     XCD's L2.
+#include <algorithm>
 #include <type_traits>
 
 #include "okq_device.h"
@@ -187,26 +188,33 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
                                                          const h2 *__restrict__ xsum, const float *__restrict__ rscale,
                                                          const uint8_t *__restrict__ W, const float *__restrict__ bias,
                                                          float *__restrict__ Y, int M, int N, int K, int tiles_m,
-                                                         int tiles) {
+                                                         int tiles, int ksplit, float *__restrict__ part) {
   constexpr int NT = BM * 2;       // threads
   constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
   constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
   __shared__ GemmSmem<BM, kLo> sm;
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
   // contiguous range of tiles (consecutive tiles share an N-tile).
+  // With split-K (ksplit > 1) workgroup (tile, z) covers super-blocks
+  // [z * nsb_all / ksplit, (z + 1) * nsb_all / ksplit) and writes its f32
+  // partial tile to part[z]; consecutive indices keep one slice z and walk
+  // the M-tiles of an N-tile (they share the weight tile in L2).
   const int b = (int)blockIdx.x;
-  const int per_xcd = (tiles + 7) / 8;
-  const int tile = (b % 8) * per_xcd + b / 8;
-  if (tile >= tiles) return;
+  const int jobs = tiles * ksplit;
+  const int per_xcd = (jobs + 7) / 8;
+  const int job = (b % 8) * per_xcd + b / 8;
+  if (job >= jobs) return;
+  const int z = job / tiles, tile = job % tiles;
   const int m0 = (tile % tiles_m) * BM;
   const int n0 = (tile / tiles_m) * kBN;
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
-  const int nsb = K / 256;
-  const int nsteps = 4 * nsb;
-  const uint32_t row_bytes = (uint32_t)nsb * kQ4KBytes;
+  const int nsb_all = K / 256;
+  const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
+  const int nsb = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;  // super-blocks of this slice
+  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
 
   const int sr = tid >> 1, sp = tid & 1;        // A: row, 32-wide half
   const int br = tid / TPR, bq = tid % TPR;     // B: weight row, byte window
@@ -217,9 +225,9 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   const Rsrc rs_w = make_rsrc(W, (uint32_t)((size_t)N * row_bytes));
   // byte offsets of this thread's rows (past the end for rows >= M / >= N:
   // the descriptors return zeros there)
-  const uint32_t a_row = (uint32_t)(m0 + sr) * K32 * 2u + 64u * (uint32_t)sp;
-  const uint32_t s_row = (uint32_t)(m0 + sr) * (K32 / 32u) * 4u + 16u * (uint32_t)sp;
-  const uint32_t w_row = (uint32_t)(n0 + br) * row_bytes;
+  const uint32_t a_row = (uint32_t)(m0 + sr) * K32 * 2u + 64u * (uint32_t)sp + 512u * (uint32_t)sb0;
+  const uint32_t s_row = (uint32_t)(m0 + sr) * (K32 / 32u) * 4u + 16u * (uint32_t)sp + 32u * (uint32_t)sb0;
+  const uint32_t w_row = (uint32_t)(n0 + br) * row_bytes + (uint32_t)sb0 * kQ4KBytes;
 
   // C = step & 3 is a compile-time constant at every call site, so the body
   // is straight-line code (no divergent branches around the loads: the wait
@@ -403,7 +411,23 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
     __syncthreads();
   }
 
-  // epilogue: C layout row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32;
+  // epilogue: C layout row = 8*(e/4) + 4*(lane/32) + e%4, col = lane%32
+  if (ksplit > 1) {  // raw partial tile; splitk_reduce_kernel scales and adds the bias
+    float *P = part + (size_t)z * M * N;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int col = n0 + wn * 64 + 32 * j + fr;
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int e = 0; e < 16; ++e) {
+          const int row = m0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
+          if (row < M) P[(size_t)row * N + col] = acc[i][j][e];
+        }
+    }
+    return;
+  }
   // undo the pre-pass's per-row power-of-two scale (exact)
   float rs[2][16];
 #pragma unroll
@@ -429,6 +453,20 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   }
 }
 
+// Sum of the split-K partials in slice order (deterministic), then the row
+// scale and the bias: Y[m, n] = (sum_z P[z][m, n]) * rscale[m] + bias[n].
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int ksplit, int M, int N,
+                                                            const float *__restrict__ rscale,
+                                                            const float *__restrict__ bias, float *__restrict__ Y) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)M * N;
+  if (i >= total) return;
+  float acc = part[i];
+  for (int z = 1; z < ksplit; ++z) acc += part[(size_t)z * total + i];
+  const int m = (int)(i / N), n = (int)(i % N);
+  Y[i] = acc * rscale[m] + (bias ? bias[n] : 0.0f);
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -440,23 +478,39 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
          w_bytes < (int64_t)UINT32_MAX;
 }
 
-size_t gemm_workspace_bytes(int64_t M, int64_t K, bool x_is_bf16) {
+GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
+  GemmPlan p{};
+  // bf16 activations with M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
+  // 64); otherwise 128 x 128 tiles (f32 activations need the second fp16
+  // plane, which only fits the LDS budget at 128 rows).
+  p.bm = (x_is_bf16 && M > 128) ? 256 : 128;
+  const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
+  // Split K when the tiles alone leave CUs idle: enough slices for about one
+  // workgroup per CU, at least two super-blocks per slice, at most 8.
+  const int64_t nsb = K / 256;
+  int64_t ks = 1;
+  if (tiles * 4 < (int64_t)cu_count * 3) ks = std::min<int64_t>({(cu_count + tiles - 1) / tiles, nsb / 2, 8});
+  p.ksplit = (int)std::max<int64_t>(1, ks);
+  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
   const size_t sums = (size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16);
-  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  return up(plane) + (x_is_bf16 ? 0 : up(plane)) + up(sums) + up((size_t)M * sizeof(float));
+  p.off_lo = up(plane);
+  p.off_sums = p.off_lo + (x_is_bf16 ? 0 : up(plane));
+  p.off_rscale = p.off_sums + up(sums);
+  p.off_part = p.off_rscale + up((size_t)M * sizeof(float));
+  p.workspace = p.off_part + (p.ksplit > 1 ? up((size_t)p.ksplit * M * N * sizeof(float)) : 0);
+  return p;
 }
 
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
-                       const float *bias, float *y, void *workspace, int cu_count, hipStream_t s) {
+                       const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
   if (type != kQ4_K) return hipErrorInvalidValue;
-  auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
-  _Float16 *xhi = static_cast<_Float16 *>(workspace);
-  _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(static_cast<char *>(workspace) + up(plane));
-  char *sums_at = static_cast<char *>(workspace) + up(plane) + (x_is_bf16 ? 0 : up(plane));
-  h2 *xsum = reinterpret_cast<h2 *>(sums_at);
-  float *rscale = reinterpret_cast<float *>(sums_at + up((size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16)));
+  char *ws = static_cast<char *>(workspace);
+  _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
+  _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);
+  h2 *xsum = reinterpret_cast<h2 *>(ws + plan.off_sums);
+  float *rscale = reinterpret_cast<float *>(ws + plan.off_rscale);
+  float *part = plan.ksplit > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
   if (x_is_bf16)
     hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum,
                        rscale);
@@ -465,22 +519,27 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
                        rscale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  // bf16 activations with M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x 64);
-  // otherwise 128 x 128 tiles (f32 activations need the second fp16 plane,
-  // which only fits the LDS budget at 128 rows).
-  (void)cu_count;
   const uint8_t *W = static_cast<const uint8_t *>(w);
-  const int m = (int)M, n = (int)N, k = (int)K;
+  const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
   const int tiles_n = (int)((N + kBN - 1) / kBN);
-  const bool big = x_is_bf16 && M > 128;
-  const int bm = big ? 256 : 128;
-  const int tiles_m = (int)((M + bm - 1) / bm);
+  const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);
   const int tiles = tiles_m * tiles_n;
-  const int per_xcd = (tiles + 7) / 8;
-  const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(bm * 2));
-  if (big) launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
-  else if (x_is_bf16) launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
-  else launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m, tiles);
+  const int per_xcd = (tiles * ks + 7) / 8;
+  const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(plan.bm * 2));
+  if (plan.bm == 256)
+    launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
+                 tiles, ks, part);
+  else if (x_is_bf16)
+    launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
+                 tiles, ks, part);
+  else
+    launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
+                 tiles, ks, part);
+  e = hipGetLastError();
+  if (e != hipSuccess || ks == 1) return e;
+  const int64_t total = M * N;
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m, n,
+                     rscale, bias, y);
   return hipGetLastError();
 }
 

@@ -46,11 +46,19 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
                              hipStream_t s);
 
 // MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
-// `workspace` holds gemm_workspace_bytes(M, K, x_is_bf16) bytes (256-aligned)
-// for the converted activations; it is reused by later calls on the stream.
+// How launch_gemm runs an (M, N, K) problem: tile rows, split-K factor and
+// the workspace layout (activation planes, per-32 sums, row scales, split-K
+// partials), 256-byte aligned offsets from the workspace base.
+struct GemmPlan {
+  int bm;
+  int ksplit;
+  size_t off_lo, off_sums, off_rscale, off_part, workspace;
+};
+GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
+// `workspace` holds plan.workspace bytes (256-aligned); it is reused by later
+// calls on the stream.
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
-                       const float *bias, float *y, void *workspace, int cu_count, hipStream_t s);
-size_t gemm_workspace_bytes(int64_t M, int64_t K, bool x_is_bf16);
+                       const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s);
 
 // True when launch_gemm supports this (type, M, K, N).
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);

@@ -221,9 +221,10 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
   }
   if (use_gemm) {
     void *ws = nullptr;
-    st = get_workspace(dev, s, okq::gemm_workspace_bytes(rows, K, x_bf16), &ws);
+    const okq::GemmPlan plan = okq::gemm_plan(rows, N, K, x_bf16, info.cu_count);
+    st = get_workspace(dev, s, plan.workspace, &ws);
     if (st != OKQ_OK) return st;
-    return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, ws, info.cu_count, s), "gemm launch");
+    return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, ws, plan, s), "gemm launch");
   }
   // GEMV path: bf16 activations are widened to f32 on the device first (exact)
   const float *xf = static_cast<const float *>(x);
