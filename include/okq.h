@@ -101,6 +101,18 @@ okq_status okq_sync(void *stream);
  * crates/loader/src/safetensors_values.rs:155-183). */
 okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float *dst, void *stream);
 
+/* Quantized embedding lookup: out[j, :] = dequantize(row ids[j] of W) for
+ * j < n_ids, bit-identical to okq_dequantize of that row.  W holds the GGUF
+ * blocks of an [ne0, ne1] tensor (ne0 = hidden, ne1 = vocab rows), w_bytes =
+ * ne1 * row_bytes(ne0); ids are in HOST memory and every id must be < ne1;
+ * out: [n_ids, ne0] f32 (device).  n_ids == 0 is a no-op.  Replaces the f32
+ * row copy of the reference's token embedding step
+ * (crates/models/src/qwen/qwen2_5/prefill.rs:95-105, decode.rs:51-52) for a
+ * quantized table such as Gemma4's Q4_K token_embd.weight [2560, 262144];
+ * the id check and its message follow decode.rs:33-38. */
+okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int64_t ne0, int64_t ne1,
+                          const uint32_t *ids, int64_t n_ids, float *out, void *stream);
+
 /* Quantized counterpart of KernelBackend::linear_out_by_in
  * (crates/kernels/src/lib.rs:106-116) and linear_d (:192-202):
  *   out[r, o] = bias[o] + sum_k x[r, k] * W[o, k]
@@ -146,6 +158,47 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
                           const float *const *bias, float *const *out, void *stream);
 
 /* ---- instrumentation --------------------------------------------------- */
+
+/* ---- neighbours of the projections ------------------------------------ */
+
+/* RMSNorm, KernelBackend::rmsnorm (crates/kernels/src/lib.rs:139-147,
+ * crates/kernels/src/rmsnorm.rs:73-128): per row of x [rows, hidden],
+ * out = (x * (1 / sqrt(sum(x^2) / hidden + epsilon))) * weight.  Device f32
+ * buffers; weight 16-byte aligned.  Errors follow rmsnorm.rs:81-114. */
+okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float epsilon, float *out,
+                       void *stream);
+
+/* RMSNorm followed by up to four quantized projections of the normalised
+ * rows (the q/k/v of an attention block):
+ *   out[i][r, o] = bias[i][o] + sum_k rmsnorm(x)[r, k] * W_i[o, k].
+ * Arguments as okq_rmsnorm and okq_gemv_multi.  Decode-sized rows run the
+ * GEMV with the normalisation folded into its activation prologue (no
+ * normalised copy of x is written); larger batches normalise into a
+ * per-stream workspace first.  No counterpart in the reference, whose blocks
+ * call rmsnorm and then each linear (crates/models/src/qwen/qwen2_5/prefill.rs). */
+okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidden, const float *norm_weight,
+                                      float epsilon, uint32_t w_type, int count, const void *const *w,
+                                      const uint64_t *w_bytes, const int64_t *out_features, const float *const *bias,
+                                      float *const *out, void *stream);
+
+/* Quantized gated-SiLU MLP, KernelBackend::mlp_gated_silu
+ * (crates/kernels/src/lib.rs:150-162, crates/kernels/src/mlp.rs:139-250):
+ *   out = down(silu(gate(x)) * up(x)),
+ * x [rows, hidden]; gate and up [hidden -> intermediate] and down
+ * [intermediate -> hidden] as GGUF blocks (rows = output features, so the
+ * byte lengths are intermediate * row_bytes(hidden) and hidden *
+ * row_bytes(intermediate)); gate_buf, up_buf [rows, intermediate] caller-owned
+ * scratch; out [rows, hidden].  Device buffers, x/gate_buf/up_buf 16-byte
+ * aligned.  Decode-sized rows (rows <= 4) run gate+up as one grouped GEMV
+ * when they share a format, and fold silu(gate) * up into the down GEMV's
+ * prologue whenever the down weight takes the streaming GEMV (gate_buf then
+ * holds gate(x)); otherwise silu(gate(x)) * up(x) is left in gate_buf, as the
+ * reference does.  up_buf always holds up(x).  Treat both as scratch.  Zero rows, hidden or
+ * intermediate are errors (mlp.rs:151-165). */
+okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, int64_t intermediate,
+                                uint32_t gate_type, const void *gate_w, uint64_t gate_bytes, uint32_t up_type,
+                                const void *up_w, uint64_t up_bytes, uint32_t down_type, const void *down_w,
+                                uint64_t down_bytes, float *gate_buf, float *up_buf, float *out, void *stream);
 
 /* The next compute kernel this thread launches through okq_dequantize,
  * okq_linear_out_by_in_q*, okq_gemv or okq_gemm* records `start` and `stop`

@@ -337,10 +337,17 @@ constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
 // that share the activation row (q/k/v, gate/up): their rows are numbered
 // consecutively and every row finds its matrix, bias and output through
 // wave-uniform scalar selects.
-template <class F, int D, int XV, bool kMulti>
+//
+// kPro transforms x before it is quantised (the decode neighbours of the
+// projections, computed by every workgroup from the same inputs in the same
+// order, so all workgroups agree): kProRms is the RMSNorm of x with weight
+// P.a (crates/kernels/src/rmsnorm.rs:73-128), kProSwiGLU is silu(x) * P.a with
+// x = gate and P.a = up (crates/kernels/src/mlp.rs:77-88, :233-238).
+template <class F, int D, int XV, bool kMulti, int kPro>
 __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ W, uint32_t w_bytes,
                                                     const float *__restrict__ x, const float *__restrict__ bias,
-                                                    float *__restrict__ y, int N, int K, int T, int G, GemvMore M) {
+                                                    float *__restrict__ y, int N, int K, int T, int G, GemvMore M,
+                                                    GemvPro P) {
   // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
   // waves (g >= G) that only help quantise x.  D <= steps (chosen at launch).
   extern __shared__ __align__(16) unsigned char smem[];
@@ -409,8 +416,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   //    cache round trip instead of behind the first rows of weights.
   const int nf = K >> 2;
   u32x4a4 xv[XV];
+  u32x4a4 av[kPro != kProNone ? XV : 1];
 #pragma unroll
   for (int i = 0; i < XV; ++i) xv[i] = ld4(rx, 16u * (uint32_t)min(tid + i * nt, nf));
+  if constexpr (kPro != kProNone) {
+    const Rsrc ra = make_rsrc(P.a, (uint32_t)K * 4u);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) av[i] = ld4(ra, 16u * (uint32_t)min(tid + i * nt, nf));
+  }
   __builtin_amdgcn_s_barrier();
 
   // 2. the first D rows of weights
@@ -422,7 +435,45 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     bs[j] = bload(row_of(j));
   }
 
-  // 3. quantise x into LDS while the weights stream in
+  // 3. (optional neighbour transform, then) quantise x into LDS while the
+  //    weights stream in.  Values past the end of x are zeros and stay zeros.
+  if constexpr (kPro == kProRms) {
+    // sum of squares: per thread, per wave (DPP), then the waves' partials in
+    // wave order, so every workgroup gets the same value
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      const float a0 = as_f32(xv[i].x), a1 = as_f32(xv[i].y), a2 = as_f32(xv[i].z), a3 = as_f32(xv[i].w);
+      ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
+    }
+    ss = wave_sum(ss);
+    float *red = part + (T > 1 ? kPartChunk * G * T : 0);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float tot = 0.0f;
+    for (int q = 0; q < (nt >> 6); ++q) tot += red[q];
+    const float inv = 1.0f / sqrtf(tot / (float)K + P.eps);  // rms = sqrt(mean + eps), then 1 / rms
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      xv[i].x = as_u32(as_f32(xv[i].x) * inv * as_f32(av[i].x));
+      xv[i].y = as_u32(as_f32(xv[i].y) * inv * as_f32(av[i].y));
+      xv[i].z = as_u32(as_f32(xv[i].z) * inv * as_f32(av[i].z));
+      xv[i].w = as_u32(as_f32(xv[i].w) * inv * as_f32(av[i].w));
+    }
+  } else if constexpr (kPro == kProSwiGLU) {
+    auto gate = [](uint32_t gb, uint32_t ub) {
+      const float gv = as_f32(gb);
+      const float sig = 1.0f / (1.0f + expf(-gv));
+      return as_u32((gv * sig) * as_f32(ub));
+    };
+#pragma unroll
+    for (int i = 0; i < XV; ++i) {
+      xv[i].x = gate(xv[i].x, av[i].x);
+      xv[i].y = gate(xv[i].y, av[i].y);
+      xv[i].z = gate(xv[i].z, av[i].z);
+      xv[i].w = gate(xv[i].w, av[i].w);
+    }
+  }
 #pragma unroll
   for (int i = 0; i < XV; ++i) quant_group<F>(xv[i], tid + i * nt, nf, xr);
   __syncthreads();
@@ -546,17 +597,28 @@ struct GemvLaunch {
   int rows;  // total over all matrices
   bool multi;
   GemvMore M;
+  GemvPro P;
 };
+
+template <class F, int D, int XV, bool kMulti>
+void launch_pro(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
+                int G) {
+  if (L.P.kind == kProRms)
+    launch_timed(gemv_kernel<F, D, XV, kMulti, kProRms>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y,
+                 L.rows, k, T, G, L.M, L.P);
+  else if (L.P.kind == kProSwiGLU)
+    launch_timed(gemv_kernel<F, D, XV, kMulti, kProSwiGLU>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
+                 L.y, L.rows, k, T, G, L.M, L.P);
+  else
+    launch_timed(gemv_kernel<F, D, XV, kMulti, kProNone>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y,
+                 L.rows, k, T, G, L.M, L.P);
+}
 
 template <class F, int D, int XV>
 void launch_multi(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
                   int G) {
-  if (L.multi)
-    launch_timed(gemv_kernel<F, D, XV, true>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y, L.rows, k,
-                 T, G, L.M);
-  else
-    launch_timed(gemv_kernel<F, D, XV, false>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y, L.rows,
-                 k, T, G, L.M);
+  if (L.multi) launch_pro<F, D, XV, true>(grid, block, lds, s, L, x, k, T, G);
+  else launch_pro<F, D, XV, false>(grid, block, lds, s, L, x, k, T, G);
 }
 
 template <class F, int XV>
@@ -626,7 +688,8 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
   const int xv = (int)((K / 4 + threads - 1) / threads);
   if (xv > kMaxXV || threads > 1024) return hipErrorInvalidConfiguration;  // excluded by fast_ok's K bound
   const dim3 grid((unsigned)blocks), block((unsigned)threads);
-  const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0);
+  const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0) +
+                     (P.P.kind == kProRms ? sizeof(float) * 16 : 0);
   const int k = (int)K, gg = (int)G;
   if (type == kQ4_K) launch_xv<FQ4K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
   else if (type == kQ6_K) launch_xv<FQ6K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
@@ -636,12 +699,15 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
 
 }  // namespace
 
+bool gemv_streams(int type, int64_t K, const void *w, int64_t N) { return fast_ok(type, K, w, N); }
+
 hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
-                             hipStream_t s) {
+                             hipStream_t s, const GemvPro &pro) {
   if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
   if (count < 1 || count > kGemvMaxProblems) return hipErrorInvalidValue;
   GemvLaunch P{};
+  P.P = pro;
   int64_t total = 0;
   bool fast = true;
   for (int i = 0; i < count; ++i) {
@@ -649,11 +715,12 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
     total += N[i];
   }
   fast = fast && total < (int64_t)INT32_MAX;
+  if (!fast && pro.kind != kProNone) return hipErrorNotSupported;  // callers check gemv_streams first
   if (!fast) {  // matrix by matrix, each on its own best path
     for (int i = 0; i < count; ++i) {
       if (N[i] == 0) continue;
       hipError_t e = fast_ok(type, K, w[i], N[i]) ? launch_gemv_multi(type, x, K, 1, &w[i], &N[i], &bias[i], &y[i],
-                                                                       cu_count, s)
+                                                                       cu_count, s, pro)
                                                   : launch_generic(type, x, K, w[i], N[i], bias[i], y[i], cu_count, s);
       if (e != hipSuccess) return e;
     }
@@ -684,7 +751,7 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
 
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s) {
-  return launch_gemv_multi(type, x, K, 1, &w, &N, &bias, &y, cu_count, s);
+  return launch_gemv_multi(type, x, K, 1, &w, &N, &bias, &y, cu_count, s, GemvPro{});
 }
 
 }  // namespace okq

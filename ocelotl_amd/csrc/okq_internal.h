@@ -33,6 +33,16 @@ hipError_t launch_fill_normal(uint64_t seed, int64_t offset, int64_t n, float si
 hipError_t launch_f32_to_bf16(const float *src, int64_t n, uint16_t *dst, hipStream_t s);
 hipError_t launch_bf16_to_f32(const uint16_t *src, int64_t n, float *dst, hipStream_t s);
 
+// Row gather: out[j, :] = dequant(W row ids[j]) for j < n (ids in host memory,
+// each < the weight's row count).  Row ids ride in the kernel arguments,
+// kGatherMaxIds per launch.
+constexpr int kGatherMaxIds = 480;
+struct GatherIds {
+  uint32_t id[kGatherMaxIds];
+};
+hipError_t launch_get_rows(int type, const void *w, int64_t row_bytes, int64_t ne0, const uint32_t *ids, int64_t n,
+                           float *out, hipStream_t s);
+
 // Fused dequant-GEMV for one activation row: y[o] = bias[o] + sum_k x[k] W[o,k].
 // cu_count sizes the persistent grid.
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
@@ -41,9 +51,25 @@ hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64
 // one launch (row-concatenated); matrices the streaming kernel cannot take
 // run on their own.  count <= kGemvMaxProblems.
 constexpr int kGemvMaxProblems = 4;
+// Optional transform of x ahead of its quantisation: none, RMSNorm with weight
+// `a` and epsilon `eps`, or the gated SiLU silu(x) * a (x = gate, a = up).
+// A transform needs every matrix of the launch to pass gemv_streams.
+enum GemvProKind { kProNone = 0, kProRms = 1, kProSwiGLU = 2 };
+struct GemvPro {
+  int kind;
+  const float *a;
+  float eps;
+};
+bool gemv_streams(int type, int64_t K, const void *w, int64_t N);
 hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
-                             hipStream_t s);
+                             hipStream_t s, const GemvPro &pro);
+
+// The same neighbours on their own (rows of `hidden` values): RMSNorm with the
+// reference's order of operations, and the gated SiLU over n values.
+hipError_t launch_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float eps, float *out,
+                          hipStream_t s);
+hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *out, hipStream_t s);
 
 // MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
 // How launch_gemm runs an (M, N, K) problem: tile rows, split-K factor and

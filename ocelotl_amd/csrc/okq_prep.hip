@@ -16,21 +16,17 @@ __device__ __forceinline__ uint32_t ld_u16(const uint8_t *p) {
   return (uint32_t)(*reinterpret_cast<const uint16_t *>(p));  // blocks are 2-byte aligned
 }
 
-__global__ __launch_bounds__(256) void dequant_q8_0_kernel(const uint8_t *__restrict__ src, int64_t n,
-                                                           float *__restrict__ dst) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint8_t *blk = src + (i >> 5) * kQ8Bytes;
+// Element i of a run of blocks starting at `base`, in the order and rounding
+// of the GGUF spec (one product or difference rounded at a time).
+__device__ __forceinline__ float dq_q8_0(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 5) * kQ8Bytes;
   float d = f16_bits_exact(ld_u16(blk));
   float q = (float)(int8_t)blk[2 + (i & 31)];
-  dst[i] = __fmul_rn(q, d);
+  return __fmul_rn(q, d);
 }
 
-__global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__restrict__ src, int64_t n,
-                                                           float *__restrict__ dst) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint8_t *blk = src + (i >> 8) * kQ4KBytes;
+__device__ __forceinline__ float dq_q4_k(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 8) * kQ4KBytes;
   uint32_t r = (uint32_t)(i & 255);
   uint32_t c = r >> 6, hi = (r >> 5) & 1u, l = r & 31u;
   uint32_t j = 2 * c + hi;
@@ -42,14 +38,11 @@ __global__ __launch_bounds__(256) void dequant_q4_k_kernel(const uint8_t *__rest
   uint32_t q = (blk[16 + 32 * c + l] >> (4 * hi)) & 15u;
   float ds = __fmul_rn(d, (float)sc);
   float dm = __fmul_rn(dmin, (float)m);
-  dst[i] = __fsub_rn(__fmul_rn(ds, (float)q), dm);
+  return __fsub_rn(__fmul_rn(ds, (float)q), dm);
 }
 
-__global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__restrict__ src, int64_t n,
-                                                           float *__restrict__ dst) {
-  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= n) return;
-  const uint8_t *blk = src + (i >> 8) * kQ6KBytes;
+__device__ __forceinline__ float dq_q6_k(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 8) * kQ6KBytes;
   uint32_t r = (uint32_t)(i & 255);
   uint32_t h = r >> 7, quarter = (r >> 5) & 3u, l = r & 31u;
   uint32_t qlb = blk[64 * h + l + ((quarter & 1u) ? 32u : 0u)];
@@ -58,7 +51,34 @@ __global__ __launch_bounds__(256) void dequant_q6_k_kernel(const uint8_t *__rest
   int q = (int)(lo4 | (hi2 << 4)) - 32;
   int sc = (int8_t)blk[192 + 8 * h + l / 16 + 2 * quarter];
   float d = f16_bits_exact(ld_u16(blk + 208));
-  dst[i] = __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+  return __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
+}
+
+template <int kType>
+__device__ __forceinline__ float dq_elem(const uint8_t *base, int64_t i) {
+  if constexpr (kType == kQ8_0) return dq_q8_0(base, i);
+  else if constexpr (kType == kQ4_K) return dq_q4_k(base, i);
+  else return dq_q6_k(base, i);
+}
+
+template <int kType>
+__global__ __launch_bounds__(256) void dequant_kernel(const uint8_t *__restrict__ src, int64_t n,
+                                                     float *__restrict__ dst) {
+  int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  dst[i] = dq_elem<kType>(src, i);
+}
+
+// Quantized row gather (token embedding lookup): output row j is weight row
+// ids[blockIdx.y] dequantized.  The ids travel in the kernel arguments, so a
+// launch needs no device staging; rows are validated on the host first.
+template <int kType>
+__global__ __launch_bounds__(256) void get_rows_kernel(const uint8_t *__restrict__ W, int64_t row_bytes, int64_t ne0,
+                                                       GatherIds ids, float *__restrict__ out) {
+  const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= ne0) return;
+  const uint8_t *row = W + (int64_t)ids.id[blockIdx.y] * row_bytes;
+  out[(int64_t)blockIdx.y * ne0 + e] = dq_elem<kType>(row, e);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,12 +266,33 @@ static inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n +
 hipError_t launch_dequantize(int type, const void *src, int64_t n, float *dst, hipStream_t s) {
   const uint8_t *p = static_cast<const uint8_t *>(src);
   switch (type) {
-  case kQ8_0: launch_timed(dequant_q8_0_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
-  case kQ4_K: launch_timed(dequant_q4_k_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
-  case kQ6_K: launch_timed(dequant_q6_k_kernel, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  case kQ8_0: launch_timed(dequant_kernel<kQ8_0>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  case kQ4_K: launch_timed(dequant_kernel<kQ4_K>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+  case kQ6_K: launch_timed(dequant_kernel<kQ6_K>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_get_rows(int type, const void *w, int64_t row_bytes, int64_t ne0, const uint32_t *ids, int64_t n,
+                           float *out, hipStream_t s) {
+  const uint8_t *p = static_cast<const uint8_t *>(w);
+  for (int64_t j0 = 0; j0 < n; j0 += kGatherMaxIds) {
+    const int64_t cnt = n - j0 < kGatherMaxIds ? n - j0 : kGatherMaxIds;
+    GatherIds g;
+    for (int64_t j = 0; j < cnt; ++j) g.id[j] = ids[j0 + j];
+    const dim3 grid(grid_for(ne0, 256), (unsigned)cnt);
+    float *o = out + j0 * ne0;
+    switch (type) {
+    case kQ8_0: hipLaunchKernelGGL(get_rows_kernel<kQ8_0>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
+    case kQ4_K: hipLaunchKernelGGL(get_rows_kernel<kQ4_K>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
+    case kQ6_K: hipLaunchKernelGGL(get_rows_kernel<kQ6_K>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
+    default: return hipErrorInvalidValue;
+    }
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_quantize(int type, const float *src, int64_t n, void *dst, hipStream_t s) {

@@ -12,6 +12,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <utility>
 
 #include "../../include/okq.h"
@@ -150,6 +151,25 @@ okq_status validate_linear(const void *x, const LinearArgs &a, const void *w, co
   return ok();
 }
 
+// Mirrors rmsnorm's checks (crates/kernels/src/rmsnorm.rs:81-114); slice
+// lengths are implied by the shape at this boundary.
+okq_status validate_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float eps,
+                            const float *out) {
+  if (hidden == 0) return fail(OKQ_E_SHAPE, "rmsnorm hidden dimension must be non-zero");
+  if (rows < 0 || hidden < 0)
+    return fail(OKQ_E_SHAPE, "rmsnorm negative dimension rows=%lld hidden=%lld", (long long)rows, (long long)hidden);
+  int64_t n;
+  if (!mul_ok(rows, hidden, n)) return fail(OKQ_E_SHAPE, "rmsnorm x length rows*hidden overflows");
+  if (!(eps >= 0.0f) || eps == INFINITY) return fail(OKQ_E_ARG, "rmsnorm epsilon must be finite and non-negative, got %g", eps);
+  if (rows > INT32_MAX) return fail(OKQ_E_SHAPE, "rmsnorm rows exceed u32 launch limits");
+  if (rows == 0) return ok();
+  if (!x || !weight) return fail(OKQ_E_ARG, "rmsnorm null pointer (x=%p weight=%p)", x, weight);
+  if (reinterpret_cast<uintptr_t>(x) & 3u || reinterpret_cast<uintptr_t>(weight) & 15u)
+    return fail(OKQ_E_ALIGN, "rmsnorm x must be 4-byte and weight 16-byte aligned");
+  if (out && (reinterpret_cast<uintptr_t>(out) & 3u)) return fail(OKQ_E_ALIGN, "rmsnorm out must be 4-byte aligned");
+  return ok();
+}
+
 // ---- GEMM workspace ----------------------------------------------------------
 // One buffer per (device, stream): work on one stream is ordered, so reuse is
 // safe; different streams never share.  Grows on demand; growing is refused
@@ -161,11 +181,14 @@ struct Workspace {
   size_t bytes = 0;
 };
 std::mutex g_ws_mutex;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<std::tuple<int, hipStream_t, int>, Workspace> g_ws;
 
-okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out) {
+// Slot 0 serves the linear itself (GEMM planes, bf16 widening); slot 1 holds
+// a neighbour's output (normalised or gated activations) that a linear then
+// reads, so the two never alias.
+okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int slot = 0) {
   std::lock_guard<std::mutex> lock(g_ws_mutex);
-  Workspace &w = g_ws[{dev, s}];
+  Workspace &w = g_ws[{dev, s, slot}];
   if (w.bytes >= bytes) {
     *out = w.ptr;
     return ok();
@@ -382,6 +405,40 @@ okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float 
                     "dequantize launch");
 }
 
+okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int64_t ne0, int64_t ne1,
+                          const uint32_t *ids, int64_t n_ids, float *out, void *stream) {
+  TypeInfo ti;
+  if (!type_info(w_type, ti) || !ti.quantized) return unsupported_type(w_type, "get_rows weight");
+  if (ne0 <= 0 || ne0 % ti.elems != 0)
+    return fail(OKQ_E_SHAPE, "get_rows ne0=%lld is not a positive multiple of the %s block size %lld", (long long)ne0,
+                type_name(w_type), (long long)ti.elems);
+  if (ne1 < 0 || n_ids < 0) return fail(OKQ_E_SHAPE, "get_rows negative ne1=%lld or n_ids=%lld", (long long)ne1,
+                                        (long long)n_ids);
+  const int64_t row_bytes = ne0 / ti.elems * ti.bytes;
+  int64_t we, oe;
+  if (!mul_ok(ne1, row_bytes, we)) return fail(OKQ_E_SHAPE, "get_rows weight byte length overflows");
+  if ((uint64_t)we != w_bytes)
+    return fail(OKQ_E_SHAPE, "get_rows weight bytes=%llu does not match ne1*row_bytes(ne0)=%lld*%lld=%lld",
+                (unsigned long long)w_bytes, (long long)ne1, (long long)row_bytes, (long long)we);
+  if (!mul_ok(n_ids, ne0, oe)) return fail(OKQ_E_SHAPE, "get_rows out length n_ids*ne0 overflows");
+  if (ne0 > INT32_MAX || n_ids > INT32_MAX) return fail(OKQ_E_SHAPE, "get_rows dimension exceeds u32 launch limits");
+  if (n_ids == 0) return ok();
+  if (!ids || !w || !out) return fail(OKQ_E_ARG, "get_rows null pointer (ids=%p w=%p out=%p)", ids, w, out);
+  for (int64_t j = 0; j < n_ids; ++j)
+    if ((int64_t)ids[j] >= ne1)
+      return fail(OKQ_E_ARG, "get_rows token id %u is out of range for vocab_size %lld", ids[j], (long long)ne1);
+  if (w_type == OKQ_TYPE_Q4_K ? (reinterpret_cast<uintptr_t>(w) & 15u) : (reinterpret_cast<uintptr_t>(w) & 1u))
+    return fail(OKQ_E_ALIGN, "get_rows weight must be %d-byte aligned", w_type == OKQ_TYPE_Q4_K ? 16 : 2);
+  if (reinterpret_cast<uintptr_t>(out) & 3u) return fail(OKQ_E_ALIGN, "get_rows out must be 4-byte aligned");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_get_rows((int)w_type, w, row_bytes, ne0, ids, n_ids, out,
+                                         static_cast<hipStream_t>(stream)),
+                    "get_rows launch");
+}
+
 okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,
                                   uint64_t w_bytes, int64_t out_features, const float *bias, float *out,
                                   void *stream) {
@@ -424,10 +481,154 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
     float *o[okq::kGemvMaxProblems];
     for (int i = 0; i < count; ++i) o[i] = out[i] + r * out_features[i];
     hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * in_features, in_features, count, w, out_features, b, o,
-                                          info.cu_count, s);
+                                          info.cu_count, s, okq::GemvPro{});
     if (e != hipSuccess) return hip_status(e, "gemv_multi launch");
   }
   return ok();
+}
+
+okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float epsilon, float *out,
+                       void *stream) {
+  okq_status st = validate_rmsnorm(x, rows, hidden, weight, epsilon, out);
+  if (st != OKQ_OK || rows == 0) return st;
+  if (!out) return fail(OKQ_E_ARG, "rmsnorm out is null");
+  int dev;
+  DevInfo info;
+  st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  return hip_status(okq::launch_rmsnorm(x, rows, hidden, weight, epsilon, out, static_cast<hipStream_t>(stream)),
+                    "rmsnorm launch");
+}
+
+okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidden, const float *norm_weight,
+                                      float epsilon, uint32_t w_type, int count, const void *const *w,
+                                      const uint64_t *w_bytes, const int64_t *out_features, const float *const *bias,
+                                      float *const *out, void *stream) {
+  okq_status st = validate_rmsnorm(x, rows, hidden, norm_weight, epsilon, nullptr);
+  if (st != OKQ_OK) return st;
+  if (count < 1 || count > okq::kGemvMaxProblems)
+    return fail(OKQ_E_ARG, "rmsnorm_linear count=%d must be between 1 and %d", count, okq::kGemvMaxProblems);
+  if (!w || !w_bytes || !out_features || !out) return fail(OKQ_E_ARG, "rmsnorm_linear null argument array");
+  bool streams = true, any = false;
+  for (int i = 0; i < count; ++i) {
+    LinearArgs a{rows, hidden, out_features[i], w_type, w_bytes[i]};
+    st = validate_linear(x, a, w[i], out[i], false);
+    if (st != OKQ_OK) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
+      return fail(st, "rmsnorm_linear matrix %d: %s", i, msg);
+    }
+    any = any || out_features[i] > 0;
+    streams = streams && okq::gemv_streams((int)w_type, hidden, w[i], out_features[i]);
+  }
+  if (rows == 0 || !any) return ok();
+  int dev;
+  DevInfo info;
+  st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
+  const float *const *b = bias ? bias : nobias;
+  if (rows <= kGemvMaxRows && streams) {  // decode: every workgroup normalises x in its prologue
+    const okq::GemvPro pro{okq::kProRms, norm_weight, epsilon};
+    for (int64_t r = 0; r < rows; ++r) {
+      float *o[okq::kGemvMaxProblems];
+      for (int i = 0; i < count; ++i) o[i] = out[i] + r * out_features[i];
+      hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * hidden, hidden, count, w, out_features, b, o,
+                                            info.cu_count, s, pro);
+      if (e != hipSuccess) return hip_status(e, "rmsnorm_linear launch");
+    }
+    return ok();
+  }
+  void *ws = nullptr;
+  st = get_workspace(dev, s, (size_t)rows * (size_t)hidden * sizeof(float), &ws, 1);
+  if (st != OKQ_OK) return st;
+  float *xn = static_cast<float *>(ws);
+  hipError_t e = okq::launch_rmsnorm(x, rows, hidden, norm_weight, epsilon, xn, s);
+  if (e != hipSuccess) return hip_status(e, "rmsnorm launch");
+  for (int i = 0; i < count; ++i) {
+    st = linear_impl(xn, false, rows, hidden, w_type, w[i], w_bytes[i], out_features[i], b[i], out[i], stream,
+                     Path::Auto);
+    if (st != OKQ_OK) return st;
+  }
+  return ok();
+}
+
+okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, int64_t intermediate,
+                                uint32_t gate_type, const void *gate_w, uint64_t gate_bytes, uint32_t up_type,
+                                const void *up_w, uint64_t up_bytes, uint32_t down_type, const void *down_w,
+                                uint64_t down_bytes, float *gate_buf, float *up_buf, float *out, void *stream) {
+  if (rows == 0) return fail(OKQ_E_SHAPE, "mlp_gated_silu seq_len must be non-zero");
+  if (hidden == 0) return fail(OKQ_E_SHAPE, "mlp_gated_silu hidden must be non-zero");
+  if (intermediate == 0) return fail(OKQ_E_SHAPE, "mlp_gated_silu intermediate must be non-zero");
+  struct Proj {
+    const char *name;
+    const float *in;
+    int64_t K, N;
+    uint32_t type;
+    const void *w;
+    uint64_t bytes;
+    float *o;
+  } proj[3] = {{"gate", x, hidden, intermediate, gate_type, gate_w, gate_bytes, gate_buf},
+               {"up", x, hidden, intermediate, up_type, up_w, up_bytes, up_buf},
+               {"down", gate_buf, intermediate, hidden, down_type, down_w, down_bytes, out}};
+  for (const Proj &p : proj) {
+    LinearArgs a{rows, p.K, p.N, p.type, p.bytes};
+    okq_status st = validate_linear(p.in, a, p.w, p.o, false);
+    if (st != OKQ_OK) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
+      return fail(st, "mlp_gated_silu %s projection: %s", p.name, msg);
+    }
+  }
+  if (!up_buf) return fail(OKQ_E_ARG, "mlp_gated_silu up_buf is null");
+  if (reinterpret_cast<uintptr_t>(up_buf) & 15u) return fail(OKQ_E_ALIGN, "mlp_gated_silu up_buf must be 16-byte aligned");
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const bool decode = rows <= kGemvMaxRows;
+  // gate and up: one grouped pass over both weights when they share a format
+  if (decode && gate_type == up_type && okq::gemv_streams((int)gate_type, hidden, gate_w, intermediate) &&
+      okq::gemv_streams((int)up_type, hidden, up_w, intermediate)) {
+    const void *ws[2] = {gate_w, up_w};
+    const int64_t ns[2] = {intermediate, intermediate};
+    const float *bs[2] = {nullptr, nullptr};
+    for (int64_t r = 0; r < rows; ++r) {
+      float *os[2] = {gate_buf + r * intermediate, up_buf + r * intermediate};
+      hipError_t e = okq::launch_gemv_multi((int)gate_type, x + r * hidden, hidden, 2, ws, ns, bs, os, info.cu_count,
+                                            s, okq::GemvPro{});
+      if (e != hipSuccess) return hip_status(e, "mlp gate/up launch");
+    }
+  } else {
+    st = linear_impl(x, false, rows, hidden, gate_type, gate_w, gate_bytes, intermediate, nullptr, gate_buf, stream,
+                     Path::Auto);
+    if (st != OKQ_OK) return st;
+    st = linear_impl(x, false, rows, hidden, up_type, up_w, up_bytes, intermediate, nullptr, up_buf, stream,
+                     Path::Auto);
+    if (st != OKQ_OK) return st;
+  }
+  // down: silu(gate) * up folded into the GEMV prologue, or materialised in
+  // gate_buf (the reference's final content of gate_buf) for the other paths
+  if (decode && okq::gemv_streams((int)down_type, intermediate, down_w, hidden)) {
+    const okq::GemvPro base{okq::kProSwiGLU, nullptr, 0.0f};
+    const float *nob = nullptr;
+    for (int64_t r = 0; r < rows; ++r) {
+      okq::GemvPro pro = base;
+      pro.a = up_buf + r * intermediate;
+      float *o = out + r * hidden;
+      const int64_t n = hidden;
+      hipError_t e = okq::launch_gemv_multi((int)down_type, gate_buf + r * intermediate, intermediate, 1, &down_w, &n,
+                                            &nob, &o, info.cu_count, s, pro);
+      if (e != hipSuccess) return hip_status(e, "mlp down launch");
+    }
+    return ok();
+  }
+  hipError_t e = okq::launch_swiglu(gate_buf, up_buf, rows * intermediate, gate_buf, s);
+  if (e != hipSuccess) return hip_status(e, "swiglu launch");
+  return linear_impl(gate_buf, false, rows, intermediate, down_type, down_w, down_bytes, hidden, nullptr, out, stream,
+                     Path::Auto);
 }
 
 okq_status okq_gemv(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,

@@ -27,6 +27,10 @@
  *     (crates/kernels/src/cpu_avx2.rs:58-253), the rows>=32 row-chunked
  *     dispatcher (lib.rs:2245, :2294-2390) and validate_linear_out_by_in
  *     (:2443-2497).
+ *   - The projections' neighbours: rmsnorm (crates/kernels/src/rmsnorm.rs:
+ *     73-128) and the gated SiLU of mlp_gated_silu (crates/kernels/src/mlp.rs:
+ *     77-88, :233-238), same loops and order.  Pinned by the reference's own
+ *     hand-checked values (rmsnorm.rs:150-258, mlp.rs:260-440).
  *
  * Build: gcc -O2 -ffp-contract=off (no FMA contraction: every product and sum
  * is rounded separately, as in the Rust scalar code).
@@ -699,4 +703,33 @@ OKR_API int okr_linear_q(int type, int mode, int threads, const float *x, int64_
     if (rc == 0) rc = okr_linear_out_by_in(mode, threads, x, rows, in_f, w, out_f, bias, out);
     free(w);
     return rc;
+}
+
+/* ---- neighbours of the projections -------------------------------------- */
+
+/* rmsnorm, crates/kernels/src/rmsnorm.rs:116-128: sequential f32 sum of
+ * squares per row, mean, sqrt(mean + eps), reciprocal, then
+ * out = row[i] * inv_rms * weight[i] left to right. */
+OKR_API void okr_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float eps, float *out) {
+  const float hidden_f = (float)hidden;
+  for (int64_t r = 0; r < rows; ++r) {
+    const float *row = x + r * hidden;
+    float sum_sq = 0.0f;
+    for (int64_t i = 0; i < hidden; ++i) sum_sq += row[i] * row[i];
+    const float mean_sq = sum_sq / hidden_f;
+    const float rms = sqrtf(mean_sq + eps);
+    const float inv_rms = 1.0f / rms;
+    for (int64_t i = 0; i < hidden; ++i) out[r * hidden + i] = row[i] * inv_rms * weight[i];
+  }
+}
+
+/* silu_inplace then the element-wise product with up, mlp.rs:77-88 and
+ * :233-238: sigmoid = 1 / (1 + exp(-g)); g *= sigmoid; g *= up. */
+OKR_API void okr_swiglu(const float *gate, const float *up, int64_t n, float *out) {
+  for (int64_t i = 0; i < n; ++i) {
+    float v = gate[i];
+    const float sigmoid = 1.0f / (1.0f + expf(-v));
+    v *= sigmoid;
+    out[i] = v * up[i];
+  }
 }

@@ -95,6 +95,10 @@ class Oracle:
         lib.okr_block_bytes.argtypes = [ctypes.c_int]
         lib.okr_block_elems.restype = _i64
         lib.okr_block_elems.argtypes = [ctypes.c_int]
+        lib.okr_rmsnorm.restype = None
+        lib.okr_rmsnorm.argtypes = [_f32p, _i64, _i64, _f32p, ctypes.c_float, _f32p]
+        lib.okr_swiglu.restype = None
+        lib.okr_swiglu.argtypes = [_f32p, _f32p, _i64, _f32p]
 
     # ---- scalar conversions -------------------------------------------------
     def f16_to_f32(self, bits: np.ndarray) -> np.ndarray:
@@ -165,6 +169,23 @@ class Oracle:
                  bias=None, mode: int = MODE_SCALAR, threads: int = 1) -> np.ndarray:
         w = self.dequantize(ggml_type, wq, out_f * in_f)
         return self.linear(x, rows, in_f, w, out_f, bias, mode, threads)
+
+    def rmsnorm(self, x: np.ndarray, rows: int, hidden: int, weight: np.ndarray, eps: float) -> np.ndarray:
+        x = np.ascontiguousarray(x, np.float32).reshape(-1)
+        w = np.ascontiguousarray(weight, np.float32).reshape(-1)
+        assert x.size == rows * hidden and w.size == hidden
+        out = np.empty(rows * hidden, np.float32)
+        self.lib.okr_rmsnorm(_ptr(x, _f32p), rows, hidden, _ptr(w, _f32p), ctypes.c_float(eps),
+                             _ptr(out, _f32p))
+        return out
+
+    def swiglu(self, gate: np.ndarray, up: np.ndarray) -> np.ndarray:
+        g = np.ascontiguousarray(gate, np.float32).reshape(-1)
+        u = np.ascontiguousarray(up, np.float32).reshape(-1)
+        assert g.size == u.size
+        out = np.empty(g.size, np.float32)
+        self.lib.okr_swiglu(_ptr(g, _f32p), _ptr(u, _f32p), g.size, _ptr(out, _f32p))
+        return out
 
     def validate(self, x_len, rows, in_f, w_len, out_f, bias_len, out_len):
         rc = self.lib.okr_validate_linear(x_len, rows, in_f, w_len, out_f, bias_len, out_len)

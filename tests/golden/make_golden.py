@@ -3,8 +3,10 @@
 * reference_kats.json -- known-answer vectors copied as data from the
   reference's own tests: fp16 -> f32 (crates/loader/src/safetensors_values.rs:
   316-351), bf16 -> f32 (:295-313), GGML type ids (gguf_inspect.rs:178-185)
-  and the GGUF fixture's ne-order shape and q4_k tag
-  (fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json).
+  the GGUF fixture's ne-order shape and q4_k tag
+  (fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json), and the
+  hand-checked rmsnorm / silu / gated-MLP values (crates/kernels/src/
+  rmsnorm.rs:150-258, crates/kernels/src/mlp.rs:260-440).
 * oracle_vectors.json -- regression vectors produced by the CPU oracle:
   the first values of the seeded generator and small quantized blocks with
   their dequantized values.  These pin the oracle against later edits; the
@@ -31,6 +33,9 @@ def reference_kats():
             "bf16": "crates/loader/src/safetensors_values.rs:295-313",
             "type_ids": "crates/loader/src/gguf_inspect.rs:170-206",
             "gguf_fixture": "fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json",
+            "rmsnorm": "crates/kernels/src/rmsnorm.rs:150-258",
+            "silu": "crates/kernels/src/mlp.rs:260-290",
+            "mlp_gated_silu": "crates/kernels/src/mlp.rs:300-440",
         },
         # (bits, expected f32 bit pattern); 0x7e00 decodes to a NaN
         "f16": [[0x3C00, 0x3F800000], [0xC100, 0xC0200000], [0x0000, 0x00000000], [0x0400, 0x38800000],
@@ -39,6 +44,25 @@ def reference_kats():
         "bf16": [[0x3F80, 0x3F800000], [0xC020, 0xC0200000], [0x0000, 0x00000000], [0x7F80, 0x7F800000]],
         "type_ids": {"F32": 0, "F16": 1, "Q8_0": 8, "Q4K": 12, "Q6K": 14, "BF16": 30},
         "gguf_fixture_token_embd": {"name": "token_embd.weight", "shape": [2560, 262144], "tensor_type": "q4_k"},
+        # rows x hidden input, weight, epsilon, expected output, absolute tolerance
+        "rmsnorm": [
+            {"x": [1, 2, 3], "rows": 1, "hidden": 3, "w": [1, 1, 1], "eps": 1e-6,
+             "want": [0.46291006, 0.9258201, 1.3887302], "tol": 1e-6},
+            {"x": [1, 2, 3], "rows": 1, "hidden": 3, "w": [2, 0.5, 1], "eps": 1e-6,
+             "want": [0.9258201, 0.46291006, 1.3887302], "tol": 1e-6},
+            {"x": [0, 0, 0, 0], "rows": 1, "hidden": 4, "w": [1.5, 2.5, 3.5, 4.5], "eps": 1e-6,
+             "want": [0, 0, 0, 0], "tol": 0.0},
+            {"x": [5], "rows": 1, "hidden": 1, "w": [1], "eps": 0.0, "want": [1.0], "tol": 1e-6},
+            {"x": [1, 2, 3, 2, 4, 6], "rows": 2, "hidden": 3, "w": [1, 1, 1], "eps": 1e-6,
+             "want": [0.46291006, 0.9258201, 1.3887302, 0.46291006, 0.9258201, 1.3887302], "tol": 1e-6},
+        ],
+        "silu": {"x": [0, 1, -1, 2, 3], "want": [0, 0.7310586, -0.26894143, 1.7615942, 2.8577223], "tol": 1e-6,
+                 "asymptotes": {"x": [-30, 30], "want": [0, 30], "tol": [1e-6, 1e-3]}},
+        # weights in the reference's [in, out] layout (mlp.rs:22-25), flattened row-major
+        "mlp_gated_silu": {"x": [1, 2, 0, 0], "rows": 2, "hidden": 2, "intermediate": 4,
+                           "gate_w": [1, 0, 1, -1, 0, 1, 1, 0], "up_w": [1, 1, 0, 2, 1, -1, 1, 0],
+                           "down_w": [1, 0, 0, 1, 1, 0, 0, 1],
+                           "want": [7.9086204, -2.299477, 0, 0], "tol": 1e-5},
     }
 
 
