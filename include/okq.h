@@ -171,10 +171,10 @@ okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float
 /* RMSNorm followed by up to four quantized projections of the normalised
  * rows (the q/k/v of an attention block):
  *   out[i][r, o] = bias[i][o] + sum_k rmsnorm(x)[r, k] * W_i[o, k].
- * Arguments as okq_rmsnorm and okq_gemv_multi.  Decode-sized rows run the
- * GEMV with the normalisation folded into its activation prologue (no
- * normalised copy of x is written); larger batches normalise into a
- * per-stream workspace first.  No counterpart in the reference, whose blocks
+ * Arguments as okq_rmsnorm and okq_gemv_multi.  A single row runs the GEMV
+ * with the normalisation folded into its activation prologue (no normalised
+ * copy of x is written); more rows normalise into a per-stream workspace
+ * first and then stream each weight once per four rows.  No counterpart in the reference, whose blocks
  * call rmsnorm and then each linear (crates/models/src/qwen/qwen2_5/prefill.rs). */
 okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidden, const float *norm_weight,
                                       float epsilon, uint32_t w_type, int count, const void *const *w,
@@ -190,10 +190,10 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
  * row_bytes(intermediate)); gate_buf, up_buf [rows, intermediate] caller-owned
  * scratch; out [rows, hidden].  Device buffers, x/gate_buf/up_buf 16-byte
  * aligned.  Decode-sized rows (rows <= 4) run gate+up as one grouped GEMV
- * when they share a format, and fold silu(gate) * up into the down GEMV's
- * prologue whenever the down weight takes the streaming GEMV (gate_buf then
- * holds gate(x)); otherwise silu(gate(x)) * up(x) is left in gate_buf, as the
- * reference does.  up_buf always holds up(x).  Treat both as scratch.  Zero rows, hidden or
+ * when they share a format.  A single row folds silu(gate) * up into the down
+ * GEMV's prologue whenever the down weight takes the streaming GEMV (gate_buf
+ * then holds gate(x)); otherwise silu(gate(x)) * up(x) is left in gate_buf,
+ * as the reference does.  up_buf always holds up(x).  Treat both as scratch.  Zero rows, hidden or
  * intermediate are errors (mlp.rs:151-165). */
 okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, int64_t intermediate,
                                 uint32_t gate_type, const void *gate_w, uint64_t gate_bytes, uint32_t up_type,

@@ -24,8 +24,9 @@ COMMON = [
     "-I", os.path.join(HERE, "..", "include"),
 ]
 # Per-file extra flags.  okq_prep.hip holds the bit-exact dequant/quantize
-# kernels: no FMA contraction there.
-EXTRA = {"okq_prep.hip": ["-ffp-contract=off"]}
+# kernels, okq_gemv.hip writes its FMAs out so that every instantiation rounds
+# alike: no FMA contraction in either.
+EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=off"]}
 
 
 def sources():

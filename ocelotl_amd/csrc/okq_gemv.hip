@@ -35,7 +35,10 @@
 //     v_alignbyte_b32; no read leaves the weight tensor.
 //   * Row sums are reduced across the wave with DPP + readlane, then (T > 1)
 //     across the team's waves through LDS once per chunk of steps, both in a
-//     fixed order (deterministic).
+//     fixed order (deterministic).  The file is compiled without FMA
+//     contraction and every FMA is written out, so a row's result does not
+//     depend on which instantiation (rows per launch, matrices per launch)
+//     computed it.
 #include "okq_device.h"
 #include "okq_internal.h"
 
@@ -143,11 +146,11 @@ struct FQ4K {
         __builtin_amdgcn_ubfe(srcm, 8 * j1 + mo, width) | ((__builtin_amdgcn_ubfe(r.hd.z, 8 * j1 + 6, 2) << 4) & himask);
     const float d = f16_bits_hw(r.hd.x & 0xffffu);
     const float dmin = f16_bits_hw(r.hd.x >> 16);
-    const float fa = (float)(ah * 256 + al);
-    const float fb = (float)(bh * 256 + bl);
-    float acc = (d * (float)scA) * (x.s[0] * fa) - (dmin * (float)mA) * x.t[0];
-    acc += (d * (float)scB) * (x.s[1] * fb) - (dmin * (float)mB) * x.t[1];
-    return acc;
+    const float pa = x.s[0] * (float)(ah * 256 + al);  // exact: power of two times an integer below 2^24
+    const float pb = x.s[1] * (float)(bh * 256 + bl);
+    const float a = fmaf(d * (float)scA, pa, -((dmin * (float)mA) * x.t[0]));
+    const float b = fmaf(d * (float)scB, pb, -((dmin * (float)mB) * x.t[1]));
+    return a + b;
   }
 };
 
@@ -216,8 +219,8 @@ struct FQ6K {
     float acc = 0.0f;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-      const float t = x.s[qq] * (float)(ah[qq] * 256 + al[qq]) - 32.0f * x.t[qq];
-      acc += (d * (float)sc[qq]) * t;
+      const float t = x.s[qq] * (float)(ah[qq] * 256 + al[qq]) - 32.0f * x.t[qq];  // both products exact
+      acc = fmaf(d * (float)sc[qq], t, acc);
     }
     return acc;
   }
@@ -262,7 +265,7 @@ struct FQ80 {
     }
     const float d0 = f16_bits_hw(w[0] & 0xffffu);
     const float d1 = f16_bits_hw(w[8] >> 16);
-    return d0 * (x.s[0] * (float)(a0h * 256 + a0l)) + d1 * (x.s[1] * (float)(a1h * 256 + a1l));
+    return fmaf(d1, x.s[1] * (float)(a1h * 256 + a1l), d0 * (x.s[0] * (float)(a0h * 256 + a0l)));
   }
 };
 
@@ -323,8 +326,19 @@ struct GemvMore {
   int start[kGemvMaxProblems - 1];
 };
 
-constexpr int kMaxXV = 4;        // float4s of x per thread (K <= 4 * 4 * 1024)
+constexpr int kMaxXV = 4;        // float4s of x per thread, one-row launches (K <= 4 * 4 * 1024)
+constexpr int kMaxXVRows = 8;    // per thread and row, multi-row launches (K <= 8 * 4 * 512)
 constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
+constexpr int kMaxRowsPerLaunch = 4;
+constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
+
+// One activation row keeps one XRec per lane in registers and 16 waves fit a
+// CU; R rows keep R of them (up to 160 VGPRs), so multi-row launches are
+// limited to 8 waves (two per SIMD).
+template <int R>
+constexpr int gemv_max_threads() {
+  return R == 1 ? 1024 : 512;
+}
 
 // Rows are swept step-major across the chip: at step s, team g of workgroup
 // b (B workgroups of G teams) takes row (s * B + b) * G + g, so the whole grid
@@ -338,31 +352,35 @@ constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
 // consecutively and every row finds its matrix, bias and output through
 // wave-uniform scalar selects.
 //
+// R activation rows (x [nrows, K], nrows <= R; y_i [nrows, N_i]) share one
+// pass over the weights: every lane holds its unit's XRec of each row and
+// contracts each weight unit it loads with all of them, so a batch of up to
+// four decode rows streams the weights once.
+//
 // kPro transforms x before it is quantised (the decode neighbours of the
 // projections, computed by every workgroup from the same inputs in the same
 // order, so all workgroups agree): kProRms is the RMSNorm of x with weight
 // P.a (crates/kernels/src/rmsnorm.rs:73-128), kProSwiGLU is silu(x) * P.a with
 // x = gate and P.a = up (crates/kernels/src/mlp.rs:77-88, :233-238).
-template <class F, int D, int XV, bool kMulti, int kPro>
-__global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ W, uint32_t w_bytes,
-                                                    const float *__restrict__ x, const float *__restrict__ bias,
-                                                    float *__restrict__ y, int N, int K, int T, int G, GemvMore M,
-                                                    GemvPro P) {
+template <class F, int D, int XV, bool kMulti, int kPro, int R>
+__global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
+    const uint8_t *__restrict__ W, uint32_t w_bytes, const float *__restrict__ x, const float *__restrict__ bias,
+    float *__restrict__ y, int N, int K, int T, int G, GemvMore M, GemvPro P, int nrows) {
+  static_assert(kPro == kProNone || R == 1, "the neighbour prologues take one activation row");
   // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
-  // waves (g >= G) that only help quantise x.  D <= steps (chosen at launch).
+  // waves (g >= G) that only help quantise x.
   extern __shared__ __align__(16) unsigned char smem[];
   const int U = K >> 6;
-  XRec *xr = reinterpret_cast<XRec *>(smem);
+  XRec *xr = reinterpret_cast<XRec *>(smem);  // [R][U]
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   const uint32_t lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: rows live in SGPRs
   const int g = wave / T, w = wave % T;
-  float *part = reinterpret_cast<float *>(smem + (size_t)U * sizeof(XRec));  // [kChunk][G][T] (T > 1)
+  float *part = reinterpret_cast<float *>(smem + (size_t)R * U * sizeof(XRec));  // [kChunk][G][T][R] (T > 1)
   const int u = w * 64 + (int)lane;
   const bool active = u < U && g < G;
   const uint32_t rb = (uint32_t)F::row_bytes(K);
   const uint32_t uoff = active ? F::unit_off(u) : 0u;
-  const Rsrc rx = make_rsrc(x, (uint32_t)K * 4u);
   const int window = (int)gridDim.x * G;         // rows per step
   const int steps = (N + window - 1) / window;  // grid-uniform
   const int end = N;
@@ -389,13 +407,18 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   };
   auto bias_of = [&](int p) { return p == 0 ? bias : p == 1 ? M.bias[0] : p == 2 ? M.bias[1] : M.bias[2]; };
   auto y_of = [&](int p) { return p == 0 ? y : p == 1 ? M.y[0] : p == 2 ? M.y[1] : M.y[2]; };
+  // rows of matrix p (the row stride of its output)
+  auto rows_of = [&](int p) {
+    if (!kMulti) return N;
+    return p == 0 ? st1 : p == 1 ? min(st2, N) - st1 : p == 2 ? min(st3, N) - st2 : N - st3;
+  };
   // Byte offset of this lane's unit in `row`; rows past the end (and idle
   // lanes) point at the end of their tensor, where buffer loads return zeros
   // without touching memory, so every load is unconditional.
-  auto wload = [&](typename F::Regs &R, int row) {
+  auto wload = [&](typename F::Regs &Rg, int row) {
     const int p = prob(row);
     const uint32_t off = (active && row < end) ? (uint32_t)(row - first_row(p)) * rb + uoff : bytes_of(p);
-    F::load(R, rsrc(p), off, lane);
+    F::load(Rg, rsrc(p), off, lane);
   };
   // bias values are wave-uniform scalar loads, outside the vector-memory
   // queue that the weight waits count
@@ -404,9 +427,9 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     const float *b = bias_of(p);
     return (b != nullptr && row < end) ? b[row - first_row(p)] : 0.0f;
   };
-  auto store = [&](int row, float v) {
+  auto store = [&](int row, int r, float v) {
     const int p = prob(row);
-    y_of(p)[row - first_row(p)] = v;
+    y_of(p)[(size_t)r * rows_of(p) + (row - first_row(p))] = v;
   };
 
   // 1. activations first, XV float4s per thread (launch: XV * threads >= K/4;
@@ -415,10 +438,14 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   //    every wave's x loads ahead of all weight loads: x arrives after one
   //    cache round trip instead of behind the first rows of weights.
   const int nf = K >> 2;
-  u32x4a4 xv[XV];
+  u32x4a4 xv[R][XV];
   u32x4a4 av[kPro != kProNone ? XV : 1];
 #pragma unroll
-  for (int i = 0; i < XV; ++i) xv[i] = ld4(rx, 16u * (uint32_t)min(tid + i * nt, nf));
+  for (int r = 0; r < R; ++r) {  // rows r >= nrows get an empty range: zeros
+    const Rsrc rx = make_rsrc(x + (size_t)r * K, r < nrows ? (uint32_t)K * 4u : 0u);
+#pragma unroll
+    for (int i = 0; i < XV; ++i) xv[r][i] = ld4(rx, 16u * (uint32_t)min(tid + i * nt, nf));
+  }
   if constexpr (kPro != kProNone) {
     const Rsrc ra = make_rsrc(P.a, (uint32_t)K * 4u);
 #pragma unroll
@@ -443,7 +470,7 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     float ss = 0.0f;
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      const float a0 = as_f32(xv[i].x), a1 = as_f32(xv[i].y), a2 = as_f32(xv[i].z), a3 = as_f32(xv[i].w);
+      const float a0 = as_f32(xv[0][i].x), a1 = as_f32(xv[0][i].y), a2 = as_f32(xv[0][i].z), a3 = as_f32(xv[0][i].w);
       ss += (a0 * a0 + a1 * a1) + (a2 * a2 + a3 * a3);
     }
     ss = wave_sum(ss);
@@ -455,10 +482,10 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     const float inv = 1.0f / sqrtf(tot / (float)K + P.eps);  // rms = sqrt(mean + eps), then 1 / rms
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      xv[i].x = as_u32(as_f32(xv[i].x) * inv * as_f32(av[i].x));
-      xv[i].y = as_u32(as_f32(xv[i].y) * inv * as_f32(av[i].y));
-      xv[i].z = as_u32(as_f32(xv[i].z) * inv * as_f32(av[i].z));
-      xv[i].w = as_u32(as_f32(xv[i].w) * inv * as_f32(av[i].w));
+      xv[0][i].x = as_u32(as_f32(xv[0][i].x) * inv * as_f32(av[i].x));
+      xv[0][i].y = as_u32(as_f32(xv[0][i].y) * inv * as_f32(av[i].y));
+      xv[0][i].z = as_u32(as_f32(xv[0][i].z) * inv * as_f32(av[i].z));
+      xv[0][i].w = as_u32(as_f32(xv[0][i].w) * inv * as_f32(av[i].w));
     }
   } else if constexpr (kPro == kProSwiGLU) {
     auto gate = [](uint32_t gb, uint32_t ub) {
@@ -468,18 +495,21 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
     };
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
-      xv[i].x = gate(xv[i].x, av[i].x);
-      xv[i].y = gate(xv[i].y, av[i].y);
-      xv[i].z = gate(xv[i].z, av[i].z);
-      xv[i].w = gate(xv[i].w, av[i].w);
+      xv[0][i].x = gate(xv[0][i].x, av[i].x);
+      xv[0][i].y = gate(xv[0][i].y, av[i].y);
+      xv[0][i].z = gate(xv[0][i].z, av[i].z);
+      xv[0][i].w = gate(xv[0][i].w, av[i].w);
     }
   }
 #pragma unroll
-  for (int i = 0; i < XV; ++i) quant_group<F>(xv[i], tid + i * nt, nf, xr);
+  for (int r = 0; r < R; ++r)
+#pragma unroll
+    for (int i = 0; i < XV; ++i) quant_group<F>(xv[r][i], tid + i * nt, nf, xr + r * U);
   __syncthreads();
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
-  XRec xreg = {};
-  if (active) xreg = xr[u];
+  XRec xreg[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) xreg[r] = active ? xr[r * U + u] : XRec{};
 
   // Teams of several waves (T > 1) park each row's per-wave sums in LDS and
   // reduce them kChunk steps at a time, one barrier per chunk.
@@ -487,29 +517,46 @@ __global__ __launch_bounds__(1024) void gemv_kernel(const uint8_t *__restrict__ 
   auto flush = [&](int step_end) {  // rows of steps [step_end - n, step_end), n = ((step_end - 1) % kChunk) + 1
     __syncthreads();
     const int first = (step_end - 1) / kChunk * kChunk;
-    if (w == 0 && lane < (uint32_t)(step_end - first)) {
-      const int st = first + (int)lane;
-      const int row = row_of(st);
-      if (row < end) {
-        const float *pp = part + ((size_t)(st % kChunk) * G + g) * T;
-        float t = 0.0f;
-        for (int q = 0; q < T; ++q) t += pp[q];
-        const int p = prob(row);
-        const float *b = bias_of(p);
-        store(row, t + (b != nullptr ? b[row - first_row(p)] : 0.0f));
+    const int n = (step_end - first) * R;  // (step, activation row) pairs
+    if (w == 0) {
+      for (int l = (int)lane; l < n; l += 64) {
+        const int st = first + l / R, r = l % R;
+        const int row = row_of(st);
+        if (row < end && r < nrows) {
+          const float *pp = part + ((size_t)(st % kChunk) * G + g) * T * R + r;
+          float t = 0.0f;
+          for (int q = 0; q < T; ++q) t += pp[q * R];
+          const int p = prob(row);
+          const float *b = bias_of(p);
+          store(row, r, t + (b != nullptr ? b[row - first_row(p)] : 0.0f));
+        }
       }
     }
     __syncthreads();  // the slots are rewritten by the next chunk
   };
   auto finish = [&](const typename F::Regs &Q, float b, int step) {
     const int row = row_of(step);
-    float acc = 0.0f;
-    if (active && row < end) acc = F::compute(Q, xreg, lane);
-    const float sum = wave_sum(acc);
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+    if (active && row < end) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = F::compute(Q, xreg[r], lane);  // the weight unpack is shared
+    }
+    float sum[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
     if (T == 1) {
-      if (lane == 0 && row < end) store(row, sum + b);
+      if (lane == 0 && row < end) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (r < nrows) store(row, r, sum[r] + b);
+      }
     } else {
-      if (lane == 0) part[((size_t)(step % kChunk) * G + g) * T + w] = sum;
+      if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; ++r) part[((size_t)(step % kChunk) * G + g) * T * R + w * R + r] = sum[r];
+      }
       if ((step + 1) % kChunk == 0) flush(step + 1);
     }
   };
@@ -576,7 +623,7 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(int type, const uint8
   for (int row = wave; row < N; row += nwaves) {
     const uint8_t *base = W + (size_t)row * row_bytes;
     float acc = 0.0f;
-    for (int k = lane; k < K; k += 64) acc = fmaf(x[k], deq_elem(type, base, (uint32_t)k), acc);
+    for (int k = lane; k < K; k += 64) acc = fmaf(x[k], deq_elem(type, base, (uint32_t)k), acc);  // explicit FMA
     const float s = wave_sum(acc);
     if (lane == 0) y[row] = s + (bias ? bias[row] : 0.0f);
   }
@@ -598,42 +645,64 @@ struct GemvLaunch {
   bool multi;
   GemvMore M;
   GemvPro P;
+  int nrows;  // activation rows of this launch (<= R)
 };
 
-template <class F, int D, int XV, bool kMulti>
+template <class F, int D, int XV, bool kMulti, int R>
 void launch_pro(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
                 int G) {
-  if (L.P.kind == kProRms)
-    launch_timed(gemv_kernel<F, D, XV, kMulti, kProRms>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y,
-                 L.rows, k, T, G, L.M, L.P);
-  else if (L.P.kind == kProSwiGLU)
-    launch_timed(gemv_kernel<F, D, XV, kMulti, kProSwiGLU>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
-                 L.y, L.rows, k, T, G, L.M, L.P);
-  else
-    launch_timed(gemv_kernel<F, D, XV, kMulti, kProNone>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias, L.y,
-                 L.rows, k, T, G, L.M, L.P);
+  if constexpr (R == 1) {
+    if (L.P.kind == kProRms) {
+      launch_timed(gemv_kernel<F, D, XV, kMulti, kProRms, 1>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
+                   L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
+      return;
+    }
+    if (L.P.kind == kProSwiGLU) {
+      launch_timed(gemv_kernel<F, D, XV, kMulti, kProSwiGLU, 1>, grid, block, (unsigned)lds, s, L.w, L.bytes, x,
+                   L.bias, L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
+      return;
+    }
+  }
+  launch_timed(gemv_kernel<F, D, XV, kMulti, kProNone, R>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
+               L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
 }
 
-template <class F, int D, int XV>
+template <class F, int D, int XV, int R>
 void launch_multi(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
                   int G) {
-  if (L.multi) launch_pro<F, D, XV, true>(grid, block, lds, s, L, x, k, T, G);
-  else launch_pro<F, D, XV, false>(grid, block, lds, s, L, x, k, T, G);
+  if (L.multi) launch_pro<F, D, XV, true, R>(grid, block, lds, s, L, x, k, T, G);
+  else launch_pro<F, D, XV, false, R>(grid, block, lds, s, L, x, k, T, G);
 }
 
-template <class F, int XV>
+// Ring depth: the format's maximum when every wave has that many rows to
+// stream, else 1 (a deeper ring than the row count would only issue loads
+// past the range).  Multi-row launches always use the maximum.
+template <class F, int XV, int R>
 void launch_depth(int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
                   const float *x, int k, int T, int G) {
-  if (steps >= F::kMaxDepth) launch_multi<F, F::kMaxDepth, XV>(grid, block, lds, s, L, x, k, T, G);
-  else launch_multi<F, 1, XV>(grid, block, lds, s, L, x, k, T, G);
+  if constexpr (R > 1) {
+    launch_multi<F, F::kMaxDepth, XV, R>(grid, block, lds, s, L, x, k, T, G);
+  } else {
+    if (steps >= F::kMaxDepth) launch_multi<F, F::kMaxDepth, XV, 1>(grid, block, lds, s, L, x, k, T, G);
+    else launch_multi<F, 1, XV, 1>(grid, block, lds, s, L, x, k, T, G);
+  }
+}
+
+template <class F, int R>
+void launch_xv(int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
+               const float *x, int k, int T, int G) {
+  if (xv <= 1) launch_depth<F, 1, R>(steps, grid, block, lds, s, L, x, k, T, G);
+  else if (xv == 2) launch_depth<F, 2, R>(steps, grid, block, lds, s, L, x, k, T, G);
+  else if (xv <= 4) launch_depth<F, 4, R>(steps, grid, block, lds, s, L, x, k, T, G);
+  else if constexpr (R > 1) launch_depth<F, 8, R>(steps, grid, block, lds, s, L, x, k, T, G);
 }
 
 template <class F>
-void launch_xv(int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
-               const float *x, int k, int T, int G) {
-  if (xv <= 1) launch_depth<F, 1>(steps, grid, block, lds, s, L, x, k, T, G);
-  else if (xv == 2) launch_depth<F, 2>(steps, grid, block, lds, s, L, x, k, T, G);
-  else launch_depth<F, 4>(steps, grid, block, lds, s, L, x, k, T, G);
+void launch_rows(int R, int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s,
+                 const GemvLaunch &L, const float *x, int k, int T, int G) {
+  if (R == 1) launch_xv<F, 1>(xv, steps, grid, block, lds, s, L, x, k, T, G);
+  else if (R == 2) launch_xv<F, 2>(xv, steps, grid, block, lds, s, L, x, k, T, G);
+  else launch_xv<F, 4>(xv, steps, grid, block, lds, s, L, x, k, T, G);
 }
 
 namespace {
@@ -665,35 +734,38 @@ hipError_t launch_generic(int type, const float *x, int64_t K, const void *w, in
 }
 
 // One streaming launch over the concatenated rows of P (all matrices pass
-// fast_ok).
-hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &P, int cu_count, hipStream_t s) {
+// fast_ok) for R activation rows (P.nrows of them real).
+hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &P, int R, int cu_count,
+                         hipStream_t s) {
   const int64_t N = P.rows;
   const int U = (int)(K / 64);
   const int T = (U + 63) / 64;  // waves per row team
+  const int max_threads = R == 1 ? gemv_max_threads<1>() : gemv_max_threads<4>();
+  const int max_xv = R == 1 ? kMaxXV : kMaxXVRows;
   // one workgroup per CU (fewer for short tensors); steps = rows per team at
   // the largest team count, then the fewest teams that still finish in that
   // many steps (so the last window is as full as possible)
   int64_t blocks = std::min<int64_t>(cu_count, N);
-  const int64_t max_g = 16 / T;
+  const int64_t max_g = std::max(1, max_threads / 64 / T);
   const int64_t steps0 = (N + blocks * max_g - 1) / (blocks * max_g);
   int64_t G = std::max<int64_t>(1, std::min<int64_t>(max_g, (N + blocks * steps0 - 1) / (blocks * steps0)));
-  // Every thread quantises at most kMaxXV float4s of x: with T == 1 extra
-  // helper waves cover x, with teams (T > 1) extra teams do (teams without
-  // rows stream nothing; K <= 16384 keeps this within 16 waves).
-  const int64_t x_threads = (K / 4 + kMaxXV - 1) / kMaxXV;
+  // Every thread quantises at most max_xv float4s of each x row: with T == 1
+  // extra helper waves cover x, with teams (T > 1) extra teams do (teams
+  // without rows stream nothing; K <= 16384 keeps this within the limit).
+  const int64_t x_threads = (K / 4 + max_xv - 1) / max_xv;
   if (T > 1) G = std::max<int64_t>(G, (x_threads + 64 * T - 1) / (64 * T));
   blocks = std::min<int64_t>(blocks, (N + G * steps0 - 1) / (G * steps0));
   int64_t threads = 64 * T * G;
-  if (T == 1) threads = std::min<int64_t>(1024, std::max(threads, (x_threads + 63) / 64 * 64));
+  if (T == 1) threads = std::min<int64_t>(max_threads, std::max(threads, (x_threads + 63) / 64 * 64));
   const int xv = (int)((K / 4 + threads - 1) / threads);
-  if (xv > kMaxXV || threads > 1024) return hipErrorInvalidConfiguration;  // excluded by fast_ok's K bound
+  if (xv > max_xv || threads > max_threads) return hipErrorInvalidConfiguration;  // excluded by fast_ok's K bound
   const dim3 grid((unsigned)blocks), block((unsigned)threads);
-  const size_t lds = (size_t)U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T : 0) +
+  const size_t lds = (size_t)R * U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T * R : 0) +
                      (P.P.kind == kProRms ? sizeof(float) * 16 : 0);
   const int k = (int)K, gg = (int)G;
-  if (type == kQ4_K) launch_xv<FQ4K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
-  else if (type == kQ6_K) launch_xv<FQ6K>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
-  else launch_xv<FQ80>(xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  if (type == kQ4_K) launch_rows<FQ4K>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  else if (type == kQ6_K) launch_rows<FQ6K>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  else launch_rows<FQ80>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
   return hipGetLastError();
 }
 
@@ -701,11 +773,12 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
 
 bool gemv_streams(int type, int64_t K, const void *w, int64_t N) { return fast_ok(type, K, w, N); }
 
-hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
+hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
                              hipStream_t s, const GemvPro &pro) {
   if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
   if (count < 1 || count > kGemvMaxProblems) return hipErrorInvalidValue;
+  if (pro.kind != kProNone && rows != 1) return hipErrorNotSupported;  // prologues run one row at a time
   GemvLaunch P{};
   P.P = pro;
   int64_t total = 0;
@@ -719,9 +792,13 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
   if (!fast) {  // matrix by matrix, each on its own best path
     for (int i = 0; i < count; ++i) {
       if (N[i] == 0) continue;
-      hipError_t e = fast_ok(type, K, w[i], N[i]) ? launch_gemv_multi(type, x, K, 1, &w[i], &N[i], &bias[i], &y[i],
-                                                                       cu_count, s, pro)
-                                                  : launch_generic(type, x, K, w[i], N[i], bias[i], y[i], cu_count, s);
+      hipError_t e = hipSuccess;
+      if (fast_ok(type, K, w[i], N[i])) {
+        e = launch_gemv_multi(type, x, K, rows, 1, &w[i], &N[i], &bias[i], &y[i], cu_count, s, pro);
+      } else {
+        for (int64_t r = 0; r < rows && e == hipSuccess; ++r)
+          e = launch_generic(type, x + r * K, K, w[i], N[i], bias[i], y[i] + r * N[i], cu_count, s);
+      }
       if (e != hipSuccess) return e;
     }
     return hipSuccess;
@@ -729,7 +806,6 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
   P.w = static_cast<const uint8_t *>(w[0]);
   P.bytes = (uint32_t)((size_t)N[0] * row_bytes_of(type, K));
   P.bias = bias[0];
-  P.y = y[0];
   P.multi = count > 1;
   int64_t start = N[0];
   for (int i = 1; i < kGemvMaxProblems; ++i) {
@@ -737,7 +813,6 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
       P.M.w[i - 1] = static_cast<const uint8_t *>(w[i]);
       P.M.bytes[i - 1] = (uint32_t)((size_t)N[i] * row_bytes_of(type, K));
       P.M.bias[i - 1] = bias[i];
-      P.M.y[i - 1] = y[i];
       P.M.start[i - 1] = (int)start;
       start += N[i];
     } else {
@@ -746,12 +821,28 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, con
   }
   P.rows = (int)total;
   if (total == 0) return hipSuccess;
-  return launch_stream(type, x, K, P, cu_count, s);
+  // up to kMaxRowsPerLaunch activation rows per pass over the weights, as
+  // many as the LDS holds: R rows of XRecs plus the teams' partial sums
+  // (<= 8 waves x kPartChunk x R floats) within 160 KiB
+  const int64_t U = K / 64;
+  int per_launch = kMaxRowsPerLaunch;
+  while (per_launch > 1 && (size_t)per_launch * (U * sizeof(XRec) + sizeof(float) * kPartChunk * 8) + 64 > kLdsBytes)
+    per_launch /= 2;
+  for (int64_t r0 = 0; r0 < rows; r0 += per_launch) {
+    const int nr = (int)std::min<int64_t>(per_launch, rows - r0);
+    P.nrows = nr;
+    P.y = y[0] + r0 * N[0];
+    for (int i = 1; i < count; ++i) P.M.y[i - 1] = y[i] + r0 * N[i];
+    const int R = nr == 1 ? 1 : nr == 2 ? 2 : 4;
+    hipError_t e = launch_stream(type, x + r0 * K, K, P, R, cu_count, s);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s) {
-  return launch_gemv_multi(type, x, K, 1, &w, &N, &bias, &y, cu_count, s, GemvPro{});
+  return launch_gemv_multi(type, x, K, 1, 1, &w, &N, &bias, &y, cu_count, s, GemvPro{});
 }
 
 }  // namespace okq

@@ -47,7 +47,7 @@ hipError_t launch_get_rows(int type, const void *w, int64_t row_bytes, int64_t n
 // cu_count sizes the persistent grid.
 hipError_t launch_gemv(int type, const float *x, int64_t K, const void *w, int64_t N, const float *bias, float *y,
                        int cu_count, hipStream_t s);
-// Several matrices of one format and K against the same activation row in
+// Several matrices of one format and K against the same activation rows in
 // one launch (row-concatenated); matrices the streaming kernel cannot take
 // run on their own.  count <= kGemvMaxProblems.
 constexpr int kGemvMaxProblems = 4;
@@ -61,7 +61,9 @@ struct GemvPro {
   float eps;
 };
 bool gemv_streams(int type, int64_t K, const void *w, int64_t N);
-hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int count, const void *const *w,
+// x [rows, K] and y[i] [rows, N[i]] row-major; every pass over the weights
+// serves up to four activation rows.  A prologue needs rows == 1.
+hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
                              hipStream_t s, const GemvPro &pro);
 

@@ -259,11 +259,10 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
     if (e != hipSuccess) return hip_status(e, "bf16 widening launch");
     xf = static_cast<const float *>(ws);
   }
-  for (int64_t r = 0; r < rows; ++r) {
-    hipError_t e = okq::launch_gemv((int)type, xf + r * K, K, w, N, bias, out + r * N, info.cu_count, s);
-    if (e != hipSuccess) return hip_status(e, "gemv launch");
-  }
-  return ok();
+  // every pass over the weights serves up to four rows
+  hipError_t e = okq::launch_gemv_multi((int)type, xf, K, rows, 1, &w, &N, &bias, &out, info.cu_count, s,
+                                        okq::GemvPro{});
+  return hip_status(e, "gemv launch");
 }
 
 }  // namespace
@@ -477,14 +476,9 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
   const float *const *b = bias ? bias : nobias;
-  for (int64_t r = 0; r < rows; ++r) {
-    float *o[okq::kGemvMaxProblems];
-    for (int i = 0; i < count; ++i) o[i] = out[i] + r * out_features[i];
-    hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * in_features, in_features, count, w, out_features, b, o,
-                                          info.cu_count, s, okq::GemvPro{});
-    if (e != hipSuccess) return hip_status(e, "gemv_multi launch");
-  }
-  return ok();
+  hipError_t e = okq::launch_gemv_multi((int)w_type, x, in_features, rows, count, w, out_features, b, out,
+                                        info.cu_count, s, okq::GemvPro{});
+  return hip_status(e, "gemv_multi launch");
 }
 
 okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float epsilon, float *out,
@@ -529,12 +523,12 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
   const float *const *b = bias ? bias : nobias;
-  if (rows <= kGemvMaxRows && streams) {  // decode: every workgroup normalises x in its prologue
+  if (rows == 1 && streams) {  // one decode row: every workgroup normalises x in its prologue
     const okq::GemvPro pro{okq::kProRms, norm_weight, epsilon};
     for (int64_t r = 0; r < rows; ++r) {
       float *o[okq::kGemvMaxProblems];
       for (int i = 0; i < count; ++i) o[i] = out[i] + r * out_features[i];
-      hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * hidden, hidden, count, w, out_features, b, o,
+      hipError_t e = okq::launch_gemv_multi((int)w_type, x + r * hidden, hidden, 1, count, w, out_features, b, o,
                                             info.cu_count, s, pro);
       if (e != hipSuccess) return hip_status(e, "rmsnorm_linear launch");
     }
@@ -595,12 +589,10 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
     const void *ws[2] = {gate_w, up_w};
     const int64_t ns[2] = {intermediate, intermediate};
     const float *bs[2] = {nullptr, nullptr};
-    for (int64_t r = 0; r < rows; ++r) {
-      float *os[2] = {gate_buf + r * intermediate, up_buf + r * intermediate};
-      hipError_t e = okq::launch_gemv_multi((int)gate_type, x + r * hidden, hidden, 2, ws, ns, bs, os, info.cu_count,
-                                            s, okq::GemvPro{});
-      if (e != hipSuccess) return hip_status(e, "mlp gate/up launch");
-    }
+    float *const os[2] = {gate_buf, up_buf};
+    hipError_t e = okq::launch_gemv_multi((int)gate_type, x, hidden, rows, 2, ws, ns, bs, os, info.cu_count, s,
+                                          okq::GemvPro{});
+    if (e != hipSuccess) return hip_status(e, "mlp gate/up launch");
   } else {
     st = linear_impl(x, false, rows, hidden, gate_type, gate_w, gate_bytes, intermediate, nullptr, gate_buf, stream,
                      Path::Auto);
@@ -611,7 +603,7 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   }
   // down: silu(gate) * up folded into the GEMV prologue, or materialised in
   // gate_buf (the reference's final content of gate_buf) for the other paths
-  if (decode && okq::gemv_streams((int)down_type, intermediate, down_w, hidden)) {
+  if (rows == 1 && okq::gemv_streams((int)down_type, intermediate, down_w, hidden)) {
     const okq::GemvPro base{okq::kProSwiGLU, nullptr, 0.0f};
     const float *nob = nullptr;
     for (int64_t r = 0; r < rows; ++r) {
@@ -619,7 +611,7 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
       pro.a = up_buf + r * intermediate;
       float *o = out + r * hidden;
       const int64_t n = hidden;
-      hipError_t e = okq::launch_gemv_multi((int)down_type, gate_buf + r * intermediate, intermediate, 1, &down_w, &n,
+      hipError_t e = okq::launch_gemv_multi((int)down_type, gate_buf + r * intermediate, intermediate, 1, 1, &down_w, &n,
                                             &nob, &o, info.cu_count, s, pro);
       if (e != hipSuccess) return hip_status(e, "mlp down launch");
     }

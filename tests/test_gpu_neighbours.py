@@ -218,10 +218,10 @@ def test_mlp_gated_silu_q_matches_reference_order(torch, okq, orc, tg, tu, td, r
     gate = orc.linear_q(tg, x, rows, hidden, gq, inter)
     up = orc.linear_q(tu, x, rows, hidden, uq, inter)
     # Each of the three projections meets the per-output rule on its own
-    # inputs.  Decode rows leave gate(x) in gate_buf (the SiLU is folded
-    # into the down GEMV's prologue; every down weight here streams); batches
-    # leave silu(gate(x)) * up(x) there, as the reference does.
-    fused = rows <= 4
+    # inputs.  A single row leaves gate(x) in gate_buf (the SiLU is folded
+    # into the down GEMV's prologue; every down weight here streams); more
+    # rows leave silu(gate(x)) * up(x) there, as the reference does.
+    fused = rows == 1
     ok, info = _rule(u_buf, up)
     assert ok, ("up", info)
     ok, info = _rule(g_buf, gate if fused else orc.swiglu(gate, up))

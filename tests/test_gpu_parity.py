@@ -221,6 +221,34 @@ def test_small_batch_rows_and_determinism(torch, okq, orc, t):
     assert (got.view(np.uint32) == again.view(np.uint32)).all()
 
 
+MULTIROW_CASES = [
+    # (type, rows, n, k): every pass over the weights serves up to four rows
+    (O.Q4_K, 2, 4096, 4096), (O.Q4_K, 3, 1024, 4096), (O.Q4_K, 4, 14336, 4096), (O.Q4_K, 4, 4096, 14336),
+    (O.Q4_K, 8, 512, 14336), (O.Q4_K, 4, 33, 8192),
+    (O.Q6_K, 2, 1024, 4096), (O.Q6_K, 4, 4096, 14336), (O.Q6_K, 7, 300, 12288),
+    (O.Q8_0, 3, 4096, 4096), (O.Q8_0, 4, 17, 16384), (O.Q8_0, 5, 300, 96),
+]
+
+
+@pytest.mark.parametrize("t,rows,n,k", MULTIROW_CASES)
+def test_multirow_gemv_equals_single_rows_bit_for_bit(torch, okq, orc, t, rows, n, k):
+    """A launch over R activation rows does each row's arithmetic exactly as a
+    one-row launch (same per-lane contraction, same reduction order), so the
+    batched GEMV must equal row-by-row GEMVs bit for bit, and the reference
+    CPU path within the rule."""
+    print(f"[gpu] multirow gemv type={t} rows={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(t, orc.normal(5000 + t + k, n * k, 0.02))
+    bias = orc.normal(5001, n, 0.1)
+    x = orc.normal(5002 + rows, rows * k, 1.0)
+    got = gpu_linear(torch, okq, t, x, rows, k, wq, n, bias, entry="okq_gemv")
+    for r in range(rows):
+        one = gpu_linear(torch, okq, t, x[r * k:(r + 1) * k], 1, k, wq, n, bias, entry="okq_gemv")
+        assert _same_bits(got[r], one[0]).all(), f"row {r}"
+    want = orc.linear_q(t, x, rows, k, wq, n, bias)
+    ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+    assert ok, f"idx={idx} max_abs={dmax}"
+
+
 def test_empty_inputs_are_noops(torch, okq):
     out = torch.full((4,), 7.0, device="cuda")
     okq.call("okq_linear_out_by_in_q", None, 0, 256, O.Q4_K, None, 144 * 4, 4, None, out.data_ptr(), None)
