@@ -421,6 +421,97 @@ def run_c4(ctx: Ctx, args, c2):
 
 
 # ---------------------------------------------------------------------------
+# C5: the 32-layer decoder-stack sweep (Q4_K_M mix)
+# ---------------------------------------------------------------------------
+
+# Llama-3-8B layer in the Q4_K_M mix: Q6_K for v and down, Q4_K for the rest
+C5_PROJ = [("q", Q4K, 4096, 4096), ("k", Q4K, 1024, 4096), ("v", Q6K, 1024, 4096), ("o", Q4K, 4096, 4096),
+           ("gate", Q4K, 14336, 4096), ("up", Q4K, 14336, 4096), ("down", Q6K, 4096, 14336)]
+C5_LAYERS = 32
+C5_HEAD = (Q6K, 128256, 4096)
+
+
+def run_c5(ctx: Ctx, args):
+    """One step = every projection of 32 layers plus the Q6_K head, back to
+    back on one stream, replayed from a HIP graph.  `grouped`: the decode
+    launches an engine issues (q+k and gate+up share x in okq_gemv_multi,
+    each pass over a weight serving up to four rows); `auto`: one
+    okq_linear_out_by_in_q per projection (the MFMA GEMM for Q4_K above four
+    rows, the multi-row GEMV otherwise)."""
+    torch = ctx.torch
+    log(f"C5: generating {C5_LAYERS} Q4_K_M layers + Q6_K head")
+    layers = [{name: ctx.quantized(t, n, k, seed=50_000 + 100 * l + i) for i, (name, t, n, k) in enumerate(C5_PROJ)}
+              for l in range(C5_LAYERS)]
+    head = ctx.quantized(*C5_HEAD, seed=59_999)
+    step_bytes = C5_LAYERS * sum(wbytes(t, n, k) for _, t, n, k in C5_PROJ) + wbytes(*C5_HEAD)
+    shape = {name: (t, n, k) for name, t, n, k in C5_PROJ}
+    res = {"weight_bytes_per_step": step_bytes, "layers": C5_LAYERS}
+    cs = torch.cuda.Stream()  # capture stream: the GEMM workspace is allocated on it before capture
+    for rows in (1, 8, 32):
+        x4 = ctx.normal(rows * 4096, 60 + rows)
+        x14 = ctx.normal(rows * 14336, 61 + rows)
+        outs = {name: torch.empty(rows * n, dtype=torch.float32, device="cuda") for name, _, n, _ in C5_PROJ}
+        yh = torch.empty(rows * C5_HEAD[1], dtype=torch.float32, device="cuda")
+
+        def one(entry, name, w, s):
+            t, n, k = shape[name]
+            x = x14 if k == 14336 else x4
+            ctx.okq.call(entry, x.data_ptr(), rows, k, t, w.data_ptr(), w.numel(), n, None, outs[name].data_ptr(), s)
+
+        def group(names, lay, s):
+            t, _, k = shape[names[0]]
+            c = len(names)
+            ctx.okq.call("okq_gemv_multi", x4.data_ptr(), rows, k, t, c,
+                         (ctypes.c_void_p * c)(*[lay[m].data_ptr() for m in names]),
+                         (ctypes.c_uint64 * c)(*[lay[m].numel() for m in names]),
+                         (ctypes.c_int64 * c)(*[shape[m][1] for m in names]), None,
+                         (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), s)
+
+        def step(mode, s):
+            for lay in layers:
+                if mode == "grouped":
+                    group(["q", "k"], lay, s)
+                    one("okq_gemv", "v", lay["v"], s)
+                    one("okq_gemv", "o", lay["o"], s)
+                    group(["gate", "up"], lay, s)
+                    one("okq_gemv", "down", lay["down"], s)
+                else:
+                    for name, _, _, _ in C5_PROJ:
+                        one("okq_linear_out_by_in_q", name, lay[name], s)
+            t, n, k = C5_HEAD
+            entry = "okq_gemv" if mode == "grouped" else "okq_linear_out_by_in_q"
+            ctx.okq.call(entry, x4.data_ptr(), rows, k, t, head.data_ptr(), head.numel(), n, None, yh.data_ptr(), s)
+
+        modes = ["grouped"] if rows == 1 else (["grouped", "auto"] if rows == 8 else ["auto"])
+        for mode in modes:
+            with torch.cuda.stream(cs):
+                step(mode, cs.cuda_stream)  # warm: allocates the GEMM workspace of this stream
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cs):
+                step(mode, cs.cuda_stream)
+            for _ in range(2):
+                g.replay()
+            torch.cuda.synchronize()
+            reps = args.c5_steps
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                g.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / reps
+            log(f"C5: batch {rows} {mode}: {ms:.3f} ms per step")
+            res[f"b{rows}_{mode}"] = {"batch": rows, "ms_per_step": round(ms, 4),
+                                     "weight_gbs": round(step_bytes / ms / 1e6, 1),
+                                     "frac_hbm": round(step_bytes / ms / 1e6 / HBM_PEAK_GBS, 4),
+                                     "tokens_per_s": round(rows * 1000.0 / ms, 1)}
+            del g
+    del layers, head
+    return res
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline (reference CPU path, oracle restatement)
 # ---------------------------------------------------------------------------
 
@@ -495,7 +586,8 @@ def main():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", default="c1,c3,c4", help="secondary configs to run (comma list of c1,c3,c4)")
+    ap.add_argument("--only", default="c1,c3,c4,c5", help="secondary configs to run (comma list of c1,c3,c4,c5)")
+    ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
     ap.add_argument("--probe", choices=["gate_up", "copy"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
                          "weight replicas, or 20 launches of a 256 MiB f32 elementwise copy (calibration)")
@@ -526,6 +618,8 @@ def main():
         extra["c3_q6_k_head"] = run_c3(ctx, args)
     if "c4" in only:
         extra["c4_q4_k_gemm_bf16"] = run_c4(ctx, args, c2)
+    if "c5" in only:
+        extra["c5_stack_sweep"] = run_c5(ctx, args)
     cpu = None if args.no_cpu else run_cpu_baseline(ctx, c2, args)
 
     rec = {
