@@ -42,17 +42,18 @@ def _compile(src: str) -> str:
     return obj
 
 
-HOST_SRC = os.path.join(HERE, "host", "kernel_backend.cpp")
+HOST_SRC = [os.path.join(HERE, "host", f) for f in ("kernel_backend.cpp", "gguf.cpp")]
 HOST_LIB = os.path.join(HERE, "libocelotl_hip.so")
 CXX = os.environ.get("CXX", "g++")
 
 
 def build_host(verbose: bool = False) -> str:
-    """The C++ mirror of the kernel boundary (host/kernel_backend.*), a plain
-    C++17 library over okq.h linked against libokq.so."""
+    """The C++ host layer (host/kernel_backend.*: the mirror of the kernel
+    boundary; host/gguf.*: the GGUF loader), a plain C++17 library over okq.h
+    linked against libokq.so."""
     tmp = HOST_LIB + ".tmp"
     cmd = [CXX, "-std=c++17", "-O2", "-Wall", "-Wextra", "-fPIC", "-shared", "-I", os.path.join(HERE, "..", "include"),
-           "-I", os.path.join(HERE, "host"), HOST_SRC, "-o", tmp, "-L", HERE, "-lokq", "-Wl,-rpath,$ORIGIN"]
+           "-I", os.path.join(HERE, "host"), *HOST_SRC, "-o", tmp, "-L", HERE, "-lokq", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"host library build failed:\n{r.stdout}\n{r.stderr}")

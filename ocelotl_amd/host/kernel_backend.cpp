@@ -71,8 +71,24 @@ OcelotlError OcelotlError::unsupported(std::string feature, std::optional<std::s
   return OcelotlError(UnsupportedError{std::move(feature), std::move(requested), std::move(supported)});
 }
 
+OcelotlError OcelotlError::invalid_model(std::optional<std::string> path, std::optional<std::string> field,
+                                         std::string message) {
+  return OcelotlError(InvalidModelError{std::move(path), std::move(field), std::move(message)});
+}
+
+OcelotlError OcelotlError::io(std::optional<std::string> path, int code) {
+  return OcelotlError(IoError{std::move(path), code, std::strerror(code)});
+}
+
 std::string OcelotlError::to_string() const {
   if (const KernelError *k = as_kernel()) return "kernel error on backend `" + k->backend + "`: " + k->message;
+  if (const InvalidModelError *m = as_invalid_model()) {
+    std::string s = "invalid model artifact";
+    if (m->path) s += " at `" + *m->path + "`";
+    if (m->field) s += " (field `" + *m->field + "`)";
+    return s + ": " + m->message;
+  }
+  if (const IoError *e = as_io()) return "IO error" + (e->path ? " on `" + *e->path + "`" : std::string()) + ": " + e->message;
   const UnsupportedError *u = as_unsupported();
   std::string s = "unsupported feature `" + u->feature + "`";
   if (u->requested) s += " (requested `" + *u->requested + "`)";

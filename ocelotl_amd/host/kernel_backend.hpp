@@ -44,24 +44,46 @@ struct UnsupportedError {
   std::vector<std::string> supported;
 };
 
-// The two OcelotlError variants this path produces (core lib.rs:15-26).
+// InvalidModelError{path, field, message} (core lib.rs:37-46): a malformed
+// model artifact (the GGUF loader's errors).
+struct InvalidModelError {
+  std::optional<std::string> path;
+  std::optional<std::string> field;
+  std::string message;
+};
+
+// IoError{path, source} (core lib.rs:87-93); `code` is the errno of the
+// failed call and `message` its strerror text.
+struct IoError {
+  std::optional<std::string> path;
+  int code;
+  std::string message;
+};
+
+// The OcelotlError variants this path produces (core lib.rs:15-31).
 class OcelotlError {
  public:
-  enum class Kind { Kernel, Unsupported };
+  enum class Kind { Kernel, Unsupported, InvalidModel, Io };
 
   static OcelotlError kernel(std::string backend, std::string message);
   static OcelotlError unsupported(std::string feature, std::optional<std::string> requested,
                                   std::vector<std::string> supported);
+  static OcelotlError invalid_model(std::optional<std::string> path, std::optional<std::string> field,
+                                    std::string message);
+  static OcelotlError io(std::optional<std::string> path, int code);
 
-  Kind kind() const { return std::holds_alternative<KernelError>(v_) ? Kind::Kernel : Kind::Unsupported; }
+  Kind kind() const { return static_cast<Kind>(v_.index()); }
   const KernelError *as_kernel() const { return std::get_if<KernelError>(&v_); }
   const UnsupportedError *as_unsupported() const { return std::get_if<UnsupportedError>(&v_); }
+  const InvalidModelError *as_invalid_model() const { return std::get_if<InvalidModelError>(&v_); }
+  const IoError *as_io() const { return std::get_if<IoError>(&v_); }
   // Display text in the reference's format ("kernel error on backend `b`: m").
   std::string to_string() const;
 
  private:
-  explicit OcelotlError(std::variant<KernelError, UnsupportedError> v) : v_(std::move(v)) {}
-  std::variant<KernelError, UnsupportedError> v_;
+  using V = std::variant<KernelError, UnsupportedError, InvalidModelError, IoError>;
+  explicit OcelotlError(V v) : v_(std::move(v)) {}
+  V v_;
 };
 
 // ocelotl_core::Result<T>.
