@@ -119,8 +119,9 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
  * x: [rows, in_features] f32 (device); w: GGUF blocks of an [out_features,
  * in_features] tensor, w_bytes = out_features * row_bytes(in_features);
  * bias: [out_features] f32 or NULL; out: [rows, out_features] f32.
- * rows == 0 or out_features == 0 is a no-op.  Small `rows` run the fused
- * dequant-GEMV, larger ones the MFMA dequant-GEMM. */
+ * rows == 0 or out_features == 0 is a no-op.  Up to 8 rows run the fused
+ * dequant-GEMV (each pass over the weights serving up to four rows); more
+ * rows run the MFMA dequant-GEMM (Q4_K, Q6_K; Q8_0 stays on the GEMV). */
 okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
                                   const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
                                   float *out, void *stream);
@@ -189,7 +190,7 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
  * byte lengths are intermediate * row_bytes(hidden) and hidden *
  * row_bytes(intermediate)); gate_buf, up_buf [rows, intermediate] caller-owned
  * scratch; out [rows, hidden].  Device buffers, x/gate_buf/up_buf 16-byte
- * aligned.  Decode-sized rows (rows <= 4) run gate+up as one grouped GEMV
+ * aligned.  Decode-sized rows (rows <= 8) run gate+up as one grouped GEMV
  * when they share a format.  A single row folds silu(gate) * up into the down
  * GEMV's prologue whenever the down weight takes the streaming GEMV (gate_buf
  * then holds gate(x)); otherwise silu(gate(x)) * up(x) is left in gate_buf,

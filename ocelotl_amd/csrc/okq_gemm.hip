@@ -8,6 +8,10 @@
 //     an fp16 lo plane (x ~= hi + lo to ~2^-22 relative) and contracted twice.
 //   * B = the integer part of the dequantised weight, exact in fp16:
 //       Q4_K: sc * q       (6-bit scale x 4-bit quant <= 945)
+//       Q6_K: sc * (q - 32) (|.| <= 4096) as two planes hi + lo, hi =
+//             fp16(sc * (q - 32)) and the exact remainder lo in {-1, 0, 1},
+//             each contracted with A (the x_lo * lo term, below 2^-22 of the
+//             result, is left out)
 //     The super-block scales d and dmin are applied in f32 to the per-super-
 //     block MFMA accumulators; the Q4_K min term  sum_s m_s * sum_{k in s} x_k
 //     is one extra K=16 MFMA per super-block on (xsum hi, xsum lo) x m.
@@ -159,31 +163,53 @@ __device__ __forceinline__ void nib4(uint32_t n4, h2 sc2, h2 off2, h2 &p0, h2 &p
 constexpr int kKB = 64;         // K per pipeline step: one 64-weight Q4_K chunk
 constexpr int kLDB = kKB + 8;   // LDS row pitch in halves (spreads rows over banks)
 
-template <int BM, bool kLo>
+template <int BM, bool kLo, int kFmt>
 struct alignas(16) GemmSmem {
+  static constexpr bool kMins = kFmt == kQ4_K;
   _Float16 A[2][BM][kLDB];
   _Float16 Alo[2][kLo ? BM : 1][kLDB];
   _Float16 B[2][kBN][kLDB];
-  _Float16 xs[2][BM][16];   // per super-block parity: xsum hi/lo of sub-blocks 0..7
-  _Float16 mn[2][kBN][16];  // per super-block parity: 6-bit mins, each twice
-  float d[2][kBN], dmin[2][kBN];
+  _Float16 Blo[2][kFmt == kQ6_K ? kBN : 1][kLDB];  // Q6_K: the exact remainder plane
+  _Float16 xs[2][kMins ? BM : 1][16];   // per super-block parity: xsum hi/lo of sub-blocks 0..7
+  _Float16 mn[2][kMins ? kBN : 1][16];  // per super-block parity: 6-bit mins, each twice
+  float d[2][kBN], dmin[2][kMins ? kBN : 1];
 };
 
 // Raw global data of one pipeline step for one thread.
-template <int BM, bool kLo>
+template <int BM, bool kLo, int kFmt>
 struct StepRegs {
   u32x4 a[4], al[kLo ? 4 : 1];  // 32 activations (fp16) of one row
   u32x4 xs;                     // 4 (hi, lo) xsum pairs (first chunk of a super-block)
   u32x4 hd;                     // Q4_K header of the weight row's super-block
   u32x4 q;                      // 16 (BM=128) or 8 (BM=256, in .x/.y) qs bytes
+  // Q6_K (BM = 128): dword windows (5 dwords for 16 bytes) of the ql bytes of
+  // k < 32, of k >= 32 and of the qh bytes; 3 dwords around the half's 8
+  // scales; d (2-byte load, first chunk of a super-block)
+  uint32_t l0[kFmt == kQ6_K ? 5 : 1], l1[kFmt == kQ6_K ? 5 : 1], hq[kFmt == kQ6_K ? 5 : 1];
+  uint32_t sc[kFmt == kQ6_K ? 3 : 1], dw;
 };
+
+// v = sc * (q - 32) for the four 6-bit values in the bytes of q4, as two
+// exact fp16 planes v = hi + lo: 0x64|q is the fp16 1024 + q, minus 1056
+// gives q - 32 exactly; hi = fp16(v) is exact while |v| <= 2048 and rounds to
+// an even integer above (|v| <= 4096), and lo = fma(q - 32, sc, -hi) is the
+// exact remainder (-1, 0 or 1).
+__device__ __forceinline__ void q6_4(uint32_t q4, h2 sc2, h2 &p0, h2 &p1, h2 &l0, h2 &l1) {
+  const h2 off = {(_Float16)-1056.0f, (_Float16)-1056.0f};
+  const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, q4, 0x04010400u)) + off;
+  const h2 b = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, q4, 0x04030402u)) + off;
+  p0 = a * sc2;
+  p1 = b * sc2;
+  l0 = __builtin_elementwise_fma(a, sc2, -p0);
+  l1 = __builtin_elementwise_fma(b, sc2, -p1);
+}
 
 // BM x 128 workgroup tile, BM/32 waves arranged (BM/64) x 2, each 64 x 64.
 // Software pipeline over 64-wide K steps: raw loads run two steps ahead in
 // registers, the dequantisation of step i+1 overlaps the MFMAs of step i, LDS
 // is double buffered, one barrier per step.
-template <int BM, bool kLo>
-__global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__restrict__ xhi,
+template <int BM, bool kLo, int kFmt>
+__global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restrict__ xhi,
                                                          const _Float16 *__restrict__ xlo,
                                                          const h2 *__restrict__ xsum, const float *__restrict__ rscale,
                                                          const uint8_t *__restrict__ W, const float *__restrict__ bias,
@@ -192,7 +218,10 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   constexpr int NT = BM * 2;       // threads
   constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
   constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
-  __shared__ GemmSmem<BM, kLo> sm;
+  constexpr bool kQ6 = kFmt == kQ6_K;
+  static_assert(!kQ6 || QB == 16, "Q6_K staging takes 16-byte windows (BM = 128)");
+  constexpr uint32_t kBlk = kQ6 ? kQ6KBytes : kQ4KBytes;
+  __shared__ GemmSmem<BM, kLo, kFmt> sm;
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
   // contiguous range of tiles (consecutive tiles share an N-tile).
   // With split-K (ksplit > 1) workgroup (tile, z) covers super-blocks
@@ -214,7 +243,7 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   const int nsb_all = K / 256;
   const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
   const int nsb = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;  // super-blocks of this slice
-  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
+  const uint32_t row_bytes = (uint32_t)nsb_all * kBlk;
 
   const int sr = tid >> 1, sp = tid & 1;        // A: row, 32-wide half
   const int br = tid / TPR, bq = tid % TPR;     // B: weight row, byte window
@@ -227,13 +256,13 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   // the descriptors return zeros there)
   const uint32_t a_row = (uint32_t)(m0 + sr) * K32 * 2u + 64u * (uint32_t)sp + 512u * (uint32_t)sb0;
   const uint32_t s_row = (uint32_t)(m0 + sr) * (K32 / 32u) * 4u + 16u * (uint32_t)sp + 32u * (uint32_t)sb0;
-  const uint32_t w_row = (uint32_t)(n0 + br) * row_bytes + (uint32_t)sb0 * kQ4KBytes;
+  const uint32_t w_row = (uint32_t)(n0 + br) * row_bytes + (uint32_t)sb0 * kBlk;
 
   // C = step & 3 is a compile-time constant at every call site, so the body
   // is straight-line code (no divergent branches around the loads: the wait
   // counters then only wait for the step actually consumed).  Steps past the
   // end read inside the next row or past the descriptor (zeros); unused.
-  auto load = [&](StepRegs<BM, kLo> &r, int step, auto Cc) {
+  auto load = [&](StepRegs<BM, kLo, kFmt> &r, int step, auto Cc) {
     constexpr int c = decltype(Cc)::value;
     const int sb = step >> 2;
     const uint32_t ka = a_row + 2u * (uint32_t)(step * kKB);
@@ -242,6 +271,26 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
     if (kLo) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) r.al[i] = bload4(rs_xl, ka + 16u * i);
+    }
+    if constexpr (kQ6) {
+      // chunk c of the super-block: half h = c / 2 (ql bytes 64h.., qh bytes
+      // 128 + 32h..); this thread's l = 16 bq .. 16 bq + 15.  Windows start at
+      // the dword below each (2-byte aligned) field.
+      constexpr uint32_t h = c >> 1;
+      const uint32_t B = w_row + (uint32_t)sb * kBlk;
+      auto win = [&](uint32_t *dst, uint32_t at, int n) {
+#pragma unroll
+        for (int t = 0; t < n; ++t) dst[t] = __builtin_amdgcn_raw_buffer_load_b32(rs_w, (at & ~3u) + 4u * t, 0, 0);
+      };
+      // both chunks of a half use the same bytes (the second read hits the cache)
+      win(r.l0, B + 64u * h + 16u * bq, 5);
+      win(r.l1, B + 64u * h + 32u + 16u * bq, 5);
+      win(r.hq, B + 128u + 32u * h + 16u * bq, 5);
+      win(r.sc, B + 192u + 8u * h, 3);
+      // d with a 2-byte load: a dword window could end past the tensor (whose
+      // size is only 2-byte aligned) and the range check would zero it
+      if constexpr (c == 0) r.dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs_w, B + 208u, 0, 0);
+      return;
     }
     if constexpr (c == 0) r.xs = bload4(rs_xs, s_row + 32u * (uint32_t)sb);
     const uint32_t blk = w_row + (uint32_t)sb * kQ4KBytes;
@@ -255,7 +304,7 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
     }
   };
 
-  auto stage = [&](const StepRegs<BM, kLo> &r, int step, int buf, auto Cc) {
+  auto stage = [&](const StepRegs<BM, kLo, kFmt> &r, int step, int buf, auto Cc) {
     constexpr int c = decltype(Cc)::value;
     const int sbp = (step >> 2) & 1;
     u32x4 *da = reinterpret_cast<u32x4 *>(&sm.A[buf][sr][32 * sp]);
@@ -265,6 +314,52 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
       u32x4 *dl = reinterpret_cast<u32x4 *>(&sm.Alo[buf][sr][32 * sp]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) dl[i] = r.al[i];
+    }
+    if constexpr (kQ6) {
+      constexpr uint32_t cc = c & 1, h = c >> 1;
+      const uint32_t B = w_row + (uint32_t)(step >> 2) * kBlk;
+      // realign each window by the field's offset within its first dword
+      auto bytes16 = [&](const uint32_t *w, uint32_t at, uint32_t o[4]) {
+        const uint32_t ra = at & 3u;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) o[t] = __builtin_amdgcn_alignbyte(w[t + 1], w[t], ra);
+      };
+      uint32_t L0[4], L1[4], H[4];
+      bytes16(r.l0, B + 64u * h + 16u * bq, L0);
+      bytes16(r.l1, B + 64u * h + 32u + 16u * bq, L1);
+      bytes16(r.hq, B + 128u + 32u * h + 16u * bq, H);
+      // int8 scales of this thread's l-run (l / 16 = bq): index 8h + bq + 2p
+      // for p = 2cc (k < 32) and 2cc + 1 (k >= 32)
+      const uint32_t sat = B + 192u + 8u * h;
+      const uint32_t s0 = __builtin_amdgcn_alignbyte(r.sc[1], r.sc[0], sat & 3u);
+      const uint32_t s1 = __builtin_amdgcn_alignbyte(r.sc[2], r.sc[1], sat & 3u);
+      const uint32_t ia = (uint32_t)bq + 4u * cc, ib = ia + 2u;  // 0..7
+      const int sca = (int)__builtin_amdgcn_sbfe((int)(ia < 4 ? s0 : s1), 8 * (ia & 3u), 8u);
+      const int scb = (int)__builtin_amdgcn_sbfe((int)(ib < 4 ? s0 : s1), 8 * (ib & 3u), 8u);
+      const _Float16 fa = (_Float16)(float)sca, fb = (_Float16)(float)scb;
+      const h2 sa = {fa, fa}, sbv = {fb, fb};
+      // first: k < 32 of the chunk, second: k >= 32; r*: the remainder plane
+      h2 fi[8], se[8], rf[8], rs[8];
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t qa = ((L0[w] >> (4 * cc)) & 0x0F0F0F0Fu) | (((H[w] >> (4 * cc)) & 0x03030303u) << 4);
+        const uint32_t qb = ((L1[w] >> (4 * cc)) & 0x0F0F0F0Fu) | (((H[w] >> (4 * cc + 2)) & 0x03030303u) << 4);
+        q6_4(qa, sa, fi[2 * w], fi[2 * w + 1], rf[2 * w], rf[2 * w + 1]);
+        q6_4(qb, sbv, se[2 * w], se[2 * w + 1], rs[2 * w], rs[2 * w + 1]);
+      }
+      auto put = [&](_Float16 *dst, const h2 *v) {
+        u32x4 *d4 = reinterpret_cast<u32x4 *>(dst);
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+          d4[t] = u32x4{__builtin_bit_cast(uint32_t, v[4 * t]), __builtin_bit_cast(uint32_t, v[4 * t + 1]),
+                        __builtin_bit_cast(uint32_t, v[4 * t + 2]), __builtin_bit_cast(uint32_t, v[4 * t + 3])};
+      };
+      put(&sm.B[buf][br][16 * bq], fi);
+      put(&sm.B[buf][br][32 + 16 * bq], se);
+      put(&sm.Blo[buf][br][16 * bq], rf);
+      put(&sm.Blo[buf][br][32 + 16 * bq], rs);
+      if constexpr (c == 0) sm.d[sbp][br] = f16_bits_hw(r.dw & 0xffffu);
+      return;
     }
     if constexpr (c == 0) *reinterpret_cast<u32x4 *>(&sm.xs[sbp][sr][8 * sp]) = r.xs;
     // low nibbles -> sub-block 2c (k = byte), high nibbles -> 2c+1 (k = 32 + byte)
@@ -345,6 +440,15 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
         for (int j = 0; j < 2; ++j)
           accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv[j], (first && ks == 0) ? zero : accs[i][j],
                                                               0, 0, 0);
+      if constexpr (kQ6) {  // the exact remainder plane of the weights (x_lo * remainder is below 2^-22)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const h8 bl = *reinterpret_cast<const h8 *>(&sm.Blo[buf][wn * 64 + 32 * j + fr][fk4 + 8 * ks]);
+#pragma unroll
+          for (int i = 0; i < 2; ++i)
+            accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bl, accs[i][j], 0, 0, 0);
+        }
+      }
       if (kLo) {
 #pragma unroll
         for (int i = 0; i < 2; ++i)
@@ -358,8 +462,19 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
     }
   };
 
-  // end of a super-block: acc += d * accs - dmin * (xsum . m)
+  // end of a super-block: acc += d * accs - dmin * (xsum . m)  (Q6_K: d * accs)
   auto scale = [&](int sbp) {
+    if constexpr (kQ6) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float dv = sm.d[sbp][wn * 64 + 32 * j + fr];
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] = fmaf(dv, accs[i][j][e], acc[i][j][e]);
+      }
+      return;
+    }
     h8 xa[2], mb[2];
 #pragma unroll
     for (int i = 0; i < 2; ++i) xa[i] = *reinterpret_cast<const h8 *>(&sm.xs[sbp][wm * 64 + 32 * i + fr][fk]);
@@ -385,7 +500,7 @@ __global__ __launch_bounds__(BM * 2) void gemm_q4k_kernel(const _Float16 *__rest
   using C1 = std::integral_constant<int, 1>;
   using C2 = std::integral_constant<int, 2>;
   using C3 = std::integral_constant<int, 3>;
-  StepRegs<BM, kLo> R0, R1;
+  StepRegs<BM, kLo, kFmt> R0, R1;
   load(R0, 0, C0{});
   load(R1, 1, C1{});
   stage(R0, 0, 0, C0{});
@@ -473,17 +588,18 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
   // 32-bit buffer offsets: activations (with a tile of padding rows) and weights
   const int64_t a_bytes = (M + 256) * K * 2;
-  const int64_t w_bytes = (N + kBN) * (K / 256) * kQ4KBytes;
-  return type == kQ4_K && K % 256 == 0 && N >= 1 && M >= 1 && a_bytes < (int64_t)UINT32_MAX &&
+  const int64_t w_bytes = (N + kBN) * (K / 256) * (type == kQ6_K ? kQ6KBytes : kQ4KBytes) + 1024;
+  return (type == kQ4_K || type == kQ6_K) && K % 256 == 0 && N >= 1 && M >= 1 && a_bytes < (int64_t)UINT32_MAX &&
          w_bytes < (int64_t)UINT32_MAX;
 }
 
-GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
+GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
-  // bf16 activations with M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
+  // Q4_K, bf16 activations, M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
   // 64); otherwise 128 x 128 tiles (f32 activations need the second fp16
-  // plane, which only fits the LDS budget at 128 rows).
-  p.bm = (x_is_bf16 && M > 128) ? 256 : 128;
+  // plane, which only fits the LDS budget at 128 rows; Q6_K stages its
+  // larger raw windows in the 4-wave tile's register budget).
+  p.bm = (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
   const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
   // Split K when the tiles alone leave CUs idle: enough slices for about one
   // workgroup per CU, at least two super-blocks per slice, at most 8.
@@ -504,7 +620,8 @@ GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count
 
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
-  if (type != kQ4_K) return hipErrorInvalidValue;
+  if (type != kQ4_K && type != kQ6_K) return hipErrorInvalidValue;
+  if (type == kQ6_K && plan.bm != 128) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);
@@ -526,15 +643,20 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   const int tiles = tiles_m * tiles_n;
   const int per_xcd = (tiles * ks + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(plan.bm * 2));
-  if (plan.bm == 256)
-    launch_timed(gemm_q4k_kernel<256, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
-                 tiles, ks, part);
-  else if (x_is_bf16)
-    launch_timed(gemm_q4k_kernel<128, false>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
-                 tiles, ks, part);
-  else
-    launch_timed(gemm_q4k_kernel<128, true>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k, tiles_m,
-                 tiles, ks, part);
+#define OKQ_GEMM(BM_, LO_, FMT_)                                                                                   \
+  launch_timed(gemm_kq_kernel<BM_, LO_, FMT_>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k,     \
+               tiles_m, tiles, ks, part)
+  if (type == kQ6_K) {
+    if (x_is_bf16) OKQ_GEMM(128, false, kQ6_K);
+    else OKQ_GEMM(128, true, kQ6_K);
+  } else if (plan.bm == 256) {
+    OKQ_GEMM(256, false, kQ4_K);
+  } else if (x_is_bf16) {
+    OKQ_GEMM(128, false, kQ4_K);
+  } else {
+    OKQ_GEMM(128, true, kQ4_K);
+  }
+#undef OKQ_GEMM
   e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   const int64_t total = M * N;

@@ -82,13 +82,13 @@ struct GemmPlan {
   int ksplit;
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };
-GemmPlan gemm_plan(int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
+GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
 // `workspace` holds plan.workspace bytes (256-aligned); it is reused by later
 // calls on the stream.
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s);
 
-// True when launch_gemm supports this (type, M, K, N).
+// True when launch_gemm supports this (type, M, K, N): Q4_K and Q6_K.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);
 
 }  // namespace okq

@@ -89,9 +89,11 @@ def test_gemm_f32_q4k_matches_reference(torch, okq, orc, rows, n, k):
     x = orc.normal(901 + rows, rows * k, 1.0)
     got = run(torch, okq, "okq_gemm", O.Q4_K, x, rows, k, wq, n)
     check_rows(orc, O.Q4_K, got, x, rows, k, wq, n, None, None)
-    # the automatic path picks the GEMM above 4 rows and agrees bit for bit
+    # the automatic path picks the GEMM above 8 rows (the GEMV up to 8) and
+    # agrees with the pinned path bit for bit
     auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q4_K, x, rows, k, wq, n)
-    assert (auto.view(np.uint32) == got.view(np.uint32)).all()
+    pinned = got if rows > 8 else run(torch, okq, "okq_gemv", O.Q4_K, x, rows, k, wq, n)
+    assert (auto.view(np.uint32) == pinned.view(np.uint32)).all()
 
 
 def test_gemm_one_hot_columns_are_exact(torch, okq, orc):
@@ -173,3 +175,61 @@ def test_gemm_wide_dynamic_range_rows(torch, okq, orc):
         assert (got[3] == got[0] * np.float32(2.0 ** 40)).all(), entry
         assert (got[4] == got[0] * np.float32(2.0 ** -60)).all(), entry
         assert (got[5] == 0.0).all(), entry
+
+
+# ---- Q6_K -----------------------------------------------------------------------
+# B = sc * (q - 32) (|.| <= 4096) enters as two exact fp16 planes, fp16(v) and
+# the remainder v - fp16(v) in {-1, 0, 1}: the products are exact as for Q4_K.
+
+Q6K_CASES = [
+    # (entry, rows, n, k)
+    ("okq_gemm_bf16", 9, 96, 256), ("okq_gemm_bf16", 33, 300, 1024), ("okq_gemm_bf16", 130, 1024, 4096),
+    ("okq_gemm_bf16", 128, 4096, 14336), ("okq_gemm", 32, 1024, 4096), ("okq_gemm", 32, 4096, 14336),
+    ("okq_gemm", 100, 257, 768), ("okq_gemm", 5, 64, 512),
+    # the last super-block of the last row ends 2 bytes past a dword (257 rows x 630 bytes)
+    ("okq_gemm_bf16", 100, 257, 768), ("okq_gemm", 32, 257, 768),
+]
+
+
+@pytest.mark.parametrize("entry,rows,n,k", Q6K_CASES)
+def test_gemm_q6k_matches_reference(torch, okq, orc, entry, rows, n, k):
+    print(f"[gpu] gemm {entry} Q6_K M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q6_K, orc.normal(900 + n + k, n * k, 0.02))
+    bias = orc.normal(901, n, 0.1)
+    if entry == "okq_gemm_bf16":
+        x, x32 = bf16_inputs(orc, 902 + rows, rows, k)
+    else:
+        x = x32 = orc.normal(903 + rows, rows * k, 1.0)
+    got = run(torch, okq, entry, O.Q6_K, x, rows, k, wq, n, bias)
+    check_rows(orc, O.Q6_K, got, x32, rows, k, wq, n, bias, None if rows <= 130 else 16)
+
+
+def test_gemm_q6k_one_hot_columns_are_exact(torch, okq, orc):
+    """x = e_j picks column j of every weight row: the GEMM returns d * (hi +
+    lo) with hi + lo = sc * (q - 32) exactly, the dequantized value bit for
+    bit (scales up to |sc| = 128 included)."""
+    rows, n, k = 16, 64, 512
+    wq = orc.quantize(O.Q6_K, orc.normal(910, n * k, 0.02))
+    w = orc.dequantize(O.Q6_K, wq, n * k).reshape(n, k)
+    blocks = np.frombuffer(wq.tobytes(), np.uint8).reshape(n, k // 256, 210)
+    assert np.abs(blocks[:, :, 192:208].view(np.int8).astype(int)).max() > 64  # products above 2048 occur
+    x = np.zeros((rows, k), np.float32)
+    cols = np.arange(rows) * 31 % k
+    x[np.arange(rows), cols] = 1.0
+    for entry, xin in (("okq_gemm", x.reshape(-1)), ("okq_gemm_bf16", orc.f32_to_bf16(x.reshape(-1)))):
+        got = run(torch, okq, entry, O.Q6_K, xin, rows, k, wq, n)
+        # values, not bits: a zero product with a negative scale dequantizes to -0.0
+        assert np.array_equal(got, w[:, cols].T), entry
+
+
+def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):
+    """okq_linear_out_by_in_q: 9+ rows of a Q6_K weight run the MFMA GEMM
+    (bit-identical to okq_gemm), up to 8 rows the GEMV (bit-identical to
+    okq_gemv)."""
+    n, k = 256, 1024
+    wq = orc.quantize(O.Q6_K, orc.normal(920, n * k, 0.02))
+    for rows, pinned in ((8, "okq_gemv"), (9, "okq_gemm")):
+        x = orc.normal(921 + rows, rows * k, 1.0)
+        auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q6_K, x, rows, k, wq, n)
+        pin = run(torch, okq, pinned, O.Q6_K, x, rows, k, wq, n)
+        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
