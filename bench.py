@@ -326,12 +326,12 @@ def measured_traffic():
 
 def roofline_from(launches):
     # dominant kernel: the gate+up launch (two 14336 x 4096 Q4_K matrices, 54%
-    # of the step's bytes; gemv_kernel<FQ4K, 2, 1, true>, an instantiation no
-    # other launch of the step uses, so rocprof's per-kernel average covers
-    # exactly these launches)
+    # of the step's bytes; gemv_kernel<FQ4K, 2, 1, true, 0, 1>, an
+    # instantiation no other launch of the step uses, so rocprof's per-kernel
+    # average covers exactly these launches and C5's identical batch-1 ones)
     s = launches["gate_up"]
     achieved = s["weight_bytes"] / s["us_mean"] / 1e3
-    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 1, true> (C2 gate+up, 2 x 14336x4096 Q4_K)",
+    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 1, true, 0, 1> (C2 gate+up, 2 x 14336x4096 Q4_K)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
