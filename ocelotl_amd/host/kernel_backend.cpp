@@ -5,6 +5,7 @@
 
 #include <cstdio>
 #include <cstring>
+#include <limits>
 
 #include "okq.h"
 
@@ -223,6 +224,97 @@ Result<DeviceTensor> HipKernelBackend::dequantize(const QuantizedWeight &weight)
 }
 
 Result<void> HipKernelBackend::synchronize() const { return check(okq_sync(stream_)); }
+
+// ---- neighbours -------------------------------------------------------------------
+
+Result<void> HipKernelBackend::rmsnorm_d(const DeviceTensor &x, size_t rows, size_t hidden, const DeviceTensor &weight,
+                                         float epsilon, const DeviceTensor &out) const {
+  // rmsnorm.rs:81-114, in order
+  if (hidden == 0) return kernel_err("rmsnorm hidden dimension must be non-zero");
+  if (weight.len() != hidden)
+    return kernel_err("rmsnorm weight length " + std::to_string(weight.len()) + " does not match hidden " +
+                      std::to_string(hidden));
+  if (x.len() != rows * hidden)
+    return kernel_err("rmsnorm x slice length " + std::to_string(x.len()) + " does not match shape " +
+                      std::to_string(rows) + "x" + std::to_string(hidden));
+  if (out.len() != x.len())
+    return kernel_err("rmsnorm out slice length " + std::to_string(out.len()) + " does not match x length " +
+                      std::to_string(x.len()));
+  if (!(epsilon >= 0.0f) || epsilon == std::numeric_limits<float>::infinity()) {
+    char buf[128];
+    std::snprintf(buf, sizeof buf, "rmsnorm epsilon must be finite and non-negative, got %g", (double)epsilon);
+    return kernel_err(buf);
+  }
+  if (rows == 0) return {};
+  return check(okq_rmsnorm(x.device_ptr(), (int64_t)rows, (int64_t)hidden, weight.device_ptr(), epsilon,
+                           out.device_ptr(), stream_));
+}
+
+Result<void> HipKernelBackend::rmsnorm(const float *x, size_t x_len, size_t rows, size_t hidden, const float *weight,
+                                       size_t weight_len, float epsilon, float *out, size_t out_len) const {
+  auto xd = upload(x, x_len);
+  if (xd.is_err()) return xd.error();
+  auto wd = upload(weight, weight_len);
+  if (wd.is_err()) return wd.error();
+  auto od = alloc(out_len);
+  if (od.is_err()) return od.error();
+  Result<void> r = rmsnorm_d(xd.value(), rows, hidden, wd.value(), epsilon, od.value());
+  if (r.is_err()) return r;
+  auto host = od.value().to_host_owned();
+  if (host.is_err()) return host.error();
+  if (out_len) std::memcpy(out, host.value().data(), out_len * sizeof(float));
+  return {};
+}
+
+Result<void> HipKernelBackend::mlp_gated_silu_q(const DeviceTensor &x, size_t rows, size_t hidden,
+                                                size_t intermediate, const QuantizedWeight &gate,
+                                                const QuantizedWeight &up, const QuantizedWeight &down,
+                                                const DeviceTensor &gate_buf, const DeviceTensor &up_buf,
+                                                const DeviceTensor &out) const {
+  // mlp.rs:151-227: zero dimensions, then every length against its shape
+  if (rows == 0) return kernel_err("mlp_gated_silu seq_len must be non-zero");
+  if (hidden == 0) return kernel_err("mlp_gated_silu hidden must be non-zero");
+  if (intermediate == 0) return kernel_err("mlp_gated_silu intermediate must be non-zero");
+  const std::string hs = std::to_string(hidden), is = std::to_string(intermediate), rs = std::to_string(rows);
+  if (x.len() != rows * hidden)
+    return kernel_err("mlp_gated_silu x slice length " + std::to_string(x.len()) + " does not match shape " + rs +
+                      "x" + hs);
+  auto shape_err = [&](const char *name, const QuantizedWeight &w, size_t ne0, size_t ne1) {
+    return kernel_err(std::string("mlp_gated_silu ") + name + " shape [" + std::to_string(w.ne0()) + ", " +
+                      std::to_string(w.ne1()) + "] does not match [" + std::to_string(ne0) + ", " +
+                      std::to_string(ne1) + "]");
+  };
+  if (gate.ne0() != hidden || gate.ne1() != intermediate) return shape_err("gate_w", gate, hidden, intermediate);
+  if (up.ne0() != hidden || up.ne1() != intermediate) return shape_err("up_w", up, hidden, intermediate);
+  if (down.ne0() != intermediate || down.ne1() != hidden) return shape_err("down_w", down, intermediate, hidden);
+  if (gate_buf.len() != rows * intermediate)
+    return kernel_err("mlp_gated_silu gate_buf length " + std::to_string(gate_buf.len()) + " does not match shape " +
+                      rs + "x" + is);
+  if (up_buf.len() != rows * intermediate)
+    return kernel_err("mlp_gated_silu up_buf length " + std::to_string(up_buf.len()) + " does not match shape " +
+                      rs + "x" + is);
+  if (out.len() != rows * hidden)
+    return kernel_err("mlp_gated_silu out length " + std::to_string(out.len()) + " does not match shape " + rs + "x" +
+                      hs);
+  return check(okq_mlp_gated_silu_q(x.device_ptr(), (int64_t)rows, (int64_t)hidden, (int64_t)intermediate,
+                                    (uint32_t)gate.tensor_type(), gate.device_ptr(), gate.byte_len(),
+                                    (uint32_t)up.tensor_type(), up.device_ptr(), up.byte_len(),
+                                    (uint32_t)down.tensor_type(), down.device_ptr(), down.byte_len(),
+                                    gate_buf.device_ptr(), up_buf.device_ptr(), out.device_ptr(), stream_));
+}
+
+Result<DeviceTensor> HipKernelBackend::embedding_rows(const QuantizedWeight &table, const uint32_t *ids,
+                                                      size_t n) const {
+  auto a = device_alloc(n * table.ne0() * sizeof(float));
+  if (a.is_err()) return a.error();
+  DeviceTensor t(a.value(), n * table.ne0(), stream_);
+  Result<void> r = check(okq_get_rows_q((uint32_t)table.tensor_type(), table.device_ptr(), table.byte_len(),
+                                        (int64_t)table.ne0(), (int64_t)table.ne1(), ids, (int64_t)n, t.device_ptr(),
+                                        stream_),
+                         (uint32_t)table.tensor_type());
+  if (r.is_err()) return r.error();
+  return t;
+}
 
 Result<void> HipKernelBackend::linear_d(const DeviceTensor &x, size_t rows, size_t in_features,
                                         const QuantizedWeight &weight, size_t out_features, const DeviceTensor *bias,

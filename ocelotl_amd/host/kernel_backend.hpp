@@ -232,6 +232,26 @@ class HipKernelBackend final : public KernelBackend {
                                            size_t len) const;
   // The weight dequantized to f32 (bit-exact with the CPU definition).
   Result<DeviceTensor> dequantize(const QuantizedWeight &weight) const;
+
+  // KernelBackend::rmsnorm over host slices (lib.rs:139-147,
+  // rmsnorm.rs:73-128), and the same on device tensors.
+  Result<void> rmsnorm(const float *x, size_t x_len, size_t rows, size_t hidden, const float *weight,
+                       size_t weight_len, float epsilon, float *out, size_t out_len) const;
+  Result<void> rmsnorm_d(const DeviceTensor &x, size_t rows, size_t hidden, const DeviceTensor &weight,
+                         float epsilon, const DeviceTensor &out) const;
+  // KernelBackend::mlp_gated_silu (lib.rs:150-162, mlp.rs:139-250) with GGUF
+  // weights on device tensors: out = down(silu(gate(x)) * up(x)).  gate and
+  // up are [ne0 = hidden, ne1 = intermediate], down is [intermediate, hidden]
+  // (rows are output features).  gate_buf / up_buf are [rows, intermediate]
+  // scratch.
+  Result<void> mlp_gated_silu_q(const DeviceTensor &x, size_t rows, size_t hidden, size_t intermediate,
+                                const QuantizedWeight &gate, const QuantizedWeight &up, const QuantizedWeight &down,
+                                const DeviceTensor &gate_buf, const DeviceTensor &up_buf,
+                                const DeviceTensor &out) const;
+  // Token embedding lookup from a quantized [hidden, vocab] table: row ids[j]
+  // dequantized into row j of the result (the f32 row copy of
+  // qwen2_5/prefill.rs:95-105 for a GGUF table).
+  Result<DeviceTensor> embedding_rows(const QuantizedWeight &table, const uint32_t *ids, size_t n) const;
   // Waits for the backend's stream.
   Result<void> synchronize() const;
 

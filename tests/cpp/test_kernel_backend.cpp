@@ -25,6 +25,8 @@ int okr_linear_q(int type, int mode, int threads, const float *x, int64_t rows, 
                  int64_t out_f, const float *bias, float *out);
 int64_t okr_block_elems(int type);
 int64_t okr_block_bytes(int type);
+void okr_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float eps, float *out);
+void okr_swiglu(const float *gate, const float *up, int64_t n, float *out);
 }
 
 using namespace ocelotl;
@@ -250,6 +252,92 @@ void linear_d_one_hot_column_is_exact() {
   }
 }
 
+// ---- neighbours (rmsnorm, gated MLP, embedding rows) ---------------------------
+
+void rmsnorm_matches_the_reference_and_its_kats() {
+  HipKernelBackend be = ok(HipKernelBackend::create(0), "create");
+  // rmsnorm.rs:150-165: x = [1, 2, 3], unit weight, eps 1e-6
+  const float x3[3] = {1, 2, 3}, w3[3] = {1, 1, 1};
+  float o3[3] = {0, 0, 0};
+  ok(be.rmsnorm(x3, 3, 1, 3, w3, 3, 1e-6f, o3, 3), "rmsnorm kat");
+  const float want3[3] = {0.46291006f, 0.9258201f, 1.3887302f};
+  for (int i = 0; i < 3; ++i) CHECK(std::fabs(o3[i] - want3[i]) <= 1e-6f, "rmsnorm kat value");
+  const size_t rows = 5, hidden = 4096;
+  std::vector<float> x = normal(61, rows * hidden, 2.0f), w = normal(62, hidden, 1.0f), got(rows * hidden),
+                     want(rows * hidden);
+  ok(be.rmsnorm(x.data(), x.size(), rows, hidden, w.data(), w.size(), 1e-5f, got.data(), got.size()), "rmsnorm");
+  okr_rmsnorm(x.data(), (int64_t)rows, (int64_t)hidden, w.data(), 1e-5f, want.data());
+  assert_close(got, want, 1e-5, "rmsnorm vs reference order");
+  // validation before launch, with the reference's messages (rmsnorm.rs:81-114)
+  auto e1 = be.rmsnorm(x.data(), x.size(), rows, hidden, w.data(), w.size() - 1, 1e-5f, got.data(), got.size());
+  CHECK(e1.is_err() && e1.error().as_kernel()->message.find("weight length 4095 does not match hidden 4096") !=
+                           std::string::npos,
+        "weight length message");
+  auto e2 = be.rmsnorm(x.data(), x.size(), rows, hidden, w.data(), w.size(), -1.0f, got.data(), got.size());
+  CHECK(e2.is_err() && e2.error().as_kernel()->message.find("epsilon must be finite and non-negative") !=
+                           std::string::npos,
+        "epsilon message");
+}
+
+void mlp_gated_silu_q_matches_the_reference_chain() {
+  HipKernelBackend be = ok(HipKernelBackend::create(0), "create");
+  const size_t hidden = 1024, inter = 2816;
+  auto gq = quantize(GgmlTensorType::Q4K, normal(71, inter * hidden, 0.02f));
+  auto uq = quantize(GgmlTensorType::Q4K, normal(72, inter * hidden, 0.02f));
+  auto dq = quantize(GgmlTensorType::Q6K, normal(73, hidden * inter, 0.02f));
+  auto G = ok(be.upload_quantized(GgmlTensorType::Q4K, hidden, inter, gq.data(), gq.size()), "gate");
+  auto U = ok(be.upload_quantized(GgmlTensorType::Q4K, hidden, inter, uq.data(), uq.size()), "up");
+  auto D = ok(be.upload_quantized(GgmlTensorType::Q6K, inter, hidden, dq.data(), dq.size()), "down");
+  for (size_t rows : {1, 3, 12}) {  // fused decode row, multi-row GEMV, MFMA GEMM
+    std::vector<float> x = normal(74 + rows, rows * hidden, 1.0f);
+    auto xd = ok(be.upload(x.data(), x.size()), "x");
+    auto gb = ok(be.alloc(rows * inter), "gate_buf");
+    auto ub = ok(be.alloc(rows * inter), "up_buf");
+    auto od = ok(be.alloc(rows * hidden), "out");
+    ok(be.mlp_gated_silu_q(xd, rows, hidden, inter, G, U, D, gb, ub, od), "mlp");
+    std::vector<float> got = ok(od.to_host_owned(), "out host");
+    std::vector<float> gate = reference(GgmlTensorType::Q4K, x, rows, hidden, gq, inter, nullptr);
+    std::vector<float> up = reference(GgmlTensorType::Q4K, x, rows, hidden, uq, inter, nullptr);
+    std::vector<float> h(rows * inter);
+    okr_swiglu(gate.data(), up.data(), (int64_t)h.size(), h.data());
+    std::vector<float> want = reference(GgmlTensorType::Q6K, h, rows, inter, dq, hidden, nullptr);
+    // normwise over the chain: silu(gate) * up amplifies the projections'
+    // per-element differences (each projection alone meets the element rule)
+    double m = 0, e = 0;
+    for (size_t i = 0; i < want.size(); ++i) m = std::max(m, (double)std::fabs(want[i])), e = std::max(e, (double)std::fabs(got[i] - want[i]));
+    CHECK(e <= 1e-3 * m, "mlp chain normwise");
+    assert_close(ok(ub.to_host_owned(), "up host"), up, 1e-3, "up(x) in up_buf");
+  }
+  // zero rows is an error (mlp.rs:151-155), checked before launch
+  auto xd = ok(be.upload(std::vector<float>(hidden, 1.0f).data(), hidden), "x");
+  auto gb = ok(be.alloc(inter), "gb");
+  auto ub = ok(be.alloc(inter), "ub");
+  auto od = ok(be.alloc(hidden), "od");
+  auto r0 = be.mlp_gated_silu_q(xd, 0, hidden, inter, G, U, D, gb, ub, od);
+  CHECK(r0.is_err() && r0.error().as_kernel()->message == "mlp_gated_silu seq_len must be non-zero", "rows 0");
+  auto r1 = be.mlp_gated_silu_q(xd, 1, hidden, inter, G, D, D, gb, ub, od);
+  CHECK(r1.is_err() && r1.error().as_kernel()->message.find("up_w shape") != std::string::npos, "up shape");
+}
+
+void embedding_rows_are_the_dequantized_rows() {
+  HipKernelBackend be = ok(HipKernelBackend::create(0), "create");
+  const size_t hidden = 2560, vocab = 300;
+  for (GgmlTensorType t : kTypes) {
+    auto q = quantize(t, normal(81 + (int)t, hidden * vocab, 0.02f));
+    auto table = ok(be.upload_quantized(t, hidden, vocab, q.data(), q.size()), "table");
+    std::vector<float> all(hidden * vocab);
+    CHECK(okr_dequantize((int)t, q.data(), (int64_t)all.size(), all.data()) == 0, "oracle dequant");
+    const uint32_t ids[5] = {299, 0, 17, 17, 150};
+    std::vector<float> got = ok(ok(be.embedding_rows(table, ids, 5), "rows").to_host_owned(), "rows host");
+    for (size_t j = 0; j < 5; ++j)
+      CHECK(std::memcmp(got.data() + j * hidden, all.data() + ids[j] * hidden, hidden * sizeof(float)) == 0,
+            "row bits");
+    const uint32_t bad[1] = {300};
+    auto e = be.embedding_rows(table, bad, 1);
+    CHECK(e.is_err() && e.error().as_kernel()->message.find("out of range") != std::string::npos, "id range");
+  }
+}
+
 struct Test {
   const char *name;
   std::function<void()> fn;
@@ -273,7 +361,10 @@ int main(int argc, char **argv) {
              {"linear_d_rejects_mismatched_lengths_before_launch", linear_d_rejects_mismatched_lengths_before_launch},
              {"upload_quantized_validates_type_and_byte_length", upload_quantized_validates_type_and_byte_length},
              {"dequantize_is_bit_exact_with_the_cpu_definition", dequantize_is_bit_exact_with_the_cpu_definition},
-             {"linear_d_one_hot_column_is_exact", linear_d_one_hot_column_is_exact}};
+             {"linear_d_one_hot_column_is_exact", linear_d_one_hot_column_is_exact},
+             {"rmsnorm_matches_the_reference_and_its_kats", rmsnorm_matches_the_reference_and_its_kats},
+             {"mlp_gated_silu_q_matches_the_reference_chain", mlp_gated_silu_q_matches_the_reference_chain},
+             {"embedding_rows_are_the_dequantized_rows", embedding_rows_are_the_dequantized_rows}};
   } else {
     std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
     return 2;
