@@ -25,7 +25,11 @@
 //     and only then do the weight loads start.  Rows are swept step-major
 //     across the chip (one contiguous window of rows per step keeps the HBM
 //     channels evenly loaded); each wave keeps a ring of D rows in flight and
-//     computes a row as soon as it arrives.  Every load is unconditional:
+//     computes a row as soon as it arrives.  The SIMD arbiters favour older
+//     waves (a workgroup's youngest waves finished ~2.7 us after its oldest
+//     on the gate/up shape), so launches with more than a few rows per wave
+//     hand out all but each wave's first D rows from a workgroup counter in
+//     LDS, in the same step-major order.  Every load is unconditional:
 //     rows past the end address past the tensor and read zeros, because a
 //     branch around a load makes the compiler wait for all outstanding loads.
 //   * Weights are read with buffer loads against one descriptor spanning the
@@ -330,6 +334,7 @@ constexpr int kMaxXV = 4;        // float4s of x per thread, one-row launches (K
 constexpr int kMaxXVRows = 8;    // per thread and row, multi-row launches (K <= 8 * 4 * 512)
 constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
 constexpr int kMaxRowsPerLaunch = 4;
+constexpr int kDynSteps = 4;     // dynamic rows above this many steps per wave (one wave per row)
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 // One activation row keeps one XRec per lane in registers and 16 waves fit a
@@ -362,11 +367,19 @@ constexpr int gemv_max_threads() {
 // order, so all workgroups agree): kProRms is the RMSNorm of x with weight
 // P.a (crates/kernels/src/rmsnorm.rs:73-128), kProSwiGLU is silu(x) * P.a with
 // x = gate and P.a = up (crates/kernels/src/mlp.rs:77-88, :233-238).
-template <class F, int D, int XV, bool kMulti, int kPro, int R>
+//
+// kDyn (one wave per row, T == 1, and more than kDynSteps steps): each wave's
+// first D rows are static, the rest are handed out in the workgroup's
+// step-major order by an LDS counter, so the waves that the SIMD arbiters
+// favour take more rows and a workgroup's waves finish together.  Results
+// are the same bits as the static order's (every row is one wave's work).
+template <class F, int D, int XV, bool kMulti, int kPro, int R, bool kDyn>
 __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     const uint8_t *__restrict__ W, uint32_t w_bytes, const float *__restrict__ x, const float *__restrict__ bias,
     float *__restrict__ y, int N, int K, int T, int G, GemvMore M, GemvPro P, int nrows) {
   static_assert(kPro == kProNone || R == 1, "the neighbour prologues take one activation row");
+  // kDyn launches have T == 1 (one wave per row), checked by the launcher
+  __shared__ unsigned next_row;  // kDyn: the workgroup's next row index
   // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
   // waves (g >= G) that only help quantise x.
   extern __shared__ __align__(16) unsigned char smem[];
@@ -381,6 +394,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   const bool active = u < U && g < G;
   const uint32_t rb = (uint32_t)F::row_bytes(K);
   const uint32_t uoff = active ? F::unit_off(u) : 0u;
+  const uint32_t idle_mask = active ? 0u : 0xFFFFFFFFu;  // kDyn
   const int window = (int)gridDim.x * G;         // rows per step
   const int steps = (N + window - 1) / window;  // grid-uniform
   const int end = N;
@@ -417,14 +431,25 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   // without touching memory, so every load is unconditional.
   auto wload = [&](typename F::Regs &Rg, int row) {
     const int p = prob(row);
-    const uint32_t off = (active && row < end) ? (uint32_t)(row - first_row(p)) * rb + uoff : bytes_of(p);
+    uint32_t off;
+    if constexpr (kDyn) {  // no branch on the lane: idle lanes select the end arithmetically
+      const uint32_t endb = bytes_of(p);
+      const uint32_t in = row < end ? (uint32_t)(row - first_row(p)) * rb + uoff : endb;
+      off = in ^ ((in ^ endb) & idle_mask);
+    } else {
+      off = (active && row < end) ? (uint32_t)(row - first_row(p)) * rb + uoff : bytes_of(p);
+    }
     F::load(Rg, rsrc(p), off, lane);
   };
   // bias values are wave-uniform scalar loads, outside the vector-memory
-  // queue that the weight waits count
+  // queue that the weight waits count (the dynamic loop reads them through
+  // the constant address space: the bias is read-only for the launch, and
+  // otherwise the compiler cannot prove it and falls back to vector loads)
   auto bload = [&](int row) -> float {
+    typedef __attribute__((address_space(4))) const float ConstF;
     const int p = prob(row);
     const float *b = bias_of(p);
+    if constexpr (kDyn) return (b != nullptr && row < end) ? ((ConstF *)b)[row - first_row(p)] : 0.0f;
     return (b != nullptr && row < end) ? b[row - first_row(p)] : 0.0f;
   };
   auto store = [&](int row, int r, float v) {
@@ -505,6 +530,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   for (int r = 0; r < R; ++r)
 #pragma unroll
     for (int i = 0; i < XV; ++i) quant_group<F>(xv[r][i], tid + i * nt, nf, xr + r * U);
+  if (kDyn && tid == 0) next_row = (unsigned)(D * G);
   __syncthreads();
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
   XRec xreg[R];
@@ -560,6 +586,57 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
       if ((step + 1) % kChunk == 0) flush(step + 1);
     }
   };
+
+  if constexpr (kDyn) {
+    // Ring slot j holds row ring_row[j]; a wave's rows increase in slot
+    // order.  Idle lanes read zeros and hold zero activations, so the compute
+    // needs no branch on the lane (a divergent branch here, like an exit
+    // between slots, makes the compiler wait for every load in flight).  The
+    // loop runs while all D slots hold rows (the last slot has the largest);
+    // the drain consumes the rest without loads.
+    int ring_row[D];
+#pragma unroll
+    for (int j = 0; j < D; ++j) ring_row[j] = row_of(j);
+    auto consume = [&](int j) {
+      const int row = ring_row[j];
+      float acc[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = F::compute(S[j], xreg[r], lane);
+      float sum[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+      if (lane == 0 && row < end) {
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+          if (r < nrows) store(row, r, sum[r] + bs[j]);
+      }
+    };
+    const int nb = (int)gridDim.x, bi = (int)blockIdx.x;
+    while (ring_row[D - 1] < end) {
+#pragma unroll
+      for (int j = 0; j < D; ++j) {
+        unsigned c = 0;
+        if (lane == 0) {
+          // LDS add with return, written out so that the compiler sees no
+          // atomic (one makes it drop the scalar bias loads); the wait is
+          // part of the statement because the compiler cannot track it
+          const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned *)&next_row;
+          asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(addr), "v"(1u));
+        }
+        consume(j);
+        c = (unsigned)__builtin_amdgcn_readfirstlane((int)c);  // the c-th row of the workgroup, step-major
+        const int cs = (int)(c / (unsigned)G);
+        const int nrow = (cs * nb + bi) * G + (int)(c - (unsigned)cs * (unsigned)G);
+        ring_row[j] = nrow;
+        wload(S[j], nrow);
+        bs[j] = bload(nrow);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (ring_row[j] < end) consume(j);
+    return;
+  }
 
   // 4. stream: consume ring slot j, then refill it D steps ahead.  The loads
   //    stay unconditional (control flow around loads makes the compiler wait
@@ -646,25 +723,35 @@ struct GemvLaunch {
   GemvMore M;
   GemvPro P;
   int nrows;  // activation rows of this launch (<= R)
+  bool dyn;   // dynamic rows (T == 1 and more than kDynSteps steps)
 };
+
+// One instantiation: the dynamic-row kernel where the launch asks for it and
+// its shape is one the dynamic kernels are built for (one wave per row means
+// K <= 4096, so at most two float4s of x per thread, and the full ring).
+template <class F, int D, int XV, bool kMulti, int kPro, int R>
+void launch_kernel(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k,
+                   int T, int G) {
+  if constexpr (XV <= 2 && D == F::kMaxDepth) {
+    if (L.dyn && T == 1) {
+      launch_timed(gemv_kernel<F, D, XV, kMulti, kPro, R, true>, grid, block, (unsigned)lds, s, L.w, L.bytes, x,
+                   L.bias, L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
+      return;
+    }
+  }
+  launch_timed(gemv_kernel<F, D, XV, kMulti, kPro, R, false>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
+               L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
+}
 
 template <class F, int D, int XV, bool kMulti, int R>
 void launch_pro(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L, const float *x, int k, int T,
                 int G) {
   if constexpr (R == 1) {
-    if (L.P.kind == kProRms) {
-      launch_timed(gemv_kernel<F, D, XV, kMulti, kProRms, 1>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
-                   L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
-      return;
-    }
-    if (L.P.kind == kProSwiGLU) {
-      launch_timed(gemv_kernel<F, D, XV, kMulti, kProSwiGLU, 1>, grid, block, (unsigned)lds, s, L.w, L.bytes, x,
-                   L.bias, L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
-      return;
-    }
+    if (L.P.kind == kProRms) return launch_kernel<F, D, XV, kMulti, kProRms, 1>(grid, block, lds, s, L, x, k, T, G);
+    if (L.P.kind == kProSwiGLU)
+      return launch_kernel<F, D, XV, kMulti, kProSwiGLU, 1>(grid, block, lds, s, L, x, k, T, G);
   }
-  launch_timed(gemv_kernel<F, D, XV, kMulti, kProNone, R>, grid, block, (unsigned)lds, s, L.w, L.bytes, x, L.bias,
-               L.y, L.rows, k, T, G, L.M, L.P, L.nrows);
+  launch_kernel<F, D, XV, kMulti, kProNone, R>(grid, block, lds, s, L, x, k, T, G);
 }
 
 template <class F, int D, int XV, int R>
@@ -763,9 +850,12 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
   const size_t lds = (size_t)R * U * sizeof(XRec) + (T > 1 ? sizeof(float) * kPartChunk * G * T * R : 0) +
                      (P.P.kind == kProRms ? sizeof(float) * 16 : 0);
   const int k = (int)K, gg = (int)G;
-  if (type == kQ4_K) launch_rows<FQ4K>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
-  else if (type == kQ6_K) launch_rows<FQ6K>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
-  else launch_rows<FQ80>(R, xv, steps0, grid, block, lds, s, P, x, k, T, gg);
+  GemvLaunch L = P;
+  const int64_t steps = (N + blocks * G - 1) / (blocks * G);  // the kernel's own count
+  L.dyn = T == 1 && steps > kDynSteps;
+  if (type == kQ4_K) launch_rows<FQ4K>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
+  else if (type == kQ6_K) launch_rows<FQ6K>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
+  else launch_rows<FQ80>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
   return hipGetLastError();
 }
 

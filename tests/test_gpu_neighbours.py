@@ -159,6 +159,8 @@ RMS_LINEAR_CASES = [
     (O.Q4_K, 9, 2048, [512, 128]),           # batch: normalise, then the MFMA GEMM
     (O.Q6_K, 6, 1024, [64]),                 # batch on the per-row GEMV
     (O.Q8_0, 1, 96, [40]),                   # odd Q8_0 block count: generic GEMV after a normalised copy
+    (O.Q4_K, 1, 4096, [14336, 14336]),       # fused prologue with dynamic rows (gate/up shape)
+    (O.Q6_K, 1, 256, [20000]),
 ]
 
 

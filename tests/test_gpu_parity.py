@@ -132,11 +132,15 @@ def test_f32_to_bf16_matches_oracle(torch, okq, orc):
 # ---------------------------------------------------------------------------
 
 GEMV_SHAPES = {
-    # few rows with long K (teams of waves per row, x covered by extra teams) included
+    # few rows with long K (teams of waves per row, x covered by extra teams) included;
+    # (20000, 256) gives one wave per row and five steps per wave: rows past each
+    # wave's first ones come from the workgroup's counter
     O.Q4_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (3, 768), (64, 20480),
-             (300, 14336), (17, 8192), (2, 16384)],
-    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480), (33, 12288)],
-    O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480), (5, 14336)],
+             (300, 14336), (17, 8192), (2, 16384), (20000, 256)],
+    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480), (33, 12288),
+             (20000, 256)],
+    O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480), (5, 14336),
+             (20000, 256)],
 }
 CASES = [(t, n, k) for t in TYPES for (n, k) in GEMV_SHAPES[t]]
 
@@ -227,6 +231,8 @@ MULTIROW_CASES = [
     (O.Q4_K, 8, 512, 14336), (O.Q4_K, 4, 33, 8192),
     (O.Q6_K, 2, 1024, 4096), (O.Q6_K, 4, 4096, 14336), (O.Q6_K, 7, 300, 12288),
     (O.Q8_0, 3, 4096, 4096), (O.Q8_0, 4, 17, 16384), (O.Q8_0, 5, 300, 96),
+    # dynamic rows in both the batched and the one-row launches
+    (O.Q8_0, 2, 20000, 256), (O.Q6_K, 3, 20000, 512),
 ]
 
 
@@ -327,7 +333,7 @@ def test_gemv_run_max_at_the_limb_boundary(torch, okq, orc, t):
 
 MULTI_CASES = [
     (O.Q4_K, 1, 4096, [4096, 1024, 1024]),   # q/k/v of a Llama-3-8B layer
-    (O.Q4_K, 1, 4096, [14336, 14336]),       # gate/up
+    (O.Q4_K, 1, 4096, [14336, 14336]),       # gate/up: dynamic rows, the single launches are static
     (O.Q4_K, 3, 14336, [300, 17]),           # K > 4096: teams of waves
     (O.Q6_K, 2, 1024, [33, 300, 5, 64]),
     (O.Q8_0, 1, 4096, [1024, 4096]),
