@@ -568,6 +568,220 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
   }
 }
 
+// ---------------------------------------------------------------------------
+// decode batches (2 <= M <= 16): a streaming kernel with MFMA contraction
+// ---------------------------------------------------------------------------
+// At most 16 activation rows: every weight meets one 16-row MFMA tile, so the
+// weights are dequantised by the lane that loads them straight into MFMA B
+// fragments (no LDS staging, no reuse to gain), and the kernel is organised
+// like the GEMV: a workgroup stages its K-slice of the activations (the
+// pre-pass planes) in LDS once, then every wave streams a sequence of items
+// (16-column tile, super-block) through a ring of D register sets with no
+// further barrier.  Operands and scaling are those of gemm_kq_kernel (exact
+// fp16 products, per-super-block f32 scaling by d and dmin).
+//
+// MFMA v_mfma_f32_16x16x32_f16: lane l holds A[l % 16][8 (l / 16) + 0..7],
+// B[8 (l / 16) + 0..7][l % 16] and D[4 (l / 16) + 0..3][l % 16].  K order
+// inside a super-block: slice t (8 per super-block) and lane group g = l / 16
+// cover k = 64g + 32(t & 1) + 8(t >> 1) + [0, 8), i.e. nibble plane t & 1 of
+// bytes 8(t >> 1) .. + 8 of qs chunk g -- a lane group reads only its own
+// 32-byte chunk (and the header) of each block.
+// Q4_K (scale, min) of sub-block j (any lane-dependent j < 8) without
+// branches: for j < 4 both are 6-bit fields of bytes 0-7; for j >= 4 a 4-bit
+// field of bytes 8-11 plus two high bits from bytes 0-7 (GGUF layout).
+__device__ __forceinline__ void q4k_scale_min_sel(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                                  uint32_t &m) {
+  const bool lowj = j < 4;
+  const uint32_t jj = j & 3u;
+  const uint32_t width = lowj ? 6u : 4u, himask = lowj ? 0u : 0x30u, mo = lowj ? 0u : 4u;
+  sc = __builtin_amdgcn_ubfe(lowj ? s0 : s2, 8 * jj, width) | ((__builtin_amdgcn_ubfe(s0, 8 * jj + 6, 2) << 4) & himask);
+  m = __builtin_amdgcn_ubfe(lowj ? s1 : s2, 8 * jj + mo, width) | ((__builtin_amdgcn_ubfe(s1, 8 * jj + 6, 2) << 4) & himask);
+}
+
+constexpr int kDecRows = 16;
+constexpr int kDecWaves = 16;
+constexpr int64_t kDecLdsBytes = 72 * 1024;  // activations of a slice, per workgroup
+constexpr int kDecStage = 4;                // 16-byte activation pieces per thread (of 1024)
+constexpr int kDecMaxTiles = 4;             // unsplit K: column tiles per wave (bias staged in LDS)
+
+template <bool kLo, int D>
+__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
+    const _Float16 *__restrict__ xhi, const _Float16 *__restrict__ xlo, const h2 *__restrict__ xsum,
+    const float *__restrict__ rscale, const uint8_t *__restrict__ W, const float *__restrict__ bias,
+    float *__restrict__ Y, int M, int N, int K, int ksplit, int groups, float *__restrict__ part) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  extern __shared__ __align__(16) unsigned char dsm[];
+  const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int z = (int)blockIdx.x % ksplit, grp = (int)blockIdx.x / ksplit;
+  const int nsb_all = K / 256;
+  const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
+  const int nsbs = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;
+  const int Ks = nsbs * 256, P = Ks + 8;  // slice width, LDS row pitch (halves)
+  // LDS: Ah [M + 1][P], Al [M + 1][P] (kLo), xs [M + 1][nsbs][16]; row M is zeros
+  _Float16 *Ah = reinterpret_cast<_Float16 *>(dsm);
+  _Float16 *Al = Ah + (size_t)(M + 1) * P;
+  _Float16 *Xs = Ah + (size_t)(M + 1) * P * (kLo ? 2 : 1);
+  // unsplit K: the bias of the workgroup's columns (tile ti of every wave:
+  // columns (ti * groups + grp) * 256 + [0, 256)) and the row scales
+  float *Bs = reinterpret_cast<float *>(Xs + (size_t)(M + 1) * nsbs * 16);  // [kDecMaxTiles][256]
+  float *Rs = Bs + kDecMaxTiles * 256;                                      // [16]
+
+  // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
+  //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
+  const int ntiles = (N + 15) / 16;
+  const int stride = groups * kDecWaves;
+  const int first = grp * kDecWaves + wave;
+  const int mytiles = first < ntiles ? (ntiles - first + stride - 1) / stride : 0;
+  const int nitems = mytiles * nsbs;
+  const int cn = lane & 15, g = lane >> 4;
+  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
+  const uint32_t w_end = (uint32_t)((size_t)N * row_bytes);
+  const Rsrc rs_w = make_rsrc(W, w_end);
+  const int arow = (lane & 15) < M ? (lane & 15) : M;  // A row (the zero row past M)
+
+  struct Item {
+    u32x4 hd, q0, q1;
+  };
+  auto tile_of = [&](int u) { return (u / nsbs) * stride + first; };
+  auto load = [&](Item &it, int u) {
+    const int sbl = u - (u / nsbs) * nsbs;
+    const int tile = tile_of(u);
+    const uint32_t n = (uint32_t)(tile * 16 + cn);  // rows >= N read past the tensor: zeros
+    const uint32_t blk = tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * kQ4KBytes : w_end;
+    it.hd = bload4(rs_w, blk);
+    it.q0 = bload4(rs_w, blk + 16u + 32u * (uint32_t)g);
+    it.q1 = bload4(rs_w, blk + 32u + 32u * (uint32_t)g);
+  };
+  // 2. the activations of the slice: this thread's 16-byte pieces (at most
+  //    kDecStage; pieces past the rows read past the planes: zeros) and xsum
+  //    piece are loaded first, then the first D items' weights, then the
+  //    pieces go to LDS -- the vector-memory counter completes in order, so
+  //    the LDS writes wait for the activations only and the weights stay in
+  //    flight across the barrier.  Row M of the LDS planes is zeros.
+  const int pr = Ks / 8;  // pieces per row
+  const uint32_t plane_end = (uint32_t)((size_t)M * K * 2);
+  const Rsrc rs_xh = make_rsrc(xhi, plane_end);
+  const Rsrc rs_xl = make_rsrc(kLo ? xlo : xhi, plane_end);
+  const Rsrc rs_xs = make_rsrc(xsum, (uint32_t)((size_t)M * (K / 32) * 4));
+  u32x4 sh[kDecStage], sl[kLo ? kDecStage : 1];
+#pragma unroll
+  for (int i = 0; i < kDecStage; ++i) {
+    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
+    const uint32_t off = r < M ? ((uint32_t)r * (uint32_t)K + (uint32_t)sb0 * 256u + 8u * (uint32_t)c) * 2u : plane_end;
+    sh[i] = bload4(rs_xh, off);
+    if (kLo) sl[i] = bload4(rs_xl, off);
+  }
+  const int xr = tid / (nsbs * 2), xrest = tid - xr * (nsbs * 2);  // 16 B = 4 (hi, lo) xsum pairs
+  const u32x4 sx = bload4(rs_xs, xr < M ? ((uint32_t)xr * (uint32_t)(K / 32) + (uint32_t)sb0 * 8u + 4u * (uint32_t)xrest) * 4u
+                                         : (uint32_t)((size_t)M * (K / 32) * 4));
+  // bias of the workgroup's columns and the row scales (unsplit K only)
+  const int bt = tid >> 8, bcol = ((bt * groups + grp) * kDecWaves) * 16 + (tid & 255);
+  const uint32_t bias_end = bias ? (uint32_t)N * 4u : 0u;
+  const uint32_t bbits = __builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(bias, bias_end), (ksplit == 1 && bt < kDecMaxTiles && bcol < N) ? (uint32_t)bcol * 4u : bias_end, 0, 0);
+  const uint32_t rbits = __builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(rscale, (uint32_t)M * 4u), tid < M ? (uint32_t)tid * 4u : (uint32_t)M * 4u, 0, 0);
+  Item S[D];
+#pragma unroll
+  for (int j = 0; j < D; ++j) load(S[j], j);
+  if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
+  if (tid < 16) Rs[tid] = __uint_as_float(rbits);
+#pragma unroll
+  for (int i = 0; i < kDecStage; ++i) {
+    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
+    if (r <= M) {
+      *reinterpret_cast<u32x4 *>(Ah + (size_t)r * P + 8 * c) = sh[i];
+      if (kLo) *reinterpret_cast<u32x4 *>(Al + (size_t)r * P + 8 * c) = sl[i];
+    }
+  }
+  if (xr <= M) *reinterpret_cast<u32x4 *>(Xs + ((size_t)xr * nsbs) * 16 + 8 * xrest) = sx;
+  __syncthreads();
+
+  const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+  f4 acc = zero4;
+  // outputs: range-checked buffer stores (out-of-range lanes are dropped by
+  // the hardware, so no branch surrounds them), scale and bias from LDS
+  const uint32_t out_end = (uint32_t)((size_t)(ksplit > 1 ? (size_t)ksplit * M : (size_t)M) * N * 4);
+  const Rsrc rs_out = make_rsrc(ksplit > 1 ? (void *)part : (void *)Y, out_end);
+  auto consume = [&](const Item &it, int u) {
+    const int ti = u / nsbs, sbl = u - ti * nsbs;
+    // scales of the lane group's sub-blocks 2g, 2g + 1; mins of 4g .. 4g + 3
+    // for the min-term MFMA (groups 2, 3 contribute zeros there)
+    h2 scv[2], offv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel(2u * (uint32_t)g + (uint32_t)j, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 sh = (_Float16)(float)sc, oh = (_Float16)(-1024.0f * (float)sc);
+      scv[j] = h2{sh, sh};
+      offv[j] = h2{oh, oh};
+    }
+    h8 mb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel((4u * (uint32_t)g + (uint32_t)j) & 7u, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 mh = g < 2 ? (_Float16)(float)mv : (_Float16)0.0f;
+      mb[2 * j] = mh;
+      mb[2 * j + 1] = mh;
+    }
+    const _Float16 *ar = Ah + (size_t)arow * P + sbl * 256 + 64 * g;
+    const _Float16 *arl = Al + (size_t)arow * P + sbl * 256 + 64 * g;
+    f4 accs = zero4;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int nib = t & 1, p8 = t >> 1;
+      const u32x4 pc = (p8 >> 1) ? it.q1 : it.q0;
+      const uint32_t d0 = (p8 & 1) ? pc.z : pc.x, d1 = (p8 & 1) ? pc.w : pc.y;
+      const uint32_t n0v = nib ? (d0 >> 4) & 0x0F0F0F0Fu : d0 & 0x0F0F0F0Fu;
+      const uint32_t n1v = nib ? (d1 >> 4) & 0x0F0F0F0Fu : d1 & 0x0F0F0F0Fu;
+      h2 p0, p1, p2, p3;
+      nib4(n0v, scv[nib], offv[nib], p0, p1);
+      nib4(n1v, scv[nib], offv[nib], p2, p3);
+      const h8 bv = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      const h8 ah = *reinterpret_cast<const h8 *>(ar + 32 * nib + 8 * p8);
+      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, accs, 0, 0, 0);
+      if (kLo) {
+        const h8 al = *reinterpret_cast<const h8 *>(arl + 32 * nib + 8 * p8);
+        accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, accs, 0, 0, 0);
+      }
+    }
+    const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(Xs + ((size_t)arow * nsbs + sbl) * 16 + 8 * g) : h8{};
+    const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
+    const float dv = f16_bits_hw(it.hd.x & 0xffffu), dm = -f16_bits_hw(it.hd.x >> 16);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) acc[v] = fmaf(dm, mins[v], fmaf(dv, accs[v], acc[v]));
+    if (sbl == nsbs - 1) {  // the tile's last super-block: write it out
+      const int col = (ti * stride + first) * 16 + cn;
+      const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 4 * g + v;
+        const float val = ksplit > 1 ? acc[v] : acc[v] * Rs[row] + bv;
+        const uint32_t off = (row < M && col < N) ? (uint32_t)(((size_t)z * M + row) * N + col) * 4u : out_end;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
+      }
+      acc = zero4;
+    }
+  };
+
+  // 3. the ring: consume slot j, refill it D items ahead; loads stay
+  //    unconditional (items past the end read past the tensor: zeros).  The
+  //    staging barrier above waits for LDS only, not for these loads.
+  int u0 = 0;
+  for (; u0 + D < nitems; u0 += D) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      consume(S[j], u0 + j);
+      load(S[j], u0 + j + D);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < D; ++j)
+    if (u0 + j < nitems) consume(S[j], u0 + j);
+}
+
 // Sum of the split-K partials in slice order (deterministic), then the row
 // scale and the bias: Y[m, n] = (sum_z P[z][m, n]) * rscale[m] + bias[n].
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int ksplit, int M, int N,
@@ -595,17 +809,42 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
 
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
+  p.dec_wgs_per_cu = 1;
   // Q4_K, bf16 activations, M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
   // 64); otherwise 128 x 128 tiles (f32 activations need the second fp16
   // plane, which only fits the LDS budget at 128 rows; Q6_K stages its
   // larger raw windows in the 4-wave tile's register budget).
-  p.bm = (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
-  const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
-  // Split K when the tiles alone leave CUs idle: enough slices for about one
-  // workgroup per CU, at least two super-blocks per slice, at most 8.
   const int64_t nsb = K / 256;
   int64_t ks = 1;
-  if (tiles * 4 < (int64_t)cu_count * 3) ks = std::min<int64_t>({(cu_count + tiles - 1) / tiles, nsb / 2, 8});
+  if (type == kQ4_K && M <= kDecRows) {
+    // decode batch: the streaming kernel.  K slices small enough for the
+    // activations to fit the LDS budget (2 * (M + 1) planes of the slice plus
+    // sums), and at least enough slices x column groups for every CU.
+    p.bm = kDecRows;
+    const int64_t per_sb = (int64_t)(M + 1) * 256 * 2 * (x_is_bf16 ? 1 : 2) + (int64_t)(M + 1) * 32;
+    // slice bounds: the LDS budget, kDecStage pieces per thread ((M + 1) rows
+    // of 32 pieces per super-block) and one xsum piece per thread
+    const int64_t max_sb = std::max<int64_t>(
+        1, std::min<int64_t>({(kDecLdsBytes - (int64_t)(M + 1) * 16 * 2 * 2) / per_sb,
+                              (int64_t)kDecStage * kDecWaves * 64 / ((M + 1) * 32), (int64_t)kDecWaves * 64 / ((M + 1) * 2)}));
+    const int64_t ntiles = (N + 15) / 16;
+    // one workgroup (16 waves) per CU: column groups of 16 tiles, at most one
+    // per CU (waves then take several tiles), and as many K slices as fit in
+    // one round of workgroups (at least what the LDS budget needs)
+    p.groups = (int)std::min<int64_t>((ntiles + kDecWaves - 1) / kDecWaves, cu_count);
+    const int64_t ks_lds = (nsb + max_sb - 1) / max_sb;
+    ks = std::min<int64_t>(nsb, std::max<int64_t>(ks_lds, cu_count / p.groups));
+    // unsplit K writes the final outputs with the bias staged for at most
+    // kDecMaxTiles tiles per wave; wider problems take the split path
+    const int64_t mytiles = (ntiles + (int64_t)p.groups * kDecWaves - 1) / ((int64_t)p.groups * kDecWaves);
+    if (ks == 1 && mytiles > kDecMaxTiles) ks = std::min<int64_t>(2, nsb);
+  } else {
+    p.bm = (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
+    const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
+    // Split K when the tiles alone leave CUs idle: enough slices for about
+    // one workgroup per CU, at least two super-blocks per slice, at most 8.
+    if (tiles * 4 < (int64_t)cu_count * 3) ks = std::min<int64_t>({(cu_count + tiles - 1) / tiles, nsb / 2, 8});
+  }
   p.ksplit = (int)std::max<int64_t>(1, ks);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
@@ -638,6 +877,19 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   if (e != hipSuccess) return e;
   const uint8_t *W = static_cast<const uint8_t *>(w);
   const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
+  if (plan.bm == kDecRows) {
+    if (type != kQ4_K || M > kDecRows) return hipErrorInvalidValue;
+    const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
+    const size_t lds = (size_t)(M + 1) * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) +
+                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 16) * sizeof(float);
+    const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
+    if (x_is_bf16)
+      launch_timed(gemm_decode_q4k_kernel<false, 3>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias,
+                   y, m, n, k, ks, plan.groups, part);
+    else
+      launch_timed(gemm_decode_q4k_kernel<true, 3>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias, y,
+                   m, n, k, ks, plan.groups, part);
+  } else {
   const int tiles_n = (int)((N + kBN - 1) / kBN);
   const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);
   const int tiles = tiles_m * tiles_n;
@@ -657,6 +909,7 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     OKQ_GEMM(128, true, kQ4_K);
   }
 #undef OKQ_GEMM
+  }
   e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   const int64_t total = M * N;

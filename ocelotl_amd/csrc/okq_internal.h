@@ -78,7 +78,9 @@ hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *o
 // the workspace layout (activation planes, per-32 sums, row scales, split-K
 // partials), 256-byte aligned offsets from the workspace base.
 struct GemmPlan {
-  int bm;
+  int bm;              // 16: the decode-batch kernel (M <= 16), else the tile height
+  int groups;          // decode-batch kernel: column groups per K slice
+  int dec_wgs_per_cu;  // decode-batch kernel: workgroups per CU aimed for
   int ksplit;
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };

@@ -217,11 +217,19 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
 
 enum class Path { Auto, Gemv, Gemm };
 
-// Rows at or below this count run the GEMV (each pass over the weights serves
-// up to four rows); above it the MFMA GEMM reuses each dequantised tile
-// across the rows.  Measured on the 32-layer Q4_K_M sweep: two four-row GEMV
-// passes beat the GEMM at 8 rows.
+// Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
+// serves up to four rows); above it the MFMA GEMM path (which takes the
+// streaming decode-batch kernel up to 16 rows of Q4_K, the tiled kernel
+// beyond).  Q4_K from kDecMinRows rows on also takes the decode-batch kernel:
+// it streams the weights once where the GEMV needs two passes (measured at 8
+// rows: gate 21 vs 28 us, down 26 vs 45 us; at 4 rows the one-pass GEMV wins).
 constexpr int64_t kGemvMaxRows = 8;
+constexpr int64_t kDecMinRows = 5;
+
+bool gemv_serves(uint32_t type, int64_t rows) {
+  if (rows > kGemvMaxRows) return false;
+  return !(type == OKQ_TYPE_Q4_K && rows >= kDecMinRows);
+}
 
 okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint32_t type, const void *w,
                        uint64_t w_bytes, int64_t N, const float *bias, float *out, void *stream, Path path) {
@@ -241,7 +249,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
                   (long long)K, (long long)N);
     use_gemm = true;
   } else if (path == Path::Auto) {
-    use_gemm = rows > kGemvMaxRows && okq::gemm_supported((int)type, rows, K, N);
+    use_gemm = !gemv_serves(type, rows) && okq::gemm_supported((int)type, rows, K, N);
   }
   if (use_gemm) {
     void *ws = nullptr;
@@ -583,7 +591,7 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   okq_status st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool decode = rows <= kGemvMaxRows;
+  const bool decode = gemv_serves(gate_type, rows);
   // gate and up: one grouped pass over both weights when they share a format
   if (decode && gate_type == up_type && okq::gemv_streams((int)gate_type, hidden, gate_w, intermediate) &&
       okq::gemv_streams((int)up_type, hidden, up_w, intermediate)) {

@@ -83,16 +83,17 @@ def test_gemm_bf16_q4k_c4_shapes_sampled_rows(torch, okq, orc, rows, n, k):
     check_rows(orc, O.Q4_K, got, x32, rows, k, wq, n, None, 24)
 
 
-@pytest.mark.parametrize("rows,n,k", [(8, 64, 256), (32, 520, 1024), (64, 4096, 4096)])
+@pytest.mark.parametrize("rows,n,k", [(4, 64, 256), (8, 64, 256), (12, 300, 1024), (32, 520, 1024),
+                                      (64, 4096, 4096)])
 def test_gemm_f32_q4k_matches_reference(torch, okq, orc, rows, n, k):
     wq = orc.quantize(O.Q4_K, orc.normal(900 + n, n * k, 0.02))
     x = orc.normal(901 + rows, rows * k, 1.0)
     got = run(torch, okq, "okq_gemm", O.Q4_K, x, rows, k, wq, n)
     check_rows(orc, O.Q4_K, got, x, rows, k, wq, n, None, None)
-    # the automatic path picks the GEMM above 8 rows (the GEMV up to 8) and
-    # agrees with the pinned path bit for bit
+    # the automatic path picks the MFMA path from 5 rows of Q4_K on (the
+    # GEMV below) and agrees with the pinned path bit for bit
     auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q4_K, x, rows, k, wq, n)
-    pinned = got if rows > 8 else run(torch, okq, "okq_gemv", O.Q4_K, x, rows, k, wq, n)
+    pinned = got if rows >= 5 else run(torch, okq, "okq_gemv", O.Q4_K, x, rows, k, wq, n)
     assert (auto.view(np.uint32) == pinned.view(np.uint32)).all()
 
 
@@ -110,15 +111,51 @@ def test_gemm_one_hot_columns_are_exact(torch, okq, orc):
 
 
 def test_gemm_is_deterministic_and_row_independent(torch, okq, orc):
+    """Same inputs, same bits; and a row's result does not depend on the
+    other rows of its batch within a kernel family: the tiled kernel (more
+    than 16 rows) and the decode-batch kernel (up to 16 rows of Q4_K) each
+    sum a row's products in one fixed order (the two families' orders differ,
+    so across the 16-row boundary results agree within the rule only)."""
     rows, n, k = 300, 384, 2048
     wq = orc.quantize(O.Q4_K, orc.normal(88, n * k, 0.02))
-    xb, _ = bf16_inputs(orc, 89, rows, k)
+    xb, x32 = bf16_inputs(orc, 89, rows, k)
     a = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb, rows, k, wq, n)
     b = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb, rows, k, wq, n)
     assert (a.view(np.uint32) == b.view(np.uint32)).all()
-    # a row computed alone equals the same row inside the big batch
+    # tiled: rows 100..163 on their own equal the same rows of the big batch
+    sub = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb.reshape(rows, k)[100:164].reshape(-1), 64, k, wq, n)
+    assert (sub.view(np.uint32) == a[100:164].view(np.uint32)).all()
+    # decode-batch kernel: a row alone equals the same row among 12
+    few = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb.reshape(rows, k)[130:142].reshape(-1), 12, k, wq, n)
     one = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb.reshape(rows, k)[137:138].reshape(-1), 1, k, wq, n)
-    assert (one[0].view(np.uint32) == a[137].view(np.uint32)).all()
+    assert (one[0].view(np.uint32) == few[7].view(np.uint32)).all()
+    check_rows(orc, O.Q4_K, few, x32.reshape(rows, k)[130:142].reshape(-1), 12, k, wq, n, None, None)
+
+
+# ---- Q4_K decode batches (up to 16 rows: one MFMA tile of rows, weights
+# dequantised into B fragments by the lanes that load them) ---------------------
+DEC_CASES = [
+    # (entry, rows, n, k): ragged N, every row count class, split and unsplit K
+    ("okq_gemm", 1, 96, 256), ("okq_gemm", 2, 17, 512), ("okq_gemm", 5, 300, 1024),
+    ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1000, 768), ("okq_gemm", 13, 4096, 14336),
+    ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm_bf16", 16, 520, 2048), ("okq_gemm_bf16", 7, 33, 256),
+    # one super-block per row: K is never split, outputs and bias written directly
+    ("okq_gemm", 3, 70001, 256), ("okq_gemm_bf16", 9, 65540, 256),
+]
+
+
+@pytest.mark.parametrize("entry,rows,n,k", DEC_CASES)
+def test_gemm_decode_batch_q4k_matches_reference(torch, okq, orc, entry, rows, n, k):
+    print(f"[gpu] gemm decode-batch {entry} Q4_K M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q4_K, orc.normal(1500 + n + k, n * k, 0.02))
+    bias = orc.normal(1501 + rows, n, 0.1)
+    if entry == "okq_gemm_bf16":
+        xin, x32 = bf16_inputs(orc, 1502 + rows, rows, k)
+    else:
+        xin = x32 = orc.normal(1502 + rows, rows * k, 1.0)
+    got = run(torch, okq, entry, O.Q4_K, xin, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q4_K, got, x32, rows, k, wq, n, bias, None if n * k <= 20_000_000 else 6)
 
 
 def q4k_parts(orc, wq, n, k):
