@@ -44,6 +44,7 @@ typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 typedef float f16x __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 // Buffer descriptor over [base, base + bytes), bytes < 2^32.  Loads past the
@@ -598,18 +599,186 @@ __device__ __forceinline__ void q4k_scale_min_sel(uint32_t j, uint32_t s0, uint3
   m = __builtin_amdgcn_ubfe(lowj ? s1 : s2, 8 * jj + mo, width) | ((__builtin_amdgcn_ubfe(s1, 8 * jj + 6, 2) << 4) & himask);
 }
 
-constexpr int kDecRows = 16;
+constexpr int kDecRows = 32;  // two 16-row MFMA groups share each B fragment above 16 rows
 constexpr int kDecWaves = 16;
-constexpr int64_t kDecLdsBytes = 72 * 1024;  // activations of a slice, per workgroup
+constexpr int64_t kDecLdsBytes = 144 * 1024;  // activations of a slice (one workgroup per CU fills its registers)
 constexpr int kDecStage = 4;                // 16-byte activation pieces per thread (of 1024)
 constexpr int kDecMaxTiles = 4;             // unsplit K: column tiles per wave (bias staged in LDS)
 
-template <bool kLo, int D>
-__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
+typedef float f4 __attribute__((ext_vector_type(4)));
+
+// Per-format parts of the decode kernel: the registers of one item (one
+// super-block of one 16-column tile, as seen by one lane), their loads, and
+// the contraction of one super-block into the lane's 4 accumulators.
+// `ar`/`arl` point at the lane's A row (hi/lo planes) at the super-block's
+// first activation, `xs` at the row's xsum pairs of the super-block.
+struct DecQ4K {
+  static constexpr uint32_t kBlk = kQ4KBytes;
+  static constexpr int kDepth = 3;
+  struct Item {
+    u32x4 hd, q0, q1;
+  };
+  // lane group g reads the header and qs chunk g (bytes 32g .. 32g + 31)
+  __device__ static void load(Item &it, Rsrc rs, uint32_t blk, int g) {
+    it.hd = bload4(rs, blk);
+    it.q0 = bload4(rs, blk + 16u + 32u * (uint32_t)g);
+    it.q1 = bload4(rs, blk + 32u + 32u * (uint32_t)g);
+  }
+  // slice t: k = 64g + 32(t & 1) + 8(t >> 1) + [0, 8) (nibble plane t & 1 of
+  // bytes 8(t >> 1) .. of chunk g); the min term is one more MFMA on
+  // (xsum hi, xsum lo) x m (lane groups 2, 3 contribute zeros)
+  template <bool kLo, int RG>
+  __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
+                                  const _Float16 *const *xs, int g, f4 *acc) {
+    const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    h2 scv[2], offv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel(2u * (uint32_t)g + (uint32_t)j, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 sh = (_Float16)(float)sc, oh = (_Float16)(-1024.0f * (float)sc);
+      scv[j] = h2{sh, sh};
+      offv[j] = h2{oh, oh};
+    }
+    h8 mb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel((4u * (uint32_t)g + (uint32_t)j) & 7u, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 mh = g < 2 ? (_Float16)(float)mv : (_Float16)0.0f;
+      mb[2 * j] = mh;
+      mb[2 * j + 1] = mh;
+    }
+    f4 accs[RG];
+#pragma unroll
+    for (int q = 0; q < RG; ++q) accs[q] = zero4;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int nib = t & 1, p8 = t >> 1;
+      const u32x4 pc = (p8 >> 1) ? it.q1 : it.q0;
+      const uint32_t d0 = (p8 & 1) ? pc.z : pc.x, d1 = (p8 & 1) ? pc.w : pc.y;
+      const uint32_t n0v = nib ? (d0 >> 4) & 0x0F0F0F0Fu : d0 & 0x0F0F0F0Fu;
+      const uint32_t n1v = nib ? (d1 >> 4) & 0x0F0F0F0Fu : d1 & 0x0F0F0F0Fu;
+      h2 p0, p1, p2, p3;
+      nib4(n0v, scv[nib], offv[nib], p0, p1);
+      nib4(n1v, scv[nib], offv[nib], p2, p3);
+      const h8 bv = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      const int ka = 64 * g + 32 * nib + 8 * p8;
+#pragma unroll
+      for (int q = 0; q < RG; ++q) {
+        const h8 ah = *reinterpret_cast<const h8 *>(ar[q] + ka);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, accs[q], 0, 0, 0);
+        if (kLo) {
+          const h8 al = *reinterpret_cast<const h8 *>(arl[q] + ka);
+          accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, accs[q], 0, 0, 0);
+        }
+      }
+    }
+    const float dv = f16_bits_hw(it.hd.x & 0xffffu), dm = -f16_bits_hw(it.hd.x >> 16);
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(xs[q] + 8 * g) : h8{};
+      const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dm, mins[v], fmaf(dv, accs[q][v], acc[q][v]));
+    }
+  }
+};
+
+struct DecQ6K {
+  static constexpr uint32_t kBlk = kQ6KBytes;
+  static constexpr int kDepth = 2;
+  // Slice t = (half hh = t >> 2, quarter qq = t & 3); lane group g covers
+  // l = 8g .. 8g + 7 of it: k = 128hh + 32qq + 8g + [0, 8), i.e. ql bytes
+  // 64hh + 32(qq & 1) + 8g .. (nibble qq >> 1), qh bytes 128 + 32hh + 8g ..
+  // (bits 2qq), scale byte 8hh + 2qq + (g >> 1).  Blocks are 2-byte aligned:
+  // each 8-byte field is read as a 3-dword window from the dword below it
+  // and realigned by r = block & 3; d with a 2-byte load (a dword around it
+  // could end past the tensor, where the range check zeroes it).
+  struct Item {
+    u32x3 ql[4], qh[2];  // ql: (hh, qq & 1) = (0,0) (0,1) (1,0) (1,1)
+    u32x4 sc4;
+    uint32_t sc1, dw, r;
+  };
+  __device__ static void load(Item &it, Rsrc rs, uint32_t blk, int g) {
+    const uint32_t r = blk & 3u, a = blk - r;
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+      it.ql[p] = __builtin_amdgcn_raw_buffer_load_b96(rs, a + 64u * (uint32_t)(p >> 1) + 32u * (uint32_t)(p & 1) + 8u * (uint32_t)g, 0, 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      it.qh[h] = __builtin_amdgcn_raw_buffer_load_b96(rs, a + 128u + 32u * (uint32_t)h + 8u * (uint32_t)g, 0, 0);
+    it.sc4 = bload4(rs, a + 192u);
+    it.sc1 = __builtin_amdgcn_raw_buffer_load_b32(rs, a + 208u, 0, 0);
+    it.dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, blk + 208u, 0, 0);
+    it.r = r;
+  }
+  template <bool kLo, int RG>
+  __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
+                                  const _Float16 *const *, int g, f4 *acc) {
+    const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    const uint32_t r = it.r;
+    uint32_t L[4][2], H[2][2];
+#pragma unroll
+    for (int p = 0; p < 4; ++p) {
+      L[p][0] = __builtin_amdgcn_alignbyte(it.ql[p].y, it.ql[p].x, r);
+      L[p][1] = __builtin_amdgcn_alignbyte(it.ql[p].z, it.ql[p].y, r);
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      H[h][0] = __builtin_amdgcn_alignbyte(it.qh[h].y, it.qh[h].x, r);
+      H[h][1] = __builtin_amdgcn_alignbyte(it.qh[h].z, it.qh[h].y, r);
+    }
+    const uint32_t S[4] = {__builtin_amdgcn_alignbyte(it.sc4.y, it.sc4.x, r),
+                           __builtin_amdgcn_alignbyte(it.sc4.z, it.sc4.y, r),
+                           __builtin_amdgcn_alignbyte(it.sc4.w, it.sc4.z, r),
+                           __builtin_amdgcn_alignbyte(it.sc1, it.sc4.w, r)};
+    const uint32_t gb = (uint32_t)g >> 1;
+    f4 accs[RG];
+#pragma unroll
+    for (int q = 0; q < RG; ++q) accs[q] = zero4;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int hh = t >> 2, qq = t & 3;
+      const uint32_t *lq = L[2 * hh + (qq & 1)];
+      const uint32_t *hq = H[hh];
+      const int sh4 = 4 * (qq >> 1), sh2 = 2 * qq;
+      const uint32_t q0 = ((lq[0] >> sh4) & 0x0F0F0F0Fu) | (((hq[0] >> sh2) & 0x03030303u) << 4);
+      const uint32_t q1 = ((lq[1] >> sh4) & 0x0F0F0F0Fu) | (((hq[1] >> sh2) & 0x03030303u) << 4);
+      const int sc = __builtin_amdgcn_sbfe((int)S[2 * hh + (qq >> 1)], 8u * (2u * (uint32_t)(qq & 1) + gb), 8u);
+      const _Float16 sf = (_Float16)(float)sc;
+      const h2 sc2 = {sf, sf};
+      h2 p0, p1, p2, p3, l0, l1, l2, l3;
+      q6_4(q0, sc2, p0, p1, l0, l1);
+      q6_4(q1, sc2, p2, p3, l2, l3);
+      const h8 bh = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      const h8 bl = {l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
+      const int ka = 128 * hh + 32 * qq + 8 * g;
+#pragma unroll
+      for (int q = 0; q < RG; ++q) {
+        const h8 ah = *reinterpret_cast<const h8 *>(ar[q] + ka);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, accs[q], 0, 0, 0);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, accs[q], 0, 0, 0);
+        if (kLo) {  // the x_lo * remainder term (below 2^-22 of the result) is left out, as in the tiled kernel
+          const h8 al = *reinterpret_cast<const h8 *>(arl[q] + ka);
+          accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, accs[q], 0, 0, 0);
+        }
+      }
+    }
+    const float dv = f16_bits_hw(it.dw & 0xffffu);
+#pragma unroll
+    for (int q = 0; q < RG; ++q)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dv, accs[q][v], acc[q][v]);
+  }
+};
+
+template <class F, bool kLo, int RG>
+__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     const _Float16 *__restrict__ xhi, const _Float16 *__restrict__ xlo, const h2 *__restrict__ xsum,
     const float *__restrict__ rscale, const uint8_t *__restrict__ W, const float *__restrict__ bias,
     float *__restrict__ Y, int M, int N, int K, int ksplit, int groups, float *__restrict__ part) {
-  typedef float f4 __attribute__((ext_vector_type(4)));
+  constexpr int D = F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -625,7 +794,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
   // unsplit K: the bias of the workgroup's columns (tile ti of every wave:
   // columns (ti * groups + grp) * 256 + [0, 256)) and the row scales
   float *Bs = reinterpret_cast<float *>(Xs + (size_t)(M + 1) * nsbs * 16);  // [kDecMaxTiles][256]
-  float *Rs = Bs + kDecMaxTiles * 256;                                      // [16]
+  float *Rs = Bs + kDecMaxTiles * 256;                                      // [32]
 
   // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
   //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
@@ -635,23 +804,21 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
   const int mytiles = first < ntiles ? (ntiles - first + stride - 1) / stride : 0;
   const int nitems = mytiles * nsbs;
   const int cn = lane & 15, g = lane >> 4;
-  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
+  const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
   const uint32_t w_end = (uint32_t)((size_t)N * row_bytes);
   const Rsrc rs_w = make_rsrc(W, w_end);
-  const int arow = (lane & 15) < M ? (lane & 15) : M;  // A row (the zero row past M)
+  // A rows of the lane's row groups (the zero row past M)
+  int arow[RG];
+#pragma unroll
+  for (int q = 0; q < RG; ++q) arow[q] = (lane & 15) + 16 * q < M ? (lane & 15) + 16 * q : M;
 
-  struct Item {
-    u32x4 hd, q0, q1;
-  };
+  using Item = typename F::Item;
   auto tile_of = [&](int u) { return (u / nsbs) * stride + first; };
   auto load = [&](Item &it, int u) {
     const int sbl = u - (u / nsbs) * nsbs;
     const int tile = tile_of(u);
     const uint32_t n = (uint32_t)(tile * 16 + cn);  // rows >= N read past the tensor: zeros
-    const uint32_t blk = tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * kQ4KBytes : w_end;
-    it.hd = bload4(rs_w, blk);
-    it.q0 = bload4(rs_w, blk + 16u + 32u * (uint32_t)g);
-    it.q1 = bload4(rs_w, blk + 32u + 32u * (uint32_t)g);
+    F::load(it, rs_w, tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
   };
   // 2. the activations of the slice: this thread's 16-byte pieces (at most
   //    kDecStage; pieces past the rows read past the planes: zeros) and xsum
@@ -686,7 +853,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
 #pragma unroll
   for (int j = 0; j < D; ++j) load(S[j], j);
   if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
-  if (tid < 16) Rs[tid] = __uint_as_float(rbits);
+  if (tid < 32) Rs[tid] = __uint_as_float(rbits);
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
     const int p = tid + i * nt, r = p / pr, c = p - r * pr;
@@ -699,70 +866,37 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_q4k_kernel(
   __syncthreads();
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
-  f4 acc = zero4;
+  f4 acc[RG];
+#pragma unroll
+  for (int q = 0; q < RG; ++q) acc[q] = zero4;
   // outputs: range-checked buffer stores (out-of-range lanes are dropped by
   // the hardware, so no branch surrounds them), scale and bias from LDS
   const uint32_t out_end = (uint32_t)((size_t)(ksplit > 1 ? (size_t)ksplit * M : (size_t)M) * N * 4);
   const Rsrc rs_out = make_rsrc(ksplit > 1 ? (void *)part : (void *)Y, out_end);
   auto consume = [&](const Item &it, int u) {
     const int ti = u / nsbs, sbl = u - ti * nsbs;
-    // scales of the lane group's sub-blocks 2g, 2g + 1; mins of 4g .. 4g + 3
-    // for the min-term MFMA (groups 2, 3 contribute zeros there)
-    h2 scv[2], offv[2];
+    const _Float16 *ar[RG], *arl[RG], *xs[RG];
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      uint32_t sc, mv;
-      q4k_scale_min_sel(2u * (uint32_t)g + (uint32_t)j, it.hd.y, it.hd.z, it.hd.w, sc, mv);
-      const _Float16 sh = (_Float16)(float)sc, oh = (_Float16)(-1024.0f * (float)sc);
-      scv[j] = h2{sh, sh};
-      offv[j] = h2{oh, oh};
+    for (int q = 0; q < RG; ++q) {
+      ar[q] = Ah + (size_t)arow[q] * P + sbl * 256;
+      arl[q] = Al + (size_t)arow[q] * P + sbl * 256;
+      xs[q] = Xs + ((size_t)arow[q] * nsbs + sbl) * 16;
     }
-    h8 mb;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      uint32_t sc, mv;
-      q4k_scale_min_sel((4u * (uint32_t)g + (uint32_t)j) & 7u, it.hd.y, it.hd.z, it.hd.w, sc, mv);
-      const _Float16 mh = g < 2 ? (_Float16)(float)mv : (_Float16)0.0f;
-      mb[2 * j] = mh;
-      mb[2 * j + 1] = mh;
-    }
-    const _Float16 *ar = Ah + (size_t)arow * P + sbl * 256 + 64 * g;
-    const _Float16 *arl = Al + (size_t)arow * P + sbl * 256 + 64 * g;
-    f4 accs = zero4;
-#pragma unroll
-    for (int t = 0; t < 8; ++t) {
-      const int nib = t & 1, p8 = t >> 1;
-      const u32x4 pc = (p8 >> 1) ? it.q1 : it.q0;
-      const uint32_t d0 = (p8 & 1) ? pc.z : pc.x, d1 = (p8 & 1) ? pc.w : pc.y;
-      const uint32_t n0v = nib ? (d0 >> 4) & 0x0F0F0F0Fu : d0 & 0x0F0F0F0Fu;
-      const uint32_t n1v = nib ? (d1 >> 4) & 0x0F0F0F0Fu : d1 & 0x0F0F0F0Fu;
-      h2 p0, p1, p2, p3;
-      nib4(n0v, scv[nib], offv[nib], p0, p1);
-      nib4(n1v, scv[nib], offv[nib], p2, p3);
-      const h8 bv = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
-      const h8 ah = *reinterpret_cast<const h8 *>(ar + 32 * nib + 8 * p8);
-      accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, accs, 0, 0, 0);
-      if (kLo) {
-        const h8 al = *reinterpret_cast<const h8 *>(arl + 32 * nib + 8 * p8);
-        accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, accs, 0, 0, 0);
-      }
-    }
-    const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(Xs + ((size_t)arow * nsbs + sbl) * 16 + 8 * g) : h8{};
-    const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
-    const float dv = f16_bits_hw(it.hd.x & 0xffffu), dm = -f16_bits_hw(it.hd.x >> 16);
-#pragma unroll
-    for (int v = 0; v < 4; ++v) acc[v] = fmaf(dm, mins[v], fmaf(dv, accs[v], acc[v]));
+    F::template contract<kLo, RG>(it, ar, arl, xs, g, acc);
     if (sbl == nsbs - 1) {  // the tile's last super-block: write it out
       const int col = (ti * stride + first) * 16 + cn;
       const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int row = 4 * g + v;
-        const float val = ksplit > 1 ? acc[v] : acc[v] * Rs[row] + bv;
-        const uint32_t off = (row < M && col < N) ? (uint32_t)(((size_t)z * M + row) * N + col) * 4u : out_end;
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
+      for (int q = 0; q < RG; ++q) {
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const int row = 16 * q + 4 * g + v;
+          const float val = ksplit > 1 ? acc[q][v] : acc[q][v] * Rs[row] + bv;
+          const uint32_t off = (row < M && col < N) ? (uint32_t)(((size_t)z * M + row) * N + col) * 4u : out_end;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
+        }
+        acc[q] = zero4;
       }
-      acc = zero4;
     }
   };
 
@@ -816,7 +950,7 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   // larger raw windows in the 4-wave tile's register budget).
   const int64_t nsb = K / 256;
   int64_t ks = 1;
-  if (type == kQ4_K && M <= kDecRows) {
+  if (M <= kDecRows) {
     // decode batch: the streaming kernel.  K slices small enough for the
     // activations to fit the LDS budget (2 * (M + 1) planes of the slice plus
     // sums), and at least enough slices x column groups for every CU.
@@ -860,7 +994,7 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
   if (type != kQ4_K && type != kQ6_K) return hipErrorInvalidValue;
-  if (type == kQ6_K && plan.bm != 128) return hipErrorInvalidValue;
+  if (type == kQ6_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);
@@ -878,17 +1012,26 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   const uint8_t *W = static_cast<const uint8_t *>(w);
   const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
   if (plan.bm == kDecRows) {
-    if (type != kQ4_K || M > kDecRows) return hipErrorInvalidValue;
+    if ((type != kQ4_K && type != kQ6_K) || M > kDecRows) return hipErrorInvalidValue;
     const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
     const size_t lds = (size_t)(M + 1) * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) +
-                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 16) * sizeof(float);
+                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 32) * sizeof(float);
     const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
-    if (x_is_bf16)
-      launch_timed(gemm_decode_q4k_kernel<false, 3>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias,
-                   y, m, n, k, ks, plan.groups, part);
-    else
-      launch_timed(gemm_decode_q4k_kernel<true, 3>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias, y,
-                   m, n, k, ks, plan.groups, part);
+#define OKQ_DEC(F_, LO_, RG_)                                                                                      \
+  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias, y, m, \
+               n, k, ks, plan.groups, part)
+#define OKQ_DEC_RG(F_, LO_)        \
+  if (M > 16) OKQ_DEC(F_, LO_, 2); \
+  else OKQ_DEC(F_, LO_, 1)
+    if (type == kQ6_K) {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
+      else OKQ_DEC_RG(DecQ6K, true);
+    } else {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
+      else OKQ_DEC_RG(DecQ4K, true);
+    }
+#undef OKQ_DEC_RG
+#undef OKQ_DEC
   } else {
   const int tiles_n = (int)((N + kBN - 1) / kBN);
   const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);

@@ -218,17 +218,23 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
-// serves up to four rows); above it the MFMA GEMM path (which takes the
-// streaming decode-batch kernel up to 16 rows of Q4_K, the tiled kernel
-// beyond).  Q4_K from kDecMinRows rows on also takes the decode-batch kernel:
-// it streams the weights once where the GEMV needs two passes (measured at 8
-// rows: gate 21 vs 28 us, down 26 vs 45 us; at 4 rows the one-pass GEMV wins).
+// serves up to four rows); above it the MFMA GEMM path (the streaming
+// decode-batch kernel up to 16 rows, the tiled kernel beyond).  Large Q4_K /
+// Q6_K matrices take the decode-batch kernel from kDecMinRows rows on: it
+// streams the weights once where the GEMV needs a second pass, and its fixed
+// cost (pre-pass, K-split reduction, ~10 us per call in a graph) is repaid
+// above ~16 MB of weights.  Measured per call in graphs, decode kernel vs
+// GEMV: Q4_K gate 20 vs 23 us at 5 rows (15 at 4), Q6_K down 31 vs 39 us at 5
+// rows, Q6_K head 125 vs 199 us at 5 rows; q/k/v/o-sized matrices favour the
+// GEMV up to 8 rows.
 constexpr int64_t kGemvMaxRows = 8;
 constexpr int64_t kDecMinRows = 5;
+constexpr uint64_t kDecMinBytes = 16u << 20;
 
-bool gemv_serves(uint32_t type, int64_t rows) {
+bool gemv_serves(uint32_t type, int64_t rows, uint64_t w_bytes) {
   if (rows > kGemvMaxRows) return false;
-  return !(type == OKQ_TYPE_Q4_K && rows >= kDecMinRows);
+  const bool dec_fmt = type == OKQ_TYPE_Q4_K || type == OKQ_TYPE_Q6_K;
+  return !(dec_fmt && rows >= kDecMinRows && w_bytes >= kDecMinBytes);
 }
 
 okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint32_t type, const void *w,
@@ -249,7 +255,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
                   (long long)K, (long long)N);
     use_gemm = true;
   } else if (path == Path::Auto) {
-    use_gemm = !gemv_serves(type, rows) && okq::gemm_supported((int)type, rows, K, N);
+    use_gemm = !gemv_serves(type, rows, w_bytes) && okq::gemm_supported((int)type, rows, K, N);
   }
   if (use_gemm) {
     void *ws = nullptr;
@@ -591,7 +597,7 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   okq_status st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool decode = gemv_serves(gate_type, rows);
+  const bool decode = gemv_serves(gate_type, rows, gate_bytes);
   // gate and up: one grouped pass over both weights when they share a format
   if (decode && gate_type == up_type && okq::gemv_streams((int)gate_type, hidden, gate_w, intermediate) &&
       okq::gemv_streams((int)up_type, hidden, up_w, intermediate)) {

@@ -90,10 +90,10 @@ def test_gemm_f32_q4k_matches_reference(torch, okq, orc, rows, n, k):
     x = orc.normal(901 + rows, rows * k, 1.0)
     got = run(torch, okq, "okq_gemm", O.Q4_K, x, rows, k, wq, n)
     check_rows(orc, O.Q4_K, got, x, rows, k, wq, n, None, None)
-    # the automatic path picks the MFMA path from 5 rows of Q4_K on (the
-    # GEMV below) and agrees with the pinned path bit for bit
+    # the automatic path picks the MFMA path above 8 rows (the GEMV up to 8
+    # for matrices this small) and agrees with the pinned path bit for bit
     auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q4_K, x, rows, k, wq, n)
-    pinned = got if rows >= 5 else run(torch, okq, "okq_gemv", O.Q4_K, x, rows, k, wq, n)
+    pinned = got if rows > 8 else run(torch, okq, "okq_gemv", O.Q4_K, x, rows, k, wq, n)
     assert (auto.view(np.uint32) == pinned.view(np.uint32)).all()
 
 
@@ -113,9 +113,9 @@ def test_gemm_one_hot_columns_are_exact(torch, okq, orc):
 def test_gemm_is_deterministic_and_row_independent(torch, okq, orc):
     """Same inputs, same bits; and a row's result does not depend on the
     other rows of its batch within a kernel family: the tiled kernel (more
-    than 16 rows) and the decode-batch kernel (up to 16 rows of Q4_K) each
-    sum a row's products in one fixed order (the two families' orders differ,
-    so across the 16-row boundary results agree within the rule only)."""
+    than 32 rows) and the decode-batch kernel (up to 32 rows) each sum a
+    row's products in one fixed order (the two families' orders differ, so
+    across the boundary results agree within the rule only)."""
     rows, n, k = 300, 384, 2048
     wq = orc.quantize(O.Q4_K, orc.normal(88, n * k, 0.02))
     xb, x32 = bf16_inputs(orc, 89, rows, k)
@@ -132,7 +132,7 @@ def test_gemm_is_deterministic_and_row_independent(torch, okq, orc):
     check_rows(orc, O.Q4_K, few, x32.reshape(rows, k)[130:142].reshape(-1), 12, k, wq, n, None, None)
 
 
-# ---- Q4_K decode batches (up to 16 rows: one MFMA tile of rows, weights
+# ---- decode batches (up to 32 rows: one or two 16-row MFMA tiles, weights
 # dequantised into B fragments by the lanes that load them) ---------------------
 DEC_CASES = [
     # (entry, rows, n, k): ragged N, every row count class, split and unsplit K
@@ -141,6 +141,18 @@ DEC_CASES = [
     ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm_bf16", 16, 520, 2048), ("okq_gemm_bf16", 7, 33, 256),
     # one super-block per row: K is never split, outputs and bias written directly
     ("okq_gemm", 3, 70001, 256), ("okq_gemm_bf16", 9, 65540, 256),
+    # 17-32 rows: two 16-row MFMA groups share each B fragment
+    ("okq_gemm", 17, 300, 1024), ("okq_gemm", 32, 4096, 4096), ("okq_gemm_bf16", 25, 1000, 768),
+    ("okq_gemm", 32, 14336, 4096),
+]
+
+
+DEC_Q6K_CASES = [
+    ("okq_gemm", 1, 96, 256), ("okq_gemm", 4, 257, 768), ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1024, 4096),
+    ("okq_gemm", 11, 4096, 14336), ("okq_gemm_bf16", 6, 300, 1024), ("okq_gemm_bf16", 16, 4095, 512),
+    # an odd super-block count per row: block starts alternate between the two 2-byte alignments
+    ("okq_gemm", 5, 333, 1280), ("okq_gemm", 2, 70003, 256),
+    ("okq_gemm", 20, 1024, 4096), ("okq_gemm", 32, 4096, 14336), ("okq_gemm_bf16", 31, 257, 768),
 ]
 
 
@@ -156,6 +168,20 @@ def test_gemm_decode_batch_q4k_matches_reference(torch, okq, orc, entry, rows, n
     got = run(torch, okq, entry, O.Q4_K, xin, rows, k, wq, n, bias)
     assert np.isfinite(got).all()
     check_rows(orc, O.Q4_K, got, x32, rows, k, wq, n, bias, None if n * k <= 20_000_000 else 6)
+
+
+@pytest.mark.parametrize("entry,rows,n,k", DEC_Q6K_CASES)
+def test_gemm_decode_batch_q6k_matches_reference(torch, okq, orc, entry, rows, n, k):
+    print(f"[gpu] gemm decode-batch {entry} Q6_K M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q6_K, orc.normal(1600 + n + k, n * k, 0.02))
+    bias = orc.normal(1601 + rows, n, 0.1)
+    if entry == "okq_gemm_bf16":
+        xin, x32 = bf16_inputs(orc, 1602 + rows, rows, k)
+    else:
+        xin = x32 = orc.normal(1602 + rows, rows * k, 1.0)
+    got = run(torch, okq, entry, O.Q6_K, xin, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q6_K, got, x32, rows, k, wq, n, bias, None if n * k <= 20_000_000 else 6)
 
 
 def q4k_parts(orc, wq, n, k):
@@ -257,6 +283,23 @@ def test_gemm_q6k_one_hot_columns_are_exact(torch, okq, orc):
         got = run(torch, okq, entry, O.Q6_K, xin, rows, k, wq, n)
         # values, not bits: a zero product with a negative scale dequantizes to -0.0
         assert np.array_equal(got, w[:, cols].T), entry
+
+
+@pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K])
+def test_linear_dispatch_large_matrices_take_the_decode_batch_kernel_from_5_rows(torch, okq, orc, t):
+    """okq_linear_out_by_in_q on a matrix of 16 MB or more: 5 rows run the
+    decode-batch kernel (bit-identical to okq_gemm), 4 rows the GEMV
+    (bit-identical to okq_gemv)."""
+    n, k = 14336 if t == O.Q4_K else 10240, 4096
+    wq = orc.quantize(t, orc.normal(930 + t, n * k, 0.02))
+    assert wq.size >= 16 << 20
+    for rows, pinned in ((4, "okq_gemv"), (5, "okq_gemm")):
+        print(f"[gpu] dispatch type={t} rows={rows} N={n} K={k}", flush=True)
+        x = orc.normal(931 + rows, rows * k, 1.0)
+        auto = run(torch, okq, "okq_linear_out_by_in_q", t, x, rows, k, wq, n)
+        pin = run(torch, okq, pinned, t, x, rows, k, wq, n)
+        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
+        check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
 
 
 def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):
