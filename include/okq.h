@@ -121,9 +121,9 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
  * bias: [out_features] f32 or NULL; out: [rows, out_features] f32.
  * rows == 0 or out_features == 0 is a no-op.  Up to 8 rows run the fused
  * dequant-GEMV (each pass over the weights serving up to four rows), except
- * Q4_K from 5 rows on; more rows run the MFMA dequant-GEMM (Q4_K, Q6_K; Q8_0
- * stays on the GEMV), whose Q4_K kernel for up to 16 rows streams the weights
- * once with the rows in one MFMA tile. */
+ * Q4_K / Q6_K matrices of 16 MB or more from 5 rows on; more rows run the
+ * MFMA dequant-GEMM (Q4_K, Q6_K; Q8_0 stays on the GEMV), which for up to 32
+ * rows streams the weights once with the rows in one or two MFMA tiles. */
 okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
                                   const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
                                   float *out, void *stream);
