@@ -326,12 +326,12 @@ def measured_traffic():
 
 def roofline_from(launches):
     # dominant kernel: the gate+up launch (two 14336 x 4096 Q4_K matrices, 54%
-    # of the step's bytes; gemv_kernel<FQ4K, 2, 1, true, 0, 1>, an
+    # of the step's bytes; gemv_kernel<FQ4K, 2, 1, true, 0, 1, true>, an
     # instantiation no other launch of the step uses, so rocprof's per-kernel
     # average covers exactly these launches and C5's identical batch-1 ones)
     s = launches["gate_up"]
     achieved = s["weight_bytes"] / s["us_mean"] / 1e3
-    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 1, true, 0, 1> (C2 gate+up, 2 x 14336x4096 Q4_K)",
+    return {"bound": "hbm", "kernel": "okq::gemv_kernel<okq::FQ4K, 2, 1, true, 0, 1, true> (C2 gate+up, 2 x 14336x4096 Q4_K)",
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
@@ -436,8 +436,10 @@ def run_c5(ctx: Ctx, args):
     back on one stream, replayed from a HIP graph.  `grouped`: the decode
     launches an engine issues (q+k and gate+up share x in okq_gemv_multi,
     each pass over a weight serving up to four rows); `auto`: one
-    okq_linear_out_by_in_q per projection (the MFMA GEMM for Q4_K above four
-    rows, the multi-row GEMV otherwise)."""
+    okq_linear_out_by_in_q per projection, whose dispatch picks the kernel
+    by shape (the streaming decode-batch MFMA kernel for Q4_K/Q6_K weights of
+    16 MB and more from five rows, and for every Q4_K/Q6_K weight above eight
+    rows; the multi-row GEMV otherwise)."""
     torch = ctx.torch
     log(f"C5: generating {C5_LAYERS} Q4_K_M layers + Q6_K head")
     layers = [{name: ctx.quantized(t, n, k, seed=50_000 + 100 * l + i) for i, (name, t, n, k) in enumerate(C5_PROJ)}
