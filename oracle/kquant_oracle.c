@@ -12,7 +12,10 @@
  *   - f32 -> fp16 / bf16 rounding (round-to-nearest-even).  Not in the
  *     reference; IEEE 754 binary16 definition.  Pinned by exhaustive checks
  *     against numpy's float16 conversion.
- *   - GGUF block dequant for Q8_0 / Q4_K / Q6_K.  The reference has none
+ *   - GGUF block dequant for Q8_0 / Q4_K / Q6_K (the linear path's weights)
+ *     and Q4_0 / Q4_1 / Q5_0 / Q5_1 / Q2_K / Q3_K / Q5_K (the other block
+ *     formats GgmlTensorType names, gguf_inspect.rs:132-167, served by the
+ *     dequantize and row-gather entry points).  The reference has none
  *     (gguf_inspect.rs:208-219 leaves quantized byte_len = None); the layouts
  *     are the public GGUF/ggml block spec.  Pinned by an independent numpy
  *     bit-field decoder, closed forms and element-order probes.
@@ -46,7 +49,10 @@
 #define OKR_API __attribute__((visibility("default")))
 
 /* GGML type ids: crates/loader/src/gguf_inspect.rs:170-206. */
-enum { OKR_F32 = 0, OKR_F16 = 1, OKR_Q8_0 = 8, OKR_Q4_K = 12, OKR_Q6_K = 14, OKR_BF16 = 30 };
+enum {
+    OKR_F32 = 0, OKR_F16 = 1, OKR_Q4_0 = 2, OKR_Q4_1 = 3, OKR_Q5_0 = 6, OKR_Q5_1 = 7, OKR_Q8_0 = 8,
+    OKR_Q2_K = 10, OKR_Q3_K = 11, OKR_Q4_K = 12, OKR_Q5_K = 13, OKR_Q6_K = 14, OKR_BF16 = 30
+};
 
 /* ------------------------------------------------------------------------ */
 /* fp16 / bf16                                                               */
@@ -144,17 +150,23 @@ OKR_API void okr_bf16_to_f32_array(const uint16_t *src, int64_t n, float *dst) {
 
 OKR_API int64_t okr_block_elems(int type) {
     switch (type) {
-    case OKR_Q8_0: return 32;
-    case OKR_Q4_K: return 256;
-    case OKR_Q6_K: return 256;
+    case OKR_Q4_0: case OKR_Q4_1: case OKR_Q5_0: case OKR_Q5_1: case OKR_Q8_0: return 32;
+    case OKR_Q2_K: case OKR_Q3_K: case OKR_Q4_K: case OKR_Q5_K: case OKR_Q6_K: return 256;
     case OKR_F32: case OKR_F16: case OKR_BF16: return 1;
     default: return -1;
     }
 }
 OKR_API int64_t okr_block_bytes(int type) {
     switch (type) {
+    case OKR_Q4_0: return 18;
+    case OKR_Q4_1: return 20;
+    case OKR_Q5_0: return 22;
+    case OKR_Q5_1: return 24;
     case OKR_Q8_0: return 34;
+    case OKR_Q2_K: return 84;
+    case OKR_Q3_K: return 110;
     case OKR_Q4_K: return 144;
+    case OKR_Q5_K: return 176;
     case OKR_Q6_K: return 210;
     case OKR_F32: return 4;
     case OKR_F16: case OKR_BF16: return 2;
@@ -245,8 +257,178 @@ OKR_API int okr_dequant_q6_k(const uint8_t *src, int64_t n, float *dst) {
     return 0;
 }
 
+/* ---- the other block formats (dequantize / row gather only) -------------- */
+
+/* Q4_0 {f16 d; u8 qs[16]}: y[j] = ((qs[j]&15) - 8)*d, y[j+16] = ((qs[j]>>4) - 8)*d */
+OKR_API int okr_dequant_q4_0(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 32) return 1;
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + b * 18;
+        float d = okr_f16_to_f32(rd_u16(blk));
+        for (int j = 0; j < 16; ++j) {
+            dst[b * 32 + j] = (float)((blk[2 + j] & 15) - 8) * d;
+            dst[b * 32 + j + 16] = (float)((blk[2 + j] >> 4) - 8) * d;
+        }
+    }
+    return 0;
+}
+
+/* Q4_1 {f16 d; f16 m; u8 qs[16]}: y = q*d + m with q the nibble as above (no offset) */
+OKR_API int okr_dequant_q4_1(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 32) return 1;
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + b * 20;
+        float d = okr_f16_to_f32(rd_u16(blk));
+        float m = okr_f16_to_f32(rd_u16(blk + 2));
+        for (int j = 0; j < 16; ++j) {
+            dst[b * 32 + j] = (float)(blk[4 + j] & 15) * d + m;
+            dst[b * 32 + j + 16] = (float)(blk[4 + j] >> 4) * d + m;
+        }
+    }
+    return 0;
+}
+
+/* Bit e (0..31) of the little-endian 32-bit high-bit word qh[4]: the fifth
+ * bit of element e of a Q5_0 / Q5_1 block. */
+static inline int q5_high_bit(const uint8_t *qh, int e) { return (qh[e >> 3] >> (e & 7)) & 1; }
+
+/* Q5_0 {f16 d; u8 qh[4]; u8 qs[16]}: y[e] = ((nibble(e) | qh_bit(e)<<4) - 16)*d */
+OKR_API int okr_dequant_q5_0(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 32) return 1;
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + b * 22;
+        float d = okr_f16_to_f32(rd_u16(blk));
+        const uint8_t *qh = blk + 2, *qs = blk + 6;
+        for (int j = 0; j < 16; ++j) {
+            int x0 = ((qs[j] & 15) | (q5_high_bit(qh, j) << 4)) - 16;
+            int x1 = ((qs[j] >> 4) | (q5_high_bit(qh, j + 16) << 4)) - 16;
+            dst[b * 32 + j] = (float)x0 * d;
+            dst[b * 32 + j + 16] = (float)x1 * d;
+        }
+    }
+    return 0;
+}
+
+/* Q5_1 {f16 d; f16 m; u8 qh[4]; u8 qs[16]}: y[e] = (nibble(e) | qh_bit(e)<<4)*d + m */
+OKR_API int okr_dequant_q5_1(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 32) return 1;
+    for (int64_t b = 0; b < n / 32; ++b) {
+        const uint8_t *blk = src + b * 24;
+        float d = okr_f16_to_f32(rd_u16(blk));
+        float m = okr_f16_to_f32(rd_u16(blk + 2));
+        const uint8_t *qh = blk + 4, *qs = blk + 8;
+        for (int j = 0; j < 16; ++j) {
+            int x0 = (qs[j] & 15) | (q5_high_bit(qh, j) << 4);
+            int x1 = (qs[j] >> 4) | (q5_high_bit(qh, j + 16) << 4);
+            dst[b * 32 + j] = (float)x0 * d + m;
+            dst[b * 32 + j + 16] = (float)x1 * d + m;
+        }
+    }
+    return 0;
+}
+
+/* Q2_K {u8 scales[16]; u8 qs[64]; f16 d; f16 dmin}: for half h (0,1) and
+ * shift step j (0..3), the 32 elements 128h+32j+s (s < 32) take 2-bit
+ * q = (qs[32h+s] >> 2j) & 3 and scale byte sc = scales[8h+2j+(s>=16)]
+ * (= scales[e/16]):  y = (d*(sc&15))*q - (dmin*(sc>>4)). */
+OKR_API int okr_dequant_q2_k(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 256) return 1;
+    for (int64_t b = 0; b < n / 256; ++b) {
+        const uint8_t *blk = src + b * 84;
+        const uint8_t *scales = blk, *qs = blk + 16;
+        float d = okr_f16_to_f32(rd_u16(blk + 80));
+        float dmin = okr_f16_to_f32(rd_u16(blk + 82));
+        float *y = dst + b * 256;
+        for (int h = 0; h < 2; ++h) {
+            for (int j = 0; j < 4; ++j) {
+                for (int half16 = 0; half16 < 2; ++half16) {
+                    uint8_t sc = scales[8 * h + 2 * j + half16];
+                    float dl = d * (float)(sc & 15), ml = dmin * (float)(sc >> 4);
+                    for (int l = 0; l < 16; ++l) {
+                        int s = 16 * half16 + l;
+                        int q = (qs[32 * h + s] >> (2 * j)) & 3;
+                        y[128 * h + 32 * j + s] = dl * (float)q - ml;
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* 6-bit scale i (0..15) of a Q3_K block from its 12 packed bytes: low four
+ * bits are the low nibble of byte i (i < 8) or the high nibble of byte i-8;
+ * the top two bits are bits 2*(i/4)..+1 of byte 8 + i%4. */
+static inline int q3k_scale(const uint8_t *s, int i) {
+    int lo = i < 8 ? (s[i] & 15) : (s[i - 8] >> 4);
+    int hi = (s[8 + (i & 3)] >> (2 * (i >> 2))) & 3;
+    return lo | (hi << 4);
+}
+
+/* Q3_K {u8 hmask[32]; u8 qs[64]; u8 scales[12]; f16 d}: element
+ * e = 128h+32j+s takes the 2 low bits (qs[32h+s] >> 2j) & 3, minus 4 when bit
+ * 4h+j of hmask[s] is clear:  y = (d*(scale(e/16) - 32)) * q. */
+OKR_API int okr_dequant_q3_k(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 256) return 1;
+    for (int64_t b = 0; b < n / 256; ++b) {
+        const uint8_t *blk = src + b * 110;
+        const uint8_t *hm = blk, *qs = blk + 32, *scales = blk + 96;
+        float d = okr_f16_to_f32(rd_u16(blk + 108));
+        float *y = dst + b * 256;
+        for (int h = 0; h < 2; ++h) {
+            for (int j = 0; j < 4; ++j) {
+                for (int half16 = 0; half16 < 2; ++half16) {
+                    int is = 8 * h + 2 * j + half16;
+                    float dl = d * (float)(q3k_scale(scales, is) - 32);
+                    for (int l = 0; l < 16; ++l) {
+                        int s = 16 * half16 + l;
+                        int q = ((qs[32 * h + s] >> (2 * j)) & 3) - (((hm[s] >> (4 * h + j)) & 1) ? 0 : 4);
+                        y[128 * h + 32 * j + s] = dl * (float)q;
+                    }
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* Q5_K {f16 d; f16 dmin; u8 scales[12]; u8 qh[32]; u8 qs[128]}: as Q4_K with
+ * a fifth bit, bit 2c+hi of qh[l], added as 16:
+ * y[64c+32hi+l] = (d*sc(2c+hi)) * (nibble + 16*bit) - (dmin*m(2c+hi)). */
+OKR_API int okr_dequant_q5_k(const uint8_t *src, int64_t n, float *dst) {
+    if (n % 256) return 1;
+    for (int64_t b = 0; b < n / 256; ++b) {
+        const uint8_t *blk = src + b * 176;
+        float d = okr_f16_to_f32(rd_u16(blk));
+        float dmin = okr_f16_to_f32(rd_u16(blk + 2));
+        const uint8_t *scales = blk + 4, *qh = blk + 16, *qs = blk + 48;
+        float *y = dst + b * 256;
+        for (int c = 0; c < 4; ++c) {
+            uint8_t sc, m;
+            q4k_scale_min(2 * c, scales, &sc, &m);
+            float d1 = d * (float)sc, m1 = dmin * (float)m;
+            q4k_scale_min(2 * c + 1, scales, &sc, &m);
+            float d2 = d * (float)sc, m2 = dmin * (float)m;
+            for (int l = 0; l < 32; ++l) {
+                int q1 = (qs[32 * c + l] & 15) + (((qh[l] >> (2 * c)) & 1) ? 16 : 0);
+                int q2 = (qs[32 * c + l] >> 4) + (((qh[l] >> (2 * c + 1)) & 1) ? 16 : 0);
+                y[64 * c + l] = d1 * (float)q1 - m1;
+                y[64 * c + 32 + l] = d2 * (float)q2 - m2;
+            }
+        }
+    }
+    return 0;
+}
+
 OKR_API int okr_dequantize(int type, const uint8_t *src, int64_t n, float *dst) {
     switch (type) {
+    case OKR_Q4_0: return okr_dequant_q4_0(src, n, dst);
+    case OKR_Q4_1: return okr_dequant_q4_1(src, n, dst);
+    case OKR_Q5_0: return okr_dequant_q5_0(src, n, dst);
+    case OKR_Q5_1: return okr_dequant_q5_1(src, n, dst);
+    case OKR_Q2_K: return okr_dequant_q2_k(src, n, dst);
+    case OKR_Q3_K: return okr_dequant_q3_k(src, n, dst);
+    case OKR_Q5_K: return okr_dequant_q5_k(src, n, dst);
     case OKR_Q8_0: return okr_dequant_q8_0(src, n, dst);
     case OKR_Q4_K: return okr_dequant_q4_k(src, n, dst);
     case OKR_Q6_K: return okr_dequant_q6_k(src, n, dst);

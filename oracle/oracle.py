@@ -31,8 +31,17 @@ LIB_PATH = os.path.join(HERE, "liboracle.so")
 
 # GGML type ids (crates/loader/src/gguf_inspect.rs:170-206)
 F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
-BLOCK_ELEMS = {Q8_0: 32, Q4_K: 256, Q6_K: 256}
-BLOCK_BYTES = {Q8_0: 34, Q4_K: 144, Q6_K: 210}
+# the other block formats GgmlTensorType names (gguf_inspect.rs:132-167) that
+# the dequantize and row-gather entry points serve
+Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K = 2, 3, 6, 7, 10, 11, 13
+LINEAR_TYPES = (Q8_0, Q4_K, Q6_K)
+GATHER_TYPES = (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
+BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32,
+               Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}
+BLOCK_BYTES = {Q4_0: 18, Q4_1: 20, Q5_0: 22, Q5_1: 24, Q8_0: 34,
+               Q2_K: 84, Q3_K: 110, Q4_K: 144, Q5_K: 176, Q6_K: 210}
+TYPE_NAMES = {Q4_0: "Q4_0", Q4_1: "Q4_1", Q5_0: "Q5_0", Q5_1: "Q5_1", Q8_0: "Q8_0",
+              Q2_K: "Q2_K", Q3_K: "Q3_K", Q4_K: "Q4_K", Q5_K: "Q5_K", Q6_K: "Q6_K"}
 
 MODE_SCALAR, MODE_OPTIMIZED, MODE_AVX2 = 0, 1, 2
 
@@ -276,7 +285,121 @@ def np_dequant_q6_k(blocks: np.ndarray) -> np.ndarray:
     return y.reshape(-1)
 
 
-NP_DEQUANT = {Q8_0: np_dequant_q8_0, Q4_K: np_dequant_q4_k, Q6_K: np_dequant_q6_k}
+def _f16_at(b: np.ndarray, off: int) -> np.ndarray:
+    return np_f16_bits_to_f32(b[:, off].astype(np.uint16) | (b[:, off + 1].astype(np.uint16) << 8))
+
+
+def _legacy32(blocks, nbytes, has_min, has_high):
+    """Q4_0 / Q4_1 / Q5_0 / Q5_1: 32 elements; element e < 16 is the low nibble
+    of qs[e], e >= 16 the high nibble of qs[e-16]; the Q5 formats add bit e of
+    the 32-bit little-endian qh word as the fifth bit; the symmetric formats
+    subtract 8 (Q4_0) or 16 (Q5_0) and have no min."""
+    b = np.asarray(blocks, np.uint8).reshape(-1, nbytes)
+    d = _f16_at(b, 0)
+    off = 2
+    m = None
+    if has_min:
+        m = _f16_at(b, 2)
+        off = 4
+    qh = None
+    if has_high:
+        qh = b[:, off:off + 4].astype(np.int64)
+        off += 4
+    qs = b[:, off:off + 16].astype(np.int64)
+    y = np.empty((b.shape[0], 32), np.float32)
+    for e in range(32):
+        v = (qs[:, e % 16] >> (4 * (e // 16))) & 15
+        if has_high:
+            v = v | (((qh[:, e // 8] >> (e % 8)) & 1) << 4)
+        if not has_min:
+            v = v - (16 if has_high else 8)
+        prod = (v.astype(np.float32) * d).astype(np.float32)
+        y[:, e] = prod if m is None else (prod + m).astype(np.float32)
+    return y.reshape(-1)
+
+
+def np_dequant_q4_0(blocks):
+    return _legacy32(blocks, 18, False, False)
+
+
+def np_dequant_q4_1(blocks):
+    return _legacy32(blocks, 20, True, False)
+
+
+def np_dequant_q5_0(blocks):
+    return _legacy32(blocks, 22, False, True)
+
+
+def np_dequant_q5_1(blocks):
+    return _legacy32(blocks, 24, True, True)
+
+
+def np_dequant_q2_k(blocks: np.ndarray) -> np.ndarray:
+    b = np.asarray(blocks, np.uint8).reshape(-1, 84)
+    d, dmin = _f16_at(b, 80), _f16_at(b, 82)
+    y = np.empty((b.shape[0], 256), np.float32)
+    for e in range(256):
+        h, r = divmod(e, 128)
+        j, s = divmod(r, 32)
+        byte = b[:, 16 + 32 * h + s].astype(np.int64)
+        q = _bit(byte, 2 * j) | (_bit(byte, 2 * j + 1) << 1)
+        sc = b[:, e // 16].astype(np.int64)
+        dl = (d * (sc & 15).astype(np.float32)).astype(np.float32)
+        ml = (dmin * (sc >> 4).astype(np.float32)).astype(np.float32)
+        y[:, e] = ((dl * q.astype(np.float32)).astype(np.float32) - ml).astype(np.float32)
+    return y.reshape(-1)
+
+
+def _q3k_field(scales: np.ndarray, i: int) -> np.ndarray:
+    """6-bit scale i of a Q3_K block, bit by bit: bits 0-3 from byte i (i < 8,
+    low nibble) or byte i-8 (high nibble); bits 4-5 from byte 8 + i%4 at bit
+    offset 2*(i//4)."""
+    s = scales.astype(np.int64)
+    v = np.zeros(s.shape[0], np.int64)
+    src, base = (i, 0) if i < 8 else (i - 8, 4)
+    for k in range(4):
+        v |= _bit(s[:, src], base + k) << k
+    for k in range(2):
+        v |= _bit(s[:, 8 + i % 4], 2 * (i // 4) + k) << (4 + k)
+    return v
+
+
+def np_dequant_q3_k(blocks: np.ndarray) -> np.ndarray:
+    b = np.asarray(blocks, np.uint8).reshape(-1, 110)
+    d = _f16_at(b, 108)
+    y = np.empty((b.shape[0], 256), np.float32)
+    for e in range(256):
+        h, r = divmod(e, 128)
+        j, s = divmod(r, 32)
+        byte = b[:, 32 + 32 * h + s].astype(np.int64)
+        q = _bit(byte, 2 * j) | (_bit(byte, 2 * j + 1) << 1)
+        q = q - 4 * (1 - _bit(b[:, s].astype(np.int64), 4 * h + j))
+        sc = _q3k_field(b[:, 96:108], e // 16) - 32
+        dl = (d * sc.astype(np.float32)).astype(np.float32)
+        y[:, e] = (dl * q.astype(np.float32)).astype(np.float32)
+    return y.reshape(-1)
+
+
+def np_dequant_q5_k(blocks: np.ndarray) -> np.ndarray:
+    b = np.asarray(blocks, np.uint8).reshape(-1, 176)
+    d, dmin = _f16_at(b, 0), _f16_at(b, 2)
+    scales = b[:, 4:16]
+    y = np.empty((b.shape[0], 256), np.float32)
+    for e in range(256):
+        c, r = divmod(e, 64)
+        hi, l = divmod(r, 32)
+        q = (b[:, 48 + 32 * c + l].astype(np.int64) >> (4 * hi)) & 15
+        q = q + 16 * _bit(b[:, 16 + l].astype(np.int64), 2 * c + hi)
+        sc, mn = _q4k_field(scales, 2 * c + hi)
+        ds = (d * sc.astype(np.float32)).astype(np.float32)
+        dm = (dmin * mn.astype(np.float32)).astype(np.float32)
+        y[:, e] = ((ds * q.astype(np.float32)).astype(np.float32) - dm).astype(np.float32)
+    return y.reshape(-1)
+
+
+NP_DEQUANT = {Q8_0: np_dequant_q8_0, Q4_K: np_dequant_q4_k, Q6_K: np_dequant_q6_k,
+              Q4_0: np_dequant_q4_0, Q4_1: np_dequant_q4_1, Q5_0: np_dequant_q5_0, Q5_1: np_dequant_q5_1,
+              Q2_K: np_dequant_q2_k, Q3_K: np_dequant_q3_k, Q5_K: np_dequant_q5_k}
 
 
 def np_linear_sequential(x: np.ndarray, w: np.ndarray, bias=None) -> np.ndarray:

@@ -42,7 +42,8 @@ def reference_kats():
                 [0x0001, 0x33800000], [0x7C00, 0x7F800000]],
         "f16_nan": [0x7E00],
         "bf16": [[0x3F80, 0x3F800000], [0xC020, 0xC0200000], [0x0000, 0x00000000], [0x7F80, 0x7F800000]],
-        "type_ids": {"F32": 0, "F16": 1, "Q8_0": 8, "Q4K": 12, "Q6K": 14, "BF16": 30},
+        "type_ids": {"F32": 0, "F16": 1, "Q4_0": 2, "Q4_1": 3, "Q5_0": 6, "Q5_1": 7, "Q8_0": 8, "Q2K": 10,
+                     "Q3K": 11, "Q4K": 12, "Q5K": 13, "Q6K": 14, "BF16": 30},
         "gguf_fixture_token_embd": {"name": "token_embd.weight", "shape": [2560, 262144], "tensor_type": "q4_k"},
         # rows x hidden input, weight, epsilon, expected output, absolute tolerance
         "rmsnorm": [
@@ -82,7 +83,35 @@ def oracle_vectors(o):
             "sha256_4096x16_seed": 2000 + t,
             "sha256_4096x16": hashlib.sha256(big.tobytes()).hexdigest(),
         }
-    return {"generator": "SplitMix64 + Irwin-Hall(12), okr_normal_at", "normal_first16": rng, "blocks": blocks}
+    # the block formats without a quantizer here: seeded random bytes (f16
+    # fields kept finite) and their dequantized values
+    raw = {}
+    for t in (O.Q4_0, O.Q4_1, O.Q5_0, O.Q5_1, O.Q2_K, O.Q3_K, O.Q5_K):
+        nb = 4 if O.BLOCK_ELEMS[t] == 256 else 16
+        b = finite_random_blocks(t, nb, 3000 + t)
+        y = o.dequantize(t, b, nb * O.BLOCK_ELEMS[t])
+        raw[O.TYPE_NAMES[t]] = {"type": t, "blocks_hex": b.tobytes().hex(),
+                                "dequant_f32_bits": [int(v) for v in y.view(np.uint32)]}
+    return {"generator": "SplitMix64 + Irwin-Hall(12), okr_normal_at", "normal_first16": rng, "blocks": blocks,
+            "raw_blocks": raw}
+
+
+# byte offsets of the f16 fields (d, and dmin or m) in each block format
+F16_FIELDS = {O.Q4_0: (0,), O.Q4_1: (0, 2), O.Q5_0: (0,), O.Q5_1: (0, 2), O.Q8_0: (0,), O.Q2_K: (80, 82),
+              O.Q3_K: (108,), O.Q4_K: (0, 2), O.Q5_K: (0, 2), O.Q6_K: (208,)}
+
+
+def finite_random_blocks(t, nb, seed):
+    """nb random blocks of type t whose f16 fields are finite values of
+    moderate size (exponent field 1..20), so every element is finite."""
+    rng = np.random.default_rng(seed)
+    b = rng.integers(0, 256, (nb, O.BLOCK_BYTES[t]), dtype=np.uint8)
+    for off in F16_FIELDS[t]:
+        h = rng.integers(0, 1 << 16, nb).astype(np.uint16)
+        h = (h & 0x83FF) | (rng.integers(1, 21, nb).astype(np.uint16) << 10)
+        b[:, off] = h & 0xFF
+        b[:, off + 1] = h >> 8
+    return b.reshape(-1)
 
 
 if __name__ == "__main__":

@@ -95,8 +95,8 @@ def test_f32_to_bf16_matches_torch(orc):
 def test_type_ids_block_sizes_and_row_bytes(kats):
     ids = kats["type_ids"]
     assert (ids["Q8_0"], ids["Q4K"], ids["Q6K"]) == (O.Q8_0, O.Q4_K, O.Q6_K)
-    assert O.BLOCK_BYTES == {O.Q8_0: 34, O.Q4_K: 144, O.Q6_K: 210}
-    assert O.BLOCK_ELEMS == {O.Q8_0: 32, O.Q4_K: 256, O.Q6_K: 256}
+    assert {t: O.BLOCK_BYTES[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 34, O.Q4_K: 144, O.Q6_K: 210}
+    assert {t: O.BLOCK_ELEMS[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 32, O.Q4_K: 256, O.Q6_K: 256}
     row = lambda t, k: k // O.BLOCK_ELEMS[t] * O.BLOCK_BYTES[t]  # noqa: E731
     assert (row(O.Q8_0, 4096), row(O.Q4_K, 4096), row(O.Q6_K, 4096)) == (4352, 2304, 3360)
     assert (row(O.Q4_K, 14336), row(O.Q6_K, 14336)) == (8064, 11760)
