@@ -48,8 +48,15 @@ typedef enum okq_status {
 enum {
     OKQ_TYPE_F32 = 0,
     OKQ_TYPE_F16 = 1,
+    OKQ_TYPE_Q4_0 = 2,  /* dequantize / get_rows only */
+    OKQ_TYPE_Q4_1 = 3,  /* dequantize / get_rows only */
+    OKQ_TYPE_Q5_0 = 6,  /* dequantize / get_rows only */
+    OKQ_TYPE_Q5_1 = 7,  /* dequantize / get_rows only */
     OKQ_TYPE_Q8_0 = 8,
+    OKQ_TYPE_Q2_K = 10, /* dequantize / get_rows only */
+    OKQ_TYPE_Q3_K = 11, /* dequantize / get_rows only */
     OKQ_TYPE_Q4_K = 12,
+    OKQ_TYPE_Q5_K = 13, /* dequantize / get_rows only */
     OKQ_TYPE_Q6_K = 14,
     OKQ_TYPE_BF16 = 30
 };
@@ -67,8 +74,11 @@ size_t okq_last_error(char *buf, size_t len);
 /* ---- GGUF tensor layout (fills the byte_len = None gap of
  *      GgmlTensorType::fixed_element_size, gguf_inspect.rs:208-219) ------- */
 
-/* Elements and bytes per block: Q8_0 32/34, Q4_K 256/144, Q6_K 256/210, and
- * 1/4, 1/2, 1/2 for F32, F16, BF16.  OKQ_E_TYPE for anything else. */
+/* Elements and bytes per block: Q8_0 32/34, Q4_K 256/144, Q6_K 256/210;
+ * Q4_0 32/18, Q4_1 32/20, Q5_0 32/22, Q5_1 32/24, Q2_K 256/84, Q3_K 256/110,
+ * Q5_K 256/176; and 1/4, 1/2, 1/2 for F32, F16, BF16.  OKQ_E_TYPE for
+ * anything else.  The linear entry points take Q8_0, Q4_K and Q6_K weights;
+ * okq_dequantize and okq_get_rows_q take every block format listed here. */
 okq_status okq_type_info(uint32_t ggml_type, int64_t *block_elems, int64_t *block_bytes);
 
 /* Bytes of one row of ne0 elements; OKQ_E_SHAPE if ne0 is not a positive
@@ -98,7 +108,8 @@ okq_status okq_sync(void *stream);
  * (lib.rs:106-116).  n must be a multiple of the block size; src holds
  * n / block_elems blocks.  Bit-exact with the CPU oracle (every product and
  * difference rounded separately, fp16 decoded exactly as
- * crates/loader/src/safetensors_values.rs:155-183). */
+ * crates/loader/src/safetensors_values.rs:155-183).  Every block format of
+ * okq_type_info; src must be 16-byte aligned for Q4_K, 2-byte otherwise. */
 okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float *dst, void *stream);
 
 /* Quantized embedding lookup: out[j, :] = dequantize(row ids[j] of W) for

@@ -80,13 +80,25 @@ class GgmlTensorType(enum.IntEnum):
     subset this path understands plus the unquantized float types."""
     F32 = 0
     F16 = 1
+    Q4_0 = 2
+    Q4_1 = 3
+    Q5_0 = 6
+    Q5_1 = 7
     Q8_0 = 8
+    Q2K = 10
+    Q3K = 11
     Q4K = 12
+    Q5K = 13
     Q6K = 14
     BF16 = 30
 
 
+# Weight formats the linear kernels execute.
 QUANTIZED = (GgmlTensorType.Q8_0, GgmlTensorType.Q4K, GgmlTensorType.Q6K)
+# Every block format dequantize and the row gather accept.
+BLOCK_FORMATS = (GgmlTensorType.Q4_0, GgmlTensorType.Q4_1, GgmlTensorType.Q5_0, GgmlTensorType.Q5_1,
+                 GgmlTensorType.Q8_0, GgmlTensorType.Q2K, GgmlTensorType.Q3K, GgmlTensorType.Q4K,
+                 GgmlTensorType.Q5K, GgmlTensorType.Q6K)
 BACKEND = "hip-gfx950"
 
 
@@ -214,11 +226,12 @@ class HipKernelBackend:
         return DeviceTensor(_torch().zeros(int(length), dtype=_torch().float32, device=self._device))
 
     def upload_quantized(self, tensor_type: int, ne0: int, ne1: int, blocks) -> QuantizedWeight:
-        """Upload raw GGUF blocks; validates the byte length first."""
+        """Upload raw GGUF blocks of any block format (dequantize serves all of
+        them; linear_d takes Q8_0 / Q4K / Q6K); validates the byte length first."""
         torch = _torch()
         tt = int(tensor_type)
-        if tt not in [int(t) for t in QUANTIZED]:
-            raise UnsupportedError("quantized_tensor_type", str(tt), [t.name for t in QUANTIZED])
+        if tt not in [int(t) for t in BLOCK_FORMATS]:
+            raise UnsupportedError("quantized_tensor_type", str(tt), [t.name for t in BLOCK_FORMATS])
         want = tensor_byte_len(tt, [ne0, ne1])
         if isinstance(blocks, np.ndarray):
             b = np.ascontiguousarray(blocks, dtype=np.uint8).reshape(-1)

@@ -5,6 +5,14 @@
 //   Q8_0  34 B / 32 weights : f16 d | i8 qs[32]
 //   Q4_K 144 B / 256 weights: f16 d | f16 dmin | u8 scales[12] | u8 qs[128]
 //   Q6_K 210 B / 256 weights: u8 ql[128] | u8 qh[64] | i8 scales[16] | f16 d
+// and, for dequantize / row gather only:
+//   Q4_0  18 B / 32 : f16 d | u8 qs[16]
+//   Q4_1  20 B / 32 : f16 d | f16 m | u8 qs[16]
+//   Q5_0  22 B / 32 : f16 d | u8 qh[4] | u8 qs[16]
+//   Q5_1  24 B / 32 : f16 d | f16 m | u8 qh[4] | u8 qs[16]
+//   Q2_K  84 B / 256: u8 scales[16] | u8 qs[64] | f16 d | f16 dmin
+//   Q3_K 110 B / 256: u8 hmask[32] | u8 qs[64] | u8 scales[12] | f16 d
+//   Q5_K 176 B / 256: f16 d | f16 dmin | u8 scales[12] | u8 qh[32] | u8 qs[128]
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -13,6 +21,10 @@ namespace okq {
 
 constexpr int kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
 constexpr int kQ8Bytes = 34, kQ4KBytes = 144, kQ6KBytes = 210;
+// Formats served by dequantize / row gather only (gguf_inspect.rs:170-206 ids).
+constexpr int kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13;
+constexpr int kQ40Bytes = 18, kQ41Bytes = 20, kQ50Bytes = 22, kQ51Bytes = 24, kQ2KBytes = 84, kQ3KBytes = 110,
+              kQ5KBytes = 176;
 
 __device__ __forceinline__ float as_f32(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t as_u32(float f) { return __float_as_uint(f); }

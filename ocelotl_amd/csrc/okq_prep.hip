@@ -54,11 +54,104 @@ __device__ __forceinline__ float dq_q6_k(const uint8_t *base, int64_t i) {
   return __fmul_rn(__fmul_rn(d, (float)sc), (float)q);
 }
 
+// ---- formats served by dequantize / row gather only ----------------------
+// Byte loads throughout: these blocks are only 2-byte aligned.
+
+// Fifth bit of element e (0..31) of a Q5_0 / Q5_1 block: bit e of the
+// little-endian 32-bit word qh.
+__device__ __forceinline__ uint32_t q5_bit(const uint8_t *qh, uint32_t e) { return (qh[e >> 3] >> (e & 7u)) & 1u; }
+
+// The 4-bit code of element e of a 16-byte qs run: low nibbles hold
+// elements 0..15, high nibbles 16..31.
+__device__ __forceinline__ uint32_t nib32(const uint8_t *qs, uint32_t e) { return (qs[e & 15u] >> ((e >> 4) * 4)) & 15u; }
+
+__device__ __forceinline__ float dq_q4_0(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 5) * kQ40Bytes;
+  const uint32_t e = (uint32_t)(i & 31);
+  const float d = f16_bits_exact(ld_u16(blk));
+  return __fmul_rn((float)((int)nib32(blk + 2, e) - 8), d);
+}
+
+__device__ __forceinline__ float dq_q4_1(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 5) * kQ41Bytes;
+  const uint32_t e = (uint32_t)(i & 31);
+  const float d = f16_bits_exact(ld_u16(blk)), m = f16_bits_exact(ld_u16(blk + 2));
+  return __fadd_rn(__fmul_rn((float)nib32(blk + 4, e), d), m);
+}
+
+__device__ __forceinline__ float dq_q5_0(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 5) * kQ50Bytes;
+  const uint32_t e = (uint32_t)(i & 31);
+  const float d = f16_bits_exact(ld_u16(blk));
+  const int q = (int)(nib32(blk + 6, e) | (q5_bit(blk + 2, e) << 4)) - 16;
+  return __fmul_rn((float)q, d);
+}
+
+__device__ __forceinline__ float dq_q5_1(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 5) * kQ51Bytes;
+  const uint32_t e = (uint32_t)(i & 31);
+  const float d = f16_bits_exact(ld_u16(blk)), m = f16_bits_exact(ld_u16(blk + 2));
+  const uint32_t q = nib32(blk + 8, e) | (q5_bit(blk + 4, e) << 4);
+  return __fadd_rn(__fmul_rn((float)q, d), m);
+}
+
+// Q2_K element r = 128h + 32j + s: 2-bit q = (qs[32h+s] >> 2j) & 3 and scale
+// byte scales[r/16] (low nibble scale, high nibble min).
+__device__ __forceinline__ float dq_q2_k(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 8) * kQ2KBytes;
+  const uint32_t r = (uint32_t)(i & 255), h = r >> 7, j = (r >> 5) & 3u, s = r & 31u;
+  const uint32_t sc = blk[r >> 4];
+  const uint32_t q = (blk[16 + 32 * h + s] >> (2 * j)) & 3u;
+  const float d = f16_bits_exact(ld_u16(blk + 80)), dmin = f16_bits_exact(ld_u16(blk + 82));
+  const float dl = __fmul_rn(d, (float)(sc & 15u)), ml = __fmul_rn(dmin, (float)(sc >> 4));
+  return __fsub_rn(__fmul_rn(dl, (float)q), ml);
+}
+
+// Q3_K element r = 128h + 32j + s: low two bits (qs[32h+s] >> 2j) & 3, minus 4
+// when bit 4h+j of hmask[s] is clear; 6-bit scale r/16 unpacked from the 12
+// packed bytes (low nibble from byte is or is-8, top two bits from byte
+// 8 + is%4 at bit 2*(is/4)), biased by 32.
+__device__ __forceinline__ float dq_q3_k(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 8) * kQ3KBytes;
+  const uint32_t r = (uint32_t)(i & 255), h = r >> 7, j = (r >> 5) & 3u, s = r & 31u, is = r >> 4;
+  const uint8_t *sb = blk + 96;
+  const uint32_t lo = is < 8 ? (sb[is] & 15u) : (sb[is - 8] >> 4);
+  const uint32_t hi = (sb[8 + (is & 3u)] >> (2 * (is >> 2))) & 3u;
+  const int scale = (int)(lo | (hi << 4)) - 32;
+  const int q = (int)((blk[32 + 32 * h + s] >> (2 * j)) & 3u) - (((blk[s] >> (4 * h + j)) & 1u) ? 0 : 4);
+  const float d = f16_bits_exact(ld_u16(blk + 108));
+  return __fmul_rn(__fmul_rn(d, (float)scale), (float)q);
+}
+
+// Q5_K element r = 64c + 32hi + l: the Q4_K nibble plus 16 when bit 2c+hi of
+// qh[l] is set; scales and mins as Q4_K.
+__device__ __forceinline__ float dq_q5_k(const uint8_t *base, int64_t i) {
+  const uint8_t *blk = base + (i >> 8) * kQ5KBytes;
+  const uint32_t r = (uint32_t)(i & 255), c = r >> 6, hi = (r >> 5) & 1u, l = r & 31u;
+  const uint8_t *sb = blk + 4;
+  const uint32_t s0 = sb[0] | (sb[1] << 8) | (sb[2] << 16) | ((uint32_t)sb[3] << 24);
+  const uint32_t s1 = sb[4] | (sb[5] << 8) | (sb[6] << 16) | ((uint32_t)sb[7] << 24);
+  const uint32_t s2 = sb[8] | (sb[9] << 8) | (sb[10] << 16) | ((uint32_t)sb[11] << 24);
+  uint32_t sc, m;
+  q4k_scale_min(2 * c + hi, s0, s1, s2, sc, m);
+  const uint32_t q = ((blk[48 + 32 * c + l] >> (4 * hi)) & 15u) + (((blk[16 + l] >> (2 * c + hi)) & 1u) << 4);
+  const float d = f16_bits_exact(ld_u16(blk)), dmin = f16_bits_exact(ld_u16(blk + 2));
+  const float ds = __fmul_rn(d, (float)sc), dm = __fmul_rn(dmin, (float)m);
+  return __fsub_rn(__fmul_rn(ds, (float)q), dm);
+}
+
 template <int kType>
 __device__ __forceinline__ float dq_elem(const uint8_t *base, int64_t i) {
   if constexpr (kType == kQ8_0) return dq_q8_0(base, i);
   else if constexpr (kType == kQ4_K) return dq_q4_k(base, i);
-  else return dq_q6_k(base, i);
+  else if constexpr (kType == kQ6_K) return dq_q6_k(base, i);
+  else if constexpr (kType == kQ4_0) return dq_q4_0(base, i);
+  else if constexpr (kType == kQ4_1) return dq_q4_1(base, i);
+  else if constexpr (kType == kQ5_0) return dq_q5_0(base, i);
+  else if constexpr (kType == kQ5_1) return dq_q5_1(base, i);
+  else if constexpr (kType == kQ2_K) return dq_q2_k(base, i);
+  else if constexpr (kType == kQ3_K) return dq_q3_k(base, i);
+  else return dq_q5_k(base, i);
 }
 
 template <int kType>
@@ -265,10 +358,13 @@ static inline unsigned grid_for(int64_t n, int threads) { return (unsigned)((n +
 
 hipError_t launch_dequantize(int type, const void *src, int64_t n, float *dst, hipStream_t s) {
   const uint8_t *p = static_cast<const uint8_t *>(src);
+  const dim3 grid(grid_for(n, 256));
   switch (type) {
-  case kQ8_0: launch_timed(dequant_kernel<kQ8_0>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
-  case kQ4_K: launch_timed(dequant_kernel<kQ4_K>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
-  case kQ6_K: launch_timed(dequant_kernel<kQ6_K>, dim3(grid_for(n, 256)), dim3(256), 0, s, p, n, dst); break;
+#define OKQ_DQ_CASE(T) \
+  case T: launch_timed(dequant_kernel<T>, grid, dim3(256), 0, s, p, n, dst); break;
+    OKQ_DQ_CASE(kQ8_0) OKQ_DQ_CASE(kQ4_K) OKQ_DQ_CASE(kQ6_K) OKQ_DQ_CASE(kQ4_0) OKQ_DQ_CASE(kQ4_1)
+    OKQ_DQ_CASE(kQ5_0) OKQ_DQ_CASE(kQ5_1) OKQ_DQ_CASE(kQ2_K) OKQ_DQ_CASE(kQ3_K) OKQ_DQ_CASE(kQ5_K)
+#undef OKQ_DQ_CASE
   default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -284,9 +380,11 @@ hipError_t launch_get_rows(int type, const void *w, int64_t row_bytes, int64_t n
     const dim3 grid(grid_for(ne0, 256), (unsigned)cnt);
     float *o = out + j0 * ne0;
     switch (type) {
-    case kQ8_0: hipLaunchKernelGGL(get_rows_kernel<kQ8_0>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
-    case kQ4_K: hipLaunchKernelGGL(get_rows_kernel<kQ4_K>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
-    case kQ6_K: hipLaunchKernelGGL(get_rows_kernel<kQ6_K>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
+#define OKQ_GR_CASE(T) \
+  case T: hipLaunchKernelGGL(get_rows_kernel<T>, grid, dim3(256), 0, s, p, row_bytes, ne0, g, o); break;
+      OKQ_GR_CASE(kQ8_0) OKQ_GR_CASE(kQ4_K) OKQ_GR_CASE(kQ6_K) OKQ_GR_CASE(kQ4_0) OKQ_GR_CASE(kQ4_1)
+      OKQ_GR_CASE(kQ5_0) OKQ_GR_CASE(kQ5_1) OKQ_GR_CASE(kQ2_K) OKQ_GR_CASE(kQ3_K) OKQ_GR_CASE(kQ5_K)
+#undef OKQ_GR_CASE
     default: return hipErrorInvalidValue;
     }
     hipError_t e = hipGetLastError();

@@ -37,26 +37,42 @@ okq_status ok() { return OKQ_OK; }
 
 struct TypeInfo {
   int64_t elems, bytes;
-  bool quantized;
+  bool quantized;  // block-encoded: dequantize and row gather serve it
+  bool linear;     // the linear kernels serve it (Q8_0, Q4_K, Q6_K)
 };
 
 bool type_info(uint32_t t, TypeInfo &ti) {
   switch (t) {
-  case OKQ_TYPE_Q8_0: ti = {32, 34, true}; return true;
-  case OKQ_TYPE_Q4_K: ti = {256, 144, true}; return true;
-  case OKQ_TYPE_Q6_K: ti = {256, 210, true}; return true;
-  case OKQ_TYPE_F32: ti = {1, 4, false}; return true;
-  case OKQ_TYPE_F16: ti = {1, 2, false}; return true;
-  case OKQ_TYPE_BF16: ti = {1, 2, false}; return true;
+  case OKQ_TYPE_Q8_0: ti = {32, 34, true, true}; return true;
+  case OKQ_TYPE_Q4_K: ti = {256, 144, true, true}; return true;
+  case OKQ_TYPE_Q6_K: ti = {256, 210, true, true}; return true;
+  case OKQ_TYPE_Q4_0: ti = {32, 18, true, false}; return true;
+  case OKQ_TYPE_Q4_1: ti = {32, 20, true, false}; return true;
+  case OKQ_TYPE_Q5_0: ti = {32, 22, true, false}; return true;
+  case OKQ_TYPE_Q5_1: ti = {32, 24, true, false}; return true;
+  case OKQ_TYPE_Q2_K: ti = {256, 84, true, false}; return true;
+  case OKQ_TYPE_Q3_K: ti = {256, 110, true, false}; return true;
+  case OKQ_TYPE_Q5_K: ti = {256, 176, true, false}; return true;
+  case OKQ_TYPE_F32: ti = {1, 4, false, false}; return true;
+  case OKQ_TYPE_F16: ti = {1, 2, false, false}; return true;
+  case OKQ_TYPE_BF16: ti = {1, 2, false, false}; return true;
   default: return false;
   }
 }
 
+// The reference's Debug names of GgmlTensorType (gguf_inspect.rs:132-167).
 const char *type_name(uint32_t t) {
   switch (t) {
   case OKQ_TYPE_Q8_0: return "Q8_0";
   case OKQ_TYPE_Q4_K: return "Q4K";
   case OKQ_TYPE_Q6_K: return "Q6K";
+  case OKQ_TYPE_Q4_0: return "Q4_0";
+  case OKQ_TYPE_Q4_1: return "Q4_1";
+  case OKQ_TYPE_Q5_0: return "Q5_0";
+  case OKQ_TYPE_Q5_1: return "Q5_1";
+  case OKQ_TYPE_Q2_K: return "Q2K";
+  case OKQ_TYPE_Q3_K: return "Q3K";
+  case OKQ_TYPE_Q5_K: return "Q5K";
   case OKQ_TYPE_F32: return "F32";
   case OKQ_TYPE_F16: return "F16";
   case OKQ_TYPE_BF16: return "BF16";
@@ -68,6 +84,17 @@ okq_status unsupported_type(uint32_t t, const char *what) {
   return fail(OKQ_E_TYPE, "unsupported %s: tensor type %s (%u); supported: Q8_0, Q4K, Q6K", what, type_name(t),
               t);
 }
+
+// Dequantize and row gather serve every block format above.
+okq_status unsupported_block_type(uint32_t t, const char *what) {
+  return fail(OKQ_E_TYPE,
+              "unsupported %s: tensor type %s (%u); supported: Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2K, Q3K, Q4K, Q5K, Q6K",
+              what, type_name(t), t);
+}
+
+// Q4_K blocks are read as dwords (16-byte aligned bases); every other block
+// format only needs the 2-byte alignment of its f16 fields.
+int block_alignment(uint32_t t) { return t == OKQ_TYPE_Q4_K ? 16 : 2; }
 
 bool mul_ok(int64_t a, int64_t b, int64_t &out) {
   if (a < 0 || b < 0) return false;
@@ -123,7 +150,7 @@ struct LinearArgs {
 // f32 weight length), then the block and 32-bit limits of the kernels.
 okq_status validate_linear(const void *x, const LinearArgs &a, const void *w, const void *out, bool x_bf16) {
   TypeInfo ti;
-  if (!type_info(a.type, ti) || !ti.quantized) return unsupported_type(a.type, "linear_out_by_in weight");
+  if (!type_info(a.type, ti) || !ti.linear) return unsupported_type(a.type, "linear_out_by_in weight");
   if (a.rows < 0 || a.K < 0 || a.N < 0)
     return fail(OKQ_E_SHAPE, "linear_out_by_in negative dimension rows=%lld in_features=%lld out_features=%lld",
                 (long long)a.rows, (long long)a.K, (long long)a.N);
@@ -402,14 +429,14 @@ okq_status okq_sync(void *stream) {
 
 okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float *dst, void *stream) {
   TypeInfo ti;
-  if (!type_info(ggml_type, ti) || !ti.quantized) return unsupported_type(ggml_type, "dequantize");
+  if (!type_info(ggml_type, ti) || !ti.quantized) return unsupported_block_type(ggml_type, "dequantize");
   if (n < 0 || n % ti.elems != 0)
     return fail(OKQ_E_SHAPE, "dequantize n=%lld is not a multiple of the %s block size %lld", (long long)n,
                 type_name(ggml_type), (long long)ti.elems);
   if (n == 0) return ok();
   if (!src || !dst) return fail(OKQ_E_ARG, "dequantize null pointer");
-  if (ggml_type == OKQ_TYPE_Q4_K ? (reinterpret_cast<uintptr_t>(src) & 15u) : (reinterpret_cast<uintptr_t>(src) & 1u))
-    return fail(OKQ_E_ALIGN, "dequantize source must be %d-byte aligned", ggml_type == OKQ_TYPE_Q4_K ? 16 : 2);
+  if (reinterpret_cast<uintptr_t>(src) % block_alignment(ggml_type))
+    return fail(OKQ_E_ALIGN, "dequantize source must be %d-byte aligned", block_alignment(ggml_type));
   if (reinterpret_cast<uintptr_t>(dst) & 3u) return fail(OKQ_E_ALIGN, "dequantize destination must be 4-byte aligned");
   int dev;
   DevInfo info;
@@ -422,7 +449,7 @@ okq_status okq_dequantize(uint32_t ggml_type, const void *src, int64_t n, float 
 okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int64_t ne0, int64_t ne1,
                           const uint32_t *ids, int64_t n_ids, float *out, void *stream) {
   TypeInfo ti;
-  if (!type_info(w_type, ti) || !ti.quantized) return unsupported_type(w_type, "get_rows weight");
+  if (!type_info(w_type, ti) || !ti.quantized) return unsupported_block_type(w_type, "get_rows weight");
   if (ne0 <= 0 || ne0 % ti.elems != 0)
     return fail(OKQ_E_SHAPE, "get_rows ne0=%lld is not a positive multiple of the %s block size %lld", (long long)ne0,
                 type_name(w_type), (long long)ti.elems);
@@ -441,8 +468,8 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
   for (int64_t j = 0; j < n_ids; ++j)
     if ((int64_t)ids[j] >= ne1)
       return fail(OKQ_E_ARG, "get_rows token id %u is out of range for vocab_size %lld", ids[j], (long long)ne1);
-  if (w_type == OKQ_TYPE_Q4_K ? (reinterpret_cast<uintptr_t>(w) & 15u) : (reinterpret_cast<uintptr_t>(w) & 1u))
-    return fail(OKQ_E_ALIGN, "get_rows weight must be %d-byte aligned", w_type == OKQ_TYPE_Q4_K ? 16 : 2);
+  if (reinterpret_cast<uintptr_t>(w) % block_alignment(w_type))
+    return fail(OKQ_E_ALIGN, "get_rows weight must be %d-byte aligned", block_alignment(w_type));
   if (reinterpret_cast<uintptr_t>(out) & 3u) return fail(OKQ_E_ALIGN, "get_rows out must be 4-byte aligned");
   int dev;
   DevInfo info;
@@ -655,7 +682,7 @@ okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, u
 
 okq_status okq_quantize(uint32_t ggml_type, const float *src, int64_t n, void *dst, void *stream) {
   TypeInfo ti;
-  if (!type_info(ggml_type, ti) || !ti.quantized) return unsupported_type(ggml_type, "quantize");
+  if (!type_info(ggml_type, ti) || !ti.linear) return unsupported_type(ggml_type, "quantize");
   if (n < 0 || n % ti.elems != 0)
     return fail(OKQ_E_SHAPE, "quantize n=%lld is not a multiple of the %s block size %lld", (long long)n,
                 type_name(ggml_type), (long long)ti.elems);

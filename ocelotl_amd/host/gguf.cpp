@@ -264,7 +264,28 @@ Result<uint64_t> alignment_from_metadata(const std::string &path, const std::vec
   return a;
 }
 
-const char *quant_name(uint32_t t) { return t == 8 ? "Q8_0" : t == 12 ? "Q4_K" : "Q6_K"; }
+// Block formats with a known layout: raw id, name, elements and bytes per block.
+struct BlockFormat {
+  uint32_t type;
+  const char *name;
+  uint64_t elems, bytes;
+};
+constexpr BlockFormat kBlockFormats[] = {{2, "Q4_0", 32, 18},   {3, "Q4_1", 32, 20},   {6, "Q5_0", 32, 22},
+                                         {7, "Q5_1", 32, 24},   {8, "Q8_0", 32, 34},   {10, "Q2_K", 256, 84},
+                                         {11, "Q3_K", 256, 110}, {12, "Q4_K", 256, 144}, {13, "Q5_K", 256, 176},
+                                         {14, "Q6_K", 256, 210}};
+
+const BlockFormat *block_format(uint32_t t) {
+  for (const BlockFormat &f : kBlockFormats)
+    if (f.type == t) return &f;
+  return nullptr;
+}
+
+const std::vector<std::string> &block_format_names() {
+  static const std::vector<std::string> v = {"Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0",
+                                             "Q2K",  "Q3K",  "Q4K",  "Q5K",  "Q6K"};
+  return v;
+}
 
 }  // namespace
 
@@ -297,16 +318,13 @@ ByteLen gguf_byte_len(uint32_t type, const std::vector<uint64_t> &shape) {
     if (!mul_ok(count, elem, out)) return {std::nullopt, "byte length overflows u64"};
     return {out, ""};
   }
-  uint64_t block_elems = 0, block_bytes = 0;
-  if (type == 8) block_elems = 32, block_bytes = 34;
-  else if (type == 12) block_elems = 256, block_bytes = 144;
-  else if (type == 14) block_elems = 256, block_bytes = 210;
-  else return {std::nullopt, ""};  // other block formats: not executed by this path
-  if (shape.empty() || shape[0] % block_elems != 0)
+  const BlockFormat *bf = block_format(type);
+  if (!bf) return {std::nullopt, ""};  // Q8_1, Q8_K, the IQ and TQ formats: layout not known here
+  if (shape.empty() || shape[0] % bf->elems != 0)
     return {std::nullopt, std::string("row of ") + std::to_string(shape.empty() ? 0 : shape[0]) +
-                              " elements is not a multiple of the " + quant_name(type) + " block size " +
-                              std::to_string(block_elems)};
-  if (!mul_ok(count / block_elems, block_bytes, out)) return {std::nullopt, "byte length overflows u64"};
+                              " elements is not a multiple of the " + bf->name + " block size " +
+                              std::to_string(bf->elems)};
+  if (!mul_ok(count / bf->elems, bf->bytes, out)) return {std::nullopt, "byte length overflows u64"};
   return {out, ""};
 }
 
@@ -430,7 +448,7 @@ Result<std::vector<uint8_t>> read_tensor_bytes(const std::string &path, const Gg
                                                const GgufTensorEntry &entry) {
   if (!entry.byte_len)
     return OcelotlError::unsupported("quantized_tensor_type", std::to_string(entry.tensor_type),
-                                     {"Q8_0", "Q4K", "Q6K"});
+                                     block_format_names());
   (void)manifest;
   Fd f;
   f.fd = open(path.c_str(), O_RDONLY | O_CLOEXEC);
@@ -454,8 +472,8 @@ Result<QuantizedWeight> load_quantized_weight(const HipKernelBackend &backend, c
                                               const GgufManifest &manifest, const std::string &name) {
   const GgufTensorEntry *t = manifest.tensor(name);
   if (!t) return invalid(path, name, "GGUF tensor `" + name + "` not found");
-  if (t->tensor_type != 8 && t->tensor_type != 12 && t->tensor_type != 14)
-    return OcelotlError::unsupported("quantized_tensor_type", std::to_string(t->tensor_type), {"Q8_0", "Q4K", "Q6K"});
+  if (!block_format(t->tensor_type))
+    return OcelotlError::unsupported("quantized_tensor_type", std::to_string(t->tensor_type), block_format_names());
   uint64_t ne1 = 1;
   for (size_t d = 1; d < t->shape.size(); ++d) ne1 *= t->shape[d];  // no overflow: checked by inspect_gguf
   auto bytes = read_tensor_bytes(path, manifest, *t);

@@ -70,7 +70,8 @@ struct GgufManifest {
 
 // Byte length of a tensor of raw type `type` and ne-order `shape`: element
 // size times count for the fixed-size types of fixed_element_size, whole
-// blocks for Q8_0 / Q4_K / Q6_K, nullopt for the other block formats.  A
+// blocks for Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K and Q6_K,
+// nullopt for the other block formats (Q8_1, Q8_K, IQ*, TQ*, MXFP4).  A
 // quantized row that is not a whole number of blocks is an error string.
 struct ByteLen {
   std::optional<uint64_t> bytes;

@@ -20,8 +20,19 @@ const std::vector<std::string> &quantized_names() {
   return v;
 }
 
-bool is_quantized(GgmlTensorType t) {
-  return t == GgmlTensorType::Q8_0 || t == GgmlTensorType::Q4K || t == GgmlTensorType::Q6K;
+const std::vector<std::string> &block_format_names() {
+  static const std::vector<std::string> v = {"Q4_0", "Q4_1", "Q5_0", "Q5_1", "Q8_0",
+                                             "Q2K",  "Q3K",  "Q4K",  "Q5K",  "Q6K"};
+  return v;
+}
+
+bool is_block_format(GgmlTensorType t) {
+  switch (t) {
+  case GgmlTensorType::Q4_0: case GgmlTensorType::Q4_1: case GgmlTensorType::Q5_0: case GgmlTensorType::Q5_1:
+  case GgmlTensorType::Q8_0: case GgmlTensorType::Q2K: case GgmlTensorType::Q3K: case GgmlTensorType::Q4K:
+  case GgmlTensorType::Q5K: case GgmlTensorType::Q6K: return true;
+  default: return false;
+  }
 }
 
 std::string last_error() {
@@ -192,8 +203,8 @@ Result<DeviceTensor> HipKernelBackend::upload(const float *host, size_t len) con
 
 Result<QuantizedWeight> HipKernelBackend::upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1,
                                                            const uint8_t *blocks, size_t len) const {
-  if (!is_quantized(type))
-    return OcelotlError::unsupported("quantized_tensor_type", std::to_string((uint32_t)type), quantized_names());
+  if (!is_block_format(type))
+    return OcelotlError::unsupported("quantized_tensor_type", std::to_string((uint32_t)type), block_format_names());
   auto want = tensor_byte_len(type, {(int64_t)ne0, (int64_t)ne1});
   if (want.is_err()) return want.error();
   if (len != want.value()) {

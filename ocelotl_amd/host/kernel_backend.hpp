@@ -129,8 +129,23 @@ struct KernelContext {
 };
 
 // Raw GGML tensor type ids (crates/loader/src/gguf_inspect.rs:170-206): the
-// quantized types this path executes plus the unquantized float types.
-enum class GgmlTensorType : uint32_t { F32 = 0, F16 = 1, Q8_0 = 8, Q4K = 12, Q6K = 14, BF16 = 30 };
+// block formats this path dequantizes and gathers (the linear kernels execute
+// Q8_0, Q4K and Q6K) plus the unquantized float types.
+enum class GgmlTensorType : uint32_t {
+  F32 = 0,
+  F16 = 1,
+  Q4_0 = 2,
+  Q4_1 = 3,
+  Q5_0 = 6,
+  Q5_1 = 7,
+  Q8_0 = 8,
+  Q2K = 10,
+  Q3K = 11,
+  Q4K = 12,
+  Q5K = 13,
+  Q6K = 14,
+  BF16 = 30
+};
 
 // (elements, bytes) per block: the byte_len that GgmlTensorType::
 // fixed_element_size leaves as None for quantized types (gguf_inspect.rs:208-219).
@@ -227,7 +242,8 @@ class HipKernelBackend final : public KernelBackend {
                         size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const override;
 
   // Uploads raw GGUF blocks after checking their byte length against the
-  // shape; only Q8_0 / Q4_K / Q6_K are accepted (Unsupported otherwise).
+  // shape; any block format is accepted (Unsupported otherwise).  linear_d
+  // takes Q8_0 / Q4K / Q6K weights, dequantize and embedding_rows all of them.
   Result<QuantizedWeight> upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1, const uint8_t *blocks,
                                            size_t len) const;
   // The weight dequantized to f32 (bit-exact with the CPU definition).

@@ -224,10 +224,13 @@ void quantized_byte_lengths_are_known_and_range_checked() {
   } ts[] = {{"a.q8_0", {64, 3}, 8, 3 * 2 * 34},
             {"b.q4_k", {512, 5}, 12, 5 * 2 * 144},
             {"c.q6_k", {256, 7}, 14, 7 * 210},
-            {"d.q5_k", {256, 2}, 13, 0}};  // another block format: length unknown, as in the reference
+            {"d.q5_k", {256, 2}, 13, 2 * 176},
+            {"e.q4_0", {96, 2}, 2, 2 * 3 * 18},
+            {"f.q3_k", {512, 1}, 11, 2 * 110},
+            {"g.q8_1", {64, 2}, 9, 0}};  // no block layout here: length unknown, as in the reference
   Writer w;
   w.b = {'G', 'G', 'U', 'F'};
-  w.u32(3), w.u64(4), w.u64(0);
+  w.u32(3), w.u64(7), w.u64(0);
   uint64_t off = 0;
   for (const T &t : ts) {
     w.tensor(t.name, t.shape, t.type, off);
@@ -237,13 +240,13 @@ void quantized_byte_lengths_are_known_and_range_checked() {
   w.b.insert(w.b.end(), off, 0);
   w.write(p);
   GgufManifest m = ok(inspect_gguf(p), "inspect quantized");
-  for (size_t i = 0; i < 3; ++i) {
+  for (size_t i = 0; i < 6; ++i) {
     CHECK(m.tensors[i].byte_len && *m.tensors[i].byte_len == ts[i].bytes, ts[i].name);
     auto b = tensor_byte_len(static_cast<GgmlTensorType>(ts[i].type),
                              {(int64_t)ts[i].shape[0], (int64_t)ts[i].shape[1]});
     CHECK(b.is_ok() && b.value() == ts[i].bytes, "agrees with okq_tensor_bytes");
   }
-  CHECK(!m.tensors[3].byte_len, "Q5_K length unknown");
+  CHECK(!m.tensors[6].byte_len, "Q8_1 length unknown");
   // the same file cut short: the last quantized tensor no longer fits
   Writer cut = w;
   cut.b.resize(cut.b.size() - off + ts[0].bytes + 32 + ts[1].bytes);

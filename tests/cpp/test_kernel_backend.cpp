@@ -101,14 +101,18 @@ void block_info_matches_gguf_block_sizes() {
   struct Case { GgmlTensorType t; int64_t e, b; };
   for (Case c : {Case{GgmlTensorType::Q8_0, 32, 34}, Case{GgmlTensorType::Q4K, 256, 144},
                  Case{GgmlTensorType::Q6K, 256, 210}, Case{GgmlTensorType::F32, 1, 4},
-                 Case{GgmlTensorType::F16, 1, 2}, Case{GgmlTensorType::BF16, 1, 2}}) {
+                 Case{GgmlTensorType::F16, 1, 2}, Case{GgmlTensorType::BF16, 1, 2},
+                 Case{GgmlTensorType::Q4_0, 32, 18}, Case{GgmlTensorType::Q4_1, 32, 20},
+                 Case{GgmlTensorType::Q5_0, 32, 22}, Case{GgmlTensorType::Q5_1, 32, 24},
+                 Case{GgmlTensorType::Q2K, 256, 84}, Case{GgmlTensorType::Q3K, 256, 110},
+                 Case{GgmlTensorType::Q5K, 256, 176}}) {
     auto info = ok(block_info(c.t), "block_info");
     CHECK(info.first == c.e && info.second == c.b, "block sizes");
   }
-  auto q4_0 = block_info((GgmlTensorType)2);  // Q4_0: named by the loader, not executed here
-  CHECK(q4_0.is_err(), "Q4_0 must be unsupported");
-  CHECK(q4_0.error().kind() == OcelotlError::Kind::Unsupported, "Q4_0 error kind");
-  CHECK(q4_0.error().as_unsupported()->feature == "quantized_tensor_type", "Q4_0 feature");
+  auto q8_1 = block_info((GgmlTensorType)9);  // Q8_1: named by the loader, no block format here
+  CHECK(q8_1.is_err(), "Q8_1 must be unsupported");
+  CHECK(q8_1.error().kind() == OcelotlError::Kind::Unsupported, "Q8_1 error kind");
+  CHECK(q8_1.error().as_unsupported()->feature == "quantized_tensor_type", "Q8_1 feature");
 }
 
 void tensor_byte_len_of_the_gemma4_fixture_tensor() {

@@ -39,7 +39,8 @@ def test_backend_name():
 
 
 @pytest.mark.parametrize("t,elems,nbytes", [(8, 32, 34), (12, 256, 144), (14, 256, 210), (0, 1, 4), (1, 1, 2),
-                                            (30, 1, 2)])
+                                            (30, 1, 2), (2, 32, 18), (3, 32, 20), (6, 32, 22), (7, 32, 24),
+                                            (10, 256, 84), (11, 256, 110), (13, 256, 176)])
 def test_type_info(okqlib, t, elems, nbytes):
     e, b = ctypes.c_int64(), ctypes.c_int64()
     assert okqlib.okq_type_info(t, ctypes.byref(e), ctypes.byref(b)) == okq.OK
@@ -48,8 +49,9 @@ def test_type_info(okqlib, t, elems, nbytes):
 
 def test_unknown_type_is_unsupported(okqlib):
     e, b = ctypes.c_int64(), ctypes.c_int64()
-    assert okqlib.okq_type_info(13, ctypes.byref(e), ctypes.byref(b)) == okq.E_TYPE  # Q5K: not this path
-    assert "Q5" in okq.last_error() or "13" in okq.last_error()
+    assert okqlib.okq_type_info(9, ctypes.byref(e), ctypes.byref(b)) == okq.E_TYPE  # Q8_1: no block format here
+    assert "(9)" in okq.last_error()
+    assert okqlib.okq_type_info(99, ctypes.byref(e), ctypes.byref(b)) == okq.E_TYPE
 
 
 def test_row_and_tensor_bytes(okqlib):
@@ -80,8 +82,10 @@ def test_linear_validation_happens_before_launch(okqlib):
     assert "does not match out_features*row_bytes" in okq.last_error()
     # in_features must be block aligned
     assert _linear(okqlib, 1, 4000, 12, 0, 10) == okq.E_SHAPE
-    # unsupported type -> Unsupported
-    assert _linear(okqlib, 1, 4096, 13, 0, 10) == okq.E_TYPE
+    # unsupported type -> Unsupported: the dequantize-only block formats too
+    for t in (2, 3, 6, 7, 10, 11, 13, 0, 9):
+        assert _linear(okqlib, 1, 4096, t, 0, 10) == okq.E_TYPE
+        assert "supported: Q8_0, Q4K, Q6K" in okq.last_error()
     # rows == 0 is a no-op even with null pointers (reference accepts empty slices)
     assert okqlib.okq_linear_out_by_in_q(None, 0, 4096, 12, None, 2304 * 10, 10, None, None, None) == okq.OK
     # null pointers with work to do
@@ -105,8 +109,9 @@ def test_compute_without_gpu_reports_nodev(okqlib):
 def test_python_mirror_maps_errors():
     from ocelotl_amd import backend as B
     with pytest.raises(B.UnsupportedError):
-        B.block_info(13)
+        B.block_info(9)  # Q8_1: no block format here
     assert B.block_info(B.GgmlTensorType.Q6K) == (256, 210)
+    assert B.block_info(B.GgmlTensorType.Q5K) == (256, 176)
     assert B.tensor_byte_len(B.GgmlTensorType.Q4K, [4096, 14336]) == 14336 * 2304
     with pytest.raises(B.KernelError) as ei:
         B.tensor_byte_len(B.GgmlTensorType.Q4K, [4000, 2])

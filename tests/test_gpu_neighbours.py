@@ -83,6 +83,27 @@ def test_get_rows_bit_exact(torch, okq, orc, t, ne0, ne1, n):
     assert _same_bits(got, table[np.asarray(ids)]).all()
 
 
+@pytest.mark.parametrize("t", [t for t in O.GATHER_TYPES if t not in TYPES])
+@pytest.mark.parametrize("ne0,ne1,n", [(256, 5, 4), (2560, 48, 97)])
+def test_get_rows_other_block_formats_bit_exact(torch, okq, orc, t, ne0, ne1, n):
+    """The dequantize-only formats (Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K)
+    gather bit-exactly too.  The oracle has no quantizer for them, so the table
+    is random block bytes with every f16 field forced finite (exponent < 31)."""
+    print(f"[gpu] get_rows other type={t} ne0={ne0} ne1={ne1} n={n}", flush=True)
+    rng = np.random.default_rng(7200 + t + ne0)
+    nb = ne0 * ne1 // O.BLOCK_ELEMS[t]
+    wq = rng.integers(0, 256, nb * O.BLOCK_BYTES[t], dtype=np.uint8).reshape(nb, O.BLOCK_BYTES[t])
+    for off in O.F16_FIELDS[t]:
+        wq[:, off + 1] &= 0x7B  # clear one exponent bit: finite halves only
+    wq = wq.reshape(-1)
+    table = orc.dequantize(t, wq, ne0 * ne1).reshape(ne1, ne0)
+    assert np.isfinite(table).all()
+    ids = list(rng.integers(0, ne1, n))
+    ids[0], ids[-1] = ne1 - 1, 0
+    got = _get_rows(torch, okq, t, wq, ne0, ne1, ids)
+    assert _same_bits(got, table[np.asarray(ids)]).all()
+
+
 def test_get_rows_rejects_out_of_range_ids_before_launch(torch, okq, orc):
     ne0, ne1 = 256, 4
     wq = orc.quantize(O.Q4_K, orc.normal(7100, ne0 * ne1, 0.02))

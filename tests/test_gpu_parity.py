@@ -71,7 +71,7 @@ def gpu_linear(torch, okq, t, x, rows, k, wq, n, bias=None, entry="okq_linear_ou
 # bit-exact data-path kernels
 # ---------------------------------------------------------------------------
 
-@pytest.mark.parametrize("t", TYPES)
+@pytest.mark.parametrize("t", O.GATHER_TYPES)
 def test_dequant_bit_exact_on_random_bytes(torch, okq, orc, t):
     print(f"[gpu] dequant random bytes type={t}", flush=True)
     rng = np.random.default_rng(10 + t)
