@@ -773,10 +773,20 @@ struct DecQ6K {
   }
 };
 
+// The activations arrive raw (f32 when kLo, else bf16): every workgroup
+// converts its own K slice, so no pre-pass launch precedes the kernel.  Each
+// row of the slice is scaled by 2^-s so its largest |x| lies in [512, 1024)
+// (rows of zeros, infinities or NaNs keep s = 0), as the tiled kernel's
+// pre-pass scales whole rows; the slice's outputs are multiplied back by 2^s
+// (exact), so split-K partials leave the kernel unscaled and
+// splitk_reduce_kernel only sums them in slice order and adds the bias.
+// (Reducing in the kernel instead -- the last workgroup of a column group to
+// count its arrival sums the partials -- needs a device-scope release per
+// workgroup, an L2 write-back that serialises per XCD: measured 1.5-2x
+// slower at the C5 shapes than the separate reduction launch.)
 template <class F, bool kLo, int RG>
 __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
-    const _Float16 *__restrict__ xhi, const _Float16 *__restrict__ xlo, const h2 *__restrict__ xsum,
-    const float *__restrict__ rscale, const uint8_t *__restrict__ W, const float *__restrict__ bias,
+    const void *__restrict__ X, const uint8_t *__restrict__ W, const float *__restrict__ bias,
     float *__restrict__ Y, int M, int N, int K, int ksplit, int groups, float *__restrict__ part) {
   constexpr int D = F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
@@ -792,9 +802,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   _Float16 *Al = Ah + (size_t)(M + 1) * P;
   _Float16 *Xs = Ah + (size_t)(M + 1) * P * (kLo ? 2 : 1);
   // unsplit K: the bias of the workgroup's columns (tile ti of every wave:
-  // columns (ti * groups + grp) * 256 + [0, 256)) and the row scales
+  // columns (ti * groups + grp) * 256 + [0, 256)); the rows' slice scales 2^s;
+  // the rows' slice maxima (|x| bits)
   float *Bs = reinterpret_cast<float *>(Xs + (size_t)(M + 1) * nsbs * 16);  // [kDecMaxTiles][256]
-  float *Rs = Bs + kDecMaxTiles * 256;                                      // [32]
+  float *Rs = Bs + kDecMaxTiles * 256;                                      // [kDecRows]
+  unsigned *Rmax = reinterpret_cast<unsigned *>(Rs + kDecRows);             // [kDecRows + 1]
+  if (tid <= M) Rmax[tid] = 0u;
 
   // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
   //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
@@ -820,49 +833,98 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     const uint32_t n = (uint32_t)(tile * 16 + cn);  // rows >= N read past the tensor: zeros
     F::load(it, rs_w, tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
   };
-  // 2. the activations of the slice: this thread's 16-byte pieces (at most
-  //    kDecStage; pieces past the rows read past the planes: zeros) and xsum
-  //    piece are loaded first, then the first D items' weights, then the
-  //    pieces go to LDS -- the vector-memory counter completes in order, so
-  //    the LDS writes wait for the activations only and the weights stay in
-  //    flight across the barrier.  Row M of the LDS planes is zeros.
+  // 2. the activations of the slice: this thread's pieces of 8 consecutive
+  //    activations of one row (at most kDecStage; pieces of row M and past it
+  //    read past x: zeros) are loaded first, then the first D items'
+  //    weights; the conversion waits for the activations only (the
+  //    vector-memory counter completes in order) and the weights stay in
+  //    flight across the barriers.
   const int pr = Ks / 8;  // pieces per row
-  const uint32_t plane_end = (uint32_t)((size_t)M * K * 2);
-  const Rsrc rs_xh = make_rsrc(xhi, plane_end);
-  const Rsrc rs_xl = make_rsrc(kLo ? xlo : xhi, plane_end);
-  const Rsrc rs_xs = make_rsrc(xsum, (uint32_t)((size_t)M * (K / 32) * 4));
-  u32x4 sh[kDecStage], sl[kLo ? kDecStage : 1];
+  const uint32_t x_end = (uint32_t)((size_t)M * K * (kLo ? 4 : 2));
+  const Rsrc rs_x = make_rsrc(X, x_end);
+  u32x4 xa[kDecStage], xb[kLo ? kDecStage : 1];  // f32: 2 x 4 values; bf16: 8 values
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
     const int p = tid + i * nt, r = p / pr, c = p - r * pr;
-    const uint32_t off = r < M ? ((uint32_t)r * (uint32_t)K + (uint32_t)sb0 * 256u + 8u * (uint32_t)c) * 2u : plane_end;
-    sh[i] = bload4(rs_xh, off);
-    if (kLo) sl[i] = bload4(rs_xl, off);
+    const uint32_t e = (uint32_t)r * (uint32_t)K + (uint32_t)sb0 * 256u + 8u * (uint32_t)c;  // first activation
+    if (kLo) {
+      xa[i] = bload4(rs_x, r < M ? e * 4u : x_end);
+      xb[i] = bload4(rs_x, r < M ? e * 4u + 16u : x_end);
+    } else {
+      xa[i] = bload4(rs_x, r < M ? e * 2u : x_end);
+    }
   }
-  const int xr = tid / (nsbs * 2), xrest = tid - xr * (nsbs * 2);  // 16 B = 4 (hi, lo) xsum pairs
-  const u32x4 sx = bload4(rs_xs, xr < M ? ((uint32_t)xr * (uint32_t)(K / 32) + (uint32_t)sb0 * 8u + 4u * (uint32_t)xrest) * 4u
-                                         : (uint32_t)((size_t)M * (K / 32) * 4));
-  // bias of the workgroup's columns and the row scales (unsplit K only)
+  // bias of the workgroup's columns (unsplit K only)
   const int bt = tid >> 8, bcol = ((bt * groups + grp) * kDecWaves) * 16 + (tid & 255);
   const uint32_t bias_end = bias ? (uint32_t)N * 4u : 0u;
   const uint32_t bbits = __builtin_amdgcn_raw_buffer_load_b32(
       make_rsrc(bias, bias_end), (ksplit == 1 && bt < kDecMaxTiles && bcol < N) ? (uint32_t)bcol * 4u : bias_end, 0, 0);
-  const uint32_t rbits = __builtin_amdgcn_raw_buffer_load_b32(
-      make_rsrc(rscale, (uint32_t)M * 4u), tid < M ? (uint32_t)tid * 4u : (uint32_t)M * 4u, 0, 0);
   Item S[D];
 #pragma unroll
   for (int j = 0; j < D; ++j) load(S[j], j);
   if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
-  if (tid < 32) Rs[tid] = __uint_as_float(rbits);
+  auto piece = [&](int i, float v[8]) {
+    if (kLo) {
+      v[0] = as_f32(xa[i].x), v[1] = as_f32(xa[i].y), v[2] = as_f32(xa[i].z), v[3] = as_f32(xa[i].w);
+      v[4] = as_f32(xb[i].x), v[5] = as_f32(xb[i].y), v[6] = as_f32(xb[i].z), v[7] = as_f32(xb[i].w);
+    } else {
+      v[0] = bf16_lo(xa[i].x), v[1] = bf16_hi(xa[i].x), v[2] = bf16_lo(xa[i].y), v[3] = bf16_hi(xa[i].y);
+      v[4] = bf16_lo(xa[i].z), v[5] = bf16_hi(xa[i].z), v[6] = bf16_lo(xa[i].w), v[7] = bf16_hi(xa[i].w);
+    }
+  };
+  __syncthreads();  // Rmax cleared
+  // the rows' slice maxima: the largest |x| of each piece (fmaxf drops NaNs),
+  // combined as bit patterns (monotonic for non-negative floats)
+#pragma unroll
+  for (int i = 0; i < kDecStage; ++i) {
+    const int p = tid + i * nt, r = p / pr;
+    float v[8];
+    piece(i, v);
+    float a = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
+    // the 32 pieces of lanes 0-31 (32-63) share one row (pieces per row and
+    // per workgroup are multiples of 32): one LDS atomic per half-wave
+#pragma unroll
+    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+    if ((lane & 31) == 0 && r < M && a > 0.0f) atomicMax(&Rmax[r], __float_as_uint(a));
+  }
+  __syncthreads();  // maxima complete
+  // scaled fp16 planes and per-32 sums (fixed order: the 8 values of a piece
+  // in order, then the 4 pieces of a run through DPP; a run's pieces sit in
+  // 4 consecutive lanes because pieces per row is a multiple of 4)
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
     const int p = tid + i * nt, r = p / pr, c = p - r * pr;
+    const float amax = r < M ? __uint_as_float(Rmax[r]) : 0.0f;
+    const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
+    float v[8];
+    piece(i, v);
+    h8 hv, lv;
+    float t = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float w = ldexpf(v[e], -sx);
+      t += w;
+      const _Float16 h = (_Float16)w;
+      hv[e] = h;
+      lv[e] = (_Float16)(w - (float)h);
+    }
+    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
     if (r <= M) {
-      *reinterpret_cast<u32x4 *>(Ah + (size_t)r * P + 8 * c) = sh[i];
-      if (kLo) *reinterpret_cast<u32x4 *>(Al + (size_t)r * P + 8 * c) = sl[i];
+      *reinterpret_cast<h8 *>(Ah + (size_t)r * P + 8 * c) = hv;
+      if (kLo) *reinterpret_cast<h8 *>(Al + (size_t)r * P + 8 * c) = lv;
+      if ((c & 3) == 0) {
+        const _Float16 sh = (_Float16)t;
+        h2 pair;
+        pair[0] = sh;
+        pair[1] = (_Float16)(t - (float)sh);
+        *reinterpret_cast<h2 *>(Xs + (size_t)r * nsbs * 16 + 2 * (c >> 2)) = pair;
+      }
+      if (c == 0 && r < M) Rs[r] = ldexpf(1.0f, sx);
     }
   }
-  if (xr <= M) *reinterpret_cast<u32x4 *>(Xs + ((size_t)xr * nsbs) * 16 + 8 * xrest) = sx;
   __syncthreads();
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -891,7 +953,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
 #pragma unroll
         for (int v = 0; v < 4; ++v) {
           const int row = 16 * q + 4 * g + v;
-          const float val = ksplit > 1 ? acc[q][v] : acc[q][v] * Rs[row] + bv;
+          // rows >= M read an unset Rs entry; the range check drops their stores
+          const float val = acc[q][v] * Rs[row] + bv;
           const uint32_t off = (row < M && col < N) ? (uint32_t)(((size_t)z * M + row) * N + col) * 4u : out_end;
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
         }
@@ -917,7 +980,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
 }
 
 // Sum of the split-K partials in slice order (deterministic), then the row
-// scale and the bias: Y[m, n] = (sum_z P[z][m, n]) * rscale[m] + bias[n].
+// scale (tiled kernel; the decode-batch kernel's partials are unscaled:
+// rscale == nullptr) and the bias: Y[m, n] = (sum_z P[z][m, n]) * rscale[m] + bias[n].
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int ksplit, int M, int N,
                                                             const float *__restrict__ rscale,
                                                             const float *__restrict__ bias, float *__restrict__ Y) {
@@ -927,7 +991,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   float acc = part[i];
   for (int z = 1; z < ksplit; ++z) acc += part[(size_t)z * total + i];
   const int m = (int)(i / N), n = (int)(i % N);
-  Y[i] = acc * rscale[m] + (bias ? bias[n] : 0.0f);
+  Y[i] = (rscale ? acc * rscale[m] : acc) + (bias ? bias[n] : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -956,11 +1020,11 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // sums), and at least enough slices x column groups for every CU.
     p.bm = kDecRows;
     const int64_t per_sb = (int64_t)(M + 1) * 256 * 2 * (x_is_bf16 ? 1 : 2) + (int64_t)(M + 1) * 32;
-    // slice bounds: the LDS budget, kDecStage pieces per thread ((M + 1) rows
-    // of 32 pieces per super-block) and one xsum piece per thread
+    // slice bounds: the LDS budget and kDecStage pieces of 8 activations per
+    // thread ((M + 1) rows of 32 pieces per super-block)
     const int64_t max_sb = std::max<int64_t>(
-        1, std::min<int64_t>({(kDecLdsBytes - (int64_t)(M + 1) * 16 * 2 * 2) / per_sb,
-                              (int64_t)kDecStage * kDecWaves * 64 / ((M + 1) * 32), (int64_t)kDecWaves * 64 / ((M + 1) * 2)}));
+        1, std::min<int64_t>((kDecLdsBytes - (int64_t)(M + 1) * 16 * 2 * 2) / per_sb,
+                             (int64_t)kDecStage * kDecWaves * 64 / ((M + 1) * 32)));
     const int64_t ntiles = (N + 15) / 16;
     // one workgroup (16 waves) per CU: column groups of 16 tiles, at most one
     // per CU (waves then take several tiles), and as many K slices as fit in
@@ -981,6 +1045,11 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   }
   p.ksplit = (int)std::max<int64_t>(1, ks);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
+  if (p.bm == kDecRows) {  // the decode-batch kernel needs only the split-K partials
+    p.off_lo = p.off_sums = p.off_rscale = p.off_part = 0;
+    p.workspace = p.ksplit > 1 ? up((size_t)p.ksplit * M * N * sizeof(float)) : 0;
+    return p;
+  }
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
   const size_t sums = (size_t)M * (size_t)(K / 32) * 2 * sizeof(_Float16);
   p.off_lo = up(plane);
@@ -996,6 +1065,38 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   if (type != kQ4_K && type != kQ6_K) return hipErrorInvalidValue;
   if (type == kQ6_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
+  const uint8_t *W = static_cast<const uint8_t *>(w);
+  const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
+  if (plan.bm == kDecRows) {
+    // the decode-batch kernel converts the activations itself: no pre-pass
+    if (M > kDecRows) return hipErrorInvalidValue;
+    float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
+    const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
+    const size_t lds = (size_t)(M + 1) * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) +
+                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
+    const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
+#define OKQ_DEC(F_, LO_, RG_)                                                                                      \
+  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, x, W, bias, y, m, n, k, ks,         \
+               plan.groups, part)
+#define OKQ_DEC_RG(F_, LO_)        \
+  if (M > 16) OKQ_DEC(F_, LO_, 2); \
+  else OKQ_DEC(F_, LO_, 1)
+    if (type == kQ6_K) {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
+      else OKQ_DEC_RG(DecQ6K, true);
+    } else {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
+      else OKQ_DEC_RG(DecQ4K, true);
+    }
+#undef OKQ_DEC_RG
+#undef OKQ_DEC
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || ks == 1) return e;
+    const int64_t total = M * N;
+    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m, n,
+                       static_cast<const float *>(nullptr), bias, y);
+    return hipGetLastError();
+  }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);
   h2 *xsum = reinterpret_cast<h2 *>(ws + plan.off_sums);
@@ -1009,30 +1110,6 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
                        rscale);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const uint8_t *W = static_cast<const uint8_t *>(w);
-  const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
-  if (plan.bm == kDecRows) {
-    if ((type != kQ4_K && type != kQ6_K) || M > kDecRows) return hipErrorInvalidValue;
-    const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
-    const size_t lds = (size_t)(M + 1) * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) +
-                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 32) * sizeof(float);
-    const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
-#define OKQ_DEC(F_, LO_, RG_)                                                                                      \
-  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, xhi, xlo, xsum, rscale, W, bias, y, m, \
-               n, k, ks, plan.groups, part)
-#define OKQ_DEC_RG(F_, LO_)        \
-  if (M > 16) OKQ_DEC(F_, LO_, 2); \
-  else OKQ_DEC(F_, LO_, 1)
-    if (type == kQ6_K) {
-      if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
-      else OKQ_DEC_RG(DecQ6K, true);
-    } else {
-      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
-      else OKQ_DEC_RG(DecQ4K, true);
-    }
-#undef OKQ_DEC_RG
-#undef OKQ_DEC
-  } else {
   const int tiles_n = (int)((N + kBN - 1) / kBN);
   const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);
   const int tiles = tiles_m * tiles_n;
@@ -1052,7 +1129,6 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     OKQ_GEMM(128, true, kQ4_K);
   }
 #undef OKQ_GEMM
-  }
   e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   const int64_t total = M * N;

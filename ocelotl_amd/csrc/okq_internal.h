@@ -75,10 +75,11 @@ hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *o
 
 // MFMA dequant-GEMM: Y[M, N] = bias + X[M, K] W[N, K]^T with X f32 or bf16.
 // How launch_gemm runs an (M, N, K) problem: tile rows, split-K factor and
-// the workspace layout (activation planes, per-32 sums, row scales, split-K
-// partials), 256-byte aligned offsets from the workspace base.
+// the workspace layout (tiled kernel: activation planes, per-32 sums, row
+// scales, split-K partials; decode-batch kernel: split-K partials only),
+// 256-byte aligned offsets from the workspace base.
 struct GemmPlan {
-  int bm;              // 16: the decode-batch kernel (M <= 16), else the tile height
+  int bm;              // 32: the decode-batch kernel (M <= 32), else the tile height
   int groups;          // decode-batch kernel: column groups per K slice
   int dec_wgs_per_cu;  // decode-batch kernel: workgroups per CU aimed for
   int ksplit;

@@ -184,6 +184,38 @@ def test_gemm_decode_batch_q6k_matches_reference(torch, okq, orc, entry, rows, n
     check_rows(orc, O.Q6_K, got, x32, rows, k, wq, n, bias, None if n * k <= 20_000_000 else 6)
 
 
+def test_gemm_decode_batch_split_k_repeat(torch, okq, orc):
+    """The decode-batch kernel scales each K slice of a row by its own power
+    of two and writes unscaled split-K partials, which the reduction sums in
+    slice order.  Many back-to-back launches on one stream, alternating
+    between problems with different column-group and slice counts (and so
+    sharing the stream's workspace), must each give the same bits as the
+    first launch of that problem, and match the reference."""
+    cases = [(O.Q4_K, 8, 14336, 4096), (O.Q6_K, 5, 4096, 14336), (O.Q4_K, 24, 1000, 2048), (O.Q6_K, 2, 333, 1280)]
+    stream = torch.cuda.current_stream().cuda_stream
+    prepared = []
+    for i, (t, rows, n, k) in enumerate(cases):
+        print(f"[gpu] gemm decode-batch split-K repeat type={t} M={rows} N={n} K={k}", flush=True)
+        wq = orc.quantize(t, orc.normal(1700 + i, n * k, 0.02))
+        x = orc.normal(1710 + i, rows * k, 1.0)
+        bias = orc.normal(1720 + i, n, 0.1)
+        dev = [torch.from_numpy(np.ascontiguousarray(a)).cuda() for a in (x, wq, bias)]
+        prepared.append((t, rows, n, k, wq, x, bias, dev))
+    outs = [[] for _ in cases]
+    for rep in range(12):
+        for i, (t, rows, n, k, wq, x, bias, (xd, wd, bd)) in enumerate(prepared):
+            out = torch.full((rows * n,), float("nan"), dtype=torch.float32, device="cuda")
+            okq.call("okq_gemm", xd.data_ptr(), rows, k, t, wd.data_ptr(), wq.size, n, bd.data_ptr(), out.data_ptr(),
+                     stream)
+            outs[i].append(out)
+    torch.cuda.synchronize()
+    for i, (t, rows, n, k, wq, x, bias, _) in enumerate(prepared):
+        first = outs[i][0].cpu().numpy()
+        for o in outs[i][1:]:
+            assert (o.cpu().numpy().view(np.uint32) == first.view(np.uint32)).all()
+        check_rows(orc, t, first.reshape(rows, n), x, rows, k, wq, n, bias, 4)
+
+
 def q4k_parts(orc, wq, n, k):
     """|d*sc*q| and |dmin*m| per weight: dequantizing with every 4-bit quant
     zeroed leaves exactly -dmin*m (Q4_K qs are bytes 16..143 of a block)."""
