@@ -797,17 +797,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
   const int nsbs = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;
   const int Ks = nsbs * 256, P = Ks + 8;  // slice width, LDS row pitch (halves)
-  // LDS: Ah [M + 1][P], Al [M + 1][P] (kLo), xs [M + 1][nsbs][16]; row M is zeros
+  // LDS: Ah [M][P], Al [M][P] (kLo), xs [M][nsbs][16]
   _Float16 *Ah = reinterpret_cast<_Float16 *>(dsm);
-  _Float16 *Al = Ah + (size_t)(M + 1) * P;
-  _Float16 *Xs = Ah + (size_t)(M + 1) * P * (kLo ? 2 : 1);
+  _Float16 *Al = Ah + (size_t)M * P;
+  _Float16 *Xs = Ah + (size_t)M * P * (kLo ? 2 : 1);
   // unsplit K: the bias of the workgroup's columns (tile ti of every wave:
   // columns (ti * groups + grp) * 256 + [0, 256)); the rows' slice scales 2^s;
   // the rows' slice maxima (|x| bits)
-  float *Bs = reinterpret_cast<float *>(Xs + (size_t)(M + 1) * nsbs * 16);  // [kDecMaxTiles][256]
+  float *Bs = reinterpret_cast<float *>(Xs + (size_t)M * nsbs * 16);  // [kDecMaxTiles][256]
   float *Rs = Bs + kDecMaxTiles * 256;                                      // [kDecRows]
   unsigned *Rmax = reinterpret_cast<unsigned *>(Rs + kDecRows);             // [kDecRows + 1]
-  if (tid <= M) Rmax[tid] = 0u;
+  if (tid < M) Rmax[tid] = 0u;
 
   // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
   //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
@@ -820,10 +820,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
   const uint32_t w_end = (uint32_t)((size_t)N * row_bytes);
   const Rsrc rs_w = make_rsrc(W, w_end);
-  // A rows of the lane's row groups (the zero row past M)
+  // A rows of the lane's row groups.  Lanes whose 16-row group reaches past
+  // M read row M - 1: they only produce MFMA output rows >= M, which are
+  // never stored, so no zero row needs staging.
   int arow[RG];
 #pragma unroll
-  for (int q = 0; q < RG; ++q) arow[q] = (lane & 15) + 16 * q < M ? (lane & 15) + 16 * q : M;
+  for (int q = 0; q < RG; ++q) arow[q] = (lane & 15) + 16 * q < M ? (lane & 15) + 16 * q : M - 1;
 
   using Item = typename F::Item;
   auto tile_of = [&](int u) { return (u / nsbs) * stride + first; };
@@ -834,8 +836,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     F::load(it, rs_w, tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
   };
   // 2. the activations of the slice: this thread's pieces of 8 consecutive
-  //    activations of one row (at most kDecStage; pieces of row M and past it
-  //    read past x: zeros) are loaded first, then the first D items'
+  //    activations of one row (at most kDecStage; pieces past the last row
+  //    read past x and are not stored) are loaded first, then the first D items'
   //    weights; the conversion waits for the activations only (the
   //    vector-memory counter completes in order) and the weights stay in
   //    flight across the barriers.
@@ -912,7 +914,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     }
     t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
     t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
-    if (r <= M) {
+    if (r < M) {
       *reinterpret_cast<h8 *>(Ah + (size_t)r * P + 8 * c) = hv;
       if (kLo) *reinterpret_cast<h8 *>(Al + (size_t)r * P + 8 * c) = lv;
       if ((c & 3) == 0) {
@@ -1016,15 +1018,15 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   int64_t ks = 1;
   if (M <= kDecRows) {
     // decode batch: the streaming kernel.  K slices small enough for the
-    // activations to fit the LDS budget (2 * (M + 1) planes of the slice plus
+    // activations to fit the LDS budget (M rows of 1 or 2 planes of the slice plus
     // sums), and at least enough slices x column groups for every CU.
     p.bm = kDecRows;
-    const int64_t per_sb = (int64_t)(M + 1) * 256 * 2 * (x_is_bf16 ? 1 : 2) + (int64_t)(M + 1) * 32;
+    const int64_t per_sb = (int64_t)M * 256 * 2 * (x_is_bf16 ? 1 : 2) + (int64_t)M * 32;
     // slice bounds: the LDS budget and kDecStage pieces of 8 activations per
-    // thread ((M + 1) rows of 32 pieces per super-block)
+    // thread (M rows of 32 pieces per super-block)
     const int64_t max_sb = std::max<int64_t>(
-        1, std::min<int64_t>((kDecLdsBytes - (int64_t)(M + 1) * 16 * 2 * 2) / per_sb,
-                             (int64_t)kDecStage * kDecWaves * 64 / ((M + 1) * 32)));
+        1, std::min<int64_t>((kDecLdsBytes - (int64_t)M * 16 * 2 * 2) / per_sb,
+                             (int64_t)kDecStage * kDecWaves * 64 / (M * 32)));
     const int64_t ntiles = (N + 15) / 16;
     // one workgroup (16 waves) per CU: column groups of 16 tiles, at most one
     // per CU (waves then take several tiles), and as many K slices as fit in
@@ -1072,8 +1074,8 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     if (M > kDecRows) return hipErrorInvalidValue;
     float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
     const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
-    const size_t lds = (size_t)(M + 1) * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) +
-                       (size_t)(M + 1) * nsbs_max * 32 + (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
+    const size_t lds = (size_t)M * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) + (size_t)M * nsbs_max * 32 +
+                       (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
     const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
 #define OKQ_DEC(F_, LO_, RG_)                                                                                      \
   launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, x, W, bias, y, m, n, k, ks,         \
