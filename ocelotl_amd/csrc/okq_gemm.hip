@@ -990,8 +990,17 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t total = (int64_t)M * N;
   if (i >= total) return;
-  float acc = part[i];
-  for (int z = 1; z < ksplit; ++z) acc += part[(size_t)z * total + i];
+  // the slices' loads go out eight at a time (not one round trip per slice);
+  // the sum runs in slice order from -0.0 (x + -0.0 == x, so p0 + p1 + ...)
+  float acc = -0.0f;
+  for (int z0 = 0; z0 < ksplit; z0 += 8) {
+    float v[8];
+#pragma unroll
+    for (int d = 0; d < 8; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+      if (z0 + d < ksplit) acc += v[d];
+  }
   const int m = (int)(i / N), n = (int)(i % N);
   Y[i] = (rscale ? acc * rscale[m] : acc) + (bias ? bias[n] : 0.0f);
 }
