@@ -861,9 +861,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   const uint32_t bias_end = bias ? (uint32_t)N * 4u : 0u;
   const uint32_t bbits = __builtin_amdgcn_raw_buffer_load_b32(
       make_rsrc(bias, bias_end), (ksplit == 1 && bt < kDecMaxTiles && bcol < N) ? (uint32_t)bcol * 4u : bias_end, 0, 0);
+  // A CU returns vector loads in issue order: without this bare barrier (no
+  // memory fence) a wave's activation loads would queue behind the weight
+  // items the workgroup's earlier waves already issued (~144 KB per CU,
+  // measured 8-14 us of staging); with it, every activation load of the
+  // workgroup is ahead of every weight load.
+  __builtin_amdgcn_s_barrier();
+  // Only the first item's weights go out before the staging: with all D
+  // items in flight the CU's vector-memory queue fills and waves stall at
+  // issue, so the staging barriers wait for weight traffic (measured 8-14
+  // us); the other D - 1 items are issued once the activations are staged.
   Item S[D];
-#pragma unroll
-  for (int j = 0; j < D; ++j) load(S[j], j);
+  load(S[0], 0);
   if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
   auto piece = [&](int i, float v[8]) {
     if (kLo) {
@@ -876,9 +885,14 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   };
   __syncthreads();  // Rmax cleared
   // the rows' slice maxima: the largest |x| of each piece (fmaxf drops NaNs),
-  // combined as bit patterns (monotonic for non-negative floats)
+  // combined as bit patterns (monotonic for non-negative floats).  Pieces
+  // past the last row are skipped (a uniform bound: i * nt >= M * pr).
+  auto dmax = [](float a, auto ctl) {
+    return fmaxf(a, as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(a), decltype(ctl)::value, 0xf, 0xf, false)));
+  };
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
+    if (i * nt >= M * pr) break;
     const int p = tid + i * nt, r = p / pr;
     float v[8];
     piece(i, v);
@@ -886,9 +900,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
 #pragma unroll
     for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
     // the 32 pieces of lanes 0-31 (32-63) share one row (pieces per row and
-    // per workgroup are multiples of 32): one LDS atomic per half-wave
-#pragma unroll
-    for (int o = 16; o >= 1; o >>= 1) a = fmaxf(a, __shfl_xor(a, o, 32));
+    // per workgroup are multiples of 32): the max of each 16-lane row by DPP,
+    // the two rows of a half-wave through readlane, one LDS atomic per
+    // half-wave
+    a = dmax(a, std::integral_constant<int, 0xB1>{});   // quad_perm 1,0,3,2
+    a = dmax(a, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
+    a = dmax(a, std::integral_constant<int, 0x141>{});  // row_half_mirror
+    a = dmax(a, std::integral_constant<int, 0x140>{});  // row_mirror
+    const float h0 = fmaxf(as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 0)),
+                           as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 16)));
+    const float h1 = fmaxf(as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 32)),
+                           as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 48)));
+    a = lane < 32 ? h0 : h1;
     if ((lane & 31) == 0 && r < M && a > 0.0f) atomicMax(&Rmax[r], __float_as_uint(a));
   }
   __syncthreads();  // maxima complete
@@ -897,6 +920,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   // 4 consecutive lanes because pieces per row is a multiple of 4)
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
+    if (i * nt >= M * pr) break;
     const int p = tid + i * nt, r = p / pr, c = p - r * pr;
     const float amax = r < M ? __uint_as_float(Rmax[r]) : 0.0f;
     const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
@@ -928,6 +952,8 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     }
   }
   __syncthreads();
+#pragma unroll
+  for (int j = 1; j < D; ++j) load(S[j], j);
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[RG];
