@@ -861,18 +861,17 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   const uint32_t bias_end = bias ? (uint32_t)N * 4u : 0u;
   const uint32_t bbits = __builtin_amdgcn_raw_buffer_load_b32(
       make_rsrc(bias, bias_end), (ksplit == 1 && bt < kDecMaxTiles && bcol < N) ? (uint32_t)bcol * 4u : bias_end, 0, 0);
-  // A CU returns vector loads in issue order: without this bare barrier (no
-  // memory fence) a wave's activation loads would queue behind the weight
-  // items the workgroup's earlier waves already issued (~144 KB per CU,
-  // measured 8-14 us of staging); with it, every activation load of the
-  // workgroup is ahead of every weight load.
+  // A CU returns vector loads in issue order: this bare barrier (no memory
+  // fence) puts every activation load of the workgroup ahead of every weight
+  // load, so no wave's activations queue behind another wave's weights.
   __builtin_amdgcn_s_barrier();
-  // Only the first item's weights go out before the staging: with all D
-  // items in flight the CU's vector-memory queue fills and waves stall at
-  // issue, so the staging barriers wait for weight traffic (measured 8-14
-  // us); the other D - 1 items are issued once the activations are staged.
+  // The weights wait for the staging: with the ring's D items in flight the
+  // CU's vector-memory queue fills and waves stall at issue, so the staging
+  // barriers waited for weight traffic (measured 8-14 us; with one item in
+  // flight 3-6 us).  Issuing them all after the staging is fastest overall
+  // (a wave's first item before the staging measured no better, even for the
+  // head's long streams).
   Item S[D];
-  load(S[0], 0);
   if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
   auto piece = [&](int i, float v[8]) {
     if (kLo) {
@@ -953,7 +952,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 1; j < D; ++j) load(S[j], j);
+  for (int j = 0; j < D; ++j) load(S[j], j);
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[RG];
