@@ -478,13 +478,19 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   }
   __builtin_amdgcn_s_barrier();
 
-  // 2. the first D rows of weights
+  // 2. the first D rows of weights.  Long (kDyn) launches issue them after
+  //    the activations are quantised instead, so no wave stalls at issue
+  //    behind a full vector-memory queue while the workgroup waits for its x
+  //    (measured: C2 step +2%, gate+up within run-to-run noise of 15.4-15.8
+  //    us); short launches lose 0.5-1 us that way and keep the early start.
   typename F::Regs S[D];
   float bs[D];
+  if constexpr (!kDyn) {
 #pragma unroll
-  for (int j = 0; j < D; ++j) {
-    wload(S[j], row_of(j));
-    bs[j] = bload(row_of(j));
+    for (int j = 0; j < D; ++j) {
+      wload(S[j], row_of(j));
+      bs[j] = bload(row_of(j));
+    }
   }
 
   // 3. (optional neighbour transform, then) quantise x into LDS while the
@@ -533,6 +539,13 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   if (kDyn && tid == 0) next_row = (unsigned)(D * G);
   __syncthreads();
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
+  if constexpr (kDyn) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      wload(S[j], row_of(j));
+      bs[j] = bload(row_of(j));
+    }
+  }
   XRec xreg[R];
 #pragma unroll
   for (int r = 0; r < R; ++r) xreg[r] = active ? xr[r * U + u] : XRec{};
