@@ -614,7 +614,9 @@ typedef float f4 __attribute__((ext_vector_type(4)));
 // first activation, `xs` at the row's xsum pairs of the super-block.
 struct DecQ4K {
   static constexpr uint32_t kBlk = kQ4KBytes;
-  static constexpr int kDepth = 3;
+  // items in flight per wave: 4 with one 16-row group (the Llama shapes give
+  // a wave 4 items, so all are issued at once), 3 with two (register budget)
+  static constexpr int kDepth = 3, kDepth1 = 4;
   struct Item {
     u32x4 hd, q0, q1;
   };
@@ -687,7 +689,7 @@ struct DecQ4K {
 
 struct DecQ6K {
   static constexpr uint32_t kBlk = kQ6KBytes;
-  static constexpr int kDepth = 2;
+  static constexpr int kDepth = 2, kDepth1 = 2;
   // Slice t = (half hh = t >> 2, quarter qq = t & 3); lane group g covers
   // l = 8g .. 8g + 7 of it: k = 128hh + 32qq + 8g + [0, 8), i.e. ql bytes
   // 64hh + 32(qq & 1) + 8g .. (nibble qq >> 1), qh bytes 128 + 32hh + 8g ..
@@ -788,7 +790,7 @@ template <class F, bool kLo, int RG>
 __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     const void *__restrict__ X, const uint8_t *__restrict__ W, const float *__restrict__ bias,
     float *__restrict__ Y, int M, int N, int K, int ksplit, int groups, float *__restrict__ part) {
-  constexpr int D = F::kDepth;
+  constexpr int D = RG == 1 ? F::kDepth1 : F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
