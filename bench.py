@@ -433,13 +433,14 @@ C5_HEAD = (Q6K, 128256, 4096)
 
 def run_c5(ctx: Ctx, args):
     """One step = every projection of 32 layers plus the Q6_K head, back to
-    back on one stream, replayed from a HIP graph.  `grouped`: the decode
-    launches an engine issues (q+k and gate+up share x in okq_gemv_multi,
-    each pass over a weight serving up to four rows); `auto`: one
-    okq_linear_out_by_in_q per projection, whose dispatch picks the kernel
-    by shape (the streaming decode-batch MFMA kernel for Q4_K/Q6_K weights of
+    back on one stream, replayed from a HIP graph.  `grouped`: the launches
+    an engine issues (q+k and gate+up share x in okq_gemv_multi, the other
+    projections through okq_linear_out_by_in_q); `auto`: one
+    okq_linear_out_by_in_q per projection.  Both dispatches pick the kernel
+    by shape: the streaming decode-batch MFMA kernel for Q4_K/Q6_K weights of
     16 MB and more from five rows, and for every Q4_K/Q6_K weight above eight
-    rows; the multi-row GEMV otherwise)."""
+    rows; the GEMV otherwise (okq_gemv_multi's matrices that stay on the GEMV
+    share one launch, each pass over a weight serving up to four rows)."""
     torch = ctx.torch
     log(f"C5: generating {C5_LAYERS} Q4_K_M layers + Q6_K head")
     layers = [{name: ctx.quantized(t, n, k, seed=50_000 + 100 * l + i) for i, (name, t, n, k) in enumerate(C5_PROJ)}
@@ -473,18 +474,18 @@ def run_c5(ctx: Ctx, args):
             for lay in layers:
                 if mode == "grouped":
                     group(["q", "k"], lay, s)
-                    one("okq_gemv", "v", lay["v"], s)
-                    one("okq_gemv", "o", lay["o"], s)
+                    one("okq_linear_out_by_in_q", "v", lay["v"], s)
+                    one("okq_linear_out_by_in_q", "o", lay["o"], s)
                     group(["gate", "up"], lay, s)
-                    one("okq_gemv", "down", lay["down"], s)
+                    one("okq_linear_out_by_in_q", "down", lay["down"], s)
                 else:
                     for name, _, _, _ in C5_PROJ:
                         one("okq_linear_out_by_in_q", name, lay[name], s)
             t, n, k = C5_HEAD
-            entry = "okq_gemv" if mode == "grouped" else "okq_linear_out_by_in_q"
-            ctx.okq.call(entry, x4.data_ptr(), rows, k, t, head.data_ptr(), head.numel(), n, None, yh.data_ptr(), s)
+            ctx.okq.call("okq_linear_out_by_in_q", x4.data_ptr(), rows, k, t, head.data_ptr(), head.numel(), n, None,
+                         yh.data_ptr(), s)
 
-        modes = ["grouped"] if rows == 1 else (["grouped", "auto"] if rows == 8 else ["auto"])
+        modes = ["grouped"] if rows == 1 else ["grouped", "auto"]
         for mode in modes:
             with torch.cuda.stream(cs):
                 step(mode, cs.cuda_stream)  # warm: allocates the GEMM workspace of this stream

@@ -161,8 +161,12 @@ okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, u
  * out_features[i] rows (w_bytes[i] bytes).  The decode GEMV streams the
  * matrices' concatenated rows in one launch per activation row, quantizing x
  * once.  `bias` may be NULL (no bias anywhere) or hold NULL entries.  Each
- * matrix is validated like okq_gemv before anything launches; results equal
- * okq_gemv's on each matrix bit for bit.  No counterpart in the reference,
+ * matrix is validated like okq_gemv before anything launches.  A matrix that
+ * okq_linear_out_by_in_q would not give to the GEMV at this row count (Q4_K /
+ * Q6_K weights of 16 MB or more from 5 rows, every Q4_K / Q6_K weight above
+ * 8 rows) is computed by that entry point's MFMA kernels instead, on its own;
+ * every output equals okq_linear_out_by_in_q's on its matrix bit for bit (and
+ * okq_gemv's wherever the GEMV serves it).  No counterpart in the reference,
  * whose callers compute such groups one projection at a time: the gate/up
  * pair of mlp_gated_silu (crates/kernels/src/lib.rs:150-162,
  * crates/kernels/src/mlp.rs:139-250) and the q/k/v projections of one

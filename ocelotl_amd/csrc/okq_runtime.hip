@@ -518,8 +518,33 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
   hipStream_t s = static_cast<hipStream_t>(stream);
   const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
   const float *const *b = bias ? bias : nobias;
-  hipError_t e = okq::launch_gemv_multi((int)w_type, x, in_features, rows, count, w, out_features, b, out,
-                                        info.cu_count, s, okq::GemvPro{});
+  // A matrix that the linear dispatch would not give to the GEMV at this row
+  // count (large Q4_K / Q6_K weights from kDecMinRows rows, every Q4_K / Q6_K
+  // weight above kGemvMaxRows) runs through that dispatch on its own (the
+  // decode-batch or tiled MFMA kernel); the others share one GEMV launch.
+  // Either way each output equals okq_linear_out_by_in_q's on its matrix.
+  const void *gw[okq::kGemvMaxProblems];
+  int64_t gn[okq::kGemvMaxProblems];
+  const float *gb[okq::kGemvMaxProblems];
+  float *go[okq::kGemvMaxProblems];
+  int shared = 0;
+  for (int i = 0; i < count; ++i) {
+    if (rows > 0 && out_features[i] > 0 && !gemv_serves(w_type, rows, w_bytes[i]) &&
+        okq::gemm_supported((int)w_type, rows, in_features, out_features[i])) {
+      st = linear_impl(x, false, rows, in_features, w_type, w[i], w_bytes[i], out_features[i], b[i], out[i], stream,
+                       Path::Auto);
+      if (st != OKQ_OK) return st;
+      continue;
+    }
+    gw[shared] = w[i];
+    gn[shared] = out_features[i];
+    gb[shared] = b[i];
+    go[shared] = out[i];
+    ++shared;
+  }
+  if (shared == 0) return ok();
+  hipError_t e = okq::launch_gemv_multi((int)w_type, x, in_features, rows, shared, gw, gn, gb, go, info.cu_count, s,
+                                        okq::GemvPro{});
   return hip_status(e, "gemv_multi launch");
 }
 

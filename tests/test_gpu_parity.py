@@ -372,6 +372,46 @@ def test_gemv_multi_equals_single_gemvs_bit_for_bit(torch, okq, orc, t, rows, k,
         assert ok, f"matrix {i} idx={idx} max_abs={dmax}"
 
 
+MULTI_BATCH_CASES = [
+    (O.Q4_K, 8, 4096, [14336, 14336]),       # gate/up at 8 rows: each on the decode-batch kernel
+    (O.Q4_K, 8, 4096, [4096, 1024, 14336]),  # q and k share the GEMV launch, the large one goes alone
+    (O.Q6_K, 24, 1024, [33, 300]),           # above 8 rows: every Q6_K matrix on the MFMA path
+    (O.Q8_0, 12, 1024, [100, 64]),           # Q8_0 stays on the GEMV at any row count
+]
+
+
+@pytest.mark.parametrize("t,rows,k,ns", MULTI_BATCH_CASES)
+def test_gemv_multi_batches_route_like_the_linear_dispatch(torch, okq, orc, t, rows, k, ns):
+    """At decode-batch row counts okq_gemv_multi sends every matrix to the
+    kernel okq_linear_out_by_in_q would pick for it: outputs equal that entry
+    point's, matrix by matrix, bit for bit, and the reference within the rule."""
+    import ctypes
+    print(f"[gpu] gemv_multi batch type={t} rows={rows} K={k} N={ns}", flush=True)
+    wqs = [orc.quantize(t, orc.normal(4300 + 17 * i + t, n * k, 0.02)) for i, n in enumerate(ns)]
+    biases = [orc.normal(4400 + i, n, 0.1) if i % 2 == 1 else None for i, n in enumerate(ns)]
+    x = orc.normal(4500 + rows, rows * k, 1.0)
+    xd = _dev(torch, x)
+    wds = [_dev(torch, wq) for wq in wqs]
+    bds = [None if b is None else _dev(torch, b) for b in biases]
+    outs = [torch.full((rows * n,), float("nan"), dtype=torch.float32, device="cuda") for n in ns]
+    c = len(ns)
+    arr = lambda ty, vals: (ty * c)(*vals)
+    okq.call("okq_gemv_multi", xd.data_ptr(), rows, k, t, c,
+             arr(ctypes.c_void_p, [w.data_ptr() for w in wds]),
+             arr(ctypes.c_uint64, [wq.size for wq in wqs]),
+             arr(ctypes.c_int64, ns),
+             arr(ctypes.c_void_p, [None if b is None else b.data_ptr() for b in bds]),
+             arr(ctypes.c_void_p, [o.data_ptr() for o in outs]), _stream(torch))
+    torch.cuda.synchronize()
+    for i, n in enumerate(ns):
+        got = _host(outs[i]).reshape(rows, n)
+        single = gpu_linear(torch, okq, t, x, rows, k, wqs[i], n, biases[i])
+        assert _same_bits(got, single).all(), f"matrix {i}"
+        want = orc.linear_q(t, x, rows, k, wqs[i], n, biases[i])
+        ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
+        assert ok, f"matrix {i} idx={idx} max_abs={dmax}"
+
+
 def test_gemv_multi_validates_every_matrix_before_launch(torch, okq, orc):
     import ctypes
     k, ns = 256, [8, 8]
