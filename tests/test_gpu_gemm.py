@@ -272,6 +272,42 @@ def test_gemm_wide_dynamic_range_rows(torch, okq, orc):
         assert (got[5] == 0.0).all(), entry
 
 
+def test_gemm_decode_batch_per_slice_scaling(torch, okq, orc):
+    """The decode-batch kernel scales each K slice of a row by its own power of
+    two (K split 16 ways here).  Checked: slices 2^60 apart in one row, rows
+    with all-zero slices, exact power-of-two homogeneity across slices, and
+    non-finite activations -- an inf or a NaN makes its own row non-finite and
+    leaves every other row bit-identical to a batch without it."""
+    rows, n, k = 6, 1000, 4096
+    wq = orc.quantize(O.Q4_K, orc.normal(95, n * k, 0.02))
+    pa, pb = q4k_parts(orc, wq, n, k)
+    x = orc.normal(96, rows * k, 1.0).reshape(rows, k)
+    x[1, : k // 2] *= np.float32(2.0 ** 30)
+    x[1, k // 2:] *= np.float32(2.0 ** -30)
+    for sl in range(0, k, 512):  # every other 256-wide slice of row 2 is zero
+        x[2, sl:sl + 256] = 0.0
+    x[5] = x[0] * np.float32(2.0 ** -100)
+    clean = x.copy()
+    x[3] = x[0]
+    x[3, 100] = np.inf
+    x[4] = x[0]
+    x[4, 3000] = np.nan
+    clean[3] = x[0]
+    clean[4] = x[0]
+    got = run(torch, okq, "okq_gemm", O.Q4_K, x.reshape(-1), rows, k, wq, n)
+    ref = run(torch, okq, "okq_gemm", O.Q4_K, clean.reshape(-1), rows, k, wq, n)
+    want = orc.linear_q(O.Q4_K, clean.reshape(-1), rows, k, wq, n, None, O.MODE_SCALAR, 1)
+    for r in (0, 1, 2):
+        ax = np.abs(clean[r].astype(np.float64))
+        bound = 1e-3 * np.abs(want[r]) + 2.0 ** -20 * (pa @ ax + pb @ ax)
+        err = np.abs(got[r].astype(np.float64) - want[r])
+        assert (err <= bound).all(), (r, float((err / bound).max()))
+    assert (got[5] == got[0] * np.float32(2.0 ** -100)).all()
+    assert not np.isfinite(got[3]).any() and np.isnan(got[4]).all()
+    for r in (0, 1, 2, 5):
+        assert (got[r].view(np.uint32) == ref[r].view(np.uint32)).all(), r
+
+
 # ---- Q6_K -----------------------------------------------------------------------
 # B = sc * (q - 32) (|.| <= 4096) enters as two exact fp16 planes, fp16(v) and
 # the remainder v - fp16(v) in {-1, 0, 1}: the products are exact as for Q4_K.
