@@ -164,9 +164,12 @@ okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, u
  * matrix is validated like okq_gemv before anything launches.  A matrix that
  * okq_linear_out_by_in_q would not give to the GEMV at this row count (Q4_K /
  * Q6_K weights of 16 MB or more from 5 rows, every Q4_K / Q6_K weight above
- * 8 rows) is computed by that entry point's MFMA kernels instead, on its own;
- * every output equals okq_linear_out_by_in_q's on its matrix bit for bit (and
- * okq_gemv's wherever the GEMV serves it).  No counterpart in the reference,
+ * 8 rows) is computed by the MFMA kernels instead: alone through that entry
+ * point's dispatch, or -- two or more of them at up to 32 rows -- together in
+ * one decode-batch launch whose K split follows their combined columns.
+ * Outputs equal okq_linear_out_by_in_q's on each matrix bit for bit, except
+ * those of such a shared decode-batch launch, which agree within the
+ * reference rule.  No counterpart in the reference,
  * whose callers compute such groups one projection at a time: the gate/up
  * pair of mlp_gated_silu (crates/kernels/src/lib.rs:150-162,
  * crates/kernels/src/mlp.rs:139-250) and the q/k/v projections of one

@@ -599,11 +599,23 @@ __device__ __forceinline__ void q4k_scale_min_sel(uint32_t j, uint32_t s0, uint3
   m = __builtin_amdgcn_ubfe(lowj ? s1 : s2, 8 * jj + mo, width) | ((__builtin_amdgcn_ubfe(s1, 8 * jj + 6, 2) << 4) & himask);
 }
 
-constexpr int kDecRows = 32;  // two 16-row MFMA groups share each B fragment above 16 rows
+constexpr int kDecRows = kGemmDecodeRows;  // two 16-row MFMA groups share each B fragment above 16 rows
 constexpr int kDecWaves = 16;
 constexpr int64_t kDecLdsBytes = 144 * 1024;  // activations of a slice (one workgroup per CU fills its registers)
 constexpr int kDecStage = 4;                // 16-byte activation pieces per thread (of 1024)
 constexpr int kDecMaxTiles = 4;             // unsplit K: column tiles per wave (bias staged in LDS)
+
+// The matrices of one decode-batch launch: matrix p owns the 16-column tiles
+// [tile0[p], tile0[p + 1]) of the launch (tile0[0] = 0; unused entries
+// INT32_MAX), has n[p] rows of weights w[p], bias bias[p] (or null) and output
+// y[p] [M][n[p]].
+struct DecMats {
+  const uint8_t *w[kDecMats];
+  const float *bias[kDecMats];
+  float *y[kDecMats];
+  int n[kDecMats];
+  int tile0[kDecMats];
+};
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
@@ -786,10 +798,16 @@ struct DecQ6K {
 // count its arrival sums the partials -- needs a device-scope release per
 // workgroup, an L2 write-back that serialises per XCD: measured 1.5-2x
 // slower at the C5 shapes than the separate reduction launch.)
+//
+// One launch may serve up to kDecMats matrices of one format and K that read
+// the same activations (gate/up): their 16-column tiles are numbered
+// consecutively (`DecMats`), and each tile finds its matrix, weights, bias and
+// output through wave-uniform scalar selects.  Split-K partials are laid out
+// over the concatenated tile columns, [ksplit][M][ntiles * 16].
 template <class F, bool kLo, int RG>
-__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
-    const void *__restrict__ X, const uint8_t *__restrict__ W, const float *__restrict__ bias,
-    float *__restrict__ Y, int M, int N, int K, int ksplit, int groups, float *__restrict__ part) {
+__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void *__restrict__ X, DecMats mats,
+                                                                     int ntiles, int M, int K, int ksplit,
+                                                                     int groups, float *__restrict__ part) {
   constexpr int D = RG == 1 ? F::kDepth1 : F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
   const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
@@ -813,15 +831,23 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
 
   // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
   //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
-  const int ntiles = (N + 15) / 16;
   const int stride = groups * kDecWaves;
   const int first = grp * kDecWaves + wave;
   const int mytiles = first < ntiles ? (ntiles - first + stride - 1) / stride : 0;
   const int nitems = mytiles * nsbs;
   const int cn = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
-  const uint32_t w_end = (uint32_t)((size_t)N * row_bytes);
-  const Rsrc rs_w = make_rsrc(W, w_end);
+  // the matrix of a tile (tiles past the end map to the last matrix; every
+  // field of `mats` is read with constant indices, so it stays in SGPRs)
+  const int st1 = mats.tile0[1], st2 = mats.tile0[2], st3 = mats.tile0[3];
+  auto mat_of = [&](int t) { return (int)(t >= st1) + (int)(t >= st2) + (int)(t >= st3); };
+  auto tile0_of = [&](int m) { return m == 0 ? 0 : m == 1 ? st1 : m == 2 ? st2 : st3; };
+  auto n_of = [&](int m) { return m == 0 ? mats.n[0] : m == 1 ? mats.n[1] : m == 2 ? mats.n[2] : mats.n[3]; };
+  const Rsrc rw0 = make_rsrc(mats.w[0], (uint32_t)((size_t)mats.n[0] * row_bytes));
+  const Rsrc rw1 = make_rsrc(mats.w[1], (uint32_t)((size_t)mats.n[1] * row_bytes));
+  const Rsrc rw2 = make_rsrc(mats.w[2], (uint32_t)((size_t)mats.n[2] * row_bytes));
+  const Rsrc rw3 = make_rsrc(mats.w[3], (uint32_t)((size_t)mats.n[3] * row_bytes));
+  auto rw_of = [&](int m) { return m == 0 ? rw0 : m == 1 ? rw1 : m == 2 ? rw2 : rw3; };
   // A rows of the lane's row groups.  Lanes whose 16-row group reaches past
   // M read row M - 1: they only produce MFMA output rows >= M, which are
   // never stored, so no zero row needs staging.
@@ -833,9 +859,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   auto tile_of = [&](int u) { return (u / nsbs) * stride + first; };
   auto load = [&](Item &it, int u) {
     const int sbl = u - (u / nsbs) * nsbs;
-    const int tile = tile_of(u);
-    const uint32_t n = (uint32_t)(tile * 16 + cn);  // rows >= N read past the tensor: zeros
-    F::load(it, rs_w, tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
+    const int tile = tile_of(u), m = mat_of(tile);
+    const uint32_t w_end = (uint32_t)((size_t)n_of(m) * row_bytes);
+    // rows past the matrix (and tiles past the end) read past the tensor: zeros
+    const uint32_t n = (uint32_t)((tile - tile0_of(m)) * 16 + cn);
+    F::load(it, rw_of(m), tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
   };
   // 2. the activations of the slice: this thread's pieces of 8 consecutive
   //    activations of one row (at most kDecStage; pieces past the last row
@@ -858,11 +886,18 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
       xa[i] = bload4(rs_x, r < M ? e * 2u : x_end);
     }
   }
-  // bias of the workgroup's columns (unsplit K only)
-  const int bt = tid >> 8, bcol = ((bt * groups + grp) * kDecWaves) * 16 + (tid & 255);
-  const uint32_t bias_end = bias ? (uint32_t)N * 4u : 0u;
-  const uint32_t bbits = __builtin_amdgcn_raw_buffer_load_b32(
-      make_rsrc(bias, bias_end), (ksplit == 1 && bt < kDecMaxTiles && bcol < N) ? (uint32_t)bcol * 4u : bias_end, 0, 0);
+  // bias of the wave's tiles (unsplit K only): lanes 0-15 of each wave load
+  // the 16 values of its tile ti (matrix selected per tile, wave-uniform)
+  uint32_t bbits[kDecMaxTiles];
+#pragma unroll
+  for (int ti = 0; ti < kDecMaxTiles; ++ti) {
+    const int tile = ti * stride + first, m = mat_of(tile);
+    const float *bp = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
+    const uint32_t bias_end = bp ? (uint32_t)n_of(m) * 4u : 0u;
+    const int col = (tile - tile0_of(m)) * 16 + lane;
+    const bool in = ksplit == 1 && lane < 16 && tile < ntiles && col < n_of(m);
+    bbits[ti] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(bp, bias_end), in ? (uint32_t)col * 4u : bias_end, 0, 0);
+  }
   // A CU returns vector loads in issue order: this bare barrier (no memory
   // fence) puts every activation load of the workgroup ahead of every weight
   // load, so no wave's activations queue behind another wave's weights.
@@ -874,7 +909,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   // (a wave's first item before the staging measured no better, even for the
   // head's long streams).
   Item S[D];
-  if (bt < kDecMaxTiles) Bs[tid] = __uint_as_float(bbits);
+  if (lane < 16) {
+#pragma unroll
+    for (int ti = 0; ti < kDecMaxTiles; ++ti) Bs[ti * 256 + wave * 16 + lane] = __uint_as_float(bbits[ti]);
+  }
   auto piece = [&](int i, float v[8]) {
     if (kLo) {
       v[0] = as_f32(xa[i].x), v[1] = as_f32(xa[i].y), v[2] = as_f32(xa[i].z), v[3] = as_f32(xa[i].w);
@@ -962,8 +1000,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
   for (int q = 0; q < RG; ++q) acc[q] = zero4;
   // outputs: range-checked buffer stores (out-of-range lanes are dropped by
   // the hardware, so no branch surrounds them), scale and bias from LDS
-  const uint32_t out_end = (uint32_t)((size_t)(ksplit > 1 ? (size_t)ksplit * M : (size_t)M) * N * 4);
-  const Rsrc rs_out = make_rsrc(ksplit > 1 ? (void *)part : (void *)Y, out_end);
+  const int ncat = ntiles * 16;  // partial columns: the concatenated tiles
+  const uint32_t part_end = (uint32_t)((size_t)ksplit * M * ncat * 4);
+  const Rsrc rs_part = make_rsrc(part, part_end);
   auto consume = [&](const Item &it, int u) {
     const int ti = u / nsbs, sbl = u - ti * nsbs;
     const _Float16 *ar[RG], *arl[RG], *xs[RG];
@@ -975,8 +1014,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
     }
     F::template contract<kLo, RG>(it, ar, arl, xs, g, acc);
     if (sbl == nsbs - 1) {  // the tile's last super-block: write it out
-      const int col = (ti * stride + first) * 16 + cn;
+      const int tile = ti * stride + first, m = mat_of(tile);
+      const int nm = n_of(m), col = (tile - tile0_of(m)) * 16 + cn;
       const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
+      // unsplit: the matrix's own output; split: the concatenated partials
+      float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
+      const uint32_t out_end = ksplit > 1 ? part_end : (uint32_t)((size_t)M * nm * 4);
+      const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(ym, out_end);
 #pragma unroll
       for (int q = 0; q < RG; ++q) {
 #pragma unroll
@@ -984,7 +1028,10 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(
           const int row = 16 * q + 4 * g + v;
           // rows >= M read an unset Rs entry; the range check drops their stores
           const float val = acc[q][v] * Rs[row] + bv;
-          const uint32_t off = (row < M && col < N) ? (uint32_t)(((size_t)z * M + row) * N + col) * 4u : out_end;
+          const uint32_t off =
+              (row < M && col < nm)
+                  ? (uint32_t)(ksplit > 1 ? ((size_t)z * M + row) * ncat + (size_t)tile * 16 + cn : (size_t)row * nm + col) * 4u
+                  : out_end;
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
         }
         acc[q] = zero4;
@@ -1030,6 +1077,36 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   }
   const int m = (int)(i / N), n = (int)(i % N);
   Y[i] = (rscale ? acc * rscale[m] : acc) + (bias ? bias[n] : 0.0f);
+}
+
+// The decode-batch kernel's partials [ksplit][M][ntiles * 16] over the
+// concatenated tiles of its matrices: the same slice-order sum, scattered to
+// each matrix's output with its bias (columns past a matrix's rows skipped).
+__global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__restrict__ part, int ksplit, int M,
+                                                                 int ntiles, DecMats mats) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int ncat = ntiles * 16;
+  const int64_t total = (int64_t)M * ncat;
+  if (i >= total) return;
+  const int row = (int)(i / ncat), cc = (int)(i - (int64_t)row * ncat), tile = cc >> 4;
+  const int m = (int)(tile >= mats.tile0[1]) + (int)(tile >= mats.tile0[2]) + (int)(tile >= mats.tile0[3]);
+  const int t0 = m == 0 ? 0 : m == 1 ? mats.tile0[1] : m == 2 ? mats.tile0[2] : mats.tile0[3];
+  const int nm = m == 0 ? mats.n[0] : m == 1 ? mats.n[1] : m == 2 ? mats.n[2] : mats.n[3];
+  const int col = (tile - t0) * 16 + (cc & 15);
+  if (col >= nm) return;
+  constexpr int kBatch = 8;
+  float acc = -0.0f;  // slice order from -0.0, as splitk_reduce_kernel
+  for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
+    float v[kBatch];
+#pragma unroll
+    for (int d = 0; d < kBatch; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
+#pragma unroll
+    for (int d = 0; d < kBatch; ++d)
+      if (z0 + d < ksplit) acc += v[d];
+  }
+  float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
+  const float *bm = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
+  ym[(size_t)row * nm + col] = acc + (bm ? bm[col] : 0.0f);
 }
 
 // ---------------------------------------------------------------------------
@@ -1083,9 +1160,9 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   }
   p.ksplit = (int)std::max<int64_t>(1, ks);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
-  if (p.bm == kDecRows) {  // the decode-batch kernel needs only the split-K partials
+  if (p.bm == kDecRows) {  // the decode-batch kernel needs only the split-K partials (whole 16-column tiles)
     p.off_lo = p.off_sums = p.off_rscale = p.off_part = 0;
-    p.workspace = p.ksplit > 1 ? up((size_t)p.ksplit * M * N * sizeof(float)) : 0;
+    p.workspace = p.ksplit > 1 ? up((size_t)p.ksplit * M * ((N + 15) / 16 * 16) * sizeof(float)) : 0;
     return p;
   }
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
@@ -1098,6 +1175,61 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   return p;
 }
 
+// The decode-batch kernel (it converts the activations itself: no pre-pass)
+// and, when K is split, the reduction of its partials.
+static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const DecMats &mats,
+                                int ntiles, char *ws, const GemmPlan &plan, hipStream_t s) {
+  const int m = (int)M, k = (int)K, ks = plan.ksplit;
+  float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
+  const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
+  const size_t lds = (size_t)M * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) + (size_t)M * nsbs_max * 32 +
+                     (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
+  const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
+#define OKQ_DEC(F_, LO_, RG_)                                                                                   \
+  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, x, mats, ntiles, m, k, ks,       \
+               plan.groups, part)
+#define OKQ_DEC_RG(F_, LO_)        \
+  if (M > 16) OKQ_DEC(F_, LO_, 2); \
+  else OKQ_DEC(F_, LO_, 1)
+  if (type == kQ6_K) {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
+    else OKQ_DEC_RG(DecQ6K, true);
+  } else {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
+    else OKQ_DEC_RG(DecQ4K, true);
+  }
+#undef OKQ_DEC_RG
+#undef OKQ_DEC
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess || ks == 1) return e;
+  const int64_t total = M * (int64_t)ntiles * 16;
+  hipLaunchKernelGGL(splitk_reduce_mats_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m,
+                     ntiles, mats);
+  return hipGetLastError();
+}
+
+hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
+                                    const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
+                                    void *workspace, const GemmPlan &plan, hipStream_t s) {
+  if ((type != kQ4_K && type != kQ6_K) || plan.bm != kDecRows || M > kDecRows || count < 1 || count > kDecMats)
+    return hipErrorInvalidValue;
+  DecMats mats{};
+  int tiles = 0;
+  for (int i = 0; i < kDecMats; ++i) {
+    if (i < count) {
+      mats.w[i] = static_cast<const uint8_t *>(w[i]);
+      mats.bias[i] = bias[i];
+      mats.y[i] = y[i];
+      mats.n[i] = (int)N[i];
+      mats.tile0[i] = tiles;
+      tiles += (int)((N[i] + 15) / 16);
+    } else {
+      mats.tile0[i] = INT32_MAX;
+    }
+  }
+  return launch_decode(type, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
+}
+
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
   if (type != kQ4_K && type != kQ6_K) return hipErrorInvalidValue;
@@ -1106,34 +1238,14 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   const uint8_t *W = static_cast<const uint8_t *>(w);
   const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
   if (plan.bm == kDecRows) {
-    // the decode-batch kernel converts the activations itself: no pre-pass
     if (M > kDecRows) return hipErrorInvalidValue;
-    float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
-    const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
-    const size_t lds = (size_t)M * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) + (size_t)M * nsbs_max * 32 +
-                       (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
-    const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
-#define OKQ_DEC(F_, LO_, RG_)                                                                                      \
-  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, x, W, bias, y, m, n, k, ks,         \
-               plan.groups, part)
-#define OKQ_DEC_RG(F_, LO_)        \
-  if (M > 16) OKQ_DEC(F_, LO_, 2); \
-  else OKQ_DEC(F_, LO_, 1)
-    if (type == kQ6_K) {
-      if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
-      else OKQ_DEC_RG(DecQ6K, true);
-    } else {
-      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
-      else OKQ_DEC_RG(DecQ4K, true);
-    }
-#undef OKQ_DEC_RG
-#undef OKQ_DEC
-    hipError_t e = hipGetLastError();
-    if (e != hipSuccess || ks == 1) return e;
-    const int64_t total = M * N;
-    hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m, n,
-                       static_cast<const float *>(nullptr), bias, y);
-    return hipGetLastError();
+    DecMats mats{};
+    mats.w[0] = W;
+    mats.bias[0] = bias;
+    mats.y[0] = y;
+    mats.n[0] = n;
+    for (int i = 1; i < kDecMats; ++i) mats.tile0[i] = INT32_MAX;
+    return launch_decode(type, x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s);
   }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);

@@ -90,6 +90,14 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
 // calls on the stream.
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s);
+// Up to kDecMats matrices of one format and K that read the same activations
+// in one decode-batch launch (plan: gemm_plan with N = sum of the matrices'
+// rows rounded up to 16 each, which must pick the decode-batch kernel).
+constexpr int kDecMats = 4;
+constexpr int kGemmDecodeRows = 32;  // batches up to this many rows take the decode-batch kernel
+hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
+                                    const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
+                                    void *workspace, const GemmPlan &plan, hipStream_t s);
 
 // True when launch_gemm supports this (type, M, K, N): Q4_K and Q6_K.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);

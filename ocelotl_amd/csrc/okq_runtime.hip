@@ -520,20 +520,28 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
   const float *const *b = bias ? bias : nobias;
   // A matrix that the linear dispatch would not give to the GEMV at this row
   // count (large Q4_K / Q6_K weights from kDecMinRows rows, every Q4_K / Q6_K
-  // weight above kGemvMaxRows) runs through that dispatch on its own (the
-  // decode-batch or tiled MFMA kernel); the others share one GEMV launch.
-  // Either way each output equals okq_linear_out_by_in_q's on its matrix.
-  const void *gw[okq::kGemvMaxProblems];
-  int64_t gn[okq::kGemvMaxProblems];
-  const float *gb[okq::kGemvMaxProblems];
-  float *go[okq::kGemvMaxProblems];
-  int shared = 0;
+  // weight above kGemvMaxRows) goes to the MFMA kernels; the others share one
+  // GEMV launch, bit-identical to okq_linear_out_by_in_q on each matrix.  Two
+  // or more MFMA matrices at a decode-batch size share one decode-batch launch
+  // (gate/up: one activation staging, one reduction); its K split follows the
+  // combined columns, so those outputs match each matrix's own call within
+  // the reference rule rather than bit for bit.  A single MFMA matrix, or
+  // larger batches, run through okq_linear_out_by_in_q's own dispatch.
+  const void *gw[okq::kGemvMaxProblems], *mw[okq::kGemvMaxProblems];
+  int64_t gn[okq::kGemvMaxProblems], mn[okq::kGemvMaxProblems];
+  const float *gb[okq::kGemvMaxProblems], *mb[okq::kGemvMaxProblems];
+  float *go[okq::kGemvMaxProblems], *mo[okq::kGemvMaxProblems];
+  uint64_t mbytes[okq::kGemvMaxProblems];
+  int shared = 0, mfma = 0;
   for (int i = 0; i < count; ++i) {
     if (rows > 0 && out_features[i] > 0 && !gemv_serves(w_type, rows, w_bytes[i]) &&
         okq::gemm_supported((int)w_type, rows, in_features, out_features[i])) {
-      st = linear_impl(x, false, rows, in_features, w_type, w[i], w_bytes[i], out_features[i], b[i], out[i], stream,
-                       Path::Auto);
-      if (st != OKQ_OK) return st;
+      mw[mfma] = w[i];
+      mn[mfma] = out_features[i];
+      mb[mfma] = b[i];
+      mo[mfma] = out[i];
+      mbytes[mfma] = w_bytes[i];
+      ++mfma;
       continue;
     }
     gw[shared] = w[i];
@@ -541,6 +549,24 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
     gb[shared] = b[i];
     go[shared] = out[i];
     ++shared;
+  }
+  bool grouped = false;
+  if (mfma > 1 && rows <= okq::kGemmDecodeRows) {
+    int64_t ncat = 0;
+    for (int i = 0; i < mfma; ++i) ncat += (mn[i] + 15) / 16 * 16;
+    const okq::GemmPlan plan = okq::gemm_plan((int)w_type, rows, ncat, in_features, false, info.cu_count);
+    void *ws = nullptr;
+    st = get_workspace(dev, s, plan.workspace, &ws);
+    if (st != OKQ_OK) return st;
+    st = hip_status(okq::launch_gemm_decode_multi((int)w_type, x, false, rows, in_features, mfma, mw, mn, mb, mo, ws,
+                                                  plan, s),
+                    "gemv_multi decode-batch launch");
+    if (st != OKQ_OK) return st;
+    grouped = true;
+  }
+  for (int i = 0; i < mfma && !grouped; ++i) {
+    st = linear_impl(x, false, rows, in_features, w_type, mw[i], mbytes[i], mn[i], mb[i], mo[i], stream, Path::Auto);
+    if (st != OKQ_OK) return st;
   }
   if (shared == 0) return ok();
   hipError_t e = okq::launch_gemv_multi((int)w_type, x, in_features, rows, shared, gw, gn, gb, go, info.cu_count, s,

@@ -373,18 +373,23 @@ def test_gemv_multi_equals_single_gemvs_bit_for_bit(torch, okq, orc, t, rows, k,
 
 
 MULTI_BATCH_CASES = [
-    (O.Q4_K, 8, 4096, [14336, 14336]),       # gate/up at 8 rows: each on the decode-batch kernel
-    (O.Q4_K, 8, 4096, [4096, 1024, 14336]),  # q and k share the GEMV launch, the large one goes alone
-    (O.Q6_K, 24, 1024, [33, 300]),           # above 8 rows: every Q6_K matrix on the MFMA path
-    (O.Q8_0, 12, 1024, [100, 64]),           # Q8_0 stays on the GEMV at any row count
+    # (type, rows, K, out_features, the MFMA matrices share one decode-batch launch)
+    (O.Q4_K, 8, 4096, [14336, 14336], True),         # gate/up at 8 rows
+    (O.Q4_K, 8, 4096, [4096, 1024, 14336], False),   # q and k share the GEMV launch, the large one goes alone
+    (O.Q6_K, 24, 1024, [33, 300], True),             # above 8 rows: every Q6_K matrix on the MFMA path
+    (O.Q4_K, 32, 1024, [17, 1000, 256, 40], True),   # four matrices, ragged tiles, two 16-row groups
+    (O.Q8_0, 12, 1024, [100, 64], False),            # Q8_0 stays on the GEMV at any row count
+    (O.Q4_K, 40, 1024, [300, 200], False),           # above 32 rows: each on the tiled GEMM
 ]
 
 
-@pytest.mark.parametrize("t,rows,k,ns", MULTI_BATCH_CASES)
-def test_gemv_multi_batches_route_like_the_linear_dispatch(torch, okq, orc, t, rows, k, ns):
+@pytest.mark.parametrize("t,rows,k,ns,shared", MULTI_BATCH_CASES)
+def test_gemv_multi_batches_route_like_the_linear_dispatch(torch, okq, orc, t, rows, k, ns, shared):
     """At decode-batch row counts okq_gemv_multi sends every matrix to the
-    kernel okq_linear_out_by_in_q would pick for it: outputs equal that entry
-    point's, matrix by matrix, bit for bit, and the reference within the rule."""
+    kernels okq_linear_out_by_in_q would pick for it: outputs equal that entry
+    point's, matrix by matrix, bit for bit -- except where several matrices
+    share one decode-batch launch (its K split follows the combined columns),
+    which must match within the rule -- and the reference within the rule."""
     import ctypes
     print(f"[gpu] gemv_multi batch type={t} rows={rows} K={k} N={ns}", flush=True)
     wqs = [orc.quantize(t, orc.normal(4300 + 17 * i + t, n * k, 0.02)) for i, n in enumerate(ns)]
@@ -406,7 +411,11 @@ def test_gemv_multi_batches_route_like_the_linear_dispatch(torch, okq, orc, t, r
     for i, n in enumerate(ns):
         got = _host(outs[i]).reshape(rows, n)
         single = gpu_linear(torch, okq, t, x, rows, k, wqs[i], n, biases[i])
-        assert _same_bits(got, single).all(), f"matrix {i}"
+        if shared:
+            ok, idx, dmax, _ = O.allclose_ref_rule(got, single, TOL)
+            assert ok, f"matrix {i} vs its own call: idx={idx} max_abs={dmax}"
+        else:
+            assert _same_bits(got, single).all(), f"matrix {i}"
         want = orc.linear_q(t, x, rows, k, wqs[i], n, biases[i])
         ok, idx, dmax, _ = O.allclose_ref_rule(got, want, TOL)
         assert ok, f"matrix {i} idx={idx} max_abs={dmax}"
