@@ -492,41 +492,22 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
   return linear_impl(x, true, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Auto);
 }
 
-okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
+// Several validated quantized linears of one format and K that read the same
+// activations x (device f32 [rows][K]); outputs out[i] [rows][N[i]].
+// A matrix that the linear dispatch would not give to the GEMV at this row
+// count (large Q4_K / Q6_K weights from kDecMinRows rows, every Q4_K / Q6_K
+// weight above kGemvMaxRows) goes to the MFMA kernels; the others share one
+// GEMV launch, bit-identical to okq_linear_out_by_in_q on each matrix.  Two
+// or more MFMA matrices at a decode-batch size share one decode-batch launch
+// (gate/up: one activation staging, one reduction); its K split follows the
+// combined columns, so those outputs match each matrix's own call within
+// the reference rule rather than bit for bit.  A single MFMA matrix, or
+// larger batches, run through okq_linear_out_by_in_q's own dispatch.
+okq_status grouped_linear(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
                           const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
-                          const float *const *bias, float *const *out, void *stream) {
-  if (count < 1 || count > okq::kGemvMaxProblems)
-    return fail(OKQ_E_ARG, "gemv_multi count=%d must be between 1 and %d", count, okq::kGemvMaxProblems);
-  if (!w || !w_bytes || !out_features || !out) return fail(OKQ_E_ARG, "gemv_multi null argument array");
-  // every matrix is validated like a single linear before anything launches
-  bool any = false;
-  for (int i = 0; i < count; ++i) {
-    LinearArgs a{rows, in_features, out_features[i], w_type, w_bytes[i]};
-    okq_status st = validate_linear(x, a, w[i], out[i], false);
-    if (st != OKQ_OK) {
-      char msg[512];
-      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
-      return fail(st, "gemv_multi matrix %d: %s", i, msg);
-    }
-    any = any || (rows > 0 && out_features[i] > 0);
-  }
-  if (!any) return ok();
-  int dev;
-  DevInfo info;
-  okq_status st = current_device(dev, info);
-  if (st != OKQ_OK) return st;
+                          const float *const *b, float *const *out, void *stream, int dev, const DevInfo &info) {
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
-  const float *const *b = bias ? bias : nobias;
-  // A matrix that the linear dispatch would not give to the GEMV at this row
-  // count (large Q4_K / Q6_K weights from kDecMinRows rows, every Q4_K / Q6_K
-  // weight above kGemvMaxRows) goes to the MFMA kernels; the others share one
-  // GEMV launch, bit-identical to okq_linear_out_by_in_q on each matrix.  Two
-  // or more MFMA matrices at a decode-batch size share one decode-batch launch
-  // (gate/up: one activation staging, one reduction); its K split follows the
-  // combined columns, so those outputs match each matrix's own call within
-  // the reference rule rather than bit for bit.  A single MFMA matrix, or
-  // larger batches, run through okq_linear_out_by_in_q's own dispatch.
+  okq_status st = OKQ_OK;
   const void *gw[okq::kGemvMaxProblems], *mw[okq::kGemvMaxProblems];
   int64_t gn[okq::kGemvMaxProblems], mn[okq::kGemvMaxProblems];
   const float *gb[okq::kGemvMaxProblems], *mb[okq::kGemvMaxProblems];
@@ -571,7 +552,35 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
   if (shared == 0) return ok();
   hipError_t e = okq::launch_gemv_multi((int)w_type, x, in_features, rows, shared, gw, gn, gb, go, info.cu_count, s,
                                         okq::GemvPro{});
-  return hip_status(e, "gemv_multi launch");
+  return hip_status(e, "grouped linear launch");
+}
+
+okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
+                          const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
+                          const float *const *bias, float *const *out, void *stream) {
+  if (count < 1 || count > okq::kGemvMaxProblems)
+    return fail(OKQ_E_ARG, "gemv_multi count=%d must be between 1 and %d", count, okq::kGemvMaxProblems);
+  if (!w || !w_bytes || !out_features || !out) return fail(OKQ_E_ARG, "gemv_multi null argument array");
+  // every matrix is validated like a single linear before anything launches
+  bool any = false;
+  for (int i = 0; i < count; ++i) {
+    LinearArgs a{rows, in_features, out_features[i], w_type, w_bytes[i]};
+    okq_status st = validate_linear(x, a, w[i], out[i], false);
+    if (st != OKQ_OK) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
+      return fail(st, "gemv_multi matrix %d: %s", i, msg);
+    }
+    any = any || (rows > 0 && out_features[i] > 0);
+  }
+  if (!any) return ok();
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
+  const float *const *b = bias ? bias : nobias;
+  return grouped_linear(x, rows, in_features, w_type, count, w, w_bytes, out_features, b, out, stream, dev, info);
 }
 
 okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float epsilon, float *out,
@@ -633,12 +642,8 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
   float *xn = static_cast<float *>(ws);
   hipError_t e = okq::launch_rmsnorm(x, rows, hidden, norm_weight, epsilon, xn, s);
   if (e != hipSuccess) return hip_status(e, "rmsnorm launch");
-  for (int i = 0; i < count; ++i) {
-    st = linear_impl(xn, false, rows, hidden, w_type, w[i], w_bytes[i], out_features[i], b[i], out[i], stream,
-                     Path::Auto);
-    if (st != OKQ_OK) return st;
-  }
-  return ok();
+  // the normalised rows then go through the grouped dispatch of okq_gemv_multi
+  return grouped_linear(xn, rows, hidden, w_type, count, w, w_bytes, out_features, b, out, stream, dev, info);
 }
 
 okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, int64_t intermediate,
@@ -675,17 +680,16 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   okq_status st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  const bool decode = gemv_serves(gate_type, rows, gate_bytes);
-  // gate and up: one grouped pass over both weights when they share a format
-  if (decode && gate_type == up_type && okq::gemv_streams((int)gate_type, hidden, gate_w, intermediate) &&
-      okq::gemv_streams((int)up_type, hidden, up_w, intermediate)) {
+  // gate and up: grouped like okq_gemv_multi when they share a format (one
+  // GEMV pass over both weights, or one decode-batch launch)
+  if (gate_type == up_type) {
     const void *ws[2] = {gate_w, up_w};
+    const uint64_t wb[2] = {gate_bytes, up_bytes};
     const int64_t ns[2] = {intermediate, intermediate};
     const float *bs[2] = {nullptr, nullptr};
     float *const os[2] = {gate_buf, up_buf};
-    hipError_t e = okq::launch_gemv_multi((int)gate_type, x, hidden, rows, 2, ws, ns, bs, os, info.cu_count, s,
-                                          okq::GemvPro{});
-    if (e != hipSuccess) return hip_status(e, "mlp gate/up launch");
+    st = grouped_linear(x, rows, hidden, gate_type, 2, ws, wb, ns, bs, os, stream, dev, info);
+    if (st != OKQ_OK) return st;
   } else {
     st = linear_impl(x, false, rows, hidden, gate_type, gate_w, gate_bytes, intermediate, nullptr, gate_buf, stream,
                      Path::Auto);

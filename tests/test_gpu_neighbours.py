@@ -180,6 +180,7 @@ RMS_LINEAR_CASES = [
     (O.Q4_K, 9, 2048, [512, 128]),           # batch: normalise, then the MFMA GEMM
     (O.Q6_K, 6, 1024, [64]),                 # batch on the per-row GEMV
     (O.Q8_0, 1, 96, [40]),                   # odd Q8_0 block count: generic GEMV after a normalised copy
+    (O.Q4_K, 12, 2048, [512, 256, 256]),     # batch above 8 rows: q/k/v in one decode-batch launch
     (O.Q4_K, 1, 4096, [14336, 14336]),       # fused prologue with dynamic rows (gate/up shape)
     (O.Q6_K, 1, 256, [20000]),
 ]
@@ -219,6 +220,7 @@ MLP_CASES = [
     (O.Q4_K, O.Q8_0, O.Q6_K, 1, 1024, 2816),   # gate and up in different formats: two passes
     (O.Q4_K, O.Q4_K, O.Q6_K, 7, 1024, 2816),   # batch: GEMM gate/up, materialised SiLU, per-row Q6_K down
     (O.Q8_0, O.Q8_0, O.Q8_0, 3, 512, 1024),
+    (O.Q4_K, O.Q4_K, O.Q6_K, 8, 4096, 14336),   # Llama-3-8B batch of 8: gate+up in one decode-batch launch
 ]
 
 
