@@ -246,22 +246,27 @@ enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
 // serves up to four rows); above it the MFMA GEMM path (the streaming
-// decode-batch kernel up to 16 rows, the tiled kernel beyond).  Large Q4_K /
-// Q6_K matrices take the decode-batch kernel from kDecMinRows rows on: it
-// streams the weights once where the GEMV needs a second pass, and its fixed
-// cost (pre-pass, K-split reduction, ~10 us per call in a graph) is repaid
-// above ~16 MB of weights.  Measured per call in graphs, decode kernel vs
-// GEMV: Q4_K gate 20 vs 23 us at 5 rows (15 at 4), Q6_K down 31 vs 39 us at 5
-// rows, Q6_K head 125 vs 199 us at 5 rows; q/k/v/o-sized matrices favour the
-// GEMV up to 8 rows.
+// decode-batch kernel up to 32 rows, the tiled kernel beyond).  Large Q4_K /
+// Q6_K matrices take the decode-batch kernel earlier: it streams the weights
+// once where the GEMV needs a second pass, and its fixed cost (the split-K
+// reduction launch) is repaid from 5 rows at 16 MB and more, and from 7 rows
+// (a second GEMV pass of 3-4 rows) at 8 MB and more.  Measured per call in
+// graphs, decode kernel vs GEMV: Q4_K gate 20 vs 23 us at 5 rows (15 at 4),
+// Q6_K down 31 vs 39 us at 5 rows, Q6_K head 125 vs 199 us at 5 rows; Q4_K
+// q (9.4 MB) 17 vs 16 us at 8 rows, 12 us on the GEMV at 5; the C5 sweep at
+// 8 rows runs 4.8% faster with q/o on the decode-batch kernel.
 constexpr int64_t kGemvMaxRows = 8;
 constexpr int64_t kDecMinRows = 5;
 constexpr uint64_t kDecMinBytes = 16u << 20;
+constexpr int64_t kDecMidRows = 7;
+constexpr uint64_t kDecMidBytes = 8u << 20;
 
 bool gemv_serves(uint32_t type, int64_t rows, uint64_t w_bytes) {
   if (rows > kGemvMaxRows) return false;
   const bool dec_fmt = type == OKQ_TYPE_Q4_K || type == OKQ_TYPE_Q6_K;
-  return !(dec_fmt && rows >= kDecMinRows && w_bytes >= kDecMinBytes);
+  if (!dec_fmt) return true;
+  if (rows >= kDecMinRows && w_bytes >= kDecMinBytes) return false;
+  return !(rows >= kDecMidRows && w_bytes >= kDecMidBytes);
 }
 
 okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint32_t type, const void *w,

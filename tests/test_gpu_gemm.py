@@ -370,6 +370,22 @@ def test_linear_dispatch_large_matrices_take_the_decode_batch_kernel_from_5_rows
         check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
 
 
+def test_linear_dispatch_mid_size_matrices_take_the_decode_batch_kernel_from_7_rows(torch, okq, orc):
+    """A Q4_K matrix of 8-16 MB (the Llama q/o projection, 9.4 MB): 6 rows run
+    the GEMV (bit-identical to okq_gemv), 7 rows the decode-batch kernel
+    (bit-identical to okq_gemm)."""
+    t, n, k = O.Q4_K, 4096, 4096
+    wq = orc.quantize(t, orc.normal(940, n * k, 0.02))
+    assert 8 << 20 <= wq.size < 16 << 20
+    for rows, pinned in ((6, "okq_gemv"), (7, "okq_gemm")):
+        print(f"[gpu] dispatch mid type={t} rows={rows} N={n} K={k}", flush=True)
+        x = orc.normal(941 + rows, rows * k, 1.0)
+        auto = run(torch, okq, "okq_linear_out_by_in_q", t, x, rows, k, wq, n)
+        pin = run(torch, okq, pinned, t, x, rows, k, wq, n)
+        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
+        check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
+
+
 def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):
     """okq_linear_out_by_in_q: 9+ rows of a Q6_K weight run the MFMA GEMM
     (bit-identical to okq_gemm), up to 8 rows the GEMV (bit-identical to
