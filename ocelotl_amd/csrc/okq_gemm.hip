@@ -965,15 +965,22 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
     const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
     float v[8];
     piece(i, v);
+    // hi = fp16 of w rounded toward zero, two values per v_cvt_pkrtz; w - hi
+    // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16, so
+    // hi + lo = w to 2^-21 relative (bf16 inputs: hi = w exactly)
     h8 hv, lv;
     float t = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float w = ldexpf(v[e], -sx);
-      t += w;
-      const _Float16 h = (_Float16)w;
-      hv[e] = h;
-      lv[e] = (_Float16)(w - (float)h);
+    for (int e = 0; e < 8; e += 2) {
+      const float w0 = ldexpf(v[e], -sx), w1 = ldexpf(v[e + 1], -sx);
+      t += w0;
+      t += w1;
+      const auto h = __builtin_amdgcn_cvt_pkrtz(w0, w1);
+      const auto l = __builtin_amdgcn_cvt_pkrtz(w0 - (float)h[0], w1 - (float)h[1]);
+      hv[e] = (_Float16)h[0];
+      hv[e + 1] = (_Float16)h[1];
+      lv[e] = (_Float16)l[0];
+      lv[e + 1] = (_Float16)l[1];
     }
     t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
     t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
