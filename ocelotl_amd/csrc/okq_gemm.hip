@@ -967,7 +967,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
     piece(i, v);
     // hi = fp16 of w rounded toward zero, two values per v_cvt_pkrtz; w - hi
     // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16, so
-    // hi + lo = w to 2^-20 relative (bf16 inputs: hi = w exactly)
+    // hi + lo = w to 2^-20 relative
     h8 hv, lv;
     float t = 0.0f;
 #pragma unroll
