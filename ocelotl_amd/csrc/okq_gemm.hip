@@ -1154,6 +1154,11 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     p.groups = (int)std::min<int64_t>((ntiles + kDecWaves - 1) / kDecWaves, cu_count);
     const int64_t ks_lds = (nsb + max_sb - 1) / max_sb;
     ks = std::min<int64_t>(nsb, std::max<int64_t>(ks_lds, cu_count / p.groups));
+    // when the LDS split alone would need more than one round of workgroups,
+    // fewer column groups (waves take more tiles) keep it to one round: each
+    // CU then stages its activation slice once
+    if (ks == ks_lds && (int64_t)p.groups * ks > cu_count && ks <= cu_count)
+      p.groups = (int)std::max<int64_t>(1, cu_count / ks);
     // unsplit K writes the final outputs with the bias staged for at most
     // kDecMaxTiles tiles per wave; wider problems take the split path
     const int64_t mytiles = (ntiles + (int64_t)p.groups * kDecWaves - 1) / ((int64_t)p.groups * kDecWaves);

@@ -144,6 +144,9 @@ DEC_CASES = [
     # 17-32 rows: two 16-row MFMA groups share each B fragment
     ("okq_gemm", 17, 300, 1024), ("okq_gemm", 32, 4096, 4096), ("okq_gemm_bf16", 25, 1000, 768),
     ("okq_gemm", 32, 14336, 4096),
+    # column groups x the LDS-bound K split exceed one round of 256 CUs: the
+    # plan takes fewer column groups and waves take several tiles (ragged)
+    ("okq_gemm", 32, 28672, 4096), ("okq_gemm_bf16", 32, 30000, 4096),
 ]
 
 
@@ -153,6 +156,8 @@ DEC_Q6K_CASES = [
     # an odd super-block count per row: block starts alternate between the two 2-byte alignments
     ("okq_gemm", 5, 333, 1280), ("okq_gemm", 2, 70003, 256),
     ("okq_gemm", 20, 1024, 4096), ("okq_gemm", 32, 4096, 14336), ("okq_gemm_bf16", 31, 257, 768),
+    # more column groups x K slices than one round of CUs (waves take 1-2 tiles)
+    ("okq_gemm", 24, 20000, 4096),
 ]
 
 
