@@ -74,30 +74,55 @@ __device__ __forceinline__ float wave_sum(float v) {
 }
 
 // Activation quantisation for the integer dot path.  A run of floats is
-// scaled by a power of two 2^-e chosen so that max|x| * 2^-e <= 0.99 * 2^15 =
-// 32440.3, rounded to an integer q and split as q = hi * 256 + lo with hi, lo
-// in [-128, 127] (hi = (q + 128) >> 8 stays <= 127 only while q <= 32639, so
-// run maxima whose mantissa f exceeds 0.99 take the next exponent: a bf16
-// maximum with f = 255/256 would otherwise give q = 32640 and hi = 128); the
-// weights' small integers then contract with hi and lo exactly through
-// v_dot4_i32_i8.  The scaling is exact (v_ldexp_f32); the only approximation
-// is the rounding of q, |error| <= 2^e / 2 <= max|x| * 2^-15.
+// scaled by a power of two 2^-e chosen so that max|x| * 2^-e <= 0.99 * 2^23,
+// rounded to an integer q and split into three signed int8 limbs
+// q = (hi * 256 + mi) * 256 + lo, each limb in [-128, 127] (lo = ((q + 128)
+// mod 256) - 128, and the same on (q - lo) / 256).  hi stays <= 127 only
+// while q <= 0x7F7F7F, so run maxima whose mantissa f exceeds 0.99 take the
+// next exponent (a bf16 maximum with f = 255/256 would otherwise reach
+// hi = 128).  The weights' small integers contract with every
+// limb exactly through v_dot4_i32_i8.  The scaling is exact (v_ldexp_f32); the
+// only approximation is the rounding of q, |error| <= 2^e / 2 <= max|x| *
+// 2^-23, so one outlier channel a thousand times its run's other values
+// leaves those values ~2^-13 relative precision (two limbs, 2^-15 of the
+// maximum, left them ~2^-5).
 __device__ __forceinline__ int x_exp(float amax) {
   int E = __builtin_amdgcn_frexp_expf(amax);    // amax = f * 2^E, f in [0.5, 1)
   float f = __builtin_amdgcn_frexp_mantf(amax);
-  return (f > 0.99f) ? E - 14 : E - 15;
+  return (f > 0.99f) ? E - 22 : E - 23;
 }
 
-__device__ __forceinline__ void x_split(float v, int e, int &hi, int &lo) {
-  int q = (int)__builtin_rintf(ldexpf(v, -e));
-  hi = (q + 128) >> 8;
-  lo = q - (hi << 8);
+// q + 0x808080: for |q| < 2^23 the three low bytes are the limbs plus 128
+// (q + 0x808080 = sum_j (limb_j + 128) 256^j with every limb_j + 128 in
+// [0, 255]), so the limbs are those bytes XOR 0x80 read as int8.
+__device__ __forceinline__ uint32_t x_digits(float v, int e) {
+  return (uint32_t)((int)__builtin_rintf(ldexpf(v, -e)) + 0x808080);
 }
 
-// Pack four int8 lanes (low byte of each) into a dword, byte 0 first.
-__device__ __forceinline__ uint32_t pack4(int a, int b, int c, int d) {
-  return (uint32_t)(a & 0xff) | ((uint32_t)(b & 0xff) << 8) | ((uint32_t)(c & 0xff) << 16) |
-         ((uint32_t)(d & 0xff) << 24);
+// Four values' digit words -> the lo, mi and hi limb dwords (byte i = value
+// i's limb): a byte transpose with v_perm_b32, then the XOR that turns each
+// biased digit into its signed limb.
+__device__ __forceinline__ void limbs4(uint32_t u0, uint32_t u1, uint32_t u2, uint32_t u3, uint32_t &hi,
+                                       uint32_t &mi, uint32_t &lo) {
+  const uint32_t a = __builtin_amdgcn_perm(u1, u0, 0x05010400u);  // u0.b0 u1.b0 u0.b1 u1.b1
+  const uint32_t b = __builtin_amdgcn_perm(u3, u2, 0x05010400u);  // u2.b0 u3.b0 u2.b1 u3.b1
+  const uint32_t c = __builtin_amdgcn_perm(u1, u0, 0x0C0C0602u);  // u0.b2 u1.b2 0 0
+  const uint32_t d = __builtin_amdgcn_perm(u3, u2, 0x0C0C0602u);  // u2.b2 u3.b2 0 0
+  lo = __builtin_amdgcn_perm(b, a, 0x05040100u) ^ 0x80808080u;
+  mi = __builtin_amdgcn_perm(b, a, 0x07060302u) ^ 0x80808080u;
+  hi = __builtin_amdgcn_perm(d, c, 0x05040100u) ^ 0x80808080u;
+}
+
+// Run sum of the three limb dot products (each an exact int32), in units of
+// the run scale 2^e: ((h * 256 + m) * 256 + l) with h * 256 + m formed in
+// int32 (|.| < 2^28 for the formats' runs), converted to f32 (exact below
+// 2^24, the Q4_K case) and one fused multiply-add, so at most two roundings
+// of 2^-24.  Without the low limb (l = 0) the value is exactly
+// (float)(h * 256 + m) * 256: hi and mi alone are q rounded to the nearest
+// multiple of 256, the 16-bit quantisation of the run (|error| <= max|x| *
+// 2^-15).
+__device__ __forceinline__ float limb_sum(int h, int m, int l) {
+  return __builtin_fmaf((float)(h * 256 + m), 256.0f, (float)l);
 }
 
 // Q4_K 6-bit (scale, min) of sub-block j from the packed scale dwords

@@ -1163,6 +1163,10 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // kDecMaxTiles tiles per wave; wider problems take the split path
     const int64_t mytiles = (ntiles + (int64_t)p.groups * kDecWaves - 1) / ((int64_t)p.groups * kDecWaves);
     if (ks == 1 && mytiles > kDecMaxTiles) ks = std::min<int64_t>(2, nsb);
+    // a single super-block per row cannot be split: more column groups
+    // (several rounds of workgroups) keep every wave within kDecMaxTiles
+    if (ks == 1 && mytiles > kDecMaxTiles)
+      p.groups = (int)((ntiles + (int64_t)kDecWaves * kDecMaxTiles - 1) / ((int64_t)kDecWaves * kDecMaxTiles));
   } else {
     p.bm = (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
     const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);

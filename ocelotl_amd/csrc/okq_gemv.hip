@@ -11,11 +11,17 @@
 //     same columns of x.
 //   * x is quantised once per workgroup, cooperatively, into LDS: each run of
 //     32 (Q4_K, Q8_0) or 16 (Q6_K) activations gets a power-of-two scale, is
-//     rounded to int16 and split into hi/lo int8 dwords, with the run's f32
-//     sum alongside (groups of 8 or 4 lanes, one float4 each, share the run's
-//     max and sum through DPP).  The weights' 4/6/8-bit integers contract with
-//     them through v_dot4_i32_i8; the partial sums are exact integers and the
-//     block scales are applied in f32.
+//     rounded to a 24-bit integer and split into three int8 limbs, with the
+//     run's f32 sum alongside (groups of 8 or 4 lanes, one float4 each, share
+//     the run's max and sum through DPP).  The weights' 4/6/8-bit integers
+//     contract with them through v_dot4_i32_i8; the partial sums are exact
+//     integers and the block scales are applied in f32.
+//   * Activations holding an infinity or a NaN (some run sum is not finite;
+//     every workgroup sees the same x, so all take the same branch) are
+//     contracted in plain f32 instead, element by element with the weights
+//     dequantised exactly, so outputs carry the reference's IEEE infinities
+//     and NaNs; rows of finite activations in the same launch keep the
+//     integer path's bits.
 //   * A row of U = K/64 units is split over a team of T = ceil(U/64) waves,
 //     so every lane owns exactly one unit and keeps its activations in
 //     registers for all rows.  A workgroup holds G teams (G*T <= 16 waves).
@@ -47,6 +53,7 @@
 #include "okq_internal.h"
 
 #include <algorithm>
+#include <type_traits>
 
 namespace okq {
 
@@ -66,17 +73,23 @@ __device__ __forceinline__ uint32_t ld16(Rsrc r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
 }
 
-// Quantised activations of one unit (160 bytes, LDS and registers):
-//   hi/lo[16]: int8 limbs of 64 activations, byte order = weight byte order
-//   s[4]     : power-of-two scale of each run (2 runs of 32 or 4 runs of 16)
-//   t[4]     : exact f32 sum of each run (for min/offset terms)
+// Quantised activations of one unit (224 bytes, LDS and registers):
+//   hi/mi/lo[16]: int8 limbs of 64 activations, byte order = weight byte order
+//   s[4]        : power-of-two scale of each run (2 runs of 32 or 4 runs of 16)
+//   t[4]        : f32 sum of each run (for min/offset terms); a run holding an
+//                 infinity or a NaN has a non-finite sum, which is how the
+//                 kernel finds activations that need the IEEE path
 struct XRec {
   uint32_t hi[16];
+  uint32_t mi[16];
   uint32_t lo[16];
   float s[4];
   float t[4];
 };
-static_assert(sizeof(XRec) == 160, "XRec layout");
+static_assert(sizeof(XRec) == 224, "XRec layout");
+// The low limbs are read from LDS where they are used (three-limb launches
+// only), so a lane's registers hold the hi/mi limbs, scales and sums.
+typedef __attribute__((address_space(3))) const uint32_t LdsU32;
 
 // 16 bytes starting at byte offset a (2-byte aligned, a & 3 == r) as four
 // dwords; reads [a - r, a - r + 16) and [a + 12 + r, a + 16 + r), both inside
@@ -98,6 +111,10 @@ __device__ __forceinline__ void realign16(const Win16 &w, uint32_t r, uint32_t o
 // ---------------------------------------------------------------------------
 struct FQ4K {
   static constexpr int kRun = 32;
+  static constexpr int kType = kQ4_K;
+  // element e < 64 of unit u is k = 64 u + e (low nibbles of the chunk's 32
+  // bytes, then the high nibbles)
+  __device__ static int kidx(int u, int e) { return 64 * u + e; }
   static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 256) * kQ4KBytes; }
   struct Regs {
     u32x4a4 hd, qa, qb;
@@ -117,17 +134,24 @@ struct FQ4K {
     word = 8 * (run & 1);
     slot = run & 1;
   }
-  __device__ static float compute(const Regs &r, const XRec &x, uint32_t lane) {
+  __device__ static float compute(const Regs &r, const XRec &x, const LdsU32 *xlo, bool lo3, uint32_t lane) {
     const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
-    int ah = 0, al = 0, bh = 0, bl = 0;
+    int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
 #pragma unroll
     for (int w = 0; w < 8; ++w) {
       const uint32_t lo4 = q[w] & 0x0F0F0F0Fu;
       const uint32_t hi4 = (q[w] >> 4) & 0x0F0F0F0Fu;
       ah = sdot4(lo4, x.hi[w], ah);
-      al = sdot4(lo4, x.lo[w], al);
+      am = sdot4(lo4, x.mi[w], am);
       bh = sdot4(hi4, x.hi[8 + w], bh);
-      bl = sdot4(hi4, x.lo[8 + w], bl);
+      bm = sdot4(hi4, x.mi[8 + w], bm);
+    }
+    if (lo3) {  // wave-uniform
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        al = sdot4(q[w] & 0x0F0F0F0Fu, xlo[w], al);
+        bl = sdot4((q[w] >> 4) & 0x0F0F0F0Fu, xlo[8 + w], bl);
+      }
     }
     // 6-bit scale/min of sub-blocks 2c and 2c+1 without divergence: for
     // c < 2 both fields are 6-bit slices of bytes 0-7, for c >= 2 a 4-bit
@@ -150,8 +174,8 @@ struct FQ4K {
         __builtin_amdgcn_ubfe(srcm, 8 * j1 + mo, width) | ((__builtin_amdgcn_ubfe(r.hd.z, 8 * j1 + 6, 2) << 4) & himask);
     const float d = f16_bits_hw(r.hd.x & 0xffffu);
     const float dmin = f16_bits_hw(r.hd.x >> 16);
-    const float pa = x.s[0] * (float)(ah * 256 + al);  // exact: power of two times an integer below 2^24
-    const float pb = x.s[1] * (float)(bh * 256 + bl);
+    const float pa = x.s[0] * limb_sum(ah, am, al);  // the power-of-two scale is exact
+    const float pb = x.s[1] * limb_sum(bh, bm, bl);
     const float a = fmaf(d * (float)scA, pa, -((dmin * (float)mA) * x.t[0]));
     const float b = fmaf(d * (float)scB, pb, -((dmin * (float)mB) * x.t[1]));
     return a + b;
@@ -163,6 +187,12 @@ struct FQ4K {
 // ---------------------------------------------------------------------------
 struct FQ6K {
   static constexpr int kRun = 16;
+  static constexpr int kType = kQ6_K;
+  // unit u = (super-block u / 4, half h = (u / 2) & 1, 16-run u2 = u & 1):
+  // element e < 64 is k = 256 sb + 128 h + 32 (e / 16) + 16 u2 + e % 16
+  __device__ static int kidx(int u, int e) {
+    return 256 * (u >> 2) + 128 * ((u >> 1) & 1) + 32 * (e >> 4) + 16 * (u & 1) + (e & 15);
+  }
   static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 256) * kQ6KBytes; }
   struct Regs {
     Win16 L, Lh, H;
@@ -193,28 +223,32 @@ struct FQ6K {
     word = 4 * qq;
     slot = qq;
   }
-  __device__ static float compute(const Regs &g, const XRec &x, uint32_t lane) {
+  __device__ static float compute(const Regs &g, const XRec &x, const LdsU32 *xlo, bool lo3, uint32_t lane) {
     uint32_t L[4], Lh[4], H[4];
     realign16(g.L, g.r, L);
     realign16(g.Lh, g.r, Lh);
     realign16(g.H, g.r, H);
     const uint32_t S0 = realign(g.sv.y, g.sv.x, g.r);
     const uint32_t S1 = realign(g.se, g.sv.y, g.r);
-    int ah[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+    int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
+    uint32_t qv[4][4];  // [w][quarter]
 #pragma unroll
     for (int w = 0; w < 4; ++w) {
-      const uint32_t q1 = (L[w] & 0x0F0F0F0Fu) | ((H[w] << 4) & 0x30303030u);
-      const uint32_t q2 = (Lh[w] & 0x0F0F0F0Fu) | ((H[w] << 2) & 0x30303030u);
-      const uint32_t q3 = ((L[w] >> 4) & 0x0F0F0F0Fu) | (H[w] & 0x30303030u);
-      const uint32_t q4 = ((Lh[w] >> 4) & 0x0F0F0F0Fu) | ((H[w] >> 2) & 0x30303030u);
-      ah[0] = sdot4(q1, x.hi[w], ah[0]);
-      al[0] = sdot4(q1, x.lo[w], al[0]);
-      ah[1] = sdot4(q2, x.hi[4 + w], ah[1]);
-      al[1] = sdot4(q2, x.lo[4 + w], al[1]);
-      ah[2] = sdot4(q3, x.hi[8 + w], ah[2]);
-      al[2] = sdot4(q3, x.lo[8 + w], al[2]);
-      ah[3] = sdot4(q4, x.hi[12 + w], ah[3]);
-      al[3] = sdot4(q4, x.lo[12 + w], al[3]);
+      qv[w][0] = (L[w] & 0x0F0F0F0Fu) | ((H[w] << 4) & 0x30303030u);
+      qv[w][1] = (Lh[w] & 0x0F0F0F0Fu) | ((H[w] << 2) & 0x30303030u);
+      qv[w][2] = ((L[w] >> 4) & 0x0F0F0F0Fu) | (H[w] & 0x30303030u);
+      qv[w][3] = ((Lh[w] >> 4) & 0x0F0F0F0Fu) | ((H[w] >> 2) & 0x30303030u);
+#pragma unroll
+      for (int qq = 0; qq < 4; ++qq) {
+        ah[qq] = sdot4(qv[w][qq], x.hi[4 * qq + w], ah[qq]);
+        am[qq] = sdot4(qv[w][qq], x.mi[4 * qq + w], am[qq]);
+      }
+    }
+    if (lo3) {  // wave-uniform
+#pragma unroll
+      for (int w = 0; w < 4; ++w)
+#pragma unroll
+        for (int qq = 0; qq < 4; ++qq) al[qq] = sdot4(qv[w][qq], xlo[4 * qq + w], al[qq]);
     }
     const uint32_t u2 = lane & 1u;
     const int sc[4] = {(int)__builtin_amdgcn_sbfe((int)S0, 8 * u2, 8u), (int)__builtin_amdgcn_sbfe((int)S0, 8 * u2 + 16, 8u),
@@ -223,7 +257,7 @@ struct FQ6K {
     float acc = 0.0f;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
-      const float t = x.s[qq] * (float)(ah[qq] * 256 + al[qq]) - 32.0f * x.t[qq];  // both products exact
+      const float t = x.s[qq] * limb_sum(ah[qq], am[qq], al[qq]) - 32.0f * x.t[qq];  // both products exact
       acc = fmaf(d * (float)sc[qq], t, acc);
     }
     return acc;
@@ -235,6 +269,9 @@ struct FQ6K {
 // ---------------------------------------------------------------------------
 struct FQ80 {
   static constexpr int kRun = 32;
+  static constexpr int kType = kQ8_0;
+  // unit u = blocks 2u and 2u + 1: k = 64 u + e
+  __device__ static int kidx(int u, int e) { return 64 * u + e; }
   static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 32) * kQ8Bytes; }
   struct Regs {
     u32x4a4 v0, v1, v2, v3;
@@ -254,66 +291,112 @@ struct FQ80 {
     word = 8 * (run & 1);
     slot = run & 1;
   }
-  __device__ static float compute(const Regs &r, const XRec &x, uint32_t) {
+  __device__ static float compute(const Regs &r, const XRec &x, const LdsU32 *xlo, bool lo3, uint32_t) {
     const uint32_t w[17] = {r.v0.x, r.v0.y, r.v0.z, r.v0.w, r.v1.x, r.v1.y, r.v1.z, r.v1.w, r.v2.x,
                             r.v2.y, r.v2.z, r.v2.w, r.v3.x, r.v3.y, r.v3.z, r.v3.w, r.v4};
-    int a0h = 0, a0l = 0, a1h = 0, a1l = 0;
+    int a0h = 0, a0m = 0, a0l = 0, a1h = 0, a1m = 0, a1l = 0;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
       const uint32_t q0 = realign(w[k + 1], w[k], 2u);  // block 0 quants: bytes 2..33
       const uint32_t q1 = w[9 + k];                       // block 1 quants: bytes 36..67
       a0h = sdot4(q0, x.hi[k], a0h);
-      a0l = sdot4(q0, x.lo[k], a0l);
+      a0m = sdot4(q0, x.mi[k], a0m);
       a1h = sdot4(q1, x.hi[8 + k], a1h);
-      a1l = sdot4(q1, x.lo[8 + k], a1l);
+      a1m = sdot4(q1, x.mi[8 + k], a1m);
+    }
+    if (lo3) {  // wave-uniform
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        a0l = sdot4(realign(w[k + 1], w[k], 2u), xlo[k], a0l);
+        a1l = sdot4(w[9 + k], xlo[8 + k], a1l);
+      }
     }
     const float d0 = f16_bits_hw(w[0] & 0xffffu);
     const float d1 = f16_bits_hw(w[8] >> 16);
-    return fmaf(d1, x.s[1] * (float)(a1h * 256 + a1l), d0 * (x.s[0] * (float)(a0h * 256 + a0l)));
+    return fmaf(d1, x.s[1] * limb_sum(a1h, a1m, a1l), d0 * (x.s[0] * limb_sum(a0h, a0m, a0l)));
   }
 };
 
 // ---------------------------------------------------------------------------
+// One weight dequantised exactly as the CPU oracle does it (every product and
+// difference rounded separately; this file is built without FMA contraction):
+// the generic fallback kernel and the IEEE path of the streaming kernel.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float deq_elem(int type, const uint8_t *row, uint32_t k) {
+  if (type == kQ8_0) {
+    const uint8_t *blk = row + (size_t)(k >> 5) * kQ8Bytes;
+    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk));
+    return (float)(int8_t)blk[2 + (k & 31)] * d;
+  } else if (type == kQ4_K) {
+    const uint8_t *blk = row + (size_t)(k >> 8) * kQ4KBytes;
+    const uint32_t rr = k & 255u, c = rr >> 6, hi = (rr >> 5) & 1u, l = rr & 31u;
+    const uint32_t *wd = reinterpret_cast<const uint32_t *>(blk);
+    uint32_t sc, m;
+    q4k_scale_min(2 * c + hi, wd[1], wd[2], wd[3], sc, m);
+    const float d = f16_bits_hw(wd[0] & 0xffffu), dmin = f16_bits_hw(wd[0] >> 16);
+    const uint32_t q = (blk[16 + 32 * c + l] >> (4 * hi)) & 15u;
+    return (d * (float)sc) * (float)q - dmin * (float)m;
+  } else {
+    const uint8_t *blk = row + (size_t)(k >> 8) * kQ6KBytes;
+    const uint32_t rr = k & 255u, hh = rr >> 7, quarter = (rr >> 5) & 3u, l = rr & 31u;
+    const uint32_t qlb = blk[64 * hh + l + ((quarter & 1u) ? 32u : 0u)];
+    const uint32_t lo4 = (qlb >> ((quarter & 2u) ? 4u : 0u)) & 15u;
+    const uint32_t hi2 = (blk[128 + 32 * hh + l] >> (2 * quarter)) & 3u;
+    const int q = (int)(lo4 | (hi2 << 4)) - 32;
+    const int sc = (int8_t)blk[192 + 8 * hh + l / 16 + 2 * quarter];
+    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk + 208));
+    return (d * (float)sc) * (float)q;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // activation prologue: lanes in groups of kRun/4 each hold one float4 of a
 // run; the group shares the run's max|x| and sum through DPP (fixed order),
-// then each lane writes one hi and one lo dword of the run's XRec.
+// then each lane writes one dword of each limb of the run's XRec.
 // ---------------------------------------------------------------------------
 template <int kCtl>
 __device__ __forceinline__ float dpp_f(float v) {
   return as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), kCtl, 0xf, 0xf, false));
 }
 
+// Returns the run's status: bit 0 when the run is wide (its largest |x|
+// exceeds 8 times its mean |x|, so the launch contracts all three limbs),
+// bit 1 when the run holds an infinity or a NaN (its sum is not finite).
 template <class F>
-__device__ __forceinline__ void quant_group(u32x4a4 raw, int f, int nf, XRec *xr) {
+__device__ __forceinline__ unsigned quant_group(u32x4a4 raw, int f, int nf, XRec *xr) {
   constexpr int GL = F::kRun / 4;  // lanes per run: 8 (runs of 32) or 4 (runs of 16)
   const float v0 = as_f32(raw.x), v1 = as_f32(raw.y), v2 = as_f32(raw.z), v3 = as_f32(raw.w);
   float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
   float t = (v0 + v1) + (v2 + v3);
+  float m = (fabsf(v0) + fabsf(v1)) + (fabsf(v2) + fabsf(v3));
   a = fmaxf(a, dpp_f<0xB1>(a));  // quad_perm 1,0,3,2
   t += dpp_f<0xB1>(t);
+  m += dpp_f<0xB1>(m);
   a = fmaxf(a, dpp_f<0x4E>(a));  // quad_perm 2,3,0,1
   t += dpp_f<0x4E>(t);
+  m += dpp_f<0x4E>(m);
   if (GL == 8) {
     a = fmaxf(a, dpp_f<0x141>(a));  // row_half_mirror: lane i <-> 7 - i within 8
     t += dpp_f<0x141>(t);
+    m += dpp_f<0x141>(m);
   }
-  if (f < nf) {
-    const int e = x_exp(a);
-    int h0, l0, h1, l1, h2, l2, h3, l3;
-    x_split(v0, e, h0, l0);
-    x_split(v1, e, h1, l1);
-    x_split(v2, e, h2, l2);
-    x_split(v3, e, h3, l3);
-    const int run = f / GL, i = f % GL;
-    int rec, word, slot;
-    F::xslot(run, rec, word, slot);
-    xr[rec].hi[word + i] = pack4(h0, h1, h2, h3);
-    xr[rec].lo[word + i] = pack4(l0, l1, l2, l3);
-    if (i == 0) {
-      xr[rec].s[slot] = ldexpf(1.0f, e);
-      xr[rec].t[slot] = t;
-    }
+  if (f >= nf) return 0u;
+  const int e = x_exp(a);
+  uint32_t hi, mi, lo;
+  limbs4(x_digits(v0, e), x_digits(v1, e), x_digits(v2, e), x_digits(v3, e), hi, mi, lo);
+  const int run = f / GL, i = f % GL;
+  int rec, word, slot;
+  F::xslot(run, rec, word, slot);
+  xr[rec].hi[word + i] = hi;
+  xr[rec].mi[word + i] = mi;
+  xr[rec].lo[word + i] = lo;
+  if (i == 0) {
+    xr[rec].s[slot] = ldexpf(1.0f, e);
+    xr[rec].t[slot] = t;
   }
+  // max <= 8 * mean: a <= m * 8 / kRun (m is the run's sum of |x|)
+  const unsigned wide = (a <= m * (8.0f / (float)F::kRun)) ? 0u : 1u;
+  return __builtin_isfinite(t) ? wide : 2u;
 }
 
 // ---------------------------------------------------------------------------
@@ -333,12 +416,12 @@ struct GemvMore {
 constexpr int kMaxXV = 4;        // float4s of x per thread, one-row launches (K <= 4 * 4 * 1024)
 constexpr int kMaxXVRows = 8;    // per thread and row, multi-row launches (K <= 8 * 4 * 512)
 constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
-constexpr int kMaxRowsPerLaunch = 4;
+constexpr int kMaxRowsPerLaunch = 2;  // three limbs of each row stay in registers (112 VGPRs)
 constexpr int kDynSteps = 4;     // dynamic rows above this many steps per wave (one wave per row)
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 // One activation row keeps one XRec per lane in registers and 16 waves fit a
-// CU; R rows keep R of them (up to 160 VGPRs), so multi-row launches are
+// CU; R rows keep R of them (112 VGPRs for two), so multi-row launches are
 // limited to 8 waves (two per SIMD).
 template <int R>
 constexpr int gemv_max_threads() {
@@ -359,8 +442,8 @@ constexpr int gemv_max_threads() {
 //
 // R activation rows (x [nrows, K], nrows <= R; y_i [nrows, N_i]) share one
 // pass over the weights: every lane holds its unit's XRec of each row and
-// contracts each weight unit it loads with all of them, so a batch of up to
-// four decode rows streams the weights once.
+// contracts each weight unit it loads with all of them, so two decode rows
+// stream the weights once.
 //
 // kPro transforms x before it is quantised (the decode neighbours of the
 // projections, computed by every workgroup from the same inputs in the same
@@ -380,6 +463,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   static_assert(kPro == kProNone || R == 1, "the neighbour prologues take one activation row");
   // kDyn launches have T == 1 (one wave per row), checked by the launcher
   __shared__ unsigned next_row;  // kDyn: the workgroup's next row index
+  __shared__ unsigned qflags[16];  // per wave: the run status bits of its lanes
   // G teams of T waves stream rows; with T == 1 the workgroup may hold extra
   // waves (g >= G) that only help quantise x.
   extern __shared__ __align__(16) unsigned char smem[];
@@ -398,6 +482,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   const int window = (int)gridDim.x * G;         // rows per step
   const int steps = (N + window - 1) / window;  // grid-uniform
   const int end = N;
+  float inv_rms = 0.0f;  // kProRms: 1 / rms of the row (the IEEE path reapplies it)
   auto row_of = [&](int step) { return step * window + (int)blockIdx.x * G + g; };
   // Matrix selection: single-matrix launches (kMulti = false) never touch M,
   // so their argument fetch is one small block; multi-matrix launches read
@@ -456,6 +541,58 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     const int p = prob(row);
     y_of(p)[(size_t)r * rows_of(p) + (row - first_row(p))] = v;
   };
+  auto wbase_of = [&](int p) { return p == 0 ? W : p == 1 ? M.w[0] : p == 2 ? M.w[1] : M.w[2]; };
+  // The IEEE path, taken by the whole launch when some activation row holds
+  // an infinity or a NaN (bit r of `slow`).  Team g's rows are shared out
+  // step by step among its T waves, and each wave computes whole rows, 64
+  // units at a time in the team's unit order.  Rows of a flagged activation
+  // row are contracted in f32 with every weight dequantised exactly (the
+  // reference's products, so its infinities and NaNs); the other rows repeat
+  // the integer path's computation and summation order, bit for bit.
+  auto ieee_rows = [&](unsigned slow_rows, unsigned wide_rows) {
+    auto xval = [&](int r, int k) -> float {
+      const float v = x[(size_t)r * K + k];
+      if constexpr (kPro == kProRms) return v * inv_rms * P.a[k];
+      if constexpr (kPro == kProSwiGLU) {
+        const float sig = 1.0f / (1.0f + expf(-v));
+        return (v * sig) * P.a[k];
+      }
+      return v;
+    };
+    for (int st = w; st < steps; st += T) {
+      const int row = row_of(st);
+      if (row >= end) break;
+      const int p = prob(row);
+      const uint32_t roff = (uint32_t)(row - first_row(p)) * rb;
+      const uint8_t *rowp = wbase_of(p) + roff;
+      const float bv = bload(row);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        if (r >= nrows) break;
+        float tot = 0.0f;
+        for (int q = 0; q < T; ++q) {
+          const int uq = 64 * q + (int)lane;
+          float acc = 0.0f;
+          if ((slow_rows >> r) & 1u) {
+            if (uq < U) {
+              for (int e = 0; e < 64; ++e) {
+                const int k = F::kidx(uq, e);
+                acc = acc + xval(r, k) * deq_elem(F::kType, rowp, (uint32_t)k);
+              }
+            }
+          } else {
+            typename F::Regs Rg;
+            F::load(Rg, rsrc(p), uq < U ? roff + F::unit_off(uq) : bytes_of(p), lane);
+            if (uq < U)
+              acc = F::compute(Rg, xr[r * U + uq], (const LdsU32 *)xr[r * U + uq].lo, (wide_rows >> r) & 1u, lane);
+          }
+          const float sum = wave_sum(acc);
+          tot = T == 1 ? sum : tot + sum;
+        }
+        if (lane == 0) store(row, r, tot + bv);
+      }
+    }
+  };
 
   // 1. activations first, XV float4s per thread (launch: XV * threads >= K/4;
   //    loads past the end of x return zeros without a memory access).  The
@@ -511,6 +648,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     float tot = 0.0f;
     for (int q = 0; q < (nt >> 6); ++q) tot += red[q];
     const float inv = 1.0f / sqrtf(tot / (float)K + P.eps);  // rms = sqrt(mean + eps), then 1 / rms
+    inv_rms = inv;
 #pragma unroll
     for (int i = 0; i < XV; ++i) {
       xv[0][i].x = as_u32(as_f32(xv[0][i].x) * inv * as_f32(av[i].x));
@@ -532,10 +670,153 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
       xv[0][i].w = gate(xv[0][i].w, av[i].w);
     }
   }
+  // 4. stream the rows, contracting two or all three limbs of each
+  //    activation row (the low limb only for rows with a wide run: a
+  //    wave-uniform branch inside the contraction)
+  auto stream_rows = [&](unsigned wide_rows) {
+    XRec xreg[R];
+    const LdsU32 *xlo[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      xreg[r] = active ? xr[r * U + u] : XRec{};
+      xlo[r] = (const LdsU32 *)xr[r * U + (active ? u : 0)].lo;
+    }
+
+    // Teams of several waves (T > 1) park each row's per-wave sums in LDS and
+    // reduce them kChunk steps at a time, one barrier per chunk.
+    constexpr int kChunk = kPartChunk;
+    auto flush = [&](int step_end) {  // rows of steps [step_end - n, step_end), n = ((step_end - 1) % kChunk) + 1
+      __syncthreads();
+      const int first = (step_end - 1) / kChunk * kChunk;
+      const int n = (step_end - first) * R;  // (step, activation row) pairs
+      if (w == 0) {
+        for (int l = (int)lane; l < n; l += 64) {
+          const int st = first + l / R, r = l % R;
+          const int row = row_of(st);
+          if (row < end && r < nrows) {
+            const float *pp = part + ((size_t)(st % kChunk) * G + g) * T * R + r;
+            float t = 0.0f;
+            for (int q = 0; q < T; ++q) t += pp[q * R];
+            const int p = prob(row);
+            const float *b = bias_of(p);
+            store(row, r, t + (b != nullptr ? b[row - first_row(p)] : 0.0f));
+          }
+        }
+      }
+      __syncthreads();  // the slots are rewritten by the next chunk
+    };
+    auto finish = [&](const typename F::Regs &Q, float b, int step) {
+      const int row = row_of(step);
+      float acc[R];
+  #pragma unroll
+      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+      if (active && row < end) {
+  #pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = F::compute(Q, xreg[r], xlo[r], (wide_rows >> r) & 1u, lane);  // the weight unpack is shared
+      }
+      float sum[R];
+  #pragma unroll
+      for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+      if (T == 1) {
+        if (lane == 0 && row < end) {
+  #pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (r < nrows) store(row, r, sum[r] + b);
+        }
+      } else {
+        if (lane == 0) {
+  #pragma unroll
+          for (int r = 0; r < R; ++r) part[((size_t)(step % kChunk) * G + g) * T * R + w * R + r] = sum[r];
+        }
+        if ((step + 1) % kChunk == 0) flush(step + 1);
+      }
+    };
+
+    if constexpr (kDyn) {
+      // Ring slot j holds row ring_row[j]; a wave's rows increase in slot
+      // order.  Idle lanes read zeros and hold zero activations, so the compute
+      // needs no branch on the lane (a divergent branch here, like an exit
+      // between slots, makes the compiler wait for every load in flight).  The
+      // loop runs while all D slots hold rows (the last slot has the largest);
+      // the drain consumes the rest without loads.
+      int ring_row[D];
+  #pragma unroll
+      for (int j = 0; j < D; ++j) ring_row[j] = row_of(j);
+      auto consume = [&](int j) {
+        const int row = ring_row[j];
+        float acc[R];
+  #pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] = F::compute(S[j], xreg[r], xlo[r], (wide_rows >> r) & 1u, lane);
+        float sum[R];
+  #pragma unroll
+        for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+        if (lane == 0 && row < end) {
+  #pragma unroll
+          for (int r = 0; r < R; ++r)
+            if (r < nrows) store(row, r, sum[r] + bs[j]);
+        }
+      };
+      const int nb = (int)gridDim.x, bi = (int)blockIdx.x;
+      while (ring_row[D - 1] < end) {
+  #pragma unroll
+        for (int j = 0; j < D; ++j) {
+          unsigned c = 0;
+          if (lane == 0) {
+            // LDS add with return, written out so that the compiler sees no
+            // atomic (one makes it drop the scalar bias loads); the wait is
+            // part of the statement because the compiler cannot track it
+            const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned *)&next_row;
+            asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(addr), "v"(1u));
+          }
+          consume(j);
+          c = (unsigned)__builtin_amdgcn_readfirstlane((int)c);  // the c-th row of the workgroup, step-major
+          const int cs = (int)(c / (unsigned)G);
+          const int nrow = (cs * nb + bi) * G + (int)(c - (unsigned)cs * (unsigned)G);
+          ring_row[j] = nrow;
+          wload(S[j], nrow);
+          bs[j] = bload(nrow);
+        }
+      }
+  #pragma unroll
+      for (int j = 0; j < D; ++j)
+        if (ring_row[j] < end) consume(j);
+      return;
+    }
+
+    // 4. stream: consume ring slot j, then refill it D steps ahead.  The loads
+    //    stay unconditional (control flow around loads makes the compiler wait
+    //    for all of them); the last pass may fetch up to D - 1 rows past the
+    //    range, which read zeros.  The final D rows are drained without loads.
+    int s0 = 0;
+    for (; s0 + D < steps; s0 += D) {
+  #pragma unroll
+      for (int j = 0; j < D; ++j) {
+        finish(S[j], bs[j], s0 + j);
+        wload(S[j], row_of(s0 + j + D));
+        bs[j] = bload(row_of(s0 + j + D));
+      }
+    }
+  #pragma unroll
+    for (int j = 0; j < D; ++j)
+      if (s0 + j < steps) finish(S[j], bs[j], s0 + j);
+    if (T > 1 && steps % kChunk != 0) flush(steps);
+  };
+
+  // Run status (quant_group): bit 2r = some run of activation row r is wide,
+  // bit 2r + 1 = some run of row r is not finite.  Each wave ORs its lanes'
+  // bits into its own LDS slot (every slot is written, so none needs
+  // clearing); after the barrier every wave ORs all slots, so the decision is
+  // the same in every wave of every workgroup (all quantised the same x).
+  unsigned qst = 0u;
 #pragma unroll
   for (int r = 0; r < R; ++r)
 #pragma unroll
-    for (int i = 0; i < XV; ++i) quant_group<F>(xv[r][i], tid + i * nt, nf, xr + r * U);
+    for (int i = 0; i < XV; ++i) qst |= quant_group<F>(xv[r][i], tid + i * nt, nf, xr + r * U) << (2 * r);
+  unsigned wst = 0u;
+#pragma unroll
+  for (int b = 0; b < 2 * R; ++b)
+    if (__ballot((qst >> b) & 1u) != 0ull) wst |= 1u << b;
+  if (lane == 0) qflags[wave] = wst;
   if (kDyn && tid == 0) next_row = (unsigned)(D * G);
   __syncthreads();
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
@@ -546,128 +827,24 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
       bs[j] = bload(row_of(j));
     }
   }
-  XRec xreg[R];
+  unsigned st_all = 0u;
+  for (int q = 0; q < (nt >> 6); ++q) st_all |= qflags[q];
+  st_all = (unsigned)__builtin_amdgcn_readfirstlane((int)st_all);
+  unsigned slow = 0u, wide = 0u;  // activation rows holding an infinity or a NaN; a wide run
 #pragma unroll
-  for (int r = 0; r < R; ++r) xreg[r] = active ? xr[r * U + u] : XRec{};
-
-  // Teams of several waves (T > 1) park each row's per-wave sums in LDS and
-  // reduce them kChunk steps at a time, one barrier per chunk.
-  constexpr int kChunk = kPartChunk;
-  auto flush = [&](int step_end) {  // rows of steps [step_end - n, step_end), n = ((step_end - 1) % kChunk) + 1
-    __syncthreads();
-    const int first = (step_end - 1) / kChunk * kChunk;
-    const int n = (step_end - first) * R;  // (step, activation row) pairs
-    if (w == 0) {
-      for (int l = (int)lane; l < n; l += 64) {
-        const int st = first + l / R, r = l % R;
-        const int row = row_of(st);
-        if (row < end && r < nrows) {
-          const float *pp = part + ((size_t)(st % kChunk) * G + g) * T * R + r;
-          float t = 0.0f;
-          for (int q = 0; q < T; ++q) t += pp[q * R];
-          const int p = prob(row);
-          const float *b = bias_of(p);
-          store(row, r, t + (b != nullptr ? b[row - first_row(p)] : 0.0f));
-        }
-      }
-    }
-    __syncthreads();  // the slots are rewritten by the next chunk
-  };
-  auto finish = [&](const typename F::Regs &Q, float b, int step) {
-    const int row = row_of(step);
-    float acc[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-    if (active && row < end) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = F::compute(Q, xreg[r], lane);  // the weight unpack is shared
-    }
-    float sum[R];
-#pragma unroll
-    for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
-    if (T == 1) {
-      if (lane == 0 && row < end) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (r < nrows) store(row, r, sum[r] + b);
-      }
-    } else {
-      if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < R; ++r) part[((size_t)(step % kChunk) * G + g) * T * R + w * R + r] = sum[r];
-      }
-      if ((step + 1) % kChunk == 0) flush(step + 1);
-    }
-  };
-
-  if constexpr (kDyn) {
-    // Ring slot j holds row ring_row[j]; a wave's rows increase in slot
-    // order.  Idle lanes read zeros and hold zero activations, so the compute
-    // needs no branch on the lane (a divergent branch here, like an exit
-    // between slots, makes the compiler wait for every load in flight).  The
-    // loop runs while all D slots hold rows (the last slot has the largest);
-    // the drain consumes the rest without loads.
-    int ring_row[D];
-#pragma unroll
-    for (int j = 0; j < D; ++j) ring_row[j] = row_of(j);
-    auto consume = [&](int j) {
-      const int row = ring_row[j];
-      float acc[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = F::compute(S[j], xreg[r], lane);
-      float sum[R];
-#pragma unroll
-      for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
-      if (lane == 0 && row < end) {
-#pragma unroll
-        for (int r = 0; r < R; ++r)
-          if (r < nrows) store(row, r, sum[r] + bs[j]);
-      }
-    };
-    const int nb = (int)gridDim.x, bi = (int)blockIdx.x;
-    while (ring_row[D - 1] < end) {
-#pragma unroll
-      for (int j = 0; j < D; ++j) {
-        unsigned c = 0;
-        if (lane == 0) {
-          // LDS add with return, written out so that the compiler sees no
-          // atomic (one makes it drop the scalar bias loads); the wait is
-          // part of the statement because the compiler cannot track it
-          const uint32_t addr = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) unsigned *)&next_row;
-          asm volatile("ds_add_rtn_u32 %0, %1, %2\n\ts_waitcnt lgkmcnt(0)" : "=v"(c) : "v"(addr), "v"(1u));
-        }
-        consume(j);
-        c = (unsigned)__builtin_amdgcn_readfirstlane((int)c);  // the c-th row of the workgroup, step-major
-        const int cs = (int)(c / (unsigned)G);
-        const int nrow = (cs * nb + bi) * G + (int)(c - (unsigned)cs * (unsigned)G);
-        ring_row[j] = nrow;
-        wload(S[j], nrow);
-        bs[j] = bload(nrow);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < D; ++j)
-      if (ring_row[j] < end) consume(j);
+  for (int r = 0; r < R; ++r) {
+    slow |= ((st_all >> (2 * r + 1)) & 1u) << r;
+    wide |= ((st_all >> (2 * r)) & 1u) << r;
+  }
+  // Every run narrow (max|x| <= 8 mean|x|): two limbs, the 16-bit
+  // quantisation, keep each activation within 2^-12 of its run's mean
+  // magnitude; a wide run (an outlier channel) makes the launch contract all
+  // three limbs, 2^-23 of the run maximum.
+  if (slow != 0u) {
+    ieee_rows(slow, wide);
     return;
   }
-
-  // 4. stream: consume ring slot j, then refill it D steps ahead.  The loads
-  //    stay unconditional (control flow around loads makes the compiler wait
-  //    for all of them); the last pass may fetch up to D - 1 rows past the
-  //    range, which read zeros.  The final D rows are drained without loads.
-  int s0 = 0;
-  for (; s0 + D < steps; s0 += D) {
-#pragma unroll
-    for (int j = 0; j < D; ++j) {
-      finish(S[j], bs[j], s0 + j);
-      wload(S[j], row_of(s0 + j + D));
-      bs[j] = bload(row_of(s0 + j + D));
-    }
-  }
-#pragma unroll
-  for (int j = 0; j < D; ++j)
-    if (s0 + j < steps) finish(S[j], bs[j], s0 + j);
-  if (T > 1 && steps % kChunk != 0) flush(steps);
+  stream_rows(wide);
 }
 
 // ---------------------------------------------------------------------------
@@ -676,33 +853,6 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
 // rows longer than 16 waves of units (K > 65536), tensors of 4 GiB or more,
 // and Q8_0 rows that are not dword aligned (an odd number of blocks per row).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float deq_elem(int type, const uint8_t *row, uint32_t k) {
-  if (type == kQ8_0) {
-    const uint8_t *blk = row + (size_t)(k >> 5) * kQ8Bytes;
-    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk));
-    return (float)(int8_t)blk[2 + (k & 31)] * d;
-  } else if (type == kQ4_K) {
-    const uint8_t *blk = row + (size_t)(k >> 8) * kQ4KBytes;
-    const uint32_t rr = k & 255u, c = rr >> 6, hi = (rr >> 5) & 1u, l = rr & 31u;
-    const uint32_t *wd = reinterpret_cast<const uint32_t *>(blk);
-    uint32_t sc, m;
-    q4k_scale_min(2 * c + hi, wd[1], wd[2], wd[3], sc, m);
-    const float d = f16_bits_hw(wd[0] & 0xffffu), dmin = f16_bits_hw(wd[0] >> 16);
-    const uint32_t q = (blk[16 + 32 * c + l] >> (4 * hi)) & 15u;
-    return (d * (float)sc) * (float)q - dmin * (float)m;
-  } else {
-    const uint8_t *blk = row + (size_t)(k >> 8) * kQ6KBytes;
-    const uint32_t rr = k & 255u, hh = rr >> 7, quarter = (rr >> 5) & 3u, l = rr & 31u;
-    const uint32_t qlb = blk[64 * hh + l + ((quarter & 1u) ? 32u : 0u)];
-    const uint32_t lo4 = (qlb >> ((quarter & 2u) ? 4u : 0u)) & 15u;
-    const uint32_t hi2 = (blk[128 + 32 * hh + l] >> (2 * quarter)) & 3u;
-    const int q = (int)(lo4 | (hi2 << 4)) - 32;
-    const int sc = (int8_t)blk[192 + 8 * hh + l / 16 + 2 * quarter];
-    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk + 208));
-    return (d * (float)sc) * (float)q;
-  }
-}
-
 __global__ __launch_bounds__(256) void gemv_generic_kernel(int type, const uint8_t *__restrict__ W,
                                                            const float *__restrict__ x,
                                                            const float *__restrict__ bias, float *__restrict__ y,
@@ -801,8 +951,7 @@ template <class F>
 void launch_rows(int R, int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s,
                  const GemvLaunch &L, const float *x, int k, int T, int G) {
   if (R == 1) launch_xv<F, 1>(xv, steps, grid, block, lds, s, L, x, k, T, G);
-  else if (R == 2) launch_xv<F, 2>(xv, steps, grid, block, lds, s, L, x, k, T, G);
-  else launch_xv<F, 4>(xv, steps, grid, block, lds, s, L, x, k, T, G);
+  else launch_xv<F, 2>(xv, steps, grid, block, lds, s, L, x, k, T, G);
 }
 
 namespace {
@@ -840,7 +989,7 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
   const int64_t N = P.rows;
   const int U = (int)(K / 64);
   const int T = (U + 63) / 64;  // waves per row team
-  const int max_threads = R == 1 ? gemv_max_threads<1>() : gemv_max_threads<4>();
+  const int max_threads = R == 1 ? gemv_max_threads<1>() : gemv_max_threads<2>();
   const int max_xv = R == 1 ? kMaxXV : kMaxXVRows;
   // one workgroup per CU (fewer for short tensors); steps = rows per team at
   // the largest team count, then the fewest teams that still finish in that
@@ -936,7 +1085,7 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, 
     P.nrows = nr;
     P.y = y[0] + r0 * N[0];
     for (int i = 1; i < count; ++i) P.M.y[i - 1] = y[i] + r0 * N[i];
-    const int R = nr == 1 ? 1 : nr == 2 ? 2 : 4;
+    const int R = nr == 1 ? 1 : 2;
     hipError_t e = launch_stream(type, x + r0 * K, K, P, R, cu_count, s);
     if (e != hipSuccess) return e;
   }

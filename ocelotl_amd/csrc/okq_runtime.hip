@@ -198,11 +198,18 @@ okq_status validate_rmsnorm(const float *x, int64_t rows, int64_t hidden, const 
 }
 
 // ---- GEMM workspace ----------------------------------------------------------
-// One buffer per (device, stream): work on one stream is ordered, so reuse is
-// safe; different streams never share.  Grows on demand; growing is refused
-// while the stream is being captured into a graph (allocation is not
+// One buffer per (device, stream, slot): work on one stream is ordered, so
+// reuse is safe; different streams never share.  Grows on demand; growing is
+// refused while the stream is being captured into a graph (allocation is not
 // capturable), so a caller that captures must run one call of at least the
 // same size on that stream first.
+//
+// A buffer is never freed once handed out.  A graph captured earlier keeps
+// the pointer it recorded, and another host thread may have looked up the
+// buffer and not yet enqueued its kernel, so a grown slot moves to a new
+// buffer and the old one stays allocated until the process ends.  Growth is
+// by half again of the request, so the buffers of one slot stay within about
+// three times its largest request.
 struct Workspace {
   void *ptr = nullptr;
   size_t bytes = 0;
@@ -226,17 +233,11 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
                 "hip-gfx950: GEMM workspace of %zu bytes is not allocated for this stream and cannot be allocated "
                 "during graph capture; run one call of this size on the stream before capturing",
                 bytes);
-  if (w.ptr) {
-    if (hipStreamSynchronize(s) != hipSuccess || hipFree(w.ptr) != hipSuccess)
-      return fail(OKQ_E_LAUNCH, "hip-gfx950: cannot release the previous GEMM workspace");
-    w.ptr = nullptr;
-    w.bytes = 0;
-  }
   const size_t want = bytes + bytes / 2;
-  if (hipMalloc(&w.ptr, want) != hipSuccess) {
-    w.ptr = nullptr;
+  void *p = nullptr;
+  if (hipMalloc(&p, want) != hipSuccess)
     return fail(OKQ_E_ALLOC, "hip-gfx950: hipMalloc of a %zu-byte GEMM workspace failed", want);
-  }
+  w.ptr = p;  // the previous buffer (if any) stays allocated: see above
   w.bytes = want;
   *out = w.ptr;
   return ok();
@@ -245,7 +246,7 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
-// serves up to four rows); above it the MFMA GEMM path (the streaming
+// serves up to two rows); above it the MFMA GEMM path (the streaming
 // decode-batch kernel up to 32 rows, the tiled kernel beyond).  Large Q4_K /
 // Q6_K matrices take the decode-batch kernel earlier: it streams the weights
 // once where the GEMV needs a second pass, and its fixed cost (the split-K
@@ -306,7 +307,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
     if (e != hipSuccess) return hip_status(e, "bf16 widening launch");
     xf = static_cast<const float *>(ws);
   }
-  // every pass over the weights serves up to four rows
+  // every pass over the weights serves up to two rows
   hipError_t e = okq::launch_gemv_multi((int)type, xf, K, rows, 1, &w, &N, &bias, &out, info.cu_count, s,
                                         okq::GemvPro{});
   return hip_status(e, "gemv launch");
