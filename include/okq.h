@@ -131,7 +131,7 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
  * in_features] tensor, w_bytes = out_features * row_bytes(in_features);
  * bias: [out_features] f32 or NULL; out: [rows, out_features] f32.
  * rows == 0 or out_features == 0 is a no-op.  Up to 8 rows run the fused
- * dequant-GEMV (each pass over the weights serving up to two rows), except
+ * dequant-GEMV (each pass over the weights serving up to four rows), except
  * Q4_K / Q6_K matrices of 16 MB or more from 5 rows on and of 8 MB or more
  * from 7 rows on; more rows run the
  * MFMA dequant-GEMM (Q4_K, Q6_K; Q8_0 stays on the GEMV), which for up to 32
@@ -197,7 +197,7 @@ okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float
  * Arguments as okq_rmsnorm and okq_gemv_multi.  A single row runs the GEMV
  * with the normalisation folded into its activation prologue (no normalised
  * copy of x is written); more rows normalise into a per-stream workspace
- * first and then stream each weight once per two rows.  No counterpart in the reference, whose blocks
+ * first and then stream each weight once per four rows.  No counterpart in the reference, whose blocks
  * call rmsnorm and then each linear (crates/models/src/qwen/qwen2_5/prefill.rs). */
 okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidden, const float *norm_weight,
                                       float epsilon, uint32_t w_type, int count, const void *const *w,

@@ -416,12 +416,13 @@ struct GemvMore {
 constexpr int kMaxXV = 4;        // float4s of x per thread, one-row launches (K <= 4 * 4 * 1024)
 constexpr int kMaxXVRows = 8;    // per thread and row, multi-row launches (K <= 8 * 4 * 512)
 constexpr int kPartChunk = 32;   // steps whose team partial sums wait in LDS
-constexpr int kMaxRowsPerLaunch = 2;  // three limbs of each row stay in registers (112 VGPRs)
+constexpr int kMaxRowsPerLaunch = 4;
 constexpr int kDynSteps = 4;     // dynamic rows above this many steps per wave (one wave per row)
 constexpr size_t kLdsBytes = 160 * 1024;  // LDS per workgroup on gfx950
 
 // One activation row keeps one XRec per lane in registers and 16 waves fit a
-// CU; R rows keep R of them (112 VGPRs for two), so multi-row launches are
+// CU; R rows keep R of them (their hi/mi limbs, scales and sums: 160 VGPRs
+// for four; the low limbs are read from LDS), so multi-row launches are
 // limited to 8 waves (two per SIMD).
 template <int R>
 constexpr int gemv_max_threads() {
@@ -442,8 +443,8 @@ constexpr int gemv_max_threads() {
 //
 // R activation rows (x [nrows, K], nrows <= R; y_i [nrows, N_i]) share one
 // pass over the weights: every lane holds its unit's XRec of each row and
-// contracts each weight unit it loads with all of them, so two decode rows
-// stream the weights once.
+// contracts each weight unit it loads with all of them, so a batch of up to
+// four decode rows streams the weights once.
 //
 // kPro transforms x before it is quantised (the decode neighbours of the
 // projections, computed by every workgroup from the same inputs in the same
@@ -951,7 +952,8 @@ template <class F>
 void launch_rows(int R, int xv, int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s,
                  const GemvLaunch &L, const float *x, int k, int T, int G) {
   if (R == 1) launch_xv<F, 1>(xv, steps, grid, block, lds, s, L, x, k, T, G);
-  else launch_xv<F, 2>(xv, steps, grid, block, lds, s, L, x, k, T, G);
+  else if (R == 2) launch_xv<F, 2>(xv, steps, grid, block, lds, s, L, x, k, T, G);
+  else launch_xv<F, 4>(xv, steps, grid, block, lds, s, L, x, k, T, G);
 }
 
 namespace {
@@ -989,7 +991,7 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
   const int64_t N = P.rows;
   const int U = (int)(K / 64);
   const int T = (U + 63) / 64;  // waves per row team
-  const int max_threads = R == 1 ? gemv_max_threads<1>() : gemv_max_threads<2>();
+  const int max_threads = R == 1 ? gemv_max_threads<1>() : gemv_max_threads<4>();
   const int max_xv = R == 1 ? kMaxXV : kMaxXVRows;
   // one workgroup per CU (fewer for short tensors); steps = rows per team at
   // the largest team count, then the fewest teams that still finish in that
@@ -1085,7 +1087,7 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, 
     P.nrows = nr;
     P.y = y[0] + r0 * N[0];
     for (int i = 1; i < count; ++i) P.M.y[i - 1] = y[i] + r0 * N[i];
-    const int R = nr == 1 ? 1 : 2;
+    const int R = nr == 1 ? 1 : nr == 2 ? 2 : 4;
     hipError_t e = launch_stream(type, x + r0 * K, K, P, R, cu_count, s);
     if (e != hipSuccess) return e;
   }

@@ -62,7 +62,7 @@ struct GemvPro {
 };
 bool gemv_streams(int type, int64_t K, const void *w, int64_t N);
 // x [rows, K] and y[i] [rows, N[i]] row-major; every pass over the weights
-// serves up to two activation rows.  A prologue needs rows == 1.
+// serves up to four activation rows.  A prologue needs rows == 1.
 hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
                              hipStream_t s, const GemvPro &pro);

@@ -246,7 +246,7 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
-// serves up to two rows); above it the MFMA GEMM path (the streaming
+// serves up to four rows); above it the MFMA GEMM path (the streaming
 // decode-batch kernel up to 32 rows, the tiled kernel beyond).  Large Q4_K /
 // Q6_K matrices take the decode-batch kernel earlier: it streams the weights
 // once where the GEMV needs a second pass, and its fixed cost (the split-K
@@ -307,7 +307,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
     if (e != hipSuccess) return hip_status(e, "bf16 widening launch");
     xf = static_cast<const float *>(ws);
   }
-  // every pass over the weights serves up to two rows
+  // every pass over the weights serves up to four rows
   hipError_t e = okq::launch_gemv_multi((int)type, xf, K, rows, 1, &w, &N, &bias, &out, info.cu_count, s,
                                         okq::GemvPro{});
   return hip_status(e, "gemv launch");

@@ -229,7 +229,7 @@ def test_small_batch_rows_and_determinism(torch, okq, orc, t):
 
 
 MULTIROW_CASES = [
-    # (type, rows, n, k): every pass over the weights serves up to two rows
+    # (type, rows, n, k): every pass over the weights serves up to four rows
     (O.Q4_K, 2, 4096, 4096), (O.Q4_K, 3, 1024, 4096), (O.Q4_K, 4, 14336, 4096), (O.Q4_K, 4, 4096, 14336),
     (O.Q4_K, 8, 512, 14336), (O.Q4_K, 4, 33, 8192),
     (O.Q6_K, 2, 1024, 4096), (O.Q6_K, 4, 4096, 14336), (O.Q6_K, 7, 300, 12288),
