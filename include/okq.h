@@ -146,6 +146,25 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
                                        const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
                                        float *out, void *stream);
 
+/* okq_linear_out_by_in_q without any device allocation: the same contract,
+ * dispatch and kernels (bit-identical outputs), with the MFMA kernels'
+ * scratch (activation planes, split-K partials) taken from a static 32 MiB
+ * device array instead of the per-stream workspace, so no call allocates or
+ * frees memory (hipMalloc, hipFree, or any library routine that allocates).
+ * No counterpart in the reference: it serves callers that cannot allocate --
+ * code under HIP graph capture, tight serving loops, harnesses that forbid
+ * allocation.  Limits: a problem whose scratch exceeds 32 MiB fails with
+ * OKQ_E_SHAPE before anything launches (f32 activations: for example up to
+ * 32 rows at any Llama-3-8B shape, and the tiled GEMM while 2 x rows x
+ * in_features x 2 bytes plus its partials fit); every call on one device
+ * shares the array and keeps the last call's contents, so calls that overlap
+ * on one device (several streams or threads at once) race.  The array's
+ * device address is resolved once per device by okq_init (or by the first
+ * call on that device). */
+okq_status okq_linear_out_by_in_q_noalloc(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
+                                          const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
+                                          float *out, void *stream);
+
 /* Explicit-path variants of okq_linear_out_by_in_q (same arguments): the fused
  * dequant-GEMV (one weight pass per activation row) and the MFMA dequant-GEMM.
  * For benchmarks and tests that pin a path. */

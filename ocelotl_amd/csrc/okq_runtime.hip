@@ -270,8 +270,47 @@ bool gemv_serves(uint32_t type, int64_t rows, uint64_t w_bytes) {
   return !(rows >= kDecMidRows && w_bytes >= kDecMidBytes);
 }
 
+// ---- static scratch for the allocation-free entry point -----------------------
+// okq_linear_out_by_in_q_noalloc takes its GEMM scratch (activation planes,
+// per-32 sums, row scales, split-K partials) from this array instead of the
+// per-stream workspace, so it never allocates.  Every device holds its own
+// copy at its own address; host code uses only the address that
+// hipGetSymbolAddress returns for the current device (the array's name is a
+// host-side stand-in).  Calls on one device share the array: overlapping calls
+// (several streams or threads at once) race.  Nothing in it needs clearing:
+// every kernel writes the scratch it later reads.
+constexpr size_t kScratchBytes = 32u << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+std::mutex g_scratch_mutex;
+void *g_scratch_ptr[64] = {};
+
+// The device address of `scratch` on device `dev` (which must be current),
+// looked up once per device.
+okq_status scratch_for(int dev, void **out) {
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(OKQ_E_LAUNCH, "hip-gfx950: cannot resolve the static scratch of device %d: %s", dev,
+                  hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return ok();
+}
+
+// Scratch of a call: the per-stream workspace (grown on demand), or the
+// static array of okq_linear_out_by_in_q_noalloc (never grown: a request
+// beyond it is an error, before anything launches).
+struct Scratch {
+  bool fixed = false;
+};
+
 okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint32_t type, const void *w,
-                       uint64_t w_bytes, int64_t N, const float *bias, float *out, void *stream, Path path) {
+                       uint64_t w_bytes, int64_t N, const float *bias, float *out, void *stream, Path path,
+                       Scratch sc = Scratch{}) {
   LinearArgs a{rows, K, N, type, w_bytes};
   okq_status st = validate_linear(x, a, w, out, x_bf16);
   if (st != OKQ_OK) return st;
@@ -293,7 +332,16 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
   if (use_gemm) {
     void *ws = nullptr;
     const okq::GemmPlan plan = okq::gemm_plan((int)type, rows, N, K, x_bf16, info.cu_count);
-    st = get_workspace(dev, s, plan.workspace, &ws);
+    if (sc.fixed) {
+      if (plan.workspace > kScratchBytes)
+        return fail(OKQ_E_SHAPE,
+                    "linear_out_by_in_noalloc: rows=%lld in_features=%lld out_features=%lld needs %zu bytes of "
+                    "scratch, more than the static %zu bytes",
+                    (long long)rows, (long long)K, (long long)N, plan.workspace, kScratchBytes);
+      st = scratch_for(dev, &ws);
+    } else {
+      st = get_workspace(dev, s, plan.workspace, &ws);
+    }
     if (st != OKQ_OK) return st;
     return hip_status(okq::launch_gemm((int)type, x, x_bf16, rows, K, w, N, bias, out, ws, plan, s), "gemm launch");
   }
@@ -394,7 +442,10 @@ okq_status okq_init(int ordinal) {
   if (hipSetDevice(ordinal) != hipSuccess) return fail(OKQ_E_NODEV, "hip-gfx950: cannot select device %d", ordinal);
   int dev;
   DevInfo info;
-  return current_device(dev, info);
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  void *p = nullptr;
+  return scratch_for(dev, &p);  // the allocation-free entry point's scratch address on this device
 }
 
 okq_status okq_alloc(void **ptr, size_t bytes) {
@@ -724,6 +775,13 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   if (e != hipSuccess) return hip_status(e, "swiglu launch");
   return linear_impl(gate_buf, false, rows, intermediate, down_type, down_w, down_bytes, hidden, nullptr, out, stream,
                      Path::Auto);
+}
+
+okq_status okq_linear_out_by_in_q_noalloc(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
+                                          const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
+                                          float *out, void *stream) {
+  return linear_impl(x, false, rows, in_features, w_type, w, w_bytes, out_features, bias, out, stream, Path::Auto,
+                     Scratch{true});
 }
 
 okq_status okq_gemv(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, const void *w,

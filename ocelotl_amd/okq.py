@@ -41,6 +41,7 @@ SIGNATURES = {
     "okq_dequantize": (_int, [_u32, _vp, _i64, _vp, _vp]),
     "okq_linear_out_by_in_q": _linear_sig,
     "okq_linear_out_by_in_q_bf16": _linear_sig,
+    "okq_linear_out_by_in_q_noalloc": _linear_sig,
     "okq_gemv": _linear_sig,
     "okq_gemm": _linear_sig,
     "okq_gemm_bf16": _linear_sig,
