@@ -170,7 +170,7 @@ struct alignas(16) GemmSmem {
   _Float16 A[2][BM][kLDB];
   _Float16 Alo[2][kLo ? BM : 1][kLDB];
   _Float16 B[2][kBN][kLDB];
-  _Float16 Blo[2][kFmt == kQ6_K ? kBN : 1][kLDB];  // Q6_K: the exact remainder plane
+  _Float16 Blo[2][kFmt == kQ6_K || kFmt == kQ8_0 ? kBN : 1][kLDB];  // Q6_K, Q8_0: the exact remainder plane
   _Float16 xs[2][kMins ? BM : 1][16];   // per super-block parity: xsum hi/lo of sub-blocks 0..7
   _Float16 mn[2][kMins ? kBN : 1][16];  // per super-block parity: 6-bit mins, each twice
   float d[2][kBN], dmin[2][kMins ? kBN : 1];
@@ -188,6 +188,8 @@ struct StepRegs {
   // scales; d (2-byte load, first chunk of a super-block)
   uint32_t l0[kFmt == kQ6_K ? 5 : 1], l1[kFmt == kQ6_K ? 5 : 1], hq[kFmt == kQ6_K ? 5 : 1];
   uint32_t sc[kFmt == kQ6_K ? 3 : 1], dw;
+  // Q8_0 (BM = 128): the dword window of this thread's 34-byte block
+  uint32_t q8[kFmt == kQ8_0 ? 9 : 1];
 };
 
 // v = sc * (q - 32) for the four 6-bit values in the bytes of q4, as two
@@ -205,6 +207,24 @@ __device__ __forceinline__ void q6_4(uint32_t q4, h2 sc2, h2 &p0, h2 &p1, h2 &l0
   l1 = __builtin_elementwise_fma(b, sc2, -p1);
 }
 
+// d * q for the four int8 quants in the bytes of q4, as two exact fp16 planes
+// d * q = hi + lo: (q ^ 0x80) | 0x6400 is the fp16 1152 + q, minus 1152 gives
+// q exactly; hi = fp16(d * q) (one rounding) and lo = fma(q, d, -hi) is the
+// exact remainder.  Exact because d * q has at most 19 significant bits whose
+// lowest is at least 2^-24 (d is an fp16), so the remainder fits an fp16, for
+// every block with |d * q| below 65520 (|d| < 511.9, any block quantised from
+// fp16-representable weights).
+__device__ __forceinline__ void q8_4(uint32_t q4, h2 d2, h2 &p0, h2 &p1, h2 &l0, h2 &l1) {
+  const h2 off = {(_Float16)-1152.0f, (_Float16)-1152.0f};
+  const uint32_t b = q4 ^ 0x80808080u;
+  const h2 a = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, b, 0x04010400u)) + off;
+  const h2 c = __builtin_bit_cast(h2, __builtin_amdgcn_perm(0x64646464u, b, 0x04030402u)) + off;
+  p0 = a * d2;
+  p1 = c * d2;
+  l0 = __builtin_elementwise_fma(a, d2, -p0);
+  l1 = __builtin_elementwise_fma(c, d2, -p1);
+}
+
 // BM x 128 workgroup tile, BM/32 waves arranged (BM/64) x 2, each 64 x 64.
 // Software pipeline over 64-wide K steps: raw loads run two steps ahead in
 // registers, the dequantisation of step i+1 overlaps the MFMAs of step i, LDS
@@ -219,9 +239,11 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
   constexpr int NT = BM * 2;       // threads
   constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
   constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
-  constexpr bool kQ6 = kFmt == kQ6_K;
+  constexpr bool kQ6 = kFmt == kQ6_K, kQ8 = kFmt == kQ8_0;
   static_assert(!kQ6 || QB == 16, "Q6_K staging takes 16-byte windows (BM = 128)");
-  constexpr uint32_t kBlk = kQ6 ? kQ6KBytes : kQ4KBytes;
+  static_assert(!kQ8 || TPR == 2, "Q8_0 staging takes one 34-byte block per thread (BM = 128)");
+  // bytes per 256 weights of a row: one super-block, or eight Q8_0 blocks
+  constexpr uint32_t kBlk = kQ6 ? kQ6KBytes : kQ8 ? 8 * kQ8Bytes : kQ4KBytes;
   __shared__ GemmSmem<BM, kLo, kFmt> sm;
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
   // contiguous range of tiles (consecutive tiles share an N-tile).
@@ -273,6 +295,18 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
 #pragma unroll
       for (int i = 0; i < 4; ++i) r.al[i] = bload4(rs_xl, ka + 16u * i);
     }
+    if constexpr (kQ8) {
+      // blocks 2c and 2c + 1 of the super-block hold this step's 64 weights;
+      // thread bq stages block 2c + bq: a 9-dword window from the dword below
+      // its (2-byte aligned) start
+      const uint32_t B = w_row + (uint32_t)sb * kBlk + (2u * c + (uint32_t)bq) * kQ8Bytes;
+      const uint32_t a = B & ~3u;
+      const u32x4 v0 = bload4(rs_w, a), v1 = bload4(rs_w, a + 16u);
+      r.q8[0] = v0.x, r.q8[1] = v0.y, r.q8[2] = v0.z, r.q8[3] = v0.w;
+      r.q8[4] = v1.x, r.q8[5] = v1.y, r.q8[6] = v1.z, r.q8[7] = v1.w;
+      r.q8[8] = __builtin_amdgcn_raw_buffer_load_b32(rs_w, a + 32u, 0, 0);
+      return;
+    }
     if constexpr (kQ6) {
       // chunk c of the super-block: half h = c / 2 (ql bytes 64h.., qh bytes
       // 128 + 32h..); this thread's l = 16 bq .. 16 bq + 15.  Windows start at
@@ -315,6 +349,32 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
       u32x4 *dl = reinterpret_cast<u32x4 *>(&sm.Alo[buf][sr][32 * sp]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) dl[i] = r.al[i];
+    }
+    if constexpr (kQ8) {
+      const uint32_t B = w_row + (uint32_t)(step >> 2) * kBlk + (2u * c + (uint32_t)bq) * kQ8Bytes;
+      const uint32_t ra = B & 3u;
+      uint32_t wv[9];  // bytes B + 4i .. of the block (realigned window)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) wv[t] = __builtin_amdgcn_alignbyte(r.q8[t + 1], r.q8[t], ra);
+      wv[8] = __builtin_amdgcn_alignbyte(0u, r.q8[8], ra);
+      const _Float16 dh = __builtin_bit_cast(_Float16, (uint16_t)(wv[0] & 0xffffu));
+      const h2 d2 = {dh, dh};
+      h2 hi[16], lo[16];
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        const uint32_t q4 = __builtin_amdgcn_alignbyte(wv[w + 1], wv[w], 2u);  // quants 4w .. 4w + 3
+        q8_4(q4, d2, hi[2 * w], hi[2 * w + 1], lo[2 * w], lo[2 * w + 1]);
+      }
+      auto put = [&](_Float16 *dst, const h2 *v) {
+        u32x4 *d4 = reinterpret_cast<u32x4 *>(dst);
+#pragma unroll
+        for (int t = 0; t < 4; ++t)
+          d4[t] = u32x4{__builtin_bit_cast(uint32_t, v[4 * t]), __builtin_bit_cast(uint32_t, v[4 * t + 1]),
+                        __builtin_bit_cast(uint32_t, v[4 * t + 2]), __builtin_bit_cast(uint32_t, v[4 * t + 3])};
+      };
+      put(&sm.B[buf][br][32 * bq], hi);
+      put(&sm.Blo[buf][br][32 * bq], lo);
+      return;
     }
     if constexpr (kQ6) {
       constexpr uint32_t cc = c & 1, h = c >> 1;
@@ -441,7 +501,7 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
         for (int j = 0; j < 2; ++j)
           accs[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv[j], (first && ks == 0) ? zero : accs[i][j],
                                                               0, 0, 0);
-      if constexpr (kQ6) {  // the exact remainder plane of the weights (x_lo * remainder is below 2^-22)
+      if constexpr (kQ6 || kQ8) {  // the exact remainder plane of the weights (x_lo * remainder is below 2^-22)
 #pragma unroll
         for (int j = 0; j < 2; ++j) {
           const h8 bl = *reinterpret_cast<const h8 *>(&sm.Blo[buf][wn * 64 + 32 * j + fr][fk4 + 8 * ks]);
@@ -465,6 +525,15 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
 
   // end of a super-block: acc += d * accs - dmin * (xsum . m)  (Q6_K: d * accs)
   auto scale = [&](int sbp) {
+    if constexpr (kQ8) {  // d is inside the B planes
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int e = 0; e < 16; ++e) acc[i][j][e] += accs[i][j][e];
+      return;
+    }
     if constexpr (kQ6) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -784,6 +853,68 @@ struct DecQ6K {
     for (int q = 0; q < RG; ++q)
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dv, accs[q][v], acc[q][v]);
+  }
+};
+
+// Q8_0: an item is 256 weights of a column, eight 34-byte blocks (272 bytes,
+// 2-byte aligned).  Lane group g covers blocks 2g and 2g + 1 (k = 64g ..
+// 64g + 63); slice t (8 per item) is k = 64g + 8t + [0, 8), quants 8(t & 3) ..
+// of block 2g + (t >> 2).  The lane reads its 68 bytes as an 18-dword window
+// from the dword below them and realigns it; d is folded into two exact fp16
+// B planes (q8_4), so the item needs no scaling afterwards.
+struct DecQ80 {
+  static constexpr uint32_t kBlk = 8 * kQ8Bytes;
+  static constexpr int kDepth = 2, kDepth1 = 3;
+  struct Item {
+    u32x4 w0, w1, w2, w3;
+    u32x2 w4;
+    uint32_t r;
+  };
+  __device__ static void load(Item &it, Rsrc rs, uint32_t blk, int g) {
+    const uint32_t S = blk + 68u * (uint32_t)g, r = S & 3u, a = S - r;
+    it.w0 = bload4(rs, a);
+    it.w1 = bload4(rs, a + 16u);
+    it.w2 = bload4(rs, a + 32u);
+    it.w3 = bload4(rs, a + 48u);
+    it.w4 = __builtin_amdgcn_raw_buffer_load_b64(rs, a + 64u, 0, 0);
+    it.r = r;
+  }
+  template <bool kLo, int RG>
+  __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
+                                  const _Float16 *const *, int g, f4 *acc) {
+    const uint32_t raw[18] = {it.w0.x, it.w0.y, it.w0.z, it.w0.w, it.w1.x, it.w1.y, it.w1.z, it.w1.w, it.w2.x,
+                              it.w2.y, it.w2.z, it.w2.w, it.w3.x, it.w3.y, it.w3.z, it.w3.w, it.w4.x, it.w4.y};
+    uint32_t w[17];  // bytes 4i .. 4i + 3 of the lane's 68 bytes
+#pragma unroll
+    for (int i = 0; i < 17; ++i) w[i] = __builtin_amdgcn_alignbyte(raw[i + 1], raw[i], it.r);
+    // block 2g: d in bytes 0-1, quants in bytes 2-33; block 2g + 1: d in bytes
+    // 34-35, quants in bytes 36-67 (dword aligned)
+    const _Float16 d0 = __builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xffffu));
+    const _Float16 d1 = __builtin_bit_cast(_Float16, (uint16_t)(w[8] >> 16));
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int blk = t >> 2, o = 2 * (t & 3);  // dword of the 8 quants within the block's quants
+      const uint32_t qa = blk ? w[9 + o] : __builtin_amdgcn_alignbyte(w[o + 1], w[o], 2u);
+      const uint32_t qb = blk ? w[10 + o] : __builtin_amdgcn_alignbyte(w[o + 2], w[o + 1], 2u);
+      const _Float16 dh = blk ? d1 : d0;
+      const h2 d2 = {dh, dh};
+      h2 p0, p1, p2, p3, l0, l1, l2, l3;
+      q8_4(qa, d2, p0, p1, l0, l1);
+      q8_4(qb, d2, p2, p3, l2, l3);
+      const h8 bh = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      const h8 bl = {l0[0], l0[1], l1[0], l1[1], l2[0], l2[1], l3[0], l3[1]};
+      const int ka = 64 * g + 8 * t;
+#pragma unroll
+      for (int q = 0; q < RG; ++q) {
+        const h8 ah = *reinterpret_cast<const h8 *>(ar[q] + ka);
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[q], 0, 0, 0);
+        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc[q], 0, 0, 0);
+        if (kLo) {  // the x_lo * remainder term (below 2^-22 of the result) is left out
+          const h8 al = *reinterpret_cast<const h8 *>(arl[q] + ka);
+          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc[q], 0, 0, 0);
+        }
+      }
+    }
   }
 };
 
@@ -1122,9 +1253,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
   // 32-bit buffer offsets: activations (with a tile of padding rows) and weights
   const int64_t a_bytes = (M + 256) * K * 2;
-  const int64_t w_bytes = (N + kBN) * (K / 256) * (type == kQ6_K ? kQ6KBytes : kQ4KBytes) + 1024;
-  return (type == kQ4_K || type == kQ6_K) && K % 256 == 0 && N >= 1 && M >= 1 && a_bytes < (int64_t)UINT32_MAX &&
-         w_bytes < (int64_t)UINT32_MAX;
+  const int64_t sb_bytes = type == kQ6_K ? kQ6KBytes : type == kQ8_0 ? 8 * kQ8Bytes : kQ4KBytes;
+  const int64_t w_bytes = (N + kBN) * (K / 256) * sb_bytes + 1024;
+  return (type == kQ4_K || type == kQ6_K || type == kQ8_0) && K % 256 == 0 && N >= 1 && M >= 1 &&
+         a_bytes < (int64_t)UINT32_MAX && w_bytes < (int64_t)UINT32_MAX;
 }
 
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
@@ -1210,6 +1342,9 @@ static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t
   if (type == kQ6_K) {
     if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
     else OKQ_DEC_RG(DecQ6K, true);
+  } else if (type == kQ8_0) {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ80, false);
+    else OKQ_DEC_RG(DecQ80, true);
   } else {
     if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
     else OKQ_DEC_RG(DecQ4K, true);
@@ -1227,7 +1362,8 @@ static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t
 hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
                                     void *workspace, const GemmPlan &plan, hipStream_t s) {
-  if ((type != kQ4_K && type != kQ6_K) || plan.bm != kDecRows || M > kDecRows || count < 1 || count > kDecMats)
+  if ((type != kQ4_K && type != kQ6_K && type != kQ8_0) || plan.bm != kDecRows || M > kDecRows || count < 1 ||
+      count > kDecMats)
     return hipErrorInvalidValue;
   DecMats mats{};
   int tiles = 0;
@@ -1248,8 +1384,8 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
 
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
-  if (type != kQ4_K && type != kQ6_K) return hipErrorInvalidValue;
-  if (type == kQ6_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
+  if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
+  if (type != kQ4_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
   const uint8_t *W = static_cast<const uint8_t *>(w);
   const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
@@ -1287,6 +1423,9 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   if (type == kQ6_K) {
     if (x_is_bf16) OKQ_GEMM(128, false, kQ6_K);
     else OKQ_GEMM(128, true, kQ6_K);
+  } else if (type == kQ8_0) {
+    if (x_is_bf16) OKQ_GEMM(128, false, kQ8_0);
+    else OKQ_GEMM(128, true, kQ8_0);
   } else if (plan.bm == 256) {
     OKQ_GEMM(256, false, kQ4_K);
   } else if (x_is_bf16) {

@@ -99,7 +99,8 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
                                     void *workspace, const GemmPlan &plan, hipStream_t s);
 
-// True when launch_gemm supports this (type, M, K, N): Q4_K and Q6_K.
+// True when launch_gemm supports this (type, M, K, N): Q4_K, Q6_K and Q8_0
+// with K a multiple of 256.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);
 
 }  // namespace okq

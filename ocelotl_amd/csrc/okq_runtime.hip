@@ -264,8 +264,6 @@ constexpr uint64_t kDecMidBytes = 8u << 20;
 
 bool gemv_serves(uint32_t type, int64_t rows, uint64_t w_bytes) {
   if (rows > kGemvMaxRows) return false;
-  const bool dec_fmt = type == OKQ_TYPE_Q4_K || type == OKQ_TYPE_Q6_K;
-  if (!dec_fmt) return true;
   if (rows >= kDecMinRows && w_bytes >= kDecMinBytes) return false;
   return !(rows >= kDecMidRows && w_bytes >= kDecMidBytes);
 }

@@ -111,9 +111,9 @@ def test_gemv_intra_run_outliers_within_reference_rule(torch, okq, orc, weights,
 @pytest.mark.parametrize("t", TYPES)
 @pytest.mark.parametrize("rows", [2, 3, 8, 32, 64])
 def test_linear_intra_run_outliers_every_row_count(torch, okq, orc, weights, t, rows):
-    """okq_linear_out_by_in_q at every row-count class (the two-row GEMV, the
-    decode-batch MFMA kernel, the tiled GEMM; Q8_0 stays on the GEMV) with
-    x1000 outlier channels in every row."""
+    """okq_linear_out_by_in_q at every row-count class (the multi-row GEMV,
+    the decode-batch MFMA kernel, the tiled GEMM) with x1000 outlier channels
+    in every row."""
     n, k = 4096, 4096
     wq = weights[(t, n, k)]
     print(f"[gpu] outliers linear type={t} rows={rows}", flush=True)

@@ -402,3 +402,82 @@ def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):
         auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q6_K, x, rows, k, wq, n)
         pin = run(torch, okq, pinned, O.Q6_K, x, rows, k, wq, n)
         assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
+
+
+# ---- Q8_0 -----------------------------------------------------------------------
+# B = d * q (d the block's fp16 scale, q its int8 quant) enters as two exact
+# fp16 planes, fp16(d * q) and the remainder d * q - fp16(d * q): the products
+# are exact as for the K-quants, and no per-block scaling follows.
+
+Q80_CASES = [
+    # decode batches (one or two 16-row MFMA groups, split and unsplit K)
+    ("okq_gemm", 1, 96, 256), ("okq_gemm", 5, 300, 1024), ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1000, 768),
+    ("okq_gemm", 13, 4096, 14336), ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm", 32, 4096, 4096),
+    ("okq_gemm", 24, 20000, 4096), ("okq_gemm", 2, 70003, 256), ("okq_gemm_bf16", 31, 257, 768),
+    # tiled GEMM (odd block counts per tile row: 2-byte aligned block starts alternate)
+    ("okq_gemm_bf16", 33, 300, 1024), ("okq_gemm_bf16", 130, 1024, 4096), ("okq_gemm_bf16", 128, 4096, 14336),
+    ("okq_gemm", 100, 257, 768), ("okq_gemm", 64, 4096, 4096), ("okq_gemm_bf16", 200, 1001, 256),
+]
+
+
+@pytest.mark.parametrize("entry,rows,n,k", Q80_CASES)
+def test_gemm_q8_0_matches_reference(torch, okq, orc, entry, rows, n, k):
+    print(f"[gpu] gemm {entry} Q8_0 M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q8_0, orc.normal(1800 + n + k, n * k, 0.02))
+    bias = orc.normal(1801 + rows, n, 0.1)
+    if entry == "okq_gemm_bf16":
+        xin, x32 = bf16_inputs(orc, 1802 + rows, rows, k)
+    else:
+        xin = x32 = orc.normal(1802 + rows, rows * k, 1.0)
+    got = run(torch, okq, entry, O.Q8_0, xin, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q8_0, got, x32, rows, k, wq, n, bias, None if n * k * rows <= 2e9 else 8)
+
+
+@pytest.mark.parametrize("rows", [128, 512, 2048])
+def test_gemm_q8_0_prefill_4096_sampled_rows(torch, okq, orc, rows):
+    """Q8_0 prefill at M in {128, 512, 2048} on 4096 x 4096 (bf16 activations)."""
+    n = k = 4096
+    print(f"[gpu] gemm Q8_0 prefill M={rows}", flush=True)
+    wq = orc.quantize(O.Q8_0, orc.normal(1850, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 1851 + rows, rows, k)
+    got = run(torch, okq, "okq_linear_out_by_in_q_bf16", O.Q8_0, xb, rows, k, wq, n)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q8_0, got, x32, rows, k, wq, n, None, 16)
+
+
+def test_gemm_q8_0_one_hot_columns_are_exact(torch, okq, orc):
+    """x = e_j returns d * q of every weight row bit for bit (hi + lo = d * q
+    exactly), on the decode-batch (16 rows) and tiled (40 rows) kernels, with
+    scales up to d = 500 (|d * q| up to 63500) in some blocks."""
+    n, k = 64, 512
+    wq = orc.quantize(O.Q8_0, orc.normal(1860, n * k, 0.02))
+    blocks = wq.reshape(-1, 34).copy()
+    big = np.array([500.0, 3.0, 2.0 ** -20, 257.125], np.float16).view(np.uint16)
+    blocks[::7, 0:2] = big[np.arange(blocks[::7].shape[0]) % 4].view(np.uint8).reshape(-1, 2)
+    wq = blocks.reshape(-1)
+    w = orc.dequantize(O.Q8_0, wq, n * k).reshape(n, k)
+    assert np.abs(w).max() > 60000
+    for rows in (16, 40):
+        x = np.zeros((rows, k), np.float32)
+        cols = (np.arange(rows) * 37) % k
+        x[np.arange(rows), cols] = 1.0
+        for entry, xin in (("okq_gemm", x.reshape(-1)), ("okq_gemm_bf16", orc.f32_to_bf16(x.reshape(-1)))):
+            got = run(torch, okq, entry, O.Q8_0, xin, rows, k, wq, n)
+            assert np.array_equal(got, w[:, cols].T), (entry, rows)
+
+
+def test_linear_dispatch_takes_the_q8_0_gemm_above_eight_rows(torch, okq, orc):
+    """okq_linear_out_by_in_q on a small Q8_0 weight: 9+ rows run the MFMA
+    kernels (bit-identical to okq_gemm), up to 8 rows the GEMV; a 17.8 MB
+    4096 x 4096 weight takes the decode-batch kernel from 5 rows."""
+    for n, k, cases in ((256, 1024, ((8, "okq_gemv"), (9, "okq_gemm"), (40, "okq_gemm"))),
+                        (4096, 4096, ((4, "okq_gemv"), (5, "okq_gemm")))):
+        wq = orc.quantize(O.Q8_0, orc.normal(1870 + n, n * k, 0.02))
+        for rows, pinned in cases:
+            print(f"[gpu] dispatch Q8_0 rows={rows} N={n} K={k}", flush=True)
+            x = orc.normal(1871 + rows, rows * k, 1.0)
+            auto = run(torch, okq, "okq_linear_out_by_in_q", O.Q8_0, x, rows, k, wq, n)
+            pin = run(torch, okq, pinned, O.Q8_0, x, rows, k, wq, n)
+            assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), (n, rows)
+            check_rows(orc, O.Q8_0, auto, x, rows, k, wq, n, None, 2)

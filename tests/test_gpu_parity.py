@@ -382,7 +382,7 @@ MULTI_BATCH_CASES = [
     (O.Q4_K, 8, 4096, [1024, 512, 14336], False),    # two on the GEMV, the large one alone
     (O.Q6_K, 24, 1024, [33, 300], True),             # above 8 rows: every Q6_K matrix on the MFMA path
     (O.Q4_K, 32, 1024, [17, 1000, 256, 40], True),   # four matrices, ragged tiles, two 16-row groups
-    (O.Q8_0, 12, 1024, [100, 64], False),            # Q8_0 stays on the GEMV at any row count
+    (O.Q8_0, 12, 1024, [100, 64], True),             # Q8_0 above 8 rows: the MFMA kernels too
     (O.Q4_K, 40, 1024, [300, 200], False),           # above 32 rows: each on the tiled GEMM
 ]
 
