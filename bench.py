@@ -26,12 +26,16 @@ The JSON line also carries:
                 (profiles/gemv_q4k_gate_up_traffic.md)
   cpu_baseline  the reference CPU path (oracle restatement of
                 linear_out_by_in, scalar mode, 1 core since rows < 32) on one
-                layer copy, dequantized once outside the timing
-  extra         per-launch and per-projection times, the 7-launch step, and
-                the secondary configs (C1, C3, C4)
+                layer copy, dequantized once outside the timing, with a check
+                that the GPU's outputs of that step match it; `configs` holds
+                bounded samples of C1, C3, C4 (scalar and AVX2, rows chunked
+                over the host cores) and C5 (one layer at batch 1, 8, 32)
+  extra         per-launch and per-projection times (mean, p10, median,
+                p90), the 7-launch step, and the secondary configs (C1, C3,
+                C4 per call, C5)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate_up|copy   (bare workload for counter passes)
+     python bench.py --probe gate_up|copy|gemm_gate512   (bare workloads for counter passes)
 """
 from __future__ import annotations
 
@@ -95,6 +99,7 @@ class Ctx:
         self.okq = okq
         self.hip = Hip()
         self.tmp = None
+        self.host = {}  # host copies of workloads for the CPU baseline leg
 
     @property
     def stream(self) -> int:
@@ -126,10 +131,10 @@ class Ctx:
     def gemv(self, t, x, k, w, n, y, entry="okq_gemv", rows=1):
         self.okq.call(entry, x.data_ptr(), rows, k, t, w.data_ptr(), w.numel(), n, None, y.data_ptr(), self.stream)
 
-    def graph_us(self, launch, n: int, reps: int = 3) -> float:
-        """Average duration (µs) of one launch inside a HIP graph of n
-        back-to-back launch(i) calls, timed with events on the stream the graph
-        is replayed on."""
+    def graph_us(self, launch, n: int, reps: int = 10):
+        """Duration (µs) of one launch inside a HIP graph of n back-to-back
+        launch(i) calls, timed with events on the stream the graph is replayed
+        on: (mean over `reps` replays, per-replay means)."""
         torch = self.torch
         launch(0)
         torch.cuda.synchronize()
@@ -139,15 +144,15 @@ class Ctx:
                 launch(i)
         g.replay()
         torch.cuda.synchronize()
-        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        e0.record()
-        for _ in range(reps):
+        evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+        evs[0].record()
+        for r in range(reps):
             g.replay()
-        e1.record()
+            evs[r + 1].record()
         torch.cuda.synchronize()
-        us = 1000.0 * e0.elapsed_time(e1) / (reps * n)
+        per = [1000.0 * evs[r].elapsed_time(evs[r + 1]) / n for r in range(reps)]
         del g
-        return us
+        return sum(per) / reps, per
 
     def replicas(self, w, min_bytes: int = 512 << 20):
         """A pool of copies of w (>= min_bytes) so that rotating launches read
@@ -210,42 +215,42 @@ def launch_group(ctx, names, ws, x, outs):
 
 
 def time_steps(ctx, args, step):
-    """Wall time of args.steps steps replayed from HIP graphs (one graph per
-    pass over all layer copies, single-step graphs for the remainder)."""
+    """Wall time of exactly args.steps steps, and per-step times (for
+    p10/median/p90).  The steps (rotating over the layer copies) are captured
+    into one HIP graph, so the timed region -- synchronize on both sides -- is
+    a single replay.  The percentiles come from a second measurement after it:
+    replays of a graph of one pass over all copies, with events between the
+    replays."""
     torch = ctx.torch
     step(0)
     torch.cuda.synchronize()
-    g_all = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g_all):
-        for c in range(args.copies):
-            step(c)
-    g_one = []
-    for c in range(args.copies):
+
+    def capture(n):
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
-            step(c)
-        g_one.append(g)
+            for c in range(n):
+                step(c)
+        return g
 
-    def run_steps(nsteps, start=0):
-        i = start
-        while nsteps > 0:
-            if i % args.copies == 0 and nsteps >= args.copies:
-                g_all.replay()
-                i += args.copies
-                nsteps -= args.copies
-            else:
-                g_one[i % args.copies].replay()
-                i += 1
-                nsteps -= 1
-        return i
-
-    i = run_steps(args.warmup)
-    i = i - i % args.copies  # restart on a copy boundary
+    g_all = capture(args.copies)
+    g_k = capture(args.steps)
+    for _ in range(max(1, -(-args.warmup // args.copies))):
+        g_all.replay()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    run_steps(args.steps, i)
+    g_k.replay()
     torch.cuda.synchronize()
-    return time.perf_counter() - t0
+    sec = time.perf_counter() - t0
+    reps = max(4, min(32, args.steps // args.copies))
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+    evs[0].record()
+    for i in range(reps):
+        g_all.replay()
+        evs[i + 1].record()
+    torch.cuda.synchronize()
+    per_step = [evs[i].elapsed_time(evs[i + 1]) / args.copies for i in range(reps)]
+    del g_all, g_k
+    return sec, per_step
 
 
 def run_c2(ctx: Ctx, args):
@@ -274,9 +279,9 @@ def run_c2(ctx: Ctx, args):
             ctx.gemv(Q4K, xin([name]), k, lay[name], n, outs[name])
 
     log(f"C2: warmup {args.warmup} steps, timing {args.steps} steps (4 launches per layer)")
-    sec = time_steps(ctx, args, step_fused)
+    sec, per_step = time_steps(ctx, args, step_fused)
     log(f"C2: the same steps as 7 single-projection launches")
-    sec_seq = time_steps(ctx, args, step_seq)
+    sec_seq, _ = time_steps(ctx, args, step_seq)
 
     # per-launch durations: graphs of back-to-back launches, each launch on the
     # next replica of the group's weights (>= 512 MB of replicas per matrix)
@@ -293,15 +298,16 @@ def run_c2(ctx: Ctx, args):
                 ws[m] = pool.narrow(0, (i % copies) * b, b)
             launch_group(ctx, names, ws, x, outs)
 
-        us = ctx.graph_us(launch, max(64, 2 * copies))
+        us, per = ctx.graph_us(launch, max(64, 2 * copies))
         b = sum(wbytes(Q4K, *C2_SHAPE[m]) for m in names)
         del pools
-        return {"matrices": names, "weight_bytes": b, "us_mean": round(us, 3), "gbs": round(b / us / 1e3, 1),
+        return {"matrices": names, "weight_bytes": b, "us_mean": round(us, 3), "us_p10": round(pct(per, 10), 3),
+                "us_median": round(median(per), 3), "us_p90": round(pct(per, 90), 3), "gbs": round(b / us / 1e3, 1),
                 "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
     launches = {g: group_time(names) for g, names in C2_GROUPS}
     shapes = {name: group_time([name]) for name, _, _ in C2_PROJ}
-    return {"gbs": step_bytes * args.steps / sec / 1e9, "sec": sec,
+    return {"gbs": step_bytes * args.steps / sec / 1e9, "sec": sec, "per_step_ms": per_step,
             "gbs_sequential": step_bytes * args.steps / sec_seq / 1e9, "sec_sequential": sec_seq,
             "step_bytes": step_bytes, "launches": launches, "shapes": shapes, "layers": layers,
             "x4096": x4096, "x14336": x14336}
@@ -348,6 +354,8 @@ def run_c3(ctx: Ctx, args):
     x = ctx.normal(k, 32)
     y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
     b = wbytes(Q6K, n, k)
+    if not args.no_cpu:  # the CPU baseline leg runs the same head and activations
+        ctx.host["c3"] = (w.cpu().numpy(), x.cpu().numpy())
     pool, copies = ctx.replicas(w)
     del w
 
@@ -355,9 +363,10 @@ def run_c3(ctx: Ctx, args):
         ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q6K, pool.data_ptr() + (i % copies) * b, b, n, None,
                      y.data_ptr(), ctx.stream)
 
-    us = ctx.graph_us(launch, 16)
+    us, per = ctx.graph_us(launch, 16)
     del pool
-    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 2),
+    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 2), "us_p10": round(pct(per, 10), 2),
+            "us_median": round(median(per), 2), "us_p90": round(pct(per, 90), 2),
             "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
@@ -368,55 +377,69 @@ def run_c1(ctx: Ctx, args):
     x = ctx.normal(k, 41)
     y = ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda")
     b = wbytes(Q8_0, n, k)
+    if not args.no_cpu:
+        ctx.host["c1"] = (w.cpu().numpy(), x.cpu().numpy())
     pool, copies = ctx.replicas(w)
 
     def launch(i):
         ctx.okq.call("okq_gemv", x.data_ptr(), 1, k, Q8_0, pool.data_ptr() + (i % copies) * b, b, n, None,
                      y.data_ptr(), ctx.stream)
 
-    us = ctx.graph_us(launch, max(64, 2 * copies))
+    us, per = ctx.graph_us(launch, max(64, 2 * copies))
     del pool
-    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 3),
+    return {"shape": [n, k], "weight_bytes": b, "us_mean": round(us, 3), "us_p10": round(pct(per, 10), 3),
+            "us_median": round(median(per), 3), "us_p90": round(pct(per, 90), 3),
             "gbs": round(b / us / 1e3, 1), "frac_hbm": round(b / us / 1e3 / HBM_PEAK_GBS, 4)}
 
 
 def run_c4(ctx: Ctx, args, c2):
-    """Q4_K prefill GEMM at M in {128, 512, 2048} with bf16 activations.
-    us_kernel: the MFMA kernel's own dispatch time; us_call: the whole entry
-    point (activation pre-pass + GEMM) timed with stream events."""
+    """Prefill dequant-GEMM at M in {128, 512, 2048} with bf16 activations:
+    Q4_K at the Llama-3-8B projection shapes (q/o 4096x4096, k/v 1024x4096,
+    gate/up 14336x4096, down 4096x14336; one of each pair) and Q8_0 at
+    4096x4096.  us_call: the whole entry point (activation pre-pass + GEMM +
+    split-K reduction), stream events around each of `reps` back-to-back calls
+    rotating over 8 weight copies (mean, p10, median, p90); us_kernel: the MFMA
+    kernel's own dispatch time.  frac_bf16_peak is per call."""
     torch = ctx.torch
     res = {}
     lay = c2["layers"]
+    q8 = [ctx.quantized(Q8_0, 4096, 4096, seed=70 + c) for c in range(8)]
+    shapes = [(Q4K, name, n, k) for name, n, k in C2_PROJ if name not in ("k", "o", "up")] + [(Q8_0, "q8_0", 4096, 4096)]
     for m in (128, 512, 2048):
-        log(f"C4: Q4_K GEMM M={m}")
+        log(f"C4: GEMM M={m}")
         xf = ctx.normal(m * 14336, 50 + m)
         xb = torch.empty(m * 14336, dtype=torch.int16, device="cuda")
         ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
-        for name, n, k in C2_PROJ:
-            if name in ("k", "o", "up"):
-                continue  # same shapes as v, q, gate
+        for t, name, n, k in shapes:
             y = torch.empty(m * n, dtype=torch.float32, device="cuda")
             reps = max(8, args.kernel_reps // 8)
+            ws = [lay[c][name] for c in range(len(lay))] if t == Q4K else q8
 
-            def call(r, name=name, n=n, k=k, y=y):
-                ctx.gemv(Q4K, xb, k, lay[r % len(lay)][name], n, y, entry="okq_gemm_bf16", rows=m)
+            def call(r, t=t, n=n, k=k, y=y, ws=ws):
+                ctx.gemv(t, xb, k, ws[r % len(ws)], n, y, entry="okq_gemm_bf16", rows=m)
 
             call(0)
             us = ctx.kernel_us(call, reps)
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
             torch.cuda.synchronize()
-            e0.record()
+            evs[0].record()
             for r in range(reps):
                 call(r)
-            e1.record()
+                evs[r + 1].record()
             torch.cuda.synchronize()
-            t_call = 1000.0 * e0.elapsed_time(e1) / reps
-            t = sum(us) / len(us)
+            per = [1000.0 * evs[r].elapsed_time(evs[r + 1]) for r in range(reps)]
+            t_call = sum(per) / reps
+            t_k = sum(us) / len(us)
             flops = 2.0 * m * n * k
-            res[f"M{m}_{name}"] = {"m": m, "n": n, "k": k, "us_kernel": round(t, 2), "us_call": round(t_call, 2),
-                                   "tflops": round(flops / t / 1e6, 1),
-                                   "frac_bf16_peak": round(flops / t / 1e6 / BF16_PEAK_TFLOPS, 4),
-                                   "tflops_call": round(flops / t_call / 1e6, 1)}
+            key = f"M{m}_{name}" if t == Q4K else f"M{m}_q8_0_4096"
+            res[key] = {"type": "Q4_K" if t == Q4K else "Q8_0", "m": m, "n": n, "k": k,
+                        "us_call": round(t_call, 2), "us_call_p10": round(pct(per, 10), 2),
+                        "us_call_median": round(median(per), 2), "us_call_p90": round(pct(per, 90), 2),
+                        "tflops_call": round(flops / t_call / 1e6, 1),
+                        "frac_bf16_peak": round(flops / t_call / 1e6 / BF16_PEAK_TFLOPS, 4),
+                        "us_kernel": round(t_k, 2), "tflops_kernel": round(flops / t_k / 1e6, 1),
+                        "frac_bf16_peak_kernel": round(flops / t_k / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del q8
     return res
 
 
@@ -518,40 +541,138 @@ def run_c5(ctx: Ctx, args):
 # CPU baseline (reference CPU path, oracle restatement)
 # ---------------------------------------------------------------------------
 
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_threads() -> int:
+    """Host threads for the reference's chunked path (rows >= 32): the box's
+    CPU share, at most 16."""
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_time(fn, seconds: float):
+    """Calls fn until `seconds` have elapsed (at least once): (s per call, calls)."""
+    calls = 0
+    t0 = time.perf_counter()
+    while True:
+        fn()
+        calls += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            return el / calls, calls
+
+
 def run_cpu_baseline(ctx: Ctx, c2, args):
+    """The reference CPU path (the oracle's restatement of linear_out_by_in,
+    crates/kernels/src/lib.rs:1974-2123, and its AVX2 variant,
+    crates/kernels/src/cpu_avx2.rs:58-253) on the host cores of the GPU box,
+    weights dequantized to f32 once outside the timing.  The reference runs
+    rows < 32 serially and chunks rows >= 32 over all cores (lib.rs:2245,
+    :2294-2390); every entry states its threads.  Headline: the C2 step on
+    one layer copy (1 core).  `configs`: bounded samples of C1, C3, C4 and C5.
+    The C2 outputs of the CPU path are checked against the GPU's for the same
+    inputs with the reference rule."""
     import numpy as np
     from oracle import oracle as O
     orc = O.Oracle()
+    model = cpu_model()
     lay = c2["layers"][0]
     log("cpu baseline: dequantizing one layer copy on the host (not timed)")
     w = {name: orc.dequantize(O.Q4_K, lay[name].cpu().numpy(), n * k).reshape(n, k) for name, n, k in C2_PROJ}
     x4096 = c2["x4096"].cpu().numpy()
     x14336 = c2["x14336"].cpu().numpy()
-    # sanity: the GPU result of the last timed step equals the CPU path within tolerance
-    passes = 0
-    t0 = time.perf_counter()
-    while True:
+    cpu_out = {}
+
+    def c2_pass():
         for name, n, k in C2_PROJ:
-            orc.linear(x14336 if k == 14336 else x4096, 1, k, w[name], n, None, O.MODE_SCALAR, 1)
-        passes += 1
-        if time.perf_counter() - t0 >= args.cpu_seconds:
-            break
-    sec = time.perf_counter() - t0
-    gbs = c2["step_bytes"] * passes / sec / 1e9
-    cpu = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    return {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            cpu_out[name] = orc.linear(x14336 if k == 14336 else x4096, 1, k, w[name], n, None, O.MODE_SCALAR, 1)
+
+    sec_pass, passes = cpu_time(c2_pass, args.cpu_seconds)
+    gbs = c2["step_bytes"] / sec_pass / 1e9
+    # the GPU's outputs of the same step (layer copy 0, the same activations)
+    gpu_out = {name: ctx.torch.empty(n, dtype=ctx.torch.float32, device="cuda") for name, n, _ in C2_PROJ}
+    for _, names in C2_GROUPS:
+        launch_group(ctx, names, lay, c2["x14336"] if C2_SHAPE[names[0]][1] == 14336 else c2["x4096"], gpu_out)
+    ctx.torch.cuda.synchronize()
+    parity = all(O.allclose_ref_rule(gpu_out[name].cpu().numpy(), cpu_out[name], 1e-3)[0] for name, _, _ in C2_PROJ)
+    head = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"C2 layer copy 0 (7 Q4_K projections, {c2['step_bytes']} quantized bytes) dequantized to f32 "
                       f"once (untimed); reference scalar linear_out_by_in, batch 1, serial (rows < 32); "
-                      f"{passes} passes in {sec:.2f} s on {cpu}",
-            "ms_per_step": round(1000.0 * sec / passes, 2)}
+                      f"{passes} passes in {sec_pass * passes:.2f} s on {model}",
+            "ms_per_step": round(1000.0 * sec_pass, 2),
+            "gpu_outputs_match_cpu_within_rule": bool(parity)}
+    if args.cpu_configs:
+        head["configs"] = run_cpu_configs(ctx, orc, O, args)
+    return head
+
+
+def run_cpu_configs(ctx: Ctx, orc, O, args):
+    """Bounded CPU samples of the secondary configs (reference scalar and AVX2
+    paths, the reference's threading rule)."""
+    import numpy as np
+    res = {}
+    thr = cpu_threads()
+    sec = args.cpu_config_seconds
+    # C1: Q8_0 4096 x 4096 at batch 1 (serial)
+    if "c1" in ctx.host:
+        wq, x = ctx.host["c1"]
+        wf = orc.dequantize(O.Q8_0, wq, 4096 * 4096)
+        for mode, label in ((O.MODE_SCALAR, "scalar"), (O.MODE_AVX2, "avx2")):
+            if mode == O.MODE_AVX2 and not orc.has_avx2():
+                continue
+            t, calls = cpu_time(lambda: orc.linear(x, 1, 4096, wf, 4096, None, mode, 1), sec)
+            res[f"c1_q8_0_{label}"] = {"us_per_call": round(1e6 * t, 1), "gbs": round(wq.size / t / 1e9, 3),
+                                       "cores": 1, "calls": calls}
+        del wf
+    # C3: the Q6_K head at batch 1 (serial)
+    if "c3" in ctx.host:
+        wq, x = ctx.host["c3"]
+        log("cpu baseline: dequantizing the Q6_K head (not timed)")
+        wf = orc.dequantize(O.Q6_K, wq, 128256 * 4096)
+        t, calls = cpu_time(lambda: orc.linear(x, 1, 4096, wf, 128256, None, O.MODE_SCALAR, 1), sec)
+        res["c3_q6_k_head_scalar"] = {"us_per_call": round(1e6 * t, 1), "gbs": round(wq.size / t / 1e9, 3), "cores": 1,
+                                      "calls": calls}
+        del wf
+    # C4: Q4_K prefill at M = 128 and 512 on q (4096 x 4096), rows chunked over the host cores
+    wq = ctx.quantized(Q4K, 4096, 4096, seed=10_000).cpu().numpy()
+    wf = orc.dequantize(O.Q4_K, wq, 4096 * 4096).reshape(4096, 4096)
+    for m in (128, 512):
+        xb = orc.f32_to_bf16(orc.normal(50 + m, m * 4096, 1.0))
+        x = orc.bf16_to_f32(xb)
+        for mode, label in ((O.MODE_SCALAR, "scalar"), (O.MODE_AVX2, "avx2")):
+            if mode == O.MODE_AVX2 and not orc.has_avx2():
+                continue
+            t, calls = cpu_time(lambda: orc.linear(x, m, 4096, wf, 4096, None, mode, thr), sec)
+            res[f"c4_M{m}_q_{label}"] = {"us_per_call": round(1e6 * t, 1),
+                                          "tflops": round(2.0 * m * 4096 * 4096 / t / 1e12, 4), "cores": thr,
+                                          "calls": calls}
+    del wf
+    # C5: one Q4_K_M layer (Q6_K v and down) at batch 1, 8 (serial) and 32 (all cores)
+    lay = {name: ctx.quantized(t, n, k, seed=50_000 + i).cpu().numpy() for i, (name, t, n, k) in enumerate(C5_PROJ)}
+    wl = {name: orc.dequantize(t, lay[name], n * k).reshape(n, k) for name, t, n, k in C5_PROJ}
+    lbytes = sum(wbytes(t, n, k) for _, t, n, k in C5_PROJ)
+    for b in (1, 8, 32):
+        x4 = orc.normal(60 + b, b * 4096, 1.0)
+        x14 = orc.normal(61 + b, b * 14336, 1.0)
+        th = thr if b >= 32 else 1
+
+        def layer():
+            for name, t, n, k in C5_PROJ:
+                orc.linear(x14 if k == 14336 else x4, b, k, wl[name], n, None, O.MODE_SCALAR, th)
+
+        t, calls = cpu_time(layer, sec)
+        res[f"c5_layer_b{b}_scalar"] = {"ms_per_layer": round(1e3 * t, 2),
+                                        "weight_gbs": round(lbytes / t / 1e9, 3), "cores": th, "calls": calls,
+                                        "tokens_per_s_32_layers": round(b / (32 * t), 2)}
+    return res
 
 
 def run_probe(ctx: Ctx, what: str):
@@ -568,6 +689,16 @@ def run_probe(ctx: Ctx, what: str):
         for i in range(20):
             launch_group(ctx, names, {m: pools[m][0].narrow(0, (i % copies) * b, b) for m in names}, x, outs)
         log(f"probe gate_up: 20 launches, {2 * b} weight bytes each")
+    elif what == "gemm_gate512":
+        n, k, m = 14336, 4096, 512
+        ws = [ctx.quantized(Q4K, n, k, seed=10_004 + c) for c in range(4)]
+        xf = ctx.normal(m * k, 562)
+        xb = torch.empty(m * k, dtype=torch.int16, device="cuda")
+        ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
+        y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+        for i in range(20):
+            ctx.gemv(Q4K, xb, k, ws[i % len(ws)], n, y, entry="okq_gemm_bf16", rows=m)
+        log(f"probe gemm_gate512: 20 Q4_K GEMM calls M={m} N={n} K={k} (bf16), {2 * m * n * k} flops each")
     else:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -586,14 +717,19 @@ def main():
     ap.add_argument("--warmup", type=int, default=40)
     ap.add_argument("--copies", type=int, default=8)
     ap.add_argument("--kernel-reps", type=int, default=200)
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--cpu-seconds", type=float, default=10.0, help="C2 CPU baseline sample (seconds)")
+    ap.add_argument("--cpu-config-seconds", type=float, default=1.5,
+                    help="CPU baseline sample per secondary config (seconds; at least one call)")
+    ap.add_argument("--no-cpu-configs", dest="cpu_configs", action="store_false",
+                    help="CPU baseline of the C2 headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
     ap.add_argument("--only", default="c1,c3,c4,c5", help="secondary configs to run (comma list of c1,c3,c4,c5)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
-    ap.add_argument("--probe", choices=["gate_up", "copy"], default=None,
+    ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
-                         "weight replicas, or 20 launches of a 256 MiB f32 elementwise copy (calibration)")
+                         "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), or 20 Q4_K "
+                         "GEMM calls at M=512 on the gate shape")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -633,6 +769,8 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(1000.0 * c2["sec"] / args.steps, 5),
+        "ms_per_step_p10_median_p90": [round(pct(c2["per_step_ms"], 10), 5), round(median(c2["per_step_ms"]), 5),
+                                       round(pct(c2["per_step_ms"], 90), 5)],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
