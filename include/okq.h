@@ -17,7 +17,9 @@
  *     asynchronously on it;
  *   - results are deterministic: fixed reduction order, no float atomics.
  * Thread safety: all entry points may be called from several host threads; the
- * device used is the calling thread's current HIP device.
+ * device used is the calling thread's current HIP device.  Calls on one
+ * stream enqueue their kernels as one uninterrupted sequence (a per-stream
+ * lock), so threads sharing a stream also share its workspace safely.
  */
 #ifndef OKQ_H
 #define OKQ_H

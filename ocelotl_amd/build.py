@@ -42,7 +42,7 @@ def _compile(src: str) -> str:
     return obj
 
 
-HOST_SRC = [os.path.join(HERE, "host", f) for f in ("kernel_backend.cpp", "gguf.cpp")]
+HOST_SRC = [os.path.join(HERE, "host", f) for f in ("kernel_backend.cpp", "gguf.cpp", "dequant_policy.cpp")]
 HOST_LIB = os.path.join(HERE, "libocelotl_hip.so")
 CXX = os.environ.get("CXX", "g++")
 

@@ -243,6 +243,20 @@ okq_status get_workspace(int dev, hipStream_t s, size_t bytes, void **out, int s
   return ok();
 }
 
+// Calls that take workspace enqueue several kernels (activation pre-pass,
+// GEMM, split-K reduction) that share the stream's buffer; a second host
+// thread enqueueing on the same stream in between would overwrite it.  Every
+// such call therefore holds its stream's lock from the workspace lookup to
+// its last launch, so calls on one stream enqueue as whole sequences (the
+// lock is recursive: the fused entry points call the linear dispatch).
+std::mutex g_stream_locks_mutex;
+std::map<std::pair<int, hipStream_t>, std::recursive_mutex> g_stream_locks;
+
+std::recursive_mutex &stream_lock(int dev, hipStream_t s) {
+  std::lock_guard<std::mutex> lock(g_stream_locks_mutex);
+  return g_stream_locks[{dev, s}];  // node-based map: the reference stays valid
+}
+
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
@@ -318,6 +332,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
   st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   bool use_gemm = false;
   if (path == Path::Gemm) {
     if (!okq::gemm_supported((int)type, rows, K, N))
@@ -562,6 +577,7 @@ okq_status grouped_linear(const float *x, int64_t rows, int64_t in_features, uin
                           const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
                           const float *const *b, float *const *out, void *stream, int dev, const DevInfo &info) {
   hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   okq_status st = OKQ_OK;
   const void *gw[okq::kGemvMaxProblems], *mw[okq::kGemvMaxProblems];
   int64_t gn[okq::kGemvMaxProblems], mn[okq::kGemvMaxProblems];
@@ -678,6 +694,7 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
   st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
   const float *const *b = bias ? bias : nobias;
   if (rows == 1 && streams) {  // one decode row: every workgroup normalises x in its prologue
@@ -735,6 +752,7 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   okq_status st = current_device(dev, info);
   if (st != OKQ_OK) return st;
   hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   // gate and up: grouped like okq_gemv_multi when they share a format (one
   // GEMV pass over both weights, or one decode-batch launch)
   if (gate_type == up_type) {

@@ -3,9 +3,11 @@
 // (crates/kernels/src/lib.rs:2443-2497); every check happens before a launch.
 #include "kernel_backend.hpp"
 
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <limits>
+#include <mutex>
 
 #include "okq.h"
 
@@ -145,9 +147,60 @@ Result<std::shared_ptr<DeviceAllocation>> device_alloc(size_t bytes) {
 }
 }  // namespace
 
-float *DeviceTensor::device_ptr() const { return static_cast<float *>(buf_->ptr); }
+struct DeviceTensor::HostStore {
+  std::mutex mu;
+  std::vector<float> v;
+};
+
+namespace {
+// The reference's tensor errors carry backend "tensor" (tensor.rs:319-324).
+OcelotlError tensor_err(const std::string &message) { return OcelotlError::kernel("tensor", message); }
+}  // namespace
+
+DeviceTensor DeviceTensor::from_host(std::vector<float> v) {
+  DeviceTensor t;
+  t.host_ = std::make_shared<HostStore>();
+  t.len_ = v.size();
+  t.host_->v = std::move(v);
+  return t;
+}
+
+DeviceTensor DeviceTensor::host_zeros(size_t len) { return from_host(std::vector<float>(len, 0.0f)); }
+
+Result<DeviceTensor> DeviceTensor::view(const DeviceTensor &source, size_t offset, size_t len) {
+  const size_t src_len = source.len();
+  if (offset > SIZE_MAX - len || offset + len > src_len) {
+    const size_t end = offset > SIZE_MAX - len ? SIZE_MAX : offset + len;
+    return tensor_err("DeviceTensor::view range " + std::to_string(offset) + ".." + std::to_string(end) +
+                      " exceeds source length " + std::to_string(src_len));
+  }
+  if (source.is_view()) return tensor_err("DeviceTensor::view does not nest; resolve the source view first");
+  DeviceTensor t;
+  t.source_ = std::make_shared<const DeviceTensor>(source);
+  t.offset_ = offset;
+  t.len_ = len;
+  return t;
+}
+
+Residency DeviceTensor::residency() const {
+  if (source_) return source_->residency();
+  if (buf_) return Residency{Residency::Kind::Device, kBackend};
+  return Residency{Residency::Kind::Host, nullptr};
+}
+
+float *DeviceTensor::device_ptr() const { return buf_ ? static_cast<float *>(buf_->ptr) : nullptr; }
 
 Result<std::vector<float>> DeviceTensor::to_host_owned() const {
+  if (host_) {
+    std::lock_guard<std::mutex> lock(host_->mu);
+    return host_->v;
+  }
+  if (source_) {
+    auto parent = source_->to_host_owned();
+    if (parent.is_err()) return parent.error();
+    return std::vector<float>(parent.value().begin() + (ptrdiff_t)offset_,
+                              parent.value().begin() + (ptrdiff_t)(offset_ + len_));
+  }
   std::vector<float> v(len_);
   if (len_ == 0) return v;
   Result<void> r = check(okq_memcpy_d2h(v.data(), buf_->ptr, len_ * sizeof(float), stream_));
@@ -159,8 +212,14 @@ Result<std::vector<float>> DeviceTensor::to_host_owned() const {
 
 Result<void> DeviceTensor::write_from_host_slice(const float *src, size_t len) const {
   if (len != len_) {
-    return kernel_err("write_from_host_slice length " + std::to_string(len) + " does not match tensor length " +
+    return tensor_err("DeviceTensor::write_from_host_slice: src.len()=" + std::to_string(len) + " != tensor len " +
                       std::to_string(len_));
+  }
+  if (source_) return tensor_err("DeviceTensor::write_from_host_slice: views are read-only");
+  if (host_) {
+    std::lock_guard<std::mutex> lock(host_->mu);
+    if (len) std::memcpy(host_->v.data(), src, len * sizeof(float));
+    return {};
   }
   if (len == 0) return {};
   Result<void> r = check(okq_memcpy_h2d(buf_->ptr, src, len * sizeof(float), stream_));
@@ -342,6 +401,24 @@ Result<void> HipKernelBackend::linear_d(const DeviceTensor &x, size_t rows, size
   }
   if (out.len() != rows * out_features)
     return kernel_err(len_mismatch("out.len()", out.len(), "rows*out_features", rows, out_features));
+  auto on_device = [](const DeviceTensor &t) { return !t.is_view() && t.device_ptr() != nullptr; };
+  if (!on_device(x) || (bias && !on_device(*bias)) || (!on_device(out) && out.len() > 0)) {
+    // wrong residency: the trait default's host bounce (lib.rs:193-217, the
+    // fallback of cubecl_backend.rs:280-292), slow but correct
+    auto xh = x.to_host_owned();
+    if (xh.is_err()) return xh.error();
+    std::vector<float> bh;
+    if (bias) {
+      auto b = bias->to_host_owned();
+      if (b.is_err()) return b.error();
+      bh = std::move(b.value());
+    }
+    std::vector<float> oh(rows * out_features, 0.0f);
+    Result<void> r = linear_out_by_in(xh.value().data(), xh.value().size(), rows, in_features, weight, out_features,
+                                      bias ? bh.data() : nullptr, bh.size(), oh.data(), oh.size());
+    if (r.is_err()) return r;
+    return out.write_from_host_slice(oh.data(), oh.size());
+  }
   return check(okq_linear_out_by_in_q(x.device_ptr(), (int64_t)rows, (int64_t)in_features,
                                       (uint32_t)weight.tensor_type(), weight.device_ptr(), weight.byte_len(),
                                       (int64_t)out_features, bias ? bias->device_ptr() : nullptr, out.device_ptr(),

@@ -157,24 +157,51 @@ Result<uint64_t> tensor_byte_len(GgmlTensorType type, const std::vector<int64_t>
 
 struct DeviceAllocation;  // okq_alloc'd bytes, freed with the last owner
 
-// f32 device-resident tensor (the Device residency of tensor.rs:87-268).
-// Copies share the buffer, as DeviceTensor's Arc does.
+// Where a tensor's data lives (tensor.rs:272-275): on the host, or on the
+// device of the backend named by `backend`.
+struct Residency {
+  enum class Kind { Host, Device } kind;
+  const char *backend;  // "hip-gfx950" for Device, null for Host
+};
+
+// The f32 tensor handle of tensor.rs:45-268 with its three variants:
+//   Host   -- a host vector behind a mutex (from_host, host_zeros);
+//   Device -- a buffer of this backend (HipKernelBackend::alloc / upload);
+//   View   -- a read-only (source, offset, len) range of another tensor,
+//             which must not itself be a view.
+// Copies share the backing, as DeviceTensor's Arc does; mutation goes through
+// `const` methods (the reference's interior mutability).
 class DeviceTensor {
  public:
+  // tensor.rs:89-101
+  static DeviceTensor from_host(std::vector<float> v);
+  static DeviceTensor host_zeros(size_t len);
+  // tensor.rs:106-129: range and nesting are checked
+  static Result<DeviceTensor> view(const DeviceTensor &source, size_t offset, size_t len);
+
   size_t len() const { return len_; }
   bool is_empty() const { return len_ == 0; }
+  Residency residency() const;  // a view reports its source's
+  bool is_view() const { return source_ != nullptr; }
+  // The device buffer of a Device tensor (null for Host and View tensors).
   float *device_ptr() const;
-  // tensor.rs:204-222 and :224-245.
+  // tensor.rs:204-222: Host copies, Device reads back, View copies its range.
   Result<std::vector<float>> to_host_owned() const;
+  // tensor.rs:224-245: length-checked; views are read-only.
   Result<void> write_from_host_slice(const float *src, size_t len) const;
 
  private:
   friend class HipKernelBackend;
+  struct HostStore;
   DeviceTensor(std::shared_ptr<DeviceAllocation> buf, size_t len, void *stream)
       : buf_(std::move(buf)), len_(len), stream_(stream) {}
-  std::shared_ptr<DeviceAllocation> buf_;
-  size_t len_;
-  void *stream_;
+  DeviceTensor() = default;
+  std::shared_ptr<HostStore> host_;                 // Host
+  std::shared_ptr<DeviceAllocation> buf_;           // Device
+  std::shared_ptr<const DeviceTensor> source_;      // View
+  size_t offset_ = 0;                               // View
+  size_t len_ = 0;
+  void *stream_ = nullptr;                          // Device
 };
 
 // A GGUF weight tensor resident on the device in its file layout:
@@ -217,8 +244,10 @@ class KernelBackend {
   virtual Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
                                         const QuantizedWeight &weight, size_t out_features, const float *bias,
                                         size_t bias_len, float *out, size_t out_len) const = 0;
-  // linear_d over device-resident tensors (lib.rs:186-217); `out` is
-  // caller-supplied and written in place.
+  // linear_d (lib.rs:186-217); `out` is caller-supplied and written in
+  // place.  Device-resident x, bias and out run on the device directly; any
+  // other residency (host tensors, views) takes the trait default's bounce:
+  // read x and bias back, run linear_out_by_in on the slices, write out.
   virtual Result<void> linear_d(const DeviceTensor &x, size_t rows, size_t in_features, const QuantizedWeight &weight,
                                 size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const = 0;
 };

@@ -14,6 +14,7 @@
 #include <string>
 #include <vector>
 
+#include "dequant_policy.hpp"
 #include "kernel_backend.hpp"
 
 extern "C" {
@@ -144,6 +145,76 @@ void create_without_a_gfx950_device_is_unsupported() {
   CHECK(be.error().as_unsupported()->feature == "gpu_backend", "require_gpu feature");
 }
 
+// DeviceTensor residency (tensor.rs:45-268): host tensors, views and their
+// errors, as the reference's own tensor tests check them.
+void host_tensors_and_views_follow_the_reference_semantics() {
+  DeviceTensor h = DeviceTensor::from_host({1.0f, 2.0f, 3.0f, 4.0f, 5.0f});
+  CHECK(h.len() == 5 && !h.is_empty() && h.residency().kind == Residency::Kind::Host, "host tensor");
+  CHECK(h.device_ptr() == nullptr, "a host tensor has no device buffer");
+  DeviceTensor v = ok(DeviceTensor::view(h, 1, 3), "view");
+  CHECK(v.len() == 3 && v.is_view() && v.residency().kind == Residency::Kind::Host, "view of host");
+  CHECK(ok(v.to_host_owned(), "view readback") == std::vector<float>({2.0f, 3.0f, 4.0f}), "view contents");
+  auto nested = DeviceTensor::view(v, 0, 1);
+  CHECK(nested.is_err() && nested.error().as_kernel()->backend == "tensor" &&
+            nested.error().as_kernel()->message == "DeviceTensor::view does not nest; resolve the source view first",
+        "views do not nest");
+  auto range = DeviceTensor::view(h, 4, 2);
+  CHECK(range.is_err() && range.error().as_kernel()->message == "DeviceTensor::view range 4..6 exceeds source length 5",
+        "view range checked");
+  const float w3[3] = {9.0f, 9.0f, 9.0f};
+  auto ro = v.write_from_host_slice(w3, 3);
+  CHECK(ro.is_err() && ro.error().as_kernel()->message == "DeviceTensor::write_from_host_slice: views are read-only",
+        "views are read-only");
+  auto bad_len = h.write_from_host_slice(w3, 3);
+  CHECK(bad_len.is_err() &&
+            bad_len.error().as_kernel()->message == "DeviceTensor::write_from_host_slice: src.len()=3 != tensor len 5",
+        "write length checked");
+  const float w5[5] = {5.0f, 4.0f, 3.0f, 2.0f, 1.0f};
+  ok(h.write_from_host_slice(w5, 5), "write host");
+  CHECK(ok(v.to_host_owned(), "view after write") == std::vector<float>({4.0f, 3.0f, 2.0f}), "views share storage");
+  DeviceTensor copy = h;  // copies share the backing, as the reference's Arc does
+  ok(copy.write_from_host_slice(w5, 5), "write through a copy");
+  CHECK(ok(h.to_host_owned(), "shared")[0] == 5.0f, "copies share storage");
+  CHECK(ok(DeviceTensor::host_zeros(3).to_host_owned(), "zeros") == std::vector<float>(3, 0.0f), "host_zeros");
+}
+
+// gemma4.rs:299-311 and the gate it feeds (:59-92), with the dequant policy.
+void dequant_policy_gate_flips_for_executable_types() {
+  for (uint32_t t = 0; t < 64; ++t) {
+    const bool plain = t == 0 || t == 1 || t == 30 || (t >= 24 && t <= 28);
+    CHECK(is_quantized_tensor_type(t) == !plain, "is_quantized_tensor_type " + std::to_string(t));
+  }
+  CHECK(is_quantized_tensor_type(1000), "unknown ids are quantized");
+  CHECK(tensor_execution(12) == TensorExecution::QuantizedLinear && tensor_execution(8) == TensorExecution::QuantizedLinear &&
+            tensor_execution(14) == TensorExecution::QuantizedLinear,
+        "Q8_0, Q4K, Q6K run the quantized linear");
+  for (uint32_t t : {2u, 3u, 6u, 7u, 10u, 11u, 13u}) CHECK(tensor_execution(t) == TensorExecution::DequantizeToF32, "dequantized");
+  for (uint32_t t : {9u, 15u, 16u, 23u, 29u, 34u, 39u, 77u}) CHECK(tensor_execution(t) == TensorExecution::None, "refused");
+  CHECK(tensor_execution(0) == TensorExecution::Float && tensor_execution(30) == TensorExecution::Float, "float");
+  CHECK(ggml_type_name(16) == "Iq2Xxs" && ggml_type_name(9) == "Q8_1" && ggml_type_name(39) == "MXFP4" &&
+            ggml_type_name(77) == "Unknown(77)",
+        "Debug names");
+  // the gemma4 fixture (fixtures/metadata/gemma4_e4b_it_q4_k_m_gguf_metadata.json): a Q4_K
+  // embedding table and an f32 norm -- the reference refuses it, the policy runs it
+  GgufManifest m;
+  m.tensors.push_back(GgufTensorEntry{"token_embd.weight", {2560, 262144}, 12, 0, 0, std::nullopt});
+  m.tensors.push_back(GgufTensorEntry{"output_norm.weight", {2560}, 0, 0, 0, std::nullopt});
+  CHECK(requires_dequant_policy(m), "a quantized tensor requires the dequant policy");
+  ok(ensure_supported_for_execution(m), "Q4_K file passes the gate");
+  m.tensors.push_back(GgufTensorEntry{"blk.0.attn_q.weight", {2560, 2048}, 16, 0, 0, std::nullopt});
+  m.tensors.push_back(GgufTensorEntry{"blk.0.attn_k.weight", {2560, 512}, 9, 0, 0, std::nullopt});
+  m.tensors.push_back(GgufTensorEntry{"blk.1.attn_q.weight", {2560, 2048}, 16, 0, 0, std::nullopt});
+  auto refused = ensure_supported_for_execution(m);
+  CHECK(refused.is_err() && refused.error().kind() == OcelotlError::Kind::Unsupported, "refused kind");
+  CHECK(refused.error().as_unsupported()->feature == "quantized_tensor_types" &&
+            refused.error().as_unsupported()->requested == std::string("Iq2Xxs,Q8_1"),
+        "refused types in first-seen order, once each");
+  GgufManifest f32_only;
+  f32_only.tensors.push_back(GgufTensorEntry{"w", {8}, 0, 0, 0, std::nullopt});
+  CHECK(!requires_dequant_policy(f32_only), "f32 files need no policy");
+  ok(ensure_supported_for_execution(f32_only), "f32 files pass");
+}
+
 // ---- GPU tests ----------------------------------------------------------------------
 
 HipKernelBackend backend() { return ok(HipKernelBackend::create(0), "create"); }
@@ -187,6 +258,47 @@ void linear_out_by_in_host_slices_match_linear_d_bit_for_bit() {
     DeviceTensor od = ok(be.alloc(rows * out_f), "alloc");
     ok(be.linear_d(xd, rows, in, w, out_f, nullptr, od), "linear_d");
     CHECK(same_bits(host_out, ok(od.to_host_owned(), "readback")), "host-slice and device paths agree");
+  }
+}
+
+// Wrong residency stays correct: host-resident x, bias and out, and views of
+// device tensors, take the trait default's bounce (lib.rs:193-217) and give
+// the device path's bits.
+void linear_d_with_host_tensors_and_views_takes_the_bounce() {
+  HipKernelBackend be = backend();
+  const size_t rows = 3, in = 1024, out_f = 200;
+  for (GgmlTensorType t : kTypes) {
+    const auto wq = quantize(t, normal(450 + (int)t, out_f * in, 0.02f));
+    const auto x = normal(451, (rows + 2) * in, 1.0f);
+    const auto bias = normal(452, out_f, 0.1f);
+    QuantizedWeight w = ok(be.upload_quantized(t, in, out_f, wq.data(), wq.size()), "upload_quantized");
+    const std::vector<float> xr(x.begin() + (ptrdiff_t)in, x.begin() + (ptrdiff_t)((rows + 1) * in));  // rows 1..3
+    DeviceTensor xd = ok(be.upload(xr.data(), xr.size()), "upload x");
+    DeviceTensor bd = ok(be.upload(bias.data(), bias.size()), "upload bias");
+    DeviceTensor od = ok(be.alloc(rows * out_f), "alloc");
+    ok(be.linear_d(xd, rows, in, w, out_f, &bd, od), "device linear_d");
+    const auto want = ok(od.to_host_owned(), "readback");
+    // host x, host bias, host out
+    DeviceTensor xh = DeviceTensor::from_host(xr), bh = DeviceTensor::from_host(bias);
+    DeviceTensor oh = DeviceTensor::host_zeros(rows * out_f);
+    ok(be.linear_d(xh, rows, in, w, out_f, &bh, oh), "host linear_d");
+    CHECK(oh.residency().kind == Residency::Kind::Host, "out stays on the host");
+    CHECK(same_bits(ok(oh.to_host_owned(), "host out"), want), "host bounce equals the device path");
+    // a view of a device tensor as x, device out
+    DeviceTensor xall = ok(be.upload(x.data(), x.size()), "upload all");
+    DeviceTensor xv = ok(DeviceTensor::view(xall, in, rows * in), "view");
+    DeviceTensor od2 = ok(be.alloc(rows * out_f), "alloc 2");
+    ok(be.linear_d(xv, rows, in, w, out_f, &bd, od2), "view linear_d");
+    CHECK(same_bits(ok(od2.to_host_owned(), "view out"), want), "view bounce equals the device path");
+    // device x, host out
+    DeviceTensor oh2 = DeviceTensor::host_zeros(rows * out_f);
+    ok(be.linear_d(xd, rows, in, w, out_f, &bd, oh2), "host out linear_d");
+    CHECK(same_bits(ok(oh2.to_host_owned(), "host out 2"), want), "host out equals the device path");
+    // a view is read-only: as out it is an error, nothing written
+    DeviceTensor ov = ok(DeviceTensor::view(xall, 0, rows * out_f), "view out");
+    auto r = be.linear_d(xd, rows, in, w, out_f, &bd, ov);
+    CHECK(r.is_err() && r.error().as_kernel()->message == "DeviceTensor::write_from_host_slice: views are read-only",
+          "views are read-only outputs");
   }
 }
 
@@ -356,13 +468,18 @@ int main(int argc, char **argv) {
     tests = {{"block_info_matches_gguf_block_sizes", block_info_matches_gguf_block_sizes},
              {"tensor_byte_len_of_the_gemma4_fixture_tensor", tensor_byte_len_of_the_gemma4_fixture_tensor},
              {"error_display_matches_the_reference_format", error_display_matches_the_reference_format},
-             {"create_without_a_gfx950_device_is_unsupported", create_without_a_gfx950_device_is_unsupported}};
+             {"create_without_a_gfx950_device_is_unsupported", create_without_a_gfx950_device_is_unsupported},
+             {"host_tensors_and_views_follow_the_reference_semantics",
+              host_tensors_and_views_follow_the_reference_semantics},
+             {"dequant_policy_gate_flips_for_executable_types", dequant_policy_gate_flips_for_executable_types}};
   } else if (suite == "gpu") {
     tests = {{"backend_identity", backend_identity},
              {"linear_d_matches_reference_cpu_path", linear_d_matches_reference_cpu_path},
              {"linear_out_by_in_host_slices_match_linear_d_bit_for_bit",
               linear_out_by_in_host_slices_match_linear_d_bit_for_bit},
              {"linear_d_rejects_mismatched_lengths_before_launch", linear_d_rejects_mismatched_lengths_before_launch},
+             {"linear_d_with_host_tensors_and_views_takes_the_bounce",
+              linear_d_with_host_tensors_and_views_takes_the_bounce},
              {"upload_quantized_validates_type_and_byte_length", upload_quantized_validates_type_and_byte_length},
              {"dequantize_is_bit_exact_with_the_cpu_definition", dequantize_is_bit_exact_with_the_cpu_definition},
              {"linear_d_one_hot_column_is_exact", linear_d_one_hot_column_is_exact},
