@@ -79,7 +79,55 @@ __device__ __forceinline__ void load8(const void *X, int64_t base, float v[8]) {
   }
 }
 
+// Shared by both forms of the pre-pass: the row's scale from its max |x|,
+// then the scaled fp16 planes and per-32 sums of 8 values (one chunk; fixed
+// order: pairs within a thread, then the four threads of the run through DPP).
+__device__ __forceinline__ int prep_exp(float amax) {
+  // 2^-s with amax * 2^-s in [512, 1024); zero, inf and NaN rows keep s = 0
+  return (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
+}
+
 template <bool kF32>
+__device__ __forceinline__ void prep_chunk(const float v[8], int s, bool ok, int64_t base, int m, int K, int c,
+                                           int tid, _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
+                                           h2 *__restrict__ xsum) {
+  h8 hv, lv;
+  float t = 0.0f;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float w = ldexpf(v[i], -s);
+    t += w;
+    const _Float16 h = (_Float16)w;
+    hv[i] = h;
+    lv[i] = (_Float16)(w - (float)h);
+  }
+  t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+  t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+  if (ok) {
+    *reinterpret_cast<h8 *>(xhi + base) = hv;
+    if (kF32) *reinterpret_cast<h8 *>(xlo + base) = lv;
+    if ((tid & 3) == 0) {
+      const _Float16 sh = (_Float16)t;
+      h2 pair;
+      pair[0] = sh;
+      pair[1] = (_Float16)(t - (float)sh);
+      xsum[(int64_t)m * (K / 32) + c / 4] = pair;
+    }
+  }
+}
+
+__device__ __forceinline__ float block_max(float amax, float *red, int tid) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// CH > 0: each thread holds its CH chunks of 8 activations in registers
+// (chunk c = tid + 256 i), so the row is read once; CH == 0: rows longer than
+// 8 chunks per thread are read twice (max, then convert).
+template <bool kF32, int CH>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__ X, int M, int K,
                                                         _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
                                                         h2 *__restrict__ xsum, float *__restrict__ rscale) {
@@ -88,6 +136,32 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
   const int tid = (int)threadIdx.x;
   const int chunks = K / 8;  // 8 activations per thread and pass; 4 consecutive threads = one 32-run
   const int64_t row = (int64_t)m * K;
+  if constexpr (CH > 0) {
+    float v[CH][8];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;
+      if (c < chunks) {
+        load8<kF32>(X, row + 8 * (int64_t)c, v[i]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < CH; ++i)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+    const int s = prep_exp(block_max(amax, red, tid));
+    if (tid == 0) rscale[m] = ldexpf(1.0f, s);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int c = tid + 256 * i;  // chunks is a multiple of 32: runs never straddle the bound
+      prep_chunk<kF32>(v[i], s, c < chunks, row + 8 * (int64_t)c, m, K, c, tid, xhi, xlo, xsum);
+    }
+    return;
+  }
   // pass 1: row max |x|
   float amax = 0.0f;
   for (int c = tid; c < chunks; c += 256) {
@@ -96,19 +170,12 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
 #pragma unroll
     for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
   }
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  // 2^-s with amax * 2^-s in [512, 1024); zero, inf and NaN rows keep s = 0
-  const int s = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
+  const int s = prep_exp(block_max(amax, red, tid));
   if (tid == 0) rscale[m] = ldexpf(1.0f, s);
-  // pass 2: scaled fp16 planes and per-32 sums (fixed order: pairs within a
-  // thread, then the four threads of the run through DPP)
+  // pass 2: scaled fp16 planes and per-32 sums
   for (int c0 = 0; c0 < chunks; c0 += 256) {
     const int c = c0 + tid;
-    const bool ok = c < chunks;  // chunks is a multiple of 32: runs never straddle the bound
+    const bool ok = c < chunks;
     float v[8];
     if (ok) {
       load8<kF32>(X, row + 8 * (int64_t)c, v);
@@ -116,30 +183,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
 #pragma unroll
       for (int i = 0; i < 8; ++i) v[i] = 0.0f;
     }
-    h8 hv, lv;
-    float t = 0.0f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float w = ldexpf(v[i], -s);
-      t += w;
-      const _Float16 h = (_Float16)w;
-      hv[i] = h;
-      lv[i] = (_Float16)(w - (float)h);
-    }
-    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
-    if (ok) {
-      const int64_t base = row + 8 * (int64_t)c;
-      *reinterpret_cast<h8 *>(xhi + base) = hv;
-      if (kF32) *reinterpret_cast<h8 *>(xlo + base) = lv;
-      if ((tid & 3) == 0) {
-        const _Float16 sh = (_Float16)t;
-        h2 pair;
-        pair[0] = sh;
-        pair[1] = (_Float16)(t - (float)sh);
-        xsum[(int64_t)m * (K / 32) + c / 4] = pair;
-      }
-    }
+    prep_chunk<kF32>(v, s, ok, row + 8 * (int64_t)c, m, K, c, tid, xhi, xlo, xsum);
   }
 }
 
@@ -1404,12 +1448,23 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   h2 *xsum = reinterpret_cast<h2 *>(ws + plan.off_sums);
   float *rscale = reinterpret_cast<float *>(ws + plan.off_rscale);
   float *part = plan.ksplit > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
-  if (x_is_bf16)
-    hipLaunchKernelGGL(gemm_prep_kernel<false>, dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum,
-                       rscale);
-  else
-    hipLaunchKernelGGL(gemm_prep_kernel<true>, dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, xsum,
-                       rscale);
+  // chunks of 8 activations per thread: 2 (K <= 4096), 4, 8 held in registers, longer rows read twice
+  const int64_t per_thread = (K / 8 + 255) / 256;
+#define OKQ_PREP(F32_, CH_)                                                                                       \
+  hipLaunchKernelGGL((gemm_prep_kernel<F32_, CH_>), dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, \
+                     xsum, rscale)
+#define OKQ_PREP_CH(F32_)                     \
+  if (per_thread <= 2) OKQ_PREP(F32_, 2);     \
+  else if (per_thread <= 4) OKQ_PREP(F32_, 4); \
+  else if (per_thread <= 8) OKQ_PREP(F32_, 8); \
+  else OKQ_PREP(F32_, 0)
+  if (x_is_bf16) {
+    OKQ_PREP_CH(false);
+  } else {
+    OKQ_PREP_CH(true);
+  }
+#undef OKQ_PREP_CH
+#undef OKQ_PREP
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   const int tiles_n = (int)((N + kBN - 1) / kBN);
