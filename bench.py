@@ -397,9 +397,11 @@ def run_c4(ctx: Ctx, args, c2):
     Q4_K at the Llama-3-8B projection shapes (q/o 4096x4096, k/v 1024x4096,
     gate/up 14336x4096, down 4096x14336; one of each pair) and Q8_0 at
     4096x4096.  us_call: the whole entry point (activation pre-pass + GEMM +
-    split-K reduction), stream events around each of `reps` back-to-back calls
-    rotating over 8 weight copies (mean, p10, median, p90); us_kernel: the MFMA
-    kernel's own dispatch time.  frac_bf16_peak is per call."""
+    split-K reduction) as a prefill issues it, back to back: `reps` calls
+    rotating over 8 weight copies captured into one HIP graph, stream events
+    around each of 10 replays (mean per call; p10, median, p90 over the
+    replays' per-call means); us_kernel: the MFMA kernel's own dispatch time.
+    frac_bf16_peak is per call."""
     torch = ctx.torch
     res = {}
     lay = c2["layers"]
@@ -420,15 +422,26 @@ def run_c4(ctx: Ctx, args, c2):
 
             call(0)
             us = ctx.kernel_us(call, reps)
-            evs = [torch.cuda.Event(enable_timing=True) for _ in range(reps + 1)]
+            cs = torch.cuda.Stream()  # capture stream: its GEMM workspace is allocated before capture
+            with torch.cuda.stream(cs):
+                call(0)
             torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=cs):
+                for r in range(reps):
+                    call(r)
+            g.replay()
+            torch.cuda.synchronize()
+            replays = 10
+            evs = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
             evs[0].record()
-            for r in range(reps):
-                call(r)
+            for r in range(replays):
+                g.replay()
                 evs[r + 1].record()
             torch.cuda.synchronize()
-            per = [1000.0 * evs[r].elapsed_time(evs[r + 1]) for r in range(reps)]
-            t_call = sum(per) / reps
+            del g
+            per = [1000.0 * evs[r].elapsed_time(evs[r + 1]) / reps for r in range(replays)]
+            t_call = sum(per) / replays
             t_k = sum(us) / len(us)
             flops = 2.0 * m * n * k
             key = f"M{m}_{name}" if t == Q4K else f"M{m}_q8_0_4096"
@@ -460,10 +473,11 @@ def run_c5(ctx: Ctx, args):
     an engine issues (q+k and gate+up share x in okq_gemv_multi, the other
     projections through okq_linear_out_by_in_q); `auto`: one
     okq_linear_out_by_in_q per projection.  Both dispatches pick the kernel
-    by shape: the streaming decode-batch MFMA kernel for Q4_K/Q6_K weights of
-    16 MB and more from five rows, and for every Q4_K/Q6_K weight above eight
-    rows; the GEMV otherwise (okq_gemv_multi's matrices that stay on the GEMV
-    share one launch, each pass over a weight serving up to four rows)."""
+    by shape: the streaming decode-batch MFMA kernel for weights from 2 MB at
+    6-8 rows (from 8 MB at 5 rows, down projections and the head from 3
+    rows), and for every weight above eight rows; the GEMV otherwise
+    (okq_gemv_multi's matrices that stay on the GEMV share one launch, each
+    pass over a weight serving up to four rows)."""
     torch = ctx.torch
     log(f"C5: generating {C5_LAYERS} Q4_K_M layers + Q6_K head")
     layers = [{name: ctx.quantized(t, n, k, seed=50_000 + 100 * l + i) for i, (name, t, n, k) in enumerate(C5_PROJ)}

@@ -134,10 +134,12 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
  * bias: [out_features] f32 or NULL; out: [rows, out_features] f32.
  * rows == 0 or out_features == 0 is a no-op.  Up to 8 rows run the fused
  * dequant-GEMV (each pass over the weights serving up to four rows), except
- * Q4_K / Q6_K matrices of 16 MB or more from 5 rows on and of 8 MB or more
- * from 7 rows on; more rows run the
- * MFMA dequant-GEMM (Q4_K, Q6_K; Q8_0 stays on the GEMV), which for up to 32
- * rows streams the weights once with the rows in one or two MFMA tiles. */
+ * weights large enough for the MFMA kernel to repay its fixed cost: from 2 MB
+ * at 6-8 rows, from 8 MB at 5 rows, and at 3-4 rows from 16 MB when
+ * in_features >= 8192 or from 64 MB otherwise; more rows run the MFMA
+ * dequant-GEMM (Q4_K, Q6_K, and Q8_0 when in_features is a multiple of 256),
+ * which for up to 32 rows streams the weights once with the rows in one or
+ * two MFMA tiles. */
 okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,
                                   const void *w, uint64_t w_bytes, int64_t out_features, const float *bias,
                                   float *out, void *stream);
@@ -184,9 +186,9 @@ okq_status okq_gemm_bf16(const uint16_t *x, int64_t rows, int64_t in_features, u
  * matrices' concatenated rows in one launch per activation row, quantizing x
  * once.  `bias` may be NULL (no bias anywhere) or hold NULL entries.  Each
  * matrix is validated like okq_gemv before anything launches.  A matrix that
- * okq_linear_out_by_in_q would not give to the GEMV at this row count (Q4_K /
- * Q6_K weights of 16 MB or more from 5 rows and of 8 MB or more from 7 rows,
- * every Q4_K / Q6_K weight above 8 rows) is computed by the MFMA kernels
+ * okq_linear_out_by_in_q would not give to the GEMV at this row count (the
+ * large weights of its 3-8 row rule, every weight above 8 rows) is computed
+ * by the MFMA kernels
  * instead: alone through that entry
  * point's dispatch, or -- two or more of them at up to 32 rows -- together in
  * one decode-batch launch whose K split follows their combined columns.

@@ -260,26 +260,31 @@ std::recursive_mutex &stream_lock(int dev, hipStream_t s) {
 enum class Path { Auto, Gemv, Gemm };
 
 // Rows at or below kGemvMaxRows run the GEMV (each pass over the weights
-// serves up to four rows); above it the MFMA GEMM path (the streaming
-// decode-batch kernel up to 32 rows, the tiled kernel beyond).  Large Q4_K /
-// Q6_K matrices take the decode-batch kernel earlier: it streams the weights
-// once where the GEMV needs a second pass, and its fixed cost (the split-K
-// reduction launch) is repaid from 5 rows at 16 MB and more, and from 7 rows
-// (a second GEMV pass of 3-4 rows) at 8 MB and more.  Measured per call in
-// graphs, decode kernel vs GEMV: Q4_K gate 20 vs 23 us at 5 rows (15 at 4),
-// Q6_K down 31 vs 39 us at 5 rows, Q6_K head 125 vs 199 us at 5 rows; Q4_K
-// q (9.4 MB) 17 vs 16 us at 8 rows, 12 us on the GEMV at 5; the C5 sweep at
-// 8 rows runs 4.8% faster with q/o on the decode-batch kernel.
+// serves up to four rows) unless the weights are large enough for the
+// streaming decode-batch MFMA kernel to repay its fixed cost (activation
+// staging, the split-K reduction launch: ~11 us); above kGemvMaxRows the MFMA
+// path always (the decode-batch kernel up to 32 rows, the tiled kernel
+// beyond).  Per call in graphs over HBM-resident weight copies, decode-batch
+// kernel vs GEMV (us):
+//   Q6_K 4096x14336 (48 MB): 24.2/21.3 at 2 rows, 23.5/32.0 at 3, 23.5/37.8 at 4
+//   Q4_K 4096x14336 (33 MB): 19.3/15.2 at 2 rows, 19.5/25.0 at 3, 19.7/40.0 at 5
+//   Q6_K head (108 MB):      118/98 at 2 rows, 118/122 at 3, 119/123 at 4
+//   Q4_K 14336x4096 (33 MB): 18.9/16.7 at 4 rows, 19.0/25.3 at 5
+//   Q4_K 4096x4096 (9.4 MB): 13.6/13.7 at 5 rows, 13.6/15.0 at 6
+//   Q6_K 1024x4096 (3.4 MB): 13.0/11.7 at 5 rows, 13.0/13.1 at 6, 13.0/15.9 at 7
+//   Q4_K 1024x4096 (2.4 MB): 11.9/11.3 at 5 rows, 12.0/12.5 at 6, 12.0/15.1 at 7
+// so: 6-8 rows from 2 MB; 5 rows from 8 MB; 3-4 rows from 16 MB when K is at
+// least 8192 (where the GEMV's extra rows cost most) and from 64 MB
+// otherwise; 1-2 rows always the GEMV.
 constexpr int64_t kGemvMaxRows = 8;
-constexpr int64_t kDecMinRows = 5;
-constexpr uint64_t kDecMinBytes = 16u << 20;
-constexpr int64_t kDecMidRows = 7;
-constexpr uint64_t kDecMidBytes = 8u << 20;
 
-bool gemv_serves(uint32_t type, int64_t rows, uint64_t w_bytes) {
+bool gemv_serves(uint32_t, int64_t rows, int64_t K, uint64_t w_bytes) {
+  constexpr uint64_t MB = 1u << 20;
   if (rows > kGemvMaxRows) return false;
-  if (rows >= kDecMinRows && w_bytes >= kDecMinBytes) return false;
-  return !(rows >= kDecMidRows && w_bytes >= kDecMidBytes);
+  if (rows >= 6) return w_bytes < 2 * MB;
+  if (rows == 5) return w_bytes < 8 * MB;
+  if (rows >= 3) return !(w_bytes >= 64 * MB || (w_bytes >= 16 * MB && K >= 8192));
+  return true;
 }
 
 // ---- static scratch for the allocation-free entry point -----------------------
@@ -340,7 +345,7 @@ okq_status linear_impl(const void *x, bool x_bf16, int64_t rows, int64_t K, uint
                   (long long)K, (long long)N);
     use_gemm = true;
   } else if (path == Path::Auto) {
-    use_gemm = !gemv_serves(type, rows, w_bytes) && okq::gemm_supported((int)type, rows, K, N);
+    use_gemm = !gemv_serves(type, rows, K, w_bytes) && okq::gemm_supported((int)type, rows, K, N);
   }
   if (use_gemm) {
     void *ws = nullptr;
@@ -565,8 +570,8 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
 // Several validated quantized linears of one format and K that read the same
 // activations x (device f32 [rows][K]); outputs out[i] [rows][N[i]].
 // A matrix that the linear dispatch would not give to the GEMV at this row
-// count (large Q4_K / Q6_K weights from kDecMinRows rows, every Q4_K / Q6_K
-// weight above kGemvMaxRows) goes to the MFMA kernels; the others share one
+// count (gemv_serves: large weights from 3-6 rows on, every weight above
+// kGemvMaxRows) goes to the MFMA kernels; the others share one
 // GEMV launch, bit-identical to okq_linear_out_by_in_q on each matrix.  Two
 // or more MFMA matrices at a decode-batch size share one decode-batch launch
 // (gate/up: one activation staging, one reduction); its K split follows the
@@ -586,7 +591,7 @@ okq_status grouped_linear(const float *x, int64_t rows, int64_t in_features, uin
   uint64_t mbytes[okq::kGemvMaxProblems];
   int shared = 0, mfma = 0;
   for (int i = 0; i < count; ++i) {
-    if (rows > 0 && out_features[i] > 0 && !gemv_serves(w_type, rows, w_bytes[i]) &&
+    if (rows > 0 && out_features[i] > 0 && !gemv_serves(w_type, rows, in_features, w_bytes[i]) &&
         okq::gemm_supported((int)w_type, rows, in_features, out_features[i])) {
       mw[mfma] = w[i];
       mn[mfma] = out_features[i];

@@ -358,37 +358,44 @@ def test_gemm_q6k_one_hot_columns_are_exact(torch, okq, orc):
         assert np.array_equal(got, w[:, cols].T), entry
 
 
+def _dispatch_pairs(torch, okq, orc, t, n, k, seed, pairs):
+    """okq_linear_out_by_in_q at each (rows, pinned entry): bit-identical to the
+    pinned path (okq_gemv: the GEMV; okq_gemm: the MFMA kernels), and within
+    the rule of the reference."""
+    wq = orc.quantize(t, orc.normal(seed, n * k, 0.02))
+    for rows, pinned in pairs:
+        print(f"[gpu] dispatch type={t} rows={rows} N={n} K={k} -> {pinned}", flush=True)
+        x = orc.normal(seed + 1 + rows, rows * k, 1.0)
+        auto = run(torch, okq, "okq_linear_out_by_in_q", t, x, rows, k, wq, n)
+        pin = run(torch, okq, pinned, t, x, rows, k, wq, n)
+        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
+        check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
+    return wq
+
+
 @pytest.mark.parametrize("t", [O.Q4_K, O.Q6_K])
 def test_linear_dispatch_large_matrices_take_the_decode_batch_kernel_from_5_rows(torch, okq, orc, t):
-    """okq_linear_out_by_in_q on a matrix of 16 MB or more: 5 rows run the
-    decode-batch kernel (bit-identical to okq_gemm), 4 rows the GEMV
-    (bit-identical to okq_gemv)."""
+    """A matrix of 8 MB or more with K = 4096 (33-34 MB here): 4 rows run the
+    GEMV, 5 rows the decode-batch kernel."""
     n, k = 14336 if t == O.Q4_K else 10240, 4096
-    wq = orc.quantize(t, orc.normal(930 + t, n * k, 0.02))
+    wq = _dispatch_pairs(torch, okq, orc, t, n, k, 930 + t, ((4, "okq_gemv"), (5, "okq_gemm")))
     assert wq.size >= 16 << 20
-    for rows, pinned in ((4, "okq_gemv"), (5, "okq_gemm")):
-        print(f"[gpu] dispatch type={t} rows={rows} N={n} K={k}", flush=True)
-        x = orc.normal(931 + rows, rows * k, 1.0)
-        auto = run(torch, okq, "okq_linear_out_by_in_q", t, x, rows, k, wq, n)
-        pin = run(torch, okq, pinned, t, x, rows, k, wq, n)
-        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
-        check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
 
 
-def test_linear_dispatch_mid_size_matrices_take_the_decode_batch_kernel_from_7_rows(torch, okq, orc):
-    """A Q4_K matrix of 8-16 MB (the Llama q/o projection, 9.4 MB): 6 rows run
-    the GEMV (bit-identical to okq_gemv), 7 rows the decode-batch kernel
-    (bit-identical to okq_gemm)."""
-    t, n, k = O.Q4_K, 4096, 4096
-    wq = orc.quantize(t, orc.normal(940, n * k, 0.02))
-    assert 8 << 20 <= wq.size < 16 << 20
-    for rows, pinned in ((6, "okq_gemv"), (7, "okq_gemm")):
-        print(f"[gpu] dispatch mid type={t} rows={rows} N={n} K={k}", flush=True)
-        x = orc.normal(941 + rows, rows * k, 1.0)
-        auto = run(torch, okq, "okq_linear_out_by_in_q", t, x, rows, k, wq, n)
-        pin = run(torch, okq, pinned, t, x, rows, k, wq, n)
-        assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), rows
-        check_rows(orc, t, auto, x, rows, k, wq, n, None, 2)
+def test_linear_dispatch_long_rows_take_the_decode_batch_kernel_from_3_rows(torch, okq, orc):
+    """A matrix of 16 MB or more with K >= 8192 (the Llama down projection,
+    33 MB, K = 14336): 2 rows run the GEMV, 3 rows the decode-batch kernel."""
+    wq = _dispatch_pairs(torch, okq, orc, O.Q4_K, 4096, 14336, 935, ((2, "okq_gemv"), (3, "okq_gemm")))
+    assert wq.size >= 16 << 20
+
+
+@pytest.mark.parametrize("n,edge", [(4096, 5), (1024, 6)])
+def test_linear_dispatch_mid_size_matrices_take_the_decode_batch_kernel(torch, okq, orc, n, edge):
+    """Q4_K with K = 4096: the 9.4 MB q/o projection runs the decode-batch
+    kernel from 5 rows, the 2.4 MB k/v projection from 6 rows; one row fewer
+    runs the GEMV."""
+    wq = _dispatch_pairs(torch, okq, orc, O.Q4_K, n, 4096, 940 + edge, ((edge - 1, "okq_gemv"), (edge, "okq_gemm")))
+    assert (8 << 20 <= wq.size < 16 << 20) if edge == 5 else (2 << 20 <= wq.size < 8 << 20)
 
 
 def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):

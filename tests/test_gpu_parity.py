@@ -378,8 +378,10 @@ def test_gemv_multi_equals_single_gemvs_bit_for_bit(torch, okq, orc, t, rows, k,
 MULTI_BATCH_CASES = [
     # (type, rows, K, out_features, the MFMA matrices share one decode-batch launch)
     (O.Q4_K, 8, 4096, [14336, 14336], True),         # gate/up at 8 rows
-    (O.Q4_K, 8, 4096, [4096, 1024, 14336], True),    # k on the GEMV, q and the large one share a decode-batch launch
-    (O.Q4_K, 8, 4096, [1024, 512, 14336], False),    # two on the GEMV, the large one alone
+    (O.Q4_K, 8, 4096, [4096, 1024, 14336], True),    # q, k (2.4 MB) and the large one share a decode-batch launch
+    (O.Q4_K, 8, 4096, [1024, 512, 14336], True),     # 512 x 4096 (1.2 MB) on the GEMV, the other two share
+    (O.Q4_K, 8, 4096, [256, 512, 14336], False),     # two under 2 MB on the GEMV, the large one alone
+    (O.Q4_K, 5, 4096, [4096, 1024, 14336], True),    # 5 rows: k on the GEMV, q and the large one share
     (O.Q6_K, 24, 1024, [33, 300], True),             # above 8 rows: every Q6_K matrix on the MFMA path
     (O.Q4_K, 32, 1024, [17, 1000, 256, 40], True),   # four matrices, ragged tiles, two 16-row groups
     (O.Q8_0, 12, 1024, [100, 64], True),             # Q8_0 above 8 rows: the MFMA kernels too
