@@ -42,6 +42,28 @@ __device__ __forceinline__ float f16_bits_exact(uint32_t h) {
   return as_f32(as_u32(v) | sign);
 }
 
+// Pins a kernel argument in scalar registers at this point.  Arguments pinned
+// at kernel entry are fetched in one batch of scalar loads; otherwise the
+// compiler fetches each on first use, which after a branch or behind a
+// computed index (a select over an argument array) becomes a chain of
+// dependent round trips to the argument segment before the first load.
+// The value is also marked wave-uniform (readfirstlane), so that selects over
+// pinned arguments stay scalar selects rather than a lookup table in private
+// memory.
+template <class T>
+__device__ __forceinline__ T sarg(T v) {
+  asm volatile("" : "+s"(v));
+  if constexpr (sizeof(T) == 4) {
+    return __builtin_bit_cast(T, __builtin_amdgcn_readfirstlane(__builtin_bit_cast(int, v)));
+  } else {
+    static_assert(sizeof(T) == 8, "32- or 64-bit arguments");
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)u);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(u >> 32));
+    return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+  }
+}
+
 // Hardware conversion for the hot loops (exact for every non-NaN input).
 __device__ __forceinline__ float f16_bits_hw(uint32_t h) {
   _Float16 v = __builtin_bit_cast(_Float16, (uint16_t)h);

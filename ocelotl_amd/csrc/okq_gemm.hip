@@ -732,6 +732,16 @@ struct DecMats {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Byte offset of the decode-batch kernel's small LDS arrays (bias, row scales,
+// row maxima): past the activation slice (planes of pitch P halves, per-32
+// sums) and, with an in-workgroup K split, past the partial tiles that reuse
+// those bytes at the end ([kDecWaves][RG] x 1 KB).
+__host__ __device__ constexpr size_t dec_tail_offset(int M, int P, int nsbs, int planes, bool kw_split, int RG) {
+  const size_t act = (size_t)M * P * 2 * planes + (size_t)M * nsbs * 32;
+  const size_t red = kw_split ? (size_t)kDecWaves * RG * 1024 : 0;
+  return ((act > red ? act : red) + 15) & ~(size_t)15;
+}
+
 // Per-format parts of the decode kernel: the registers of one item (one
 // super-block of one 16-column tile, as seen by one lane), their loads, and
 // the contraction of one super-block into the lane's 4 accumulators.
@@ -756,7 +766,7 @@ struct DecQ4K {
   // (xsum hi, xsum lo) x m (lane groups 2, 3 contribute zeros)
   template <bool kLo, int RG>
   __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
-                                  const _Float16 *const *xs, int g, f4 *acc) {
+                                  const _Float16 *const *xs, const float *rsc, int g, f4 *acc) {
     const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     h2 scv[2], offv[2];
 #pragma unroll
@@ -806,8 +816,9 @@ struct DecQ4K {
     for (int q = 0; q < RG; ++q) {
       const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(xs[q] + 8 * g) : h8{};
       const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
+      const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dm, mins[v], fmaf(dv, accs[q][v], acc[q][v]));
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dm * s4[v], mins[v], fmaf(dv * s4[v], accs[q][v], acc[q][v]));
     }
   }
 };
@@ -842,7 +853,7 @@ struct DecQ6K {
   }
   template <bool kLo, int RG>
   __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
-                                  const _Float16 *const *, int g, f4 *acc) {
+                                  const _Float16 *const *, const float *rsc, int g, f4 *acc) {
     const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
     const uint32_t r = it.r;
     uint32_t L[4][2], H[2][2];
@@ -894,9 +905,11 @@ struct DecQ6K {
     }
     const float dv = f16_bits_hw(it.dw & 0xffffu);
 #pragma unroll
-    for (int q = 0; q < RG; ++q)
+    for (int q = 0; q < RG; ++q) {
+      const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dv, accs[q][v], acc[q][v]);
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dv * s4[v], accs[q][v], acc[q][v]);
+    }
   }
 };
 
@@ -925,7 +938,7 @@ struct DecQ80 {
   }
   template <bool kLo, int RG>
   __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
-                                  const _Float16 *const *, int g, f4 *acc) {
+                                  const _Float16 *const *, const float *rsc, int g, f4 *acc) {
     const uint32_t raw[18] = {it.w0.x, it.w0.y, it.w0.z, it.w0.w, it.w1.x, it.w1.y, it.w1.z, it.w1.w, it.w2.x,
                               it.w2.y, it.w2.z, it.w2.w, it.w3.x, it.w3.y, it.w3.z, it.w3.w, it.w4.x, it.w4.y};
     uint32_t w[17];  // bytes 4i .. 4i + 3 of the lane's 68 bytes
@@ -935,6 +948,10 @@ struct DecQ80 {
     // 34-35, quants in bytes 36-67 (dword aligned)
     const _Float16 d0 = __builtin_bit_cast(_Float16, (uint16_t)(w[0] & 0xffffu));
     const _Float16 d1 = __builtin_bit_cast(_Float16, (uint16_t)(w[8] >> 16));
+    const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    f4 accs[RG];
+#pragma unroll
+    for (int q = 0; q < RG; ++q) accs[q] = zero4;
 #pragma unroll
     for (int t = 0; t < 8; ++t) {
       const int blk = t >> 2, o = 2 * (t & 3);  // dword of the 8 quants within the block's quants
@@ -951,13 +968,19 @@ struct DecQ80 {
 #pragma unroll
       for (int q = 0; q < RG; ++q) {
         const h8 ah = *reinterpret_cast<const h8 *>(ar[q] + ka);
-        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, acc[q], 0, 0, 0);
-        acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, acc[q], 0, 0, 0);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bh, accs[q], 0, 0, 0);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bl, accs[q], 0, 0, 0);
         if (kLo) {  // the x_lo * remainder term (below 2^-22 of the result) is left out
           const h8 al = *reinterpret_cast<const h8 *>(arl[q] + ka);
-          acc[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, acc[q], 0, 0, 0);
+          accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bh, accs[q], 0, 0, 0);
         }
       }
+    }
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(s4[v], accs[q][v], acc[q][v]);
     }
   }
 };
@@ -979,37 +1002,60 @@ struct DecQ80 {
 // consecutively (`DecMats`), and each tile finds its matrix, weights, bias and
 // output through wave-uniform scalar selects.  Split-K partials are laid out
 // over the concatenated tile columns, [ksplit][M][ntiles * 16].
-template <class F, bool kLo, int RG>
-__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void *__restrict__ X, DecMats mats,
-                                                                     int ntiles, int M, int K, int ksplit,
-                                                                     int groups, float *__restrict__ part) {
+// Index arithmetic stays off the scalar ALU, which one CU's 16 waves share:
+// the grid is (column group, K slice), the host passes the slice partition
+// (slice z holds base + (z < rem) super-blocks) and the power of two kw as a
+// shift, and the ring walks its items with counters instead of divisions.
+template <class F, bool kLo, int RG, bool kW>
+__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void *__restrict__ X_arg, DecMats mats,
+                                                                     int ntiles_arg, int M_arg, int K_arg,
+                                                                     int sl_base_arg, int sl_rem_arg,
+                                                                     int kw_shift_arg, float *__restrict__ part_arg) {
+  // every argument in scalar registers up front (one batch of argument loads)
+  const void *const X = sarg(X_arg);
+  float *const part = sarg(part_arg);
+  const int ntiles = sarg(ntiles_arg), M = sarg(M_arg), K = sarg(K_arg);
+  const int sl_base = sarg(sl_base_arg), sl_rem = sarg(sl_rem_arg);
+  // kW: an in-workgroup K split (unsplit K across workgroups, one 16-row group)
+  const int kw_shift = kW ? sarg(kw_shift_arg) : 0, kw = 1 << kw_shift;
+  const int ksplit = (int)gridDim.y, groups = (int)gridDim.x;
   constexpr int D = RG == 1 ? F::kDepth1 : F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
-  const int tid = (int)threadIdx.x, nt = (int)blockDim.x;
+  constexpr int nt = kDecWaves * 64;
+  const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int z = (int)blockIdx.x % ksplit, grp = (int)blockIdx.x / ksplit;
-  const int nsb_all = K / 256;
-  const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
-  const int nsbs = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;
+  const int grp = (int)blockIdx.x, z = (int)blockIdx.y;
+  const int nsb_all = (int)((uint32_t)K >> 8);
+  const int sb0 = z * sl_base + (z < sl_rem ? z : sl_rem);
+  const int nsbs = sl_base + (z < sl_rem ? 1 : 0);
   const int Ks = nsbs * 256, P = Ks + 8;  // slice width, LDS row pitch (halves)
-  // LDS: Ah [M][P], Al [M][P] (kLo), xs [M][nsbs][16]
+  // LDS: Ah [M][P], Al [M][P] (kLo), xs [M][nsbs][16]; with kw > 1 the same
+  // bytes hold the waves' partial tiles once the activations are consumed
   _Float16 *Ah = reinterpret_cast<_Float16 *>(dsm);
   _Float16 *Al = Ah + (size_t)M * P;
   _Float16 *Xs = Ah + (size_t)M * P * (kLo ? 2 : 1);
-  // unsplit K: the bias of the workgroup's columns (tile ti of every wave:
-  // columns (ti * groups + grp) * 256 + [0, 256)); the rows' slice scales 2^s;
-  // the rows' slice maxima (|x| bits)
-  float *Bs = reinterpret_cast<float *>(Xs + (size_t)M * nsbs * 16);  // [kDecMaxTiles][256]
-  float *Rs = Bs + kDecMaxTiles * 256;                                      // [kDecRows]
-  unsigned *Rmax = reinterpret_cast<unsigned *>(Rs + kDecRows);             // [kDecRows + 1]
-  if (tid < M) Rmax[tid] = 0u;
+  // unsplit K: the bias of every wave's tiles (tile ti of wave w at
+  // [ti][16 w .. 16 w + 15]); the power-of-two scale of every (super-block,
+  // row) of the slice
+  float *Bs = reinterpret_cast<float *>(dsm + dec_tail_offset(M, P, nsbs, kLo ? 2 : 1, kW, RG));  // [kDecMaxTiles][256]
+  float *Rsb = Bs + kDecMaxTiles * 256;  // [nsbs][kDecRows]: the 2^s of each (super-block, row)
 
-  // 1. this wave's items: tile ti of the wave (ti = 0, 1, ...) is column tile
-  //    (ti * groups + grp) * waves + wave; item u = (ti = u / nsbs, u % nsbs)
-  const int stride = groups * kDecWaves;
-  const int first = grp * kDecWaves + wave;
-  const int mytiles = first < ntiles ? (ntiles - first + stride - 1) / stride : 0;
-  const int nitems = mytiles * nsbs;
+  // 1. this wave's items.  The kDecWaves waves form T = kDecWaves / kw tile
+  //    slots of kw waves each: slot ts's tile of round ti is column tile
+  //    (ti * groups + grp) * T + ts, and wave kp of the slot takes the slice's
+  //    super-blocks kp, kp + kw, ... (kw > 1 only with unsplit K: the slot's
+  //    waves then sum their partial tiles through LDS at the end).  Item
+  //    (ti, jj) is round ti's super-block kp + kw jj, jj < cnt.
+  // (all wave-uniform: readfirstlane keeps them, and the matrix selects and
+  // weight descriptors built from them, in scalar registers -- a descriptor
+  // the compiler takes for divergent costs a waterfall loop per load)
+  const int T = kDecWaves >> kw_shift, ts = wave >> kw_shift, kp = wave & (kw - 1);
+  const int stride = __builtin_amdgcn_readfirstlane(groups * T);
+  const int first = __builtin_amdgcn_readfirstlane(grp * T + ts);
+  const int cnt = __builtin_amdgcn_readfirstlane(nsbs > kp ? (nsbs - kp + kw - 1) >> kw_shift : 0);  // items per tile
+  const int mytiles =
+      __builtin_amdgcn_readfirstlane(first < ntiles && cnt > 0 ? (ntiles - first + stride - 1) / stride : 0);
+  const int nitems = mytiles * cnt;
   const int cn = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
   // the matrix of a tile (tiles past the end map to the last matrix; every
@@ -1031,10 +1077,15 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   for (int q = 0; q < RG; ++q) arow[q] = (lane & 15) + 16 * q < M ? (lane & 15) + 16 * q : M - 1;
 
   using Item = typename F::Item;
-  auto tile_of = [&](int u) { return (u / nsbs) * stride + first; };
-  auto load = [&](Item &it, int u) {
-    const int sbl = u - (u / nsbs) * nsbs;
-    const int tile = tile_of(u), m = mat_of(tile);
+  // item positions advance by counters: (ti, jj) -> next item
+  auto advance = [&](int &ti, int &jj) {
+    const bool wrap = jj + 1 == cnt;
+    jj = wrap ? 0 : jj + 1;
+    ti += wrap ? 1 : 0;
+  };
+  auto load = [&](Item &it, int ti, int jj) {
+    const int sbl = kp + (jj << kw_shift);
+    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
     const uint32_t w_end = (uint32_t)((size_t)n_of(m) * row_bytes);
     // rows past the matrix (and tiles past the end) read past the tensor: zeros
     const uint32_t n = (uint32_t)((tile - tile0_of(m)) * 16 + cn);
@@ -1066,7 +1117,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   uint32_t bbits[kDecMaxTiles];
 #pragma unroll
   for (int ti = 0; ti < kDecMaxTiles; ++ti) {
-    const int tile = ti * stride + first, m = mat_of(tile);
+    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
     const float *bp = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
     const uint32_t bias_end = bp ? (uint32_t)n_of(m) * 4u : 0u;
     const int col = (tile - tile0_of(m)) * 16 + lane;
@@ -1097,26 +1148,25 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
       v[4] = bf16_lo(xa[i].z), v[5] = bf16_hi(xa[i].z), v[6] = bf16_lo(xa[i].w), v[7] = bf16_hi(xa[i].w);
     }
   };
-  __syncthreads();  // Rmax cleared
-  // the rows' slice maxima: the largest |x| of each piece (fmaxf drops NaNs),
-  // combined as bit patterns (monotonic for non-negative floats).  Pieces
-  // past the last row are skipped (a uniform bound: i * nt >= M * pr).
+  // Scaled fp16 planes and per-32 sums, one pass: each (row, super-block) of
+  // the slice is scaled by its own 2^-s (its largest |x| into [512, 1024);
+  // zero, inf and NaN blocks keep s = 0), applied back in f32 with the
+  // super-block's d.  The 32 pieces of lanes 0-31 (32-63) are one row's
+  // super-block (pieces per row are a multiple of 32), so its max is a
+  // half-wave reduction: DPP within each 16-lane row, readlane across the
+  // two.  Pieces past the last row are skipped (a uniform bound).
   auto dmax = [](float a, auto ctl) {
     return fmaxf(a, as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(a), decltype(ctl)::value, 0xf, 0xf, false)));
   };
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
     if (i * nt >= M * pr) break;
-    const int p = tid + i * nt, r = p / pr;
+    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
     float v[8];
     piece(i, v);
-    float a = 0.0f;
+    float a = 0.0f;  // fmaxf drops NaNs
 #pragma unroll
     for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
-    // the 32 pieces of lanes 0-31 (32-63) share one row (pieces per row and
-    // per workgroup are multiples of 32): the max of each 16-lane row by DPP,
-    // the two rows of a half-wave through readlane, one LDS atomic per
-    // half-wave
     a = dmax(a, std::integral_constant<int, 0xB1>{});   // quad_perm 1,0,3,2
     a = dmax(a, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
     a = dmax(a, std::integral_constant<int, 0x141>{});  // row_half_mirror
@@ -1125,24 +1175,12 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
                            as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 16)));
     const float h1 = fmaxf(as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 32)),
                            as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 48)));
-    a = lane < 32 ? h0 : h1;
-    if ((lane & 31) == 0 && r < M && a > 0.0f) atomicMax(&Rmax[r], __float_as_uint(a));
-  }
-  __syncthreads();  // maxima complete
-  // scaled fp16 planes and per-32 sums (fixed order: the 8 values of a piece
-  // in order, then the 4 pieces of a run through DPP; a run's pieces sit in
-  // 4 consecutive lanes because pieces per row is a multiple of 4)
-#pragma unroll
-  for (int i = 0; i < kDecStage; ++i) {
-    if (i * nt >= M * pr) break;
-    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
-    const float amax = r < M ? __uint_as_float(Rmax[r]) : 0.0f;
+    const float amax = lane < 32 ? h0 : h1;
     const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
-    float v[8];
-    piece(i, v);
     // hi = fp16 of w rounded toward zero, two values per v_cvt_pkrtz; w - hi
     // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16, so
-    // hi + lo = w to 2^-20 relative
+    // hi + lo = w to 2^-20 relative.  Sums: the 8 values of a piece in order,
+    // then the 4 pieces of a run (4 consecutive lanes) through DPP.
     h8 hv, lv;
     float t = 0.0f;
 #pragma unroll
@@ -1169,12 +1207,16 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
         pair[1] = (_Float16)(t - (float)sh);
         *reinterpret_cast<h2 *>(Xs + (size_t)r * nsbs * 16 + 2 * (c >> 2)) = pair;
       }
-      if (c == 0 && r < M) Rs[r] = ldexpf(1.0f, sx);
+      if ((c & 31) == 0) Rsb[(c >> 5) * kDecRows + r] = ldexpf(1.0f, sx);
     }
   }
   __syncthreads();
+  int l_ti = 0, l_jj = 0;  // the next item to load
 #pragma unroll
-  for (int j = 0; j < D; ++j) load(S[j], j);
+  for (int j = 0; j < D; ++j) {
+    load(S[j], l_ti, l_jj);
+    advance(l_ti, l_jj);
+  }
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
   f4 acc[RG];
@@ -1185,8 +1227,32 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   const int ncat = ntiles * 16;  // partial columns: the concatenated tiles
   const uint32_t part_end = (uint32_t)((size_t)ksplit * M * ncat * 4);
   const Rsrc rs_part = make_rsrc(part, part_end);
-  auto consume = [&](const Item &it, int u) {
-    const int ti = u / nsbs, sbl = u - ti * nsbs;
+  // a finished tile (round ti of this wave's slot): scaled back by the rows'
+  // 2^s, plus the bias (unsplit K), or the raw partial of slice z
+  auto store = [&](int ti, const f4 *vals) {
+    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
+    const int nm = n_of(m), col = (tile - tile0_of(m)) * 16 + cn;
+    const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
+    // unsplit: the matrix's own output; split: the concatenated partials
+    float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
+    const uint32_t out_end = ksplit > 1 ? part_end : (uint32_t)((size_t)M * nm * 4);
+    const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(ym, out_end);
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * q + 4 * g + v;
+        const float val = vals[q][v] + bv;  // rows >= M: the range check drops their stores
+        const uint32_t off =
+            (row < M && col < nm)
+                ? (uint32_t)(ksplit > 1 ? ((size_t)z * M + row) * ncat + (size_t)tile * 16 + cn : (size_t)row * nm + col) * 4u
+                : out_end;
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
+      }
+    }
+  };
+  auto consume = [&](const Item &it, int ti, int jj) {
+    const int sbl = kp + (jj << kw_shift);
     const _Float16 *ar[RG], *arl[RG], *xs[RG];
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
@@ -1194,47 +1260,54 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
       arl[q] = Al + (size_t)arow[q] * P + sbl * 256;
       xs[q] = Xs + ((size_t)arow[q] * nsbs + sbl) * 16;
     }
-    F::template contract<kLo, RG>(it, ar, arl, xs, g, acc);
-    if (sbl == nsbs - 1) {  // the tile's last super-block: write it out
-      const int tile = ti * stride + first, m = mat_of(tile);
-      const int nm = n_of(m), col = (tile - tile0_of(m)) * 16 + cn;
-      const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
-      // unsplit: the matrix's own output; split: the concatenated partials
-      float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
-      const uint32_t out_end = ksplit > 1 ? part_end : (uint32_t)((size_t)M * nm * 4);
-      const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(ym, out_end);
+    F::template contract<kLo, RG>(it, ar, arl, xs, Rsb + sbl * kDecRows + 4 * g, g, acc);
+    // the tile's last super-block: write it out (kw > 1: a slot has at most
+    // one tile, and acc keeps this wave's part of it for the LDS sum below)
+    if (jj == cnt - 1 && kw == 1) {
+      store(ti, acc);
 #pragma unroll
-      for (int q = 0; q < RG; ++q) {
-#pragma unroll
-        for (int v = 0; v < 4; ++v) {
-          const int row = 16 * q + 4 * g + v;
-          // rows >= M read an unset Rs entry; the range check drops their stores
-          const float val = acc[q][v] * Rs[row] + bv;
-          const uint32_t off =
-              (row < M && col < nm)
-                  ? (uint32_t)(ksplit > 1 ? ((size_t)z * M + row) * ncat + (size_t)tile * 16 + cn : (size_t)row * nm + col) * 4u
-                  : out_end;
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
-        }
-        acc[q] = zero4;
-      }
+      for (int q = 0; q < RG; ++q) acc[q] = zero4;
     }
   };
 
   // 3. the ring: consume slot j, refill it D items ahead; loads stay
   //    unconditional (items past the end read past the tensor: zeros).  The
   //    staging barrier above waits for LDS only, not for these loads.
+  int c_ti = 0, c_jj = 0;  // the next item to consume
   int u0 = 0;
   for (; u0 + D < nitems; u0 += D) {
 #pragma unroll
     for (int j = 0; j < D; ++j) {
-      consume(S[j], u0 + j);
-      load(S[j], u0 + j + D);
+      consume(S[j], c_ti, c_jj);
+      advance(c_ti, c_jj);
+      load(S[j], l_ti, l_jj);
+      advance(l_ti, l_jj);
     }
   }
 #pragma unroll
   for (int j = 0; j < D; ++j)
-    if (u0 + j < nitems) consume(S[j], u0 + j);
+    if (u0 + j < nitems) {
+      consume(S[j], c_ti, c_jj);
+      advance(c_ti, c_jj);
+    }
+  if constexpr (!kW) return;
+  // 4. kw > 1: the kw waves of each slot hold partial sums of its one tile
+  //    over disjoint super-blocks.  Once every wave is past the activations,
+  //    their LDS holds the partials [wave][RG][lane][4]; the slot's first
+  //    wave sums them in wave order (a fixed order: deterministic) and writes
+  //    the tile.
+  __syncthreads();
+  f4 *Red = reinterpret_cast<f4 *>(dsm);
+  if (mytiles > 0) {
+#pragma unroll
+    for (int q = 0; q < RG; ++q) Red[(wave * RG + q) * 64 + lane] = acc[q];
+  }
+  __syncthreads();
+  if (kp != 0 || mytiles == 0) return;
+  for (int k2 = 1; k2 < kw; ++k2)
+#pragma unroll
+    for (int q = 0; q < RG; ++q) acc[q] += Red[((wave + k2) * RG + q) * 64 + lane];
+  store(0, acc);
 }
 
 // Sum of the split-K partials in slice order (deterministic), then the row
@@ -1271,9 +1344,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   const int64_t total = (int64_t)M * ncat;
   if (i >= total) return;
   const int row = (int)(i / ncat), cc = (int)(i - (int64_t)row * ncat), tile = cc >> 4;
-  const int m = (int)(tile >= mats.tile0[1]) + (int)(tile >= mats.tile0[2]) + (int)(tile >= mats.tile0[3]);
-  const int t0 = m == 0 ? 0 : m == 1 ? mats.tile0[1] : m == 2 ? mats.tile0[2] : mats.tile0[3];
-  const int nm = m == 0 ? mats.n[0] : m == 1 ? mats.n[1] : m == 2 ? mats.n[2] : mats.n[3];
+  const int st1 = sarg(mats.tile0[1]), st2 = sarg(mats.tile0[2]), st3 = sarg(mats.tile0[3]);
+  const int mn0 = sarg(mats.n[0]), mn1 = sarg(mats.n[1]), mn2 = sarg(mats.n[2]), mn3 = sarg(mats.n[3]);
+  const int m = (int)(tile >= st1) + (int)(tile >= st2) + (int)(tile >= st3);
+  const int t0 = m == 0 ? 0 : m == 1 ? st1 : m == 2 ? st2 : st3;
+  const int nm = m == 0 ? mn0 : m == 1 ? mn1 : m == 2 ? mn2 : mn3;
   const int col = (tile - t0) * 16 + (cc & 15);
   if (col >= nm) return;
   constexpr int kBatch = 8;
@@ -1286,8 +1361,11 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
     for (int d = 0; d < kBatch; ++d)
       if (z0 + d < ksplit) acc += v[d];
   }
-  float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
-  const float *bm = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
+  float *const y0 = sarg(mats.y[0]), *const y1 = sarg(mats.y[1]), *const y2 = sarg(mats.y[2]), *const y3 = sarg(mats.y[3]);
+  const float *const b0 = sarg(mats.bias[0]), *const b1 = sarg(mats.bias[1]), *const b2 = sarg(mats.bias[2]),
+              *const b3 = sarg(mats.bias[3]);
+  float *ym = m == 0 ? y0 : m == 1 ? y1 : m == 2 ? y2 : y3;
+  const float *bm = m == 0 ? b0 : m == 1 ? b1 : m == 2 ? b2 : b3;
   ym[(size_t)row * nm + col] = acc + (bm ? bm[col] : 0.0f);
 }
 
@@ -1305,7 +1383,7 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
 
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
-  p.dec_wgs_per_cu = 1;
+  p.kwaves = 1;
   // Q4_K, bf16 activations, M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
   // 64); otherwise 128 x 128 tiles (f32 activations need the second fp16
   // plane, which only fits the LDS budget at 128 rows; Q6_K stages its
@@ -1324,11 +1402,29 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
         1, std::min<int64_t>((kDecLdsBytes - (int64_t)M * 16 * 2 * 2) / per_sb,
                              (int64_t)kDecStage * kDecWaves * 64 / (M * 32)));
     const int64_t ntiles = (N + 15) / 16;
+    const int64_t ks_lds = (nsb + max_sb - 1) / max_sb;
+    // The whole K fits one workgroup's LDS, the rows one 16-row MFMA group,
+    // and the tiles fill no more than one round of 16-wave workgroups: keep
+    // K unsplit across workgroups (no
+    // partials, no reduction launch) and let kw waves share each tile, each
+    // taking every kw-th super-block; T = 16 / kw tiles per workgroup, with T
+    // the smallest power of two that puts at most one workgroup on each CU.
+    const int64_t per_wg = (ntiles + cu_count - 1) / cu_count;
+    if (ks_lds == 1 && per_wg < kDecWaves && M <= 16) {
+      int64_t T = 1;
+      while (T < per_wg) T *= 2;
+      while (kDecWaves / T > nsb) T *= 2;  // every wave needs at least one super-block
+      p.kwaves = (int)(kDecWaves / T);
+      p.groups = (int)((ntiles + T - 1) / T);
+      p.ksplit = 1;
+      p.off_lo = p.off_sums = p.off_rscale = p.off_part = 0;
+      p.workspace = 0;
+      return p;
+    }
     // one workgroup (16 waves) per CU: column groups of 16 tiles, at most one
     // per CU (waves then take several tiles), and as many K slices as fit in
     // one round of workgroups (at least what the LDS budget needs)
     p.groups = (int)std::min<int64_t>((ntiles + kDecWaves - 1) / kDecWaves, cu_count);
-    const int64_t ks_lds = (nsb + max_sb - 1) / max_sb;
     ks = std::min<int64_t>(nsb, std::max<int64_t>(ks_lds, cu_count / p.groups));
     // when the LDS split alone would need more than one round of workgroups,
     // fewer column groups (waves take more tiles) keep it to one round: each
@@ -1373,16 +1469,24 @@ static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t
                                 int ntiles, char *ws, const GemmPlan &plan, hipStream_t s) {
   const int m = (int)M, k = (int)K, ks = plan.ksplit;
   float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
-  const int nsbs_max = (int)((K / 256 + ks - 1) / ks);
-  const size_t lds = (size_t)M * (256 * nsbs_max + 8) * 2 * (x_is_bf16 ? 1 : 2) + (size_t)M * nsbs_max * 32 +
-                     (kDecMaxTiles * 256 + 2 * kDecRows + 1) * sizeof(float);
-  const dim3 grid((unsigned)(plan.groups * ks)), block(kDecWaves * 64);
-#define OKQ_DEC(F_, LO_, RG_)                                                                                   \
-  launch_timed(gemm_decode_kernel<F_, LO_, RG_>, grid, block, (unsigned)lds, s, x, mats, ntiles, m, k, ks,       \
-               plan.groups, part)
-#define OKQ_DEC_RG(F_, LO_)        \
-  if (M > 16) OKQ_DEC(F_, LO_, 2); \
-  else OKQ_DEC(F_, LO_, 1)
+  const int nsb = (int)(K / 256), sl_base = nsb / ks, sl_rem = nsb % ks;  // slice z: sl_base + (z < sl_rem)
+  const int nsbs_max = sl_base + (sl_rem > 0 ? 1 : 0);
+  int kw_shift = 0;
+  while ((1 << kw_shift) < plan.kwaves) ++kw_shift;
+  const bool split_w = plan.kwaves > 1;
+  const size_t lds = dec_tail_offset(m, 256 * nsbs_max + 8, nsbs_max, x_is_bf16 ? 1 : 2, split_w, M > 16 ? 2 : 1) +
+                     ((size_t)kDecMaxTiles * 256 + (size_t)nsbs_max * kDecRows) * sizeof(float);
+  if (lds > 160 * 1024 || (1 << kw_shift) != plan.kwaves || kDecWaves % plan.kwaves != 0 ||
+      (split_w && (ks != 1 || M > 16)))
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)plan.groups, (unsigned)ks), block(kDecWaves * 64);
+#define OKQ_DEC(F_, LO_, RG_, W_)                                                                               \
+  launch_timed(gemm_decode_kernel<F_, LO_, RG_, W_>, grid, block, (unsigned)lds, s, x, mats, ntiles, m, k,       \
+               sl_base, sl_rem, kw_shift, part)
+#define OKQ_DEC_RG(F_, LO_)                 \
+  if (M > 16) OKQ_DEC(F_, LO_, 2, false);   \
+  else if (split_w) OKQ_DEC(F_, LO_, 1, true); \
+  else OKQ_DEC(F_, LO_, 1, false)
   if (type == kQ6_K) {
     if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
     else OKQ_DEC_RG(DecQ6K, true);

@@ -81,7 +81,7 @@ hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *o
 struct GemmPlan {
   int bm;              // 32: the decode-batch kernel (M <= 32), else the tile height
   int groups;          // decode-batch kernel: column groups per K slice
-  int dec_wgs_per_cu;  // decode-batch kernel: workgroups per CU aimed for
+  int kwaves;          // decode-batch kernel, unsplit K: waves that split a tile's K inside the workgroup
   int ksplit;
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };

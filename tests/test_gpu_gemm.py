@@ -138,6 +138,8 @@ DEC_CASES = [
     # (entry, rows, n, k): ragged N, every row count class, split and unsplit K
     ("okq_gemm", 1, 96, 256), ("okq_gemm", 2, 17, 512), ("okq_gemm", 5, 300, 1024),
     ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1000, 768), ("okq_gemm", 13, 4096, 14336),
+    # K unsplit across workgroups, 8 waves share each tile (2 tiles per workgroup)
+    ("okq_gemm", 6, 8000, 4096),
     ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm_bf16", 16, 520, 2048), ("okq_gemm_bf16", 7, 33, 256),
     # one super-block per row: K is never split, outputs and bias written directly
     ("okq_gemm", 3, 70001, 256), ("okq_gemm_bf16", 9, 65540, 256),
@@ -190,12 +192,13 @@ def test_gemm_decode_batch_q6k_matches_reference(torch, okq, orc, entry, rows, n
 
 
 def test_gemm_decode_batch_split_k_repeat(torch, okq, orc):
-    """The decode-batch kernel scales each K slice of a row by its own power
-    of two and writes unscaled split-K partials, which the reduction sums in
-    slice order.  Many back-to-back launches on one stream, alternating
-    between problems with different column-group and slice counts (and so
-    sharing the stream's workspace), must each give the same bits as the
-    first launch of that problem, and match the reference."""
+    """The decode-batch kernel either splits K across workgroups (partials in
+    the stream's workspace, summed in slice order by the reduction) or, when the
+    whole K fits one workgroup, splits it among the waves that share a tile
+    (summed through LDS in wave order).  Many back-to-back launches on one
+    stream, alternating between problems of both kinds and different column
+    group and slice counts, must each give the same bits as the first launch
+    of that problem, and match the reference."""
     cases = [(O.Q4_K, 8, 14336, 4096), (O.Q6_K, 5, 4096, 14336), (O.Q4_K, 24, 1000, 2048), (O.Q6_K, 2, 333, 1280)]
     stream = torch.cuda.current_stream().cuda_stream
     prepared = []
@@ -278,12 +281,13 @@ def test_gemm_wide_dynamic_range_rows(torch, okq, orc):
 
 
 def test_gemm_decode_batch_per_slice_scaling(torch, okq, orc):
-    """The decode-batch kernel scales each K slice of a row by its own power of
-    two (K split 16 ways here).  Checked: slices 2^60 apart in one row, rows
-    with all-zero slices, exact power-of-two homogeneity across slices, and
-    non-finite activations -- an inf or a NaN makes its own row non-finite and
-    leaves every other row bit-identical to a batch without it."""
-    rows, n, k = 6, 1000, 4096
+    """The decode-batch kernel scales each 256-wide super-block of a row by its
+    own power of two (and splits K 56 ways here).  Checked: halves 2^60 apart
+    in one row, rows with all-zero super-blocks, exact power-of-two
+    homogeneity, and non-finite activations -- an inf or a NaN makes its own
+    row non-finite and leaves every other row bit-identical to a batch
+    without it."""
+    rows, n, k = 6, 1000, 14336  # K split across workgroups (a 4096-long row fits one workgroup's LDS)
     wq = orc.quantize(O.Q4_K, orc.normal(95, n * k, 0.02))
     pa, pb = q4k_parts(orc, wq, n, k)
     x = orc.normal(96, rows * k, 1.0).reshape(rows, k)
