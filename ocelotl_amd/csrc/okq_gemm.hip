@@ -732,6 +732,13 @@ struct DecMats {
 
 typedef float f4 __attribute__((ext_vector_type(4)));
 
+// Workgroup barrier for LDS only: waits for this wave's LDS operations, not
+// for its vector-memory loads (loads issued ahead stay in flight across it).
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // gfx9 encoding: lgkmcnt(0), vmcnt and expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+}
+
 // Byte offset of the decode-batch kernel's small LDS arrays (bias, row scales,
 // row maxima): past the activation slice (planes of pitch P halves, per-32
 // sums) and, with an in-workgroup K split, past the partial tiles that reuse
@@ -749,6 +756,7 @@ __host__ __device__ constexpr size_t dec_tail_offset(int M, int P, int nsbs, int
 // first activation, `xs` at the row's xsum pairs of the super-block.
 struct DecQ4K {
   static constexpr uint32_t kBlk = kQ4KBytes;
+  static constexpr bool kSums = true;  // the min term contracts the per-32 activation sums
   // items in flight per wave: 4 with one 16-row group (the Llama shapes give
   // a wave 4 items, so all are issued at once), 3 with two (register budget)
   static constexpr int kDepth = 3, kDepth1 = 4;
@@ -825,6 +833,7 @@ struct DecQ4K {
 
 struct DecQ6K {
   static constexpr uint32_t kBlk = kQ6KBytes;
+  static constexpr bool kSums = false;
   static constexpr int kDepth = 2, kDepth1 = 2;
   // Slice t = (half hh = t >> 2, quarter qq = t & 3); lane group g covers
   // l = 8g .. 8g + 7 of it: k = 128hh + 32qq + 8g + [0, 8), i.e. ql bytes
@@ -921,6 +930,7 @@ struct DecQ6K {
 // B planes (q8_4), so the item needs no scaling afterwards.
 struct DecQ80 {
   static constexpr uint32_t kBlk = 8 * kQ8Bytes;
+  static constexpr bool kSums = false;
   static constexpr int kDepth = 2, kDepth1 = 3;
   struct Item {
     u32x4 w0, w1, w2, w3;
@@ -1128,13 +1138,13 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   // fence) puts every activation load of the workgroup ahead of every weight
   // load, so no wave's activations queue behind another wave's weights.
   __builtin_amdgcn_s_barrier();
-  // The weights wait for the staging: with the ring's D items in flight the
-  // CU's vector-memory queue fills and waves stall at issue, so the staging
-  // barriers waited for weight traffic (measured 8-14 us; with one item in
-  // flight 3-6 us).  Issuing them all after the staging is fastest overall
-  // (a wave's first item before the staging measured no better, even for the
-  // head's long streams).
+  // With one 16-row group the weights go out once the wave's first
+  // activations have arrived (after its first piece below), so that the rest
+  // of the conversion overlaps their latency; issued before that, they delay
+  // the activations themselves.  The staging's closing barrier waits for LDS
+  // only, not for these loads.
   Item S[D];
+  int l_ti = 0, l_jj = 0;  // the next item to load
   if (lane < 16) {
 #pragma unroll
     for (int ti = 0; ti < kDecMaxTiles; ++ti) Bs[ti * 256 + wave * 16 + lane] = __uint_as_float(bbits[ti]);
@@ -1178,29 +1188,35 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
     const float amax = lane < 32 ? h0 : h1;
     const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
     // hi = fp16 of w rounded toward zero, two values per v_cvt_pkrtz; w - hi
-    // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16, so
-    // hi + lo = w to 2^-20 relative.  Sums: the 8 values of a piece in order,
-    // then the 4 pieces of a run (4 consecutive lanes) through DPP.
+    // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16 (rounded to
+    // nearest once), so hi + lo = w to 2^-21 relative.  Sums (Q4_K): the 8
+    // values of a piece in order, then the 4 pieces of a run (4 consecutive
+    // lanes) through DPP.
     h8 hv, lv;
     float t = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e += 2) {
       const float w0 = ldexpf(v[e], -sx), w1 = ldexpf(v[e + 1], -sx);
-      t += w0;
-      t += w1;
+      if (F::kSums) {
+        t += w0;
+        t += w1;
+      }
       const auto h = __builtin_amdgcn_cvt_pkrtz(w0, w1);
-      const auto l = __builtin_amdgcn_cvt_pkrtz(w0 - (float)h[0], w1 - (float)h[1]);
       hv[e] = (_Float16)h[0];
       hv[e + 1] = (_Float16)h[1];
-      lv[e] = (_Float16)l[0];
-      lv[e + 1] = (_Float16)l[1];
+      if (kLo) {
+        lv[e] = (_Float16)__builtin_fmaf(w0, 1.0f, -(float)h[0]);
+        lv[e + 1] = (_Float16)__builtin_fmaf(w1, 1.0f, -(float)h[1]);
+      }
     }
-    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-    t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    if (F::kSums) {
+      t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
+      t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+    }
     if (r < M) {
       *reinterpret_cast<h8 *>(Ah + (size_t)r * P + 8 * c) = hv;
       if (kLo) *reinterpret_cast<h8 *>(Al + (size_t)r * P + 8 * c) = lv;
-      if ((c & 3) == 0) {
+      if (F::kSums && (c & 3) == 0) {
         const _Float16 sh = (_Float16)t;
         h2 pair;
         pair[0] = sh;
@@ -1209,13 +1225,23 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
       }
       if ((c & 31) == 0) Rsb[(c >> 5) * kDecRows + r] = ldexpf(1.0f, sx);
     }
-  }
-  __syncthreads();
-  int l_ti = 0, l_jj = 0;  // the next item to load
+    if (RG == 1 && i == 0) {  // (two 16-row groups: registers allow the items only after the staging)
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int j = 0; j < D; ++j) {
-    load(S[j], l_ti, l_jj);
-    advance(l_ti, l_jj);
+      for (int j = 0; j < D; ++j) {
+        load(S[j], l_ti, l_jj);
+        advance(l_ti, l_jj);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  lds_barrier();
+  if constexpr (RG != 1) {
+#pragma unroll
+    for (int j = 0; j < D; ++j) {
+      load(S[j], l_ti, l_jj);
+      advance(l_ti, l_jj);
+    }
   }
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
