@@ -143,6 +143,9 @@ DEC_CASES = [
     ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm_bf16", 16, 520, 2048), ("okq_gemm_bf16", 7, 33, 256),
     # one super-block per row: K is never split, outputs and bias written directly
     ("okq_gemm", 3, 70001, 256), ("okq_gemm_bf16", 9, 65540, 256),
+    # more column tiles than 256 CUs x 16 waves x 4 staged biases: more column groups keep every wave
+    # within its staged bias tiles
+    ("okq_gemm", 8, 270000, 256),
     # 17-32 rows: two 16-row MFMA groups share each B fragment
     ("okq_gemm", 17, 300, 1024), ("okq_gemm", 32, 4096, 4096), ("okq_gemm_bf16", 25, 1000, 768),
     ("okq_gemm", 32, 14336, 4096),
