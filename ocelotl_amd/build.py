@@ -26,7 +26,10 @@ COMMON = [
 # Per-file extra flags.  okq_prep.hip holds the bit-exact dequant/quantize
 # kernels, okq_gemv.hip writes its FMAs out so that every instantiation rounds
 # alike: no FMA contraction in either.
-EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=off"]}
+EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=off"],
+         # MFMA accumulators in VGPRs where they fit: the per-super-block sums
+         # then feed the f32 scaling without AGPR round trips
+         "okq_gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

@@ -161,4 +161,16 @@ __device__ __forceinline__ void q4k_scale_min(uint32_t j, uint32_t s0, uint32_t 
   }
 }
 
+// Q4_K (scale, min) of sub-block j (any lane-dependent j < 8) without
+// branches: for j < 4 both are 6-bit fields of bytes 0-7; for j >= 4 a 4-bit
+// field of bytes 8-11 plus two high bits from bytes 0-7 (GGUF layout).
+__device__ __forceinline__ void q4k_scale_min_sel(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
+                                                  uint32_t &m) {
+  const bool lowj = j < 4;
+  const uint32_t jj = j & 3u;
+  const uint32_t width = lowj ? 6u : 4u, himask = lowj ? 0u : 0x30u, mo = lowj ? 0u : 4u;
+  sc = __builtin_amdgcn_ubfe(lowj ? s0 : s2, 8 * jj, width) | ((__builtin_amdgcn_ubfe(s0, 8 * jj + 6, 2) << 4) & himask);
+  m = __builtin_amdgcn_ubfe(lowj ? s1 : s2, 8 * jj + mo, width) | ((__builtin_amdgcn_ubfe(s1, 8 * jj + 6, 2) << 4) & himask);
+}
+
 }  // namespace okq

@@ -700,18 +700,6 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
 // cover k = 64g + 32(t & 1) + 8(t >> 1) + [0, 8), i.e. nibble plane t & 1 of
 // bytes 8(t >> 1) .. + 8 of qs chunk g -- a lane group reads only its own
 // 32-byte chunk (and the header) of each block.
-// Q4_K (scale, min) of sub-block j (any lane-dependent j < 8) without
-// branches: for j < 4 both are 6-bit fields of bytes 0-7; for j >= 4 a 4-bit
-// field of bytes 8-11 plus two high bits from bytes 0-7 (GGUF layout).
-__device__ __forceinline__ void q4k_scale_min_sel(uint32_t j, uint32_t s0, uint32_t s1, uint32_t s2, uint32_t &sc,
-                                                  uint32_t &m) {
-  const bool lowj = j < 4;
-  const uint32_t jj = j & 3u;
-  const uint32_t width = lowj ? 6u : 4u, himask = lowj ? 0u : 0x30u, mo = lowj ? 0u : 4u;
-  sc = __builtin_amdgcn_ubfe(lowj ? s0 : s2, 8 * jj, width) | ((__builtin_amdgcn_ubfe(s0, 8 * jj + 6, 2) << 4) & himask);
-  m = __builtin_amdgcn_ubfe(lowj ? s1 : s2, 8 * jj + mo, width) | ((__builtin_amdgcn_ubfe(s1, 8 * jj + 6, 2) << 4) & himask);
-}
-
 constexpr int kDecRows = kGemmDecodeRows;  // two 16-row MFMA groups share each B fragment above 16 rows
 constexpr int kDecWaves = 16;
 constexpr int64_t kDecLdsBytes = 144 * 1024;  // activations of a slice (one workgroup per CU fills its registers)
@@ -1410,10 +1398,12 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
   p.kwaves = 1;
-  // Q4_K, bf16 activations, M > 128: 256 x 128 tiles (8 waves, 4 x 2 of 64 x
-  // 64); otherwise 128 x 128 tiles (f32 activations need the second fp16
-  // plane, which only fits the LDS budget at 128 rows; Q6_K stages its
-  // larger raw windows in the 4-wave tile's register budget).
+  // More than 32 rows: Q4_K with bf16 activations takes gemm_wide_q4k_kernel
+  // (okq_gemm_wide.hip); the tiled kernel takes the rest with 128 x 128 tiles
+  // (f32 activations need the second fp16 plane, which only fits the LDS
+  // budget at 128 rows; Q6_K stages its larger raw windows in the 4-wave
+  // tile's register budget), or 256 x 128 tiles for bf16 Q4_K shapes beyond
+  // the wide kernel's 32-bit offsets.
   const int64_t nsb = K / 256;
   int64_t ks = 1;
   if (M <= kDecRows) {
@@ -1466,8 +1456,11 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     if (ks == 1 && mytiles > kDecMaxTiles)
       p.groups = (int)((ntiles + (int64_t)kDecWaves * kDecMaxTiles - 1) / ((int64_t)kDecWaves * kDecMaxTiles));
   } else {
-    p.bm = (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
-    const int64_t tiles = ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
+    // Q4_K with bf16 activations: the kernel that dequantises the weights in
+    // registers (128 x 256 tiles); everything else: the tiled kernel
+    p.wide = x_is_bf16 && gemm_wide_supported(type, M, K, N) ? 1 : 0;
+    p.bm = p.wide ? 128 : (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
+    const int64_t tiles = p.wide ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
     // Split K when the tiles alone leave CUs idle: enough slices for about
     // one workgroup per CU, at least two super-blocks per slice, at most 8.
     if (tiles * 4 < (int64_t)cu_count * 3) ks = std::min<int64_t>({(cu_count + tiles - 1) / tiles, nsb / 2, 8});
@@ -1556,13 +1549,44 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
   return launch_decode(type, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
 }
 
+// The tiled kernel over the pre-pass's planes (every format; f32 or bf16).
+static hipError_t launch_gemm_tiled(int type, bool x_is_bf16, _Float16 *xhi, _Float16 *xlo, h2 *xsum, float *rscale,
+                                    const uint8_t *W, const float *bias, float *y, int64_t M, int64_t N, int64_t K,
+                                    const GemmPlan &plan, float *part, hipStream_t s) {
+  const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
+  const int tiles_n = (int)((N + kBN - 1) / kBN);
+  const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);
+  const int tiles = tiles_m * tiles_n;
+  const int per_xcd = (tiles * ks + 7) / 8;
+  const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(plan.bm * 2));
+#define OKQ_GEMM(BM_, LO_, FMT_)                                                                                   \
+  launch_timed(gemm_kq_kernel<BM_, LO_, FMT_>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k,     \
+               tiles_m, tiles, ks, part)
+  if (type == kQ6_K) {
+    if (x_is_bf16) OKQ_GEMM(128, false, kQ6_K);
+    else OKQ_GEMM(128, true, kQ6_K);
+  } else if (type == kQ8_0) {
+    if (x_is_bf16) OKQ_GEMM(128, false, kQ8_0);
+    else OKQ_GEMM(128, true, kQ8_0);
+  } else if (plan.bm == 256) {
+    OKQ_GEMM(256, false, kQ4_K);
+  } else if (x_is_bf16) {
+    OKQ_GEMM(128, false, kQ4_K);
+  } else {
+    OKQ_GEMM(128, true, kQ4_K);
+  }
+#undef OKQ_GEMM
+  return hipGetLastError();
+}
+
+
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
   if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
   if (type != kQ4_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
   const uint8_t *W = static_cast<const uint8_t *>(w);
-  const int m = (int)M, n = (int)N, k = (int)K, ks = plan.ksplit;
+  const int m = (int)M, n = (int)N, ks = plan.ksplit;
   if (plan.bm == kDecRows) {
     if (M > kDecRows) return hipErrorInvalidValue;
     DecMats mats{};
@@ -1597,29 +1621,11 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
 #undef OKQ_PREP
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const int tiles_n = (int)((N + kBN - 1) / kBN);
-  const int tiles_m = (int)((M + plan.bm - 1) / plan.bm);
-  const int tiles = tiles_m * tiles_n;
-  const int per_xcd = (tiles * ks + 7) / 8;
-  const dim3 grid((unsigned)(per_xcd * 8)), block((unsigned)(plan.bm * 2));
-#define OKQ_GEMM(BM_, LO_, FMT_)                                                                                   \
-  launch_timed(gemm_kq_kernel<BM_, LO_, FMT_>, grid, block, 0u, s, xhi, xlo, xsum, rscale, W, bias, y, m, n, k,     \
-               tiles_m, tiles, ks, part)
-  if (type == kQ6_K) {
-    if (x_is_bf16) OKQ_GEMM(128, false, kQ6_K);
-    else OKQ_GEMM(128, true, kQ6_K);
-  } else if (type == kQ8_0) {
-    if (x_is_bf16) OKQ_GEMM(128, false, kQ8_0);
-    else OKQ_GEMM(128, true, kQ8_0);
-  } else if (plan.bm == 256) {
-    OKQ_GEMM(256, false, kQ4_K);
-  } else if (x_is_bf16) {
-    OKQ_GEMM(128, false, kQ4_K);
+  if (plan.wide) {
+    e = launch_gemm_wide(xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
   } else {
-    OKQ_GEMM(128, true, kQ4_K);
+    e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);
   }
-#undef OKQ_GEMM
-  e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   const int64_t total = M * N;
   hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m, n,

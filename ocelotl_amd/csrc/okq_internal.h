@@ -83,6 +83,7 @@ struct GemmPlan {
   int groups;          // decode-batch kernel: column groups per K slice
   int kwaves;          // decode-batch kernel, unsplit K: waves that split a tile's K inside the workgroup
   int ksplit;
+  int wide;            // 1: gemm_wide_q4k_kernel (128 x 256 tiles, weights dequantised in registers)
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
@@ -102,5 +103,14 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
 // True when launch_gemm supports this (type, M, K, N): Q4_K, Q6_K and Q8_0
 // with K a multiple of 256.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);
+
+// The Q4_K prefill kernel with register-dequantised weights (okq_gemm_wide.hip)
+// over the pre-pass's planes: its shape limits, its 128 x 256 tile count, and
+// its launch (ksplit > 1: raw partials [ksplit][M][N] for splitk_reduce_kernel).
+bool gemm_wide_supported(int type, int64_t M, int64_t K, int64_t N);
+int gemm_wide_tiles(int64_t M, int64_t N);
+hipError_t launch_gemm_wide(const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
+                            const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
+                            hipStream_t s);
 
 }  // namespace okq

@@ -495,3 +495,44 @@ def test_linear_dispatch_takes_the_q8_0_gemm_above_eight_rows(torch, okq, orc):
             pin = run(torch, okq, pinned, O.Q8_0, x, rows, k, wq, n)
             assert np.array_equal(auto.view(np.uint32), pin.view(np.uint32)), (n, rows)
             check_rows(orc, O.Q8_0, auto, x, rows, k, wq, n, None, 2)
+
+
+# ---- Q4_K prefill with bf16 activations: weights dequantised in registers --------
+# gemm_wide_q4k_kernel: 128 x 256 tiles, each weight column owned by one wave,
+# the min term contracted exactly (dmin * m as two fp16 planes), split-K when
+# the tiles leave CUs idle.
+
+WIDE_CASES = [
+    # (rows, n, k): ragged M and N (partial tiles, columns past N), one
+    # super-block, split K (few tiles), a long K, several M-tiles per N-tile
+    (33, 257, 256), (129, 300, 1024), (100, 4096, 4096), (256, 1000, 14336), (300, 520, 2048),
+    (512, 1024, 4096), (777, 2100, 768),
+]
+
+
+@pytest.mark.parametrize("rows,n,k", WIDE_CASES)
+def test_gemm_wide_q4k_bf16_matches_reference(torch, okq, orc, rows, n, k):
+    print(f"[gpu] gemm wide bf16 Q4_K M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q4_K, orc.normal(2100 + n + k, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 2101 + rows, rows, k)
+    bias = orc.normal(2102, n, 0.1)
+    got = run(torch, okq, "okq_gemm_bf16", O.Q4_K, xb, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q4_K, got, x32, rows, k, wq, n, bias, None if rows * n * k <= 4e8 else 16)
+
+
+def test_gemm_wide_one_hot_columns_are_exact(torch, okq, orc):
+    """x = e_j (40 rows, bf16) returns the dequantised weights bit for bit:
+    d * (sc * q) + (-(dmin * m))_hi + (-(dmin * m))_lo is the reference's
+    d * sc * q - dmin * m when every product is exact, which the one-hot
+    column makes the case (a single nonzero activation per row)."""
+    n, k = 300, 1024
+    wq = orc.quantize(O.Q4_K, orc.normal(2110, n * k, 0.02))
+    w = orc.dequantize(O.Q4_K, wq, n * k).reshape(n, k)
+    cols = np.array([0, 1, 7, 31, 32, 63, 64, 100, 127, 128, 200, 255, 256, 257, 300, 383, 384, 500, 511, 512,
+                     600, 640, 700, 767, 768, 800, 900, 959, 960, 1000, 1010, 1015, 1016, 1017, 1020, 1021, 1022,
+                     1023, 2, 3])
+    x = np.zeros((cols.size, k), np.float32)
+    x[np.arange(cols.size), cols] = 1.0
+    got = run(torch, okq, "okq_gemm_bf16", O.Q4_K, orc.f32_to_bf16(x.reshape(-1)), cols.size, k, wq, n)
+    assert np.array_equal(got, w[:, cols].T)
