@@ -470,8 +470,9 @@ C5_HEAD = (Q6K, 128256, 4096)
 def run_c5(ctx: Ctx, args):
     """One step = every projection of 32 layers plus the Q6_K head, back to
     back on one stream, replayed from a HIP graph.  `grouped`: the launches
-    an engine issues (q+k and gate+up share x in okq_gemv_multi, the other
-    projections through okq_linear_out_by_in_q); `auto`: one
+    an engine issues (q, k and v share x in okq_linear_multi_q -- Q4_K and
+    Q6_K matrices in one launch at batch sizes -- gate+up in okq_gemv_multi,
+    o and down through okq_linear_out_by_in_q); `auto`: one
     okq_linear_out_by_in_q per projection.  Both dispatches pick the kernel
     by shape: the streaming decode-batch MFMA kernel for weights from 2 MB at
     6-8 rows (from 8 MB at 5 rows, down projections and the head from 3
@@ -507,11 +508,20 @@ def run_c5(ctx: Ctx, args):
                          (ctypes.c_int64 * c)(*[shape[m][1] for m in names]), None,
                          (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), s)
 
+        def qkv(lay, s):
+            names = ["q", "k", "v"]
+            c = len(names)
+            ctx.okq.call("okq_linear_multi_q", x4.data_ptr(), rows, 4096, c,
+                         (ctypes.c_uint32 * c)(*[shape[m][0] for m in names]),
+                         (ctypes.c_void_p * c)(*[lay[m].data_ptr() for m in names]),
+                         (ctypes.c_uint64 * c)(*[lay[m].numel() for m in names]),
+                         (ctypes.c_int64 * c)(*[shape[m][1] for m in names]), None,
+                         (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), s)
+
         def step(mode, s):
             for lay in layers:
                 if mode == "grouped":
-                    group(["q", "k"], lay, s)
-                    one("okq_linear_out_by_in_q", "v", lay["v"], s)
+                    qkv(lay, s)
                     one("okq_linear_out_by_in_q", "o", lay["o"], s)
                     group(["gate", "up"], lay, s)
                     one("okq_linear_out_by_in_q", "down", lay["down"], s)

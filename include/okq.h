@@ -203,6 +203,18 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
                           const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
                           const float *const *bias, float *const *out, void *stream);
 
+/* okq_gemv_multi for matrices of different formats: w_types[i] is matrix i's
+ * GGML type (the layers of a Q4_K_M model store q/k in Q4_K and v in Q6_K).
+ * Matrices of one format are grouped as okq_gemv_multi groups them; at
+ * decode-batch row counts (up to 32) the Q4_K and Q6_K matrices that
+ * okq_linear_out_by_in_q gives to the MFMA kernels share one decode-batch
+ * launch, whose outputs agree with each matrix's own call within the
+ * reference rule.  Validation and errors as okq_gemv_multi.  No counterpart in
+ * the reference (its callers compute q, k and v one linear at a time). */
+okq_status okq_linear_multi_q(const float *x, int64_t rows, int64_t in_features, int count, const uint32_t *w_types,
+                              const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
+                              const float *const *bias, float *const *out, void *stream);
+
 /* ---- instrumentation --------------------------------------------------- */
 
 /* ---- neighbours of the projections ------------------------------------ */

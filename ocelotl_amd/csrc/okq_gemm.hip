@@ -1004,25 +1004,22 @@ struct DecQ80 {
 // the grid is (column group, K slice), the host passes the slice partition
 // (slice z holds base + (z < rem) super-blocks) and the power of two kw as a
 // shift, and the ring walks its items with counters instead of divisions.
+// The body of one decode-batch workgroup for format F: column group grp of
+// `groups` over the tiles [tbase, tbase + ntl) of the launch (one format's
+// tiles; `ntiles` counts every tile of the launch, the partials' width).
 template <class F, bool kLo, int RG, bool kW>
-__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void *__restrict__ X_arg, DecMats mats,
-                                                                     int ntiles_arg, int M_arg, int K_arg,
-                                                                     int sl_base_arg, int sl_rem_arg,
-                                                                     int kw_shift_arg, float *__restrict__ part_arg) {
-  // every argument in scalar registers up front (one batch of argument loads)
-  const void *const X = sarg(X_arg);
-  float *const part = sarg(part_arg);
-  const int ntiles = sarg(ntiles_arg), M = sarg(M_arg), K = sarg(K_arg);
-  const int sl_base = sarg(sl_base_arg), sl_rem = sarg(sl_rem_arg);
+__device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMats &mats, int ntiles, int M, int K,
+                                        int sl_base, int sl_rem, int kw_shift_arg, float *__restrict__ part,
+                                        int grp, int groups, int tbase, int ntl) {
   // kW: an in-workgroup K split (unsplit K across workgroups, one 16-row group)
-  const int kw_shift = kW ? sarg(kw_shift_arg) : 0, kw = 1 << kw_shift;
-  const int ksplit = (int)gridDim.y, groups = (int)gridDim.x;
+  const int kw_shift = kW ? kw_shift_arg : 0, kw = 1 << kw_shift;
+  const int ksplit = (int)gridDim.y;
   constexpr int D = RG == 1 ? F::kDepth1 : F::kDepth;
   extern __shared__ __align__(16) unsigned char dsm[];
   constexpr int nt = kDecWaves * 64;
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = (int)blockIdx.x, z = (int)blockIdx.y;
+  const int z = (int)blockIdx.y;
   const int nsb_all = (int)((uint32_t)K >> 8);
   const int sb0 = z * sl_base + (z < sl_rem ? z : sl_rem);
   const int nsbs = sl_base + (z < sl_rem ? 1 : 0);
@@ -1043,7 +1040,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   //    (ti * groups + grp) * T + ts, and wave kp of the slot takes the slice's
   //    super-blocks kp, kp + kw, ... (kw > 1 only with unsplit K: the slot's
   //    waves then sum their partial tiles through LDS at the end).  Item
-  //    (ti, jj) is round ti's super-block kp + kw jj, jj < cnt.
+  //    (ti, jj) is round ti's super-block kp + kw jj, jj < cnt.  Tile numbers
+  //    are local to the workgroup's format (tiles [tbase, tbase + ntl) of the
+  //    launch); gtile() gives the launch's tile number (matrix, partials).
   // (all wave-uniform: readfirstlane keeps them, and the matrix selects and
   // weight descriptors built from them, in scalar registers -- a descriptor
   // the compiler takes for divergent costs a waterfall loop per load)
@@ -1052,7 +1051,9 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   const int first = __builtin_amdgcn_readfirstlane(grp * T + ts);
   const int cnt = __builtin_amdgcn_readfirstlane(nsbs > kp ? (nsbs - kp + kw - 1) >> kw_shift : 0);  // items per tile
   const int mytiles =
-      __builtin_amdgcn_readfirstlane(first < ntiles && cnt > 0 ? (ntiles - first + stride - 1) / stride : 0);
+      __builtin_amdgcn_readfirstlane(first < ntl && cnt > 0 ? (ntl - first + stride - 1) / stride : 0);
+  // a local tile's launch tile (tiles past the end: the format's last one)
+  auto gtile = [&](int t) { return tbase + (t < ntl ? t : ntl - 1); };
   const int nitems = mytiles * cnt;
   const int cn = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
@@ -1083,11 +1084,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   };
   auto load = [&](Item &it, int ti, int jj) {
     const int sbl = kp + (jj << kw_shift);
-    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
+    const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
     const uint32_t w_end = (uint32_t)((size_t)n_of(m) * row_bytes);
     // rows past the matrix (and tiles past the end) read past the tensor: zeros
     const uint32_t n = (uint32_t)((tile - tile0_of(m)) * 16 + cn);
-    F::load(it, rw_of(m), tile < ntiles ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
+    F::load(it, rw_of(m), lt < ntl ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
   };
   // 2. the activations of the slice: this thread's pieces of 8 consecutive
   //    activations of one row (at most kDecStage; pieces past the last row
@@ -1115,11 +1116,11 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   uint32_t bbits[kDecMaxTiles];
 #pragma unroll
   for (int ti = 0; ti < kDecMaxTiles; ++ti) {
-    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
+    const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
     const float *bp = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
     const uint32_t bias_end = bp ? (uint32_t)n_of(m) * 4u : 0u;
     const int col = (tile - tile0_of(m)) * 16 + lane;
-    const bool in = ksplit == 1 && lane < 16 && tile < ntiles && col < n_of(m);
+    const bool in = ksplit == 1 && lane < 16 && lt < ntl && col < n_of(m);
     bbits[ti] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(bp, bias_end), in ? (uint32_t)col * 4u : bias_end, 0, 0);
   }
   // A CU returns vector loads in issue order: this bare barrier (no memory
@@ -1175,26 +1176,34 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
                            as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 48)));
     const float amax = lane < 32 ? h0 : h1;
     const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
-    // hi = fp16 of w rounded toward zero, two values per v_cvt_pkrtz; w - hi
-    // is exact in f32 (hi is w cut to 11 bits), and lo = its fp16 (rounded to
-    // nearest once), so hi + lo = w to 2^-21 relative.  Sums (Q4_K): the 8
-    // values of a piece in order, then the 4 pieces of a run (4 consecutive
-    // lanes) through DPP.
+    // hi = fp16 of w = x * 2^-sx rounded to nearest, lo = fp16 of the exact
+    // residue w - hi (rounded to nearest once), so hi + lo = w to 2^-22
+    // relative.  Sums (Q4_K): the 8 values of a piece in order, then the 4
+    // pieces of a run (4 consecutive lanes) through DPP.  Fast path (every
+    // block of the wave has |sx| <= 100, so 2^-sx is a normal f32 and the raw
+    // values and their sums stay far from overflow): one v_fma_mix per fp16
+    // value, and the sum taken on the raw values and then scaled (a power of
+    // two, exact).  Otherwise v_ldexp on every value.
     h8 hv, lv;
     float t = 0.0f;
+    if (__builtin_amdgcn_ballot_w64(sx < -100 || sx > 100) == 0) {
+      const float sc = ldexpf(1.0f, -sx);
 #pragma unroll
-    for (int e = 0; e < 8; e += 2) {
-      const float w0 = ldexpf(v[e], -sx), w1 = ldexpf(v[e + 1], -sx);
-      if (F::kSums) {
-        t += w0;
-        t += w1;
+      for (int e = 0; e < 8; ++e) {
+        if (F::kSums) t += v[e];
+        const _Float16 h = (_Float16)(v[e] * sc);
+        hv[e] = h;
+        if (kLo) lv[e] = (_Float16)__builtin_fmaf(v[e], sc, -(float)h);
       }
-      const auto h = __builtin_amdgcn_cvt_pkrtz(w0, w1);
-      hv[e] = (_Float16)h[0];
-      hv[e + 1] = (_Float16)h[1];
-      if (kLo) {
-        lv[e] = (_Float16)__builtin_fmaf(w0, 1.0f, -(float)h[0]);
-        lv[e + 1] = (_Float16)__builtin_fmaf(w1, 1.0f, -(float)h[1]);
+      if (F::kSums) t *= sc;
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float w = ldexpf(v[e], -sx);
+        if (F::kSums) t += w;
+        const _Float16 h = (_Float16)w;
+        hv[e] = h;
+        if (kLo) lv[e] = (_Float16)(w - (float)h);
       }
     }
     if (F::kSums) {
@@ -1244,7 +1253,7 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
   // a finished tile (round ti of this wave's slot): scaled back by the rows'
   // 2^s, plus the bias (unsplit K), or the raw partial of slice z
   auto store = [&](int ti, const f4 *vals) {
-    const int tile = __builtin_amdgcn_readfirstlane(ti * stride + first), m = mat_of(tile);
+    const int tile = gtile(__builtin_amdgcn_readfirstlane(ti * stride + first)), m = mat_of(tile);
     const int nm = n_of(m), col = (tile - tile0_of(m)) * 16 + cn;
     const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
     // unsplit: the matrix's own output; split: the concatenated partials
@@ -1322,6 +1331,35 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
 #pragma unroll
     for (int q = 0; q < RG; ++q) acc[q] += Red[((wave + k2) * RG + q) * 64 + lane];
   store(0, acc);
+}
+
+// One format (F1 == F2: every workgroup) or two: workgroups below g_split run
+// F1 over the launch's first nt1 tiles (its first matrices), the rest run F2
+// over the others.  Both read the same activations; the split-K partials of
+// both go to one array over the concatenated tiles.
+template <class F1, class F2, bool kLo, int RG, bool kW>
+__global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void *__restrict__ X_arg, DecMats mats,
+                                                                     int ntiles_arg, int M_arg, int K_arg,
+                                                                     int sl_base_arg, int sl_rem_arg,
+                                                                     int kw_shift_arg, float *__restrict__ part_arg,
+                                                                     int g_split_arg, int nt1_arg) {
+  // every argument in scalar registers up front (one batch of argument loads)
+  const void *const X = sarg(X_arg);
+  float *const part = sarg(part_arg);
+  const int ntiles = sarg(ntiles_arg), M = sarg(M_arg), K = sarg(K_arg);
+  const int sl_base = sarg(sl_base_arg), sl_rem = sarg(sl_rem_arg);
+  const int kw_shift = kW ? sarg(kw_shift_arg) : 0;
+  const int b = (int)blockIdx.x, groups = (int)gridDim.x;
+  if constexpr (std::is_same<F1, F2>::value) {
+    dec_run<F1, kLo, RG, kW>(X, mats, ntiles, M, K, sl_base, sl_rem, kw_shift, part, b, groups, 0, ntiles);
+  } else {
+    const int g_split = sarg(g_split_arg), nt1 = sarg(nt1_arg);
+    if (b < g_split)
+      dec_run<F1, kLo, RG, kW>(X, mats, ntiles, M, K, sl_base, sl_rem, kw_shift, part, b, g_split, 0, nt1);
+    else
+      dec_run<F2, kLo, RG, kW>(X, mats, ntiles, M, K, sl_base, sl_rem, kw_shift, part, b - g_split, groups - g_split,
+                               nt1, ntiles - nt1);
+  }
 }
 
 // Sum of the split-K partials in slice order (deterministic), then the row
@@ -1484,8 +1522,14 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
 
 // The decode-batch kernel (it converts the activations itself: no pre-pass)
 // and, when K is split, the reduction of its partials.
-static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const DecMats &mats,
-                                int ntiles, char *ws, const GemmPlan &plan, hipStream_t s) {
+// The decode-batch kernel (it converts the activations itself: no pre-pass)
+// and, when K is split, the reduction of its partials.  type2 != type: the
+// first nt1 tiles (matrices) are of format `type`, the rest of type2 (Q4_K
+// then Q6_K); the plan's column groups are shared out in proportion to the
+// two formats' tiles, each format's group keeping at most the plan's tiles
+// per wave.
+static hipError_t launch_decode(int type, int type2, int nt1, const void *x, bool x_is_bf16, int64_t M, int64_t K,
+                                const DecMats &mats, int ntiles, char *ws, const GemmPlan &plan, hipStream_t s) {
   const int m = (int)M, k = (int)K, ks = plan.ksplit;
   float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
   const int nsb = (int)(K / 256), sl_base = nsb / ks, sl_rem = nsb % ks;  // slice z: sl_base + (z < sl_rem)
@@ -1498,23 +1542,34 @@ static hipError_t launch_decode(int type, const void *x, bool x_is_bf16, int64_t
   if (lds > 160 * 1024 || (1 << kw_shift) != plan.kwaves || kDecWaves % plan.kwaves != 0 ||
       (split_w && (ks != 1 || M > 16)))
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)plan.groups, (unsigned)ks), block(kDecWaves * 64);
-#define OKQ_DEC(F_, LO_, RG_, W_)                                                                               \
-  launch_timed(gemm_decode_kernel<F_, LO_, RG_, W_>, grid, block, (unsigned)lds, s, x, mats, ntiles, m, k,       \
-               sl_base, sl_rem, kw_shift, part)
-#define OKQ_DEC_RG(F_, LO_)                 \
-  if (M > 16) OKQ_DEC(F_, LO_, 2, false);   \
-  else if (split_w) OKQ_DEC(F_, LO_, 1, true); \
-  else OKQ_DEC(F_, LO_, 1, false)
-  if (type == kQ6_K) {
-    if (x_is_bf16) OKQ_DEC_RG(DecQ6K, false);
-    else OKQ_DEC_RG(DecQ6K, true);
+  const bool mixed = type2 != type;
+  if (mixed && (type != kQ4_K || type2 != kQ6_K || nt1 < 1 || nt1 >= ntiles)) return hipErrorInvalidValue;
+  int g_split = plan.groups, groups = plan.groups;
+  if (mixed) {
+    auto share = [&](int64_t nt) { return (int)std::max<int64_t>(1, ((int64_t)plan.groups * nt + ntiles - 1) / ntiles); };
+    g_split = share(nt1);
+    groups = g_split + share(ntiles - nt1);
+  }
+  const dim3 grid((unsigned)groups, (unsigned)ks), block(kDecWaves * 64);
+#define OKQ_DEC(F1_, F2_, LO_, RG_, W_)                                                                          \
+  launch_timed(gemm_decode_kernel<F1_, F2_, LO_, RG_, W_>, grid, block, (unsigned)lds, s, x, mats, ntiles, m, k, \
+               sl_base, sl_rem, kw_shift, part, g_split, nt1)
+#define OKQ_DEC_RG(F1_, F2_, LO_)                 \
+  if (M > 16) OKQ_DEC(F1_, F2_, LO_, 2, false);   \
+  else if (split_w) OKQ_DEC(F1_, F2_, LO_, 1, true); \
+  else OKQ_DEC(F1_, F2_, LO_, 1, false)
+  if (mixed) {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ6K, false);
+    else OKQ_DEC_RG(DecQ4K, DecQ6K, true);
+  } else if (type == kQ6_K) {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ6K, DecQ6K, false);
+    else OKQ_DEC_RG(DecQ6K, DecQ6K, true);
   } else if (type == kQ8_0) {
-    if (x_is_bf16) OKQ_DEC_RG(DecQ80, false);
-    else OKQ_DEC_RG(DecQ80, true);
+    if (x_is_bf16) OKQ_DEC_RG(DecQ80, DecQ80, false);
+    else OKQ_DEC_RG(DecQ80, DecQ80, true);
   } else {
-    if (x_is_bf16) OKQ_DEC_RG(DecQ4K, false);
-    else OKQ_DEC_RG(DecQ4K, true);
+    if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ4K, false);
+    else OKQ_DEC_RG(DecQ4K, DecQ4K, true);
   }
 #undef OKQ_DEC_RG
 #undef OKQ_DEC
@@ -1546,7 +1601,34 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
       mats.tile0[i] = INT32_MAX;
     }
   }
-  return launch_decode(type, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
+  return launch_decode(type, type, tiles, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
+}
+
+hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, int64_t K, int count, const int *types,
+                                    const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
+                                    void *workspace, const GemmPlan &plan, hipStream_t s) {
+  if (plan.bm != kDecRows || M > kDecRows || count < 2 || count > kDecMats) return hipErrorInvalidValue;
+  DecMats mats{};
+  int tiles = 0, nt1 = 0;
+  // the Q4_K matrices first, then the Q6_K ones, at least one of each
+  if (types[0] != kQ4_K || types[count - 1] != kQ6_K) return hipErrorInvalidValue;
+  for (int i = 1; i < count; ++i)
+    if ((types[i] != kQ4_K && types[i] != kQ6_K) || (types[i - 1] == kQ6_K && types[i] != kQ6_K))
+      return hipErrorInvalidValue;
+  for (int i = 0; i < kDecMats; ++i) {
+    if (i < count) {
+      mats.w[i] = static_cast<const uint8_t *>(w[i]);
+      mats.bias[i] = bias[i];
+      mats.y[i] = y[i];
+      mats.n[i] = (int)N[i];
+      mats.tile0[i] = tiles;
+      tiles += (int)((N[i] + 15) / 16);
+      if (types[i] == kQ4_K) nt1 = tiles;
+    } else {
+      mats.tile0[i] = INT32_MAX;
+    }
+  }
+  return launch_decode(kQ4_K, kQ6_K, nt1, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
 }
 
 // The tiled kernel over the pre-pass's planes (every format; f32 or bf16).
@@ -1595,7 +1677,7 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     mats.y[0] = y;
     mats.n[0] = n;
     for (int i = 1; i < kDecMats; ++i) mats.tile0[i] = INT32_MAX;
-    return launch_decode(type, x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s);
+    return launch_decode(type, type, (int)((N + 15) / 16), x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s);
   }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);

@@ -100,6 +100,14 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
                                     void *workspace, const GemmPlan &plan, hipStream_t s);
 
+// Q4_K and Q6_K matrices that read the same activations in one decode-batch
+// launch: types[] lists the Q4_K matrices first, then the Q6_K ones (at least
+// one of each, count <= kDecMats); the plan is gemm_plan's for their combined
+// tile columns.  Each workgroup runs one format; one split-K reduction.
+hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, int64_t K, int count, const int *types,
+                                    const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
+                                    void *workspace, const GemmPlan &plan, hipStream_t s);
+
 // True when launch_gemm supports this (type, M, K, N): Q4_K, Q6_K and Q8_0
 // with K a multiple of 256.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);

@@ -659,6 +659,100 @@ okq_status okq_gemv_multi(const float *x, int64_t rows, int64_t in_features, uin
   return grouped_linear(x, rows, in_features, w_type, count, w, w_bytes, out_features, b, out, stream, dev, info);
 }
 
+// Projections of mixed formats that read the same activations (q/k in Q4_K
+// and v in Q6_K in a Q4_K_M layer).  The Q4_K and Q6_K matrices that the
+// linear dispatch gives to the MFMA kernels share one decode-batch launch at
+// up to 32 rows (workgroups of either format, one activation staging per
+// workgroup, one reduction); everything else runs through okq_gemv_multi's
+// grouping, one format at a time.
+okq_status okq_linear_multi_q(const float *x, int64_t rows, int64_t in_features, int count, const uint32_t *w_types,
+                              const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
+                              const float *const *bias, float *const *out, void *stream) {
+  if (count < 1 || count > okq::kGemvMaxProblems)
+    return fail(OKQ_E_ARG, "linear_multi count=%d must be between 1 and %d", count, okq::kGemvMaxProblems);
+  if (!w_types || !w || !w_bytes || !out_features || !out) return fail(OKQ_E_ARG, "linear_multi null argument array");
+  bool any = false;
+  for (int i = 0; i < count; ++i) {
+    LinearArgs a{rows, in_features, out_features[i], w_types[i], w_bytes[i]};
+    okq_status st = validate_linear(x, a, w[i], out[i], false);
+    if (st != OKQ_OK) {
+      char msg[512];
+      snprintf(msg, sizeof msg, "%s", g_last_error.c_str());
+      return fail(st, "linear_multi matrix %d: %s", i, msg);
+    }
+    any = any || (rows > 0 && out_features[i] > 0);
+  }
+  if (!any) return ok();
+  int dev;
+  DevInfo info;
+  okq_status st = current_device(dev, info);
+  if (st != OKQ_OK) return st;
+  const float *nobias[okq::kGemvMaxProblems] = {nullptr, nullptr, nullptr, nullptr};
+  const float *const *b = bias ? bias : nobias;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
+  // the MFMA-routed Q4_K matrices, then the Q6_K ones
+  int mtype[okq::kGemvMaxProblems], midx[okq::kGemvMaxProblems], mfma = 0, n4 = 0, n6 = 0;
+  bool taken[okq::kGemvMaxProblems] = {false, false, false, false};
+  for (int pass = 0; pass < 2; ++pass) {
+    const uint32_t t = pass == 0 ? OKQ_TYPE_Q4_K : OKQ_TYPE_Q6_K;
+    for (int i = 0; i < count; ++i) {
+      if (w_types[i] != t || rows <= 0 || out_features[i] <= 0) continue;
+      if (gemv_serves(t, rows, in_features, w_bytes[i]) ||
+          !okq::gemm_supported((int)t, rows, in_features, out_features[i]))
+        continue;
+      mtype[mfma] = (int)t;
+      midx[mfma++] = i;
+      (pass == 0 ? n4 : n6) += 1;
+    }
+  }
+  if (rows <= okq::kGemmDecodeRows && n4 > 0 && n6 > 0) {
+    const void *mw[okq::kGemvMaxProblems];
+    int64_t mn[okq::kGemvMaxProblems], ncat = 0;
+    const float *mb[okq::kGemvMaxProblems];
+    float *mo[okq::kGemvMaxProblems];
+    for (int j = 0; j < mfma; ++j) {
+      const int i = midx[j];
+      mw[j] = w[i];
+      mn[j] = out_features[i];
+      mb[j] = b[i];
+      mo[j] = out[i];
+      ncat += (mn[j] + 15) / 16 * 16;
+      taken[i] = true;
+    }
+    const okq::GemmPlan plan = okq::gemm_plan(OKQ_TYPE_Q4_K, rows, ncat, in_features, false, info.cu_count);
+    void *ws = nullptr;
+    st = get_workspace(dev, s, plan.workspace, &ws);
+    if (st != OKQ_OK) return st;
+    st = hip_status(okq::launch_gemm_decode_mixed(x, false, rows, in_features, mfma, mtype, mw, mn, mb, mo, ws, plan, s),
+                    "linear_multi decode-batch launch");
+    if (st != OKQ_OK) return st;
+  }
+  // the rest: okq_gemv_multi's grouping per format, in order of first appearance
+  bool done[okq::kGemvMaxProblems] = {false, false, false, false};
+  for (int i = 0; i < count; ++i) {
+    if (done[i] || taken[i]) continue;
+    const void *gw[okq::kGemvMaxProblems];
+    uint64_t gbytes[okq::kGemvMaxProblems];
+    int64_t gn[okq::kGemvMaxProblems];
+    const float *gb[okq::kGemvMaxProblems];
+    float *go[okq::kGemvMaxProblems];
+    int c = 0;
+    for (int j = i; j < count; ++j) {
+      if (done[j] || taken[j] || w_types[j] != w_types[i]) continue;
+      gw[c] = w[j];
+      gbytes[c] = w_bytes[j];
+      gn[c] = out_features[j];
+      gb[c] = b[j];
+      go[c++] = out[j];
+      done[j] = true;
+    }
+    st = grouped_linear(x, rows, in_features, w_types[i], c, gw, gbytes, gn, gb, go, stream, dev, info);
+    if (st != OKQ_OK) return st;
+  }
+  return ok();
+}
+
 okq_status okq_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float epsilon, float *out,
                        void *stream) {
   okq_status st = validate_rmsnorm(x, rows, hidden, weight, epsilon, out);

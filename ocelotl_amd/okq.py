@@ -46,6 +46,7 @@ SIGNATURES = {
     "okq_gemm": _linear_sig,
     "okq_gemm_bf16": _linear_sig,
     "okq_gemv_multi": (_int, [_vp, _i64, _i64, _u32, _int, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "okq_linear_multi_q": (_int, [_vp, _i64, _i64, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "okq_get_rows_q": (_int, [_u32, _vp, _u64, _i64, _i64, _vp, _i64, _vp, _vp]),
     "okq_rmsnorm": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _vp, _vp]),
     "okq_rmsnorm_linear_q_multi": (_int, [_vp, _i64, _i64, _vp, ctypes.c_float, _u32, _int, _vp, _vp, _vp, _vp,
