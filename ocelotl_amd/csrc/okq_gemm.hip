@@ -1403,8 +1403,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   const int nm = m == 0 ? mn0 : m == 1 ? mn1 : m == 2 ? mn2 : mn3;
   const int col = (tile - t0) * 16 + (cc & 15);
   if (col >= nm) return;
-  constexpr int kBatch = 8;
-  float acc = -0.0f;  // slice order from -0.0, as splitk_reduce_kernel
+  // every slice's load in flight at once (one memory round trip for up to
+  // 16 slices), then the sum in slice order from -0.0, as splitk_reduce_kernel
+  constexpr int kBatch = 16;
+  float acc = -0.0f;
   for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
     float v[kBatch];
 #pragma unroll
