@@ -708,13 +708,20 @@ constexpr int kDecMaxTiles = 4;             // unsplit K: column tiles per wave 
 
 // The matrices of one decode-batch launch: matrix p owns the 16-column tiles
 // [tile0[p], tile0[p + 1]) of the launch (tile0[0] = 0; unused entries
-// INT32_MAX), has n[p] rows of weights w[p], bias bias[p] (or null) and output
-// y[p] [M][n[p]].
+// INT32_MAX) and has n rows of weights w (w_bytes), bias `bias` (bias_bytes,
+// 0 when null) and output y [M][n].  A kernel reads a matrix's record with
+// scalar loads from its arguments (a wave-uniform index), once per tile it
+// moves to; the byte sizes come from the host, so no select or branch
+// builds the buffer descriptors.
+struct DecMat {
+  const uint8_t *w;
+  const float *bias;
+  float *y;
+  int n, tile0;
+  uint32_t w_bytes, bias_bytes;
+};
 struct DecMats {
-  const uint8_t *w[kDecMats];
-  const float *bias[kDecMats];
-  float *y[kDecMats];
-  int n[kDecMats];
+  DecMat mat[kDecMats];
   int tile0[kDecMats];
 };
 
@@ -727,12 +734,22 @@ __device__ __forceinline__ void lds_barrier() {
   __builtin_amdgcn_s_barrier();
 }
 
+// Activation row r of a decode-batch plane (row pitch P halves, P = 8 mod
+// 256) starts at dec_row(r, P) halves: rows 8-15 of each 16-row group sit
+// 64 halves (128 B) further.  A ds_read_b128 serves 32 lanes per pass over
+// 512 B of banks; the pass's two lane groups read 16 rows each at k and
+// k + 64, which with a plain pitch would put rows 8-15 of the first group on
+// the banks of rows 0-7 of the second (measured 1.8x slower per read).  The
+// shifts use kDecRowExtra halves past M * P.
+constexpr int kDecRowExtra = 128;
+__host__ __device__ constexpr int dec_row(int r, int P) { return r * P + 64 * ((r + 8) >> 4); }
+
 // Byte offset of the decode-batch kernel's small LDS arrays (bias, row scales,
-// row maxima): past the activation slice (planes of pitch P halves, per-32
-// sums) and, with an in-workgroup K split, past the partial tiles that reuse
-// those bytes at the end ([kDecWaves][RG] x 1 KB).
+// row maxima): past the activation slice (planes of M * P + kDecRowExtra
+// halves, per-32 sums) and, with an in-workgroup K split, past the partial
+// tiles that reuse those bytes at the end ([kDecWaves][RG] x 1 KB).
 __host__ __device__ constexpr size_t dec_tail_offset(int M, int P, int nsbs, int planes, bool kw_split, int RG) {
-  const size_t act = (size_t)M * P * 2 * planes + (size_t)M * nsbs * 32;
+  const size_t act = ((size_t)M * P + kDecRowExtra) * 2 * planes + (size_t)M * nsbs * 32;
   const size_t red = kw_split ? (size_t)kDecWaves * RG * 1024 : 0;
   return ((act > red ? act : red) + 15) & ~(size_t)15;
 }
@@ -1024,11 +1041,13 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   const int sb0 = z * sl_base + (z < sl_rem ? z : sl_rem);
   const int nsbs = sl_base + (z < sl_rem ? 1 : 0);
   const int Ks = nsbs * 256, P = Ks + 8;  // slice width, LDS row pitch (halves)
-  // LDS: Ah [M][P], Al [M][P] (kLo), xs [M][nsbs][16]; with kw > 1 the same
-  // bytes hold the waves' partial tiles once the activations are consumed
+  // LDS: Ah and Al (kLo) of M rows at dec_row(r, P), xs [nsbs][M][16] (a
+  // row's 32-byte records of consecutive rows adjacent: the 32 lanes reading
+  // them hit 32 distinct 16-byte bank groups); with kw > 1 the same bytes
+  // hold the waves' partial tiles once the activations are consumed
   _Float16 *Ah = reinterpret_cast<_Float16 *>(dsm);
-  _Float16 *Al = Ah + (size_t)M * P;
-  _Float16 *Xs = Ah + (size_t)M * P * (kLo ? 2 : 1);
+  _Float16 *Al = Ah + (size_t)M * P + kDecRowExtra;
+  _Float16 *Xs = Ah + ((size_t)M * P + kDecRowExtra) * (kLo ? 2 : 1);
   // unsplit K: the bias of every wave's tiles (tile ti of wave w at
   // [ti][16 w .. 16 w + 15]); the power-of-two scale of every (super-block,
   // row) of the slice
@@ -1057,17 +1076,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   const int nitems = mytiles * cnt;
   const int cn = lane & 15, g = lane >> 4;
   const uint32_t row_bytes = (uint32_t)nsb_all * F::kBlk;
-  // the matrix of a tile (tiles past the end map to the last matrix; every
-  // field of `mats` is read with constant indices, so it stays in SGPRs)
+  // the matrix of a tile (tiles past the end map to the last matrix): the
+  // tile boundaries stay in SGPRs (t >= st as the sign of st - 1 - t: shifts,
+  // not compares and selects), the matrix's record is a scalar load
   const int st1 = mats.tile0[1], st2 = mats.tile0[2], st3 = mats.tile0[3];
-  auto mat_of = [&](int t) { return (int)(t >= st1) + (int)(t >= st2) + (int)(t >= st3); };
-  auto tile0_of = [&](int m) { return m == 0 ? 0 : m == 1 ? st1 : m == 2 ? st2 : st3; };
-  auto n_of = [&](int m) { return m == 0 ? mats.n[0] : m == 1 ? mats.n[1] : m == 2 ? mats.n[2] : mats.n[3]; };
-  const Rsrc rw0 = make_rsrc(mats.w[0], (uint32_t)((size_t)mats.n[0] * row_bytes));
-  const Rsrc rw1 = make_rsrc(mats.w[1], (uint32_t)((size_t)mats.n[1] * row_bytes));
-  const Rsrc rw2 = make_rsrc(mats.w[2], (uint32_t)((size_t)mats.n[2] * row_bytes));
-  const Rsrc rw3 = make_rsrc(mats.w[3], (uint32_t)((size_t)mats.n[3] * row_bytes));
-  auto rw_of = [&](int m) { return m == 0 ? rw0 : m == 1 ? rw1 : m == 2 ? rw2 : rw3; };
+  auto ge = [](int t, int st) { return (int)((uint32_t)(st - 1 - t) >> 31); };
+  auto mat_of = [&](int t) { return ge(t, st1) + ge(t, st2) + ge(t, st3); };
   // A rows of the lane's row groups.  Lanes whose 16-row group reaches past
   // M read row M - 1: they only produce MFMA output rows >= M, which are
   // never stored, so no zero row needs staging.
@@ -1082,13 +1096,31 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     jj = wrap ? 0 : jj + 1;
     ti += wrap ? 1 : 0;
   };
-  auto load = [&](Item &it, int ti, int jj) {
-    const int sbl = kp + (jj << kw_shift);
+  // The weights of the wave's tile of round ti: the matrix's descriptor and
+  // this lane's byte offset of its column's first super-block of the slice.
+  // Rows past the matrix (and tiles past the end) read past the tensor:
+  // zeros.  Set once per tile, so an item's load costs one address add.
+  struct WTile {
+    Rsrc rs;
+    uint32_t base;
+  };
+  auto wtile = [&](int ti) {
     const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
-    const uint32_t w_end = (uint32_t)((size_t)n_of(m) * row_bytes);
-    // rows past the matrix (and tiles past the end) read past the tensor: zeros
-    const uint32_t n = (uint32_t)((tile - tile0_of(m)) * 16 + cn);
-    F::load(it, rw_of(m), lt < ntl ? n * row_bytes + (uint32_t)(sb0 + sbl) * F::kBlk : w_end, g);
+    const DecMat &mt = mats.mat[m];
+    const uint32_t n = (uint32_t)((tile - mt.tile0) * 16 + cn);
+    WTile wt;
+    wt.rs = make_rsrc(mt.w, mt.w_bytes);
+    wt.base = lt < ntl ? n * row_bytes + (uint32_t)sb0 * F::kBlk : mt.w_bytes;
+    return wt;
+  };
+  WTile lw = wtile(0);
+  int l_ti = 0, l_jj = 0;  // the next item to load
+  auto load_next = [&](Item &it) {
+    F::load(it, lw.rs, lw.base + (uint32_t)(kp + (l_jj << kw_shift)) * F::kBlk, g);
+    if (++l_jj == cnt) {
+      l_jj = 0;
+      lw = wtile(++l_ti);
+    }
   };
   // 2. the activations of the slice: this thread's pieces of 8 consecutive
   //    activations of one row (at most kDecStage; pieces past the last row
@@ -1099,10 +1131,26 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   const int pr = Ks / 8;  // pieces per row
   const uint32_t x_end = (uint32_t)((size_t)M * K * (kLo ? 4 : 2));
   const Rsrc rs_x = make_rsrc(X, x_end);
+  // piece i of this thread is piece tid + i * nt of the slice: row pc_r[i],
+  // piece pc_c[i] of the row (one division per thread; each step adds
+  // divmod(nt, pr) with a carry)
+  int pc_r[kDecStage], pc_c[kDecStage];
+  {
+    const int dq = nt / pr, dr = nt - dq * pr;
+    int r = tid / pr, c = tid - r * pr;
+#pragma unroll
+    for (int i = 0; i < kDecStage; ++i) {
+      pc_r[i] = r;
+      pc_c[i] = c;
+      c += dr;
+      r += dq + (c >= pr ? 1 : 0);
+      c -= c >= pr ? pr : 0;
+    }
+  }
   u32x4 xa[kDecStage], xb[kLo ? kDecStage : 1];  // f32: 2 x 4 values; bf16: 8 values
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
-    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
+    const int r = pc_r[i], c = pc_c[i];
     const uint32_t e = (uint32_t)r * (uint32_t)K + (uint32_t)sb0 * 256u + 8u * (uint32_t)c;  // first activation
     if (kLo) {
       xa[i] = bload4(rs_x, r < M ? e * 4u : x_end);
@@ -1111,17 +1159,19 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
       xa[i] = bload4(rs_x, r < M ? e * 2u : x_end);
     }
   }
-  // bias of the wave's tiles (unsplit K only): lanes 0-15 of each wave load
-  // the 16 values of its tile ti (matrix selected per tile, wave-uniform)
-  uint32_t bbits[kDecMaxTiles];
+  // bias of the wave's tiles (unsplit K only; split K adds it in the
+  // reduction): lanes 0-15 of each wave load the 16 values of its tile ti
+  uint32_t bbits[kDecMaxTiles] = {};
+  if (ksplit == 1) {
 #pragma unroll
-  for (int ti = 0; ti < kDecMaxTiles; ++ti) {
-    const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
-    const float *bp = m == 0 ? mats.bias[0] : m == 1 ? mats.bias[1] : m == 2 ? mats.bias[2] : mats.bias[3];
-    const uint32_t bias_end = bp ? (uint32_t)n_of(m) * 4u : 0u;
-    const int col = (tile - tile0_of(m)) * 16 + lane;
-    const bool in = ksplit == 1 && lane < 16 && lt < ntl && col < n_of(m);
-    bbits[ti] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(bp, bias_end), in ? (uint32_t)col * 4u : bias_end, 0, 0);
+    for (int ti = 0; ti < kDecMaxTiles; ++ti) {
+      const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
+      const DecMat &mt = mats.mat[m];
+      // columns past the matrix fall past bias_bytes: the range check reads 0
+      const uint32_t col = (uint32_t)((tile - mt.tile0) * 16 + lane);
+      bbits[ti] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(mt.bias, mt.bias_bytes),
+                                                       lane < 16 && lt < ntl ? col * 4u : mt.bias_bytes, 0, 0);
+    }
   }
   // A CU returns vector loads in issue order: this bare barrier (no memory
   // fence) puts every activation load of the workgroup ahead of every weight
@@ -1133,8 +1183,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // the activations themselves.  The staging's closing barrier waits for LDS
   // only, not for these loads.
   Item S[D];
-  int l_ti = 0, l_jj = 0;  // the next item to load
-  if (lane < 16) {
+  if (ksplit == 1 && lane < 16) {
 #pragma unroll
     for (int ti = 0; ti < kDecMaxTiles; ++ti) Bs[ti * 256 + wave * 16 + lane] = __uint_as_float(bbits[ti]);
   }
@@ -1160,7 +1209,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
     if (i * nt >= M * pr) break;
-    const int p = tid + i * nt, r = p / pr, c = p - r * pr;
+    const int r = pc_r[i], c = pc_c[i];
     float v[8];
     piece(i, v);
     float a = 0.0f;  // fmaxf drops NaNs
@@ -1211,34 +1260,28 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
       t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
     }
     if (r < M) {
-      *reinterpret_cast<h8 *>(Ah + (size_t)r * P + 8 * c) = hv;
-      if (kLo) *reinterpret_cast<h8 *>(Al + (size_t)r * P + 8 * c) = lv;
+      *reinterpret_cast<h8 *>(Ah + dec_row(r, P) + 8 * c) = hv;
+      if (kLo) *reinterpret_cast<h8 *>(Al + dec_row(r, P) + 8 * c) = lv;
       if (F::kSums && (c & 3) == 0) {
         const _Float16 sh = (_Float16)t;
         h2 pair;
         pair[0] = sh;
         pair[1] = (_Float16)(t - (float)sh);
-        *reinterpret_cast<h2 *>(Xs + (size_t)r * nsbs * 16 + 2 * (c >> 2)) = pair;
+        *reinterpret_cast<h2 *>(Xs + ((size_t)(c >> 5) * M + r) * 16 + 2 * ((c >> 2) & 7)) = pair;
       }
       if ((c & 31) == 0) Rsb[(c >> 5) * kDecRows + r] = ldexpf(1.0f, sx);
     }
     if (RG == 1 && i == 0) {  // (two 16-row groups: registers allow the items only after the staging)
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int j = 0; j < D; ++j) {
-        load(S[j], l_ti, l_jj);
-        advance(l_ti, l_jj);
-      }
+      for (int j = 0; j < D; ++j) load_next(S[j]);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
   lds_barrier();
   if constexpr (RG != 1) {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      load(S[j], l_ti, l_jj);
-      advance(l_ti, l_jj);
-    }
+    for (int j = 0; j < D; ++j) load_next(S[j]);
   }
 
   const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -1254,12 +1297,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // 2^s, plus the bias (unsplit K), or the raw partial of slice z
   auto store = [&](int ti, const f4 *vals) {
     const int tile = gtile(__builtin_amdgcn_readfirstlane(ti * stride + first)), m = mat_of(tile);
-    const int nm = n_of(m), col = (tile - tile0_of(m)) * 16 + cn;
+    const DecMat &mt = mats.mat[m];
+    const int nm = mt.n, col = (tile - mt.tile0) * 16 + cn;
     const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
     // unsplit: the matrix's own output; split: the concatenated partials
-    float *ym = m == 0 ? mats.y[0] : m == 1 ? mats.y[1] : m == 2 ? mats.y[2] : mats.y[3];
     const uint32_t out_end = ksplit > 1 ? part_end : (uint32_t)((size_t)M * nm * 4);
-    const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(ym, out_end);
+    const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(mt.y, out_end);
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
 #pragma unroll
@@ -1279,9 +1322,9 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     const _Float16 *ar[RG], *arl[RG], *xs[RG];
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
-      ar[q] = Ah + (size_t)arow[q] * P + sbl * 256;
-      arl[q] = Al + (size_t)arow[q] * P + sbl * 256;
-      xs[q] = Xs + ((size_t)arow[q] * nsbs + sbl) * 16;
+      ar[q] = Ah + dec_row(arow[q], P) + sbl * 256;
+      arl[q] = Al + dec_row(arow[q], P) + sbl * 256;
+      xs[q] = Xs + ((size_t)sbl * M + arow[q]) * 16;
     }
     F::template contract<kLo, RG>(it, ar, arl, xs, Rsb + sbl * kDecRows + 4 * g, g, acc);
     // the tile's last super-block: write it out (kw > 1: a slot has at most
@@ -1303,8 +1346,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     for (int j = 0; j < D; ++j) {
       consume(S[j], c_ti, c_jj);
       advance(c_ti, c_jj);
-      load(S[j], l_ti, l_jj);
-      advance(l_ti, l_jj);
+      load_next(S[j]);
     }
   }
 #pragma unroll
@@ -1397,7 +1439,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   if (i >= total) return;
   const int row = (int)(i / ncat), cc = (int)(i - (int64_t)row * ncat), tile = cc >> 4;
   const int st1 = sarg(mats.tile0[1]), st2 = sarg(mats.tile0[2]), st3 = sarg(mats.tile0[3]);
-  const int mn0 = sarg(mats.n[0]), mn1 = sarg(mats.n[1]), mn2 = sarg(mats.n[2]), mn3 = sarg(mats.n[3]);
+  const int mn0 = sarg(mats.mat[0].n), mn1 = sarg(mats.mat[1].n), mn2 = sarg(mats.mat[2].n), mn3 = sarg(mats.mat[3].n);
   const int m = (int)(tile >= st1) + (int)(tile >= st2) + (int)(tile >= st3);
   const int t0 = m == 0 ? 0 : m == 1 ? st1 : m == 2 ? st2 : st3;
   const int nm = m == 0 ? mn0 : m == 1 ? mn1 : m == 2 ? mn2 : mn3;
@@ -1415,9 +1457,10 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
     for (int d = 0; d < kBatch; ++d)
       if (z0 + d < ksplit) acc += v[d];
   }
-  float *const y0 = sarg(mats.y[0]), *const y1 = sarg(mats.y[1]), *const y2 = sarg(mats.y[2]), *const y3 = sarg(mats.y[3]);
-  const float *const b0 = sarg(mats.bias[0]), *const b1 = sarg(mats.bias[1]), *const b2 = sarg(mats.bias[2]),
-              *const b3 = sarg(mats.bias[3]);
+  float *const y0 = sarg(mats.mat[0].y), *const y1 = sarg(mats.mat[1].y), *const y2 = sarg(mats.mat[2].y),
+              *const y3 = sarg(mats.mat[3].y);
+  const float *const b0 = sarg(mats.mat[0].bias), *const b1 = sarg(mats.mat[1].bias),
+              *const b2 = sarg(mats.mat[2].bias), *const b3 = sarg(mats.mat[3].bias);
   float *ym = m == 0 ? y0 : m == 1 ? y1 : m == 2 ? y2 : y3;
   const float *bm = m == 0 ? b0 : m == 1 ? b1 : m == 2 ? b2 : b3;
   ym[(size_t)row * nm + col] = acc + (bm ? bm[col] : 0.0f);
@@ -1455,7 +1498,7 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // slice bounds: the LDS budget and kDecStage pieces of 8 activations per
     // thread (M rows of 32 pieces per super-block)
     const int64_t max_sb = std::max<int64_t>(
-        1, std::min<int64_t>((kDecLdsBytes - (int64_t)M * 16 * 2 * 2) / per_sb,
+        1, std::min<int64_t>((kDecLdsBytes - (int64_t)M * 16 * 2 * 2 - kDecRowExtra * 2 * 2) / per_sb,
                              (int64_t)kDecStage * kDecWaves * 64 / (M * 32)));
     const int64_t ntiles = (N + 15) / 16;
     const int64_t ks_lds = (nsb + max_sb - 1) / max_sb;
@@ -1583,6 +1626,21 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
   return hipGetLastError();
 }
 
+// A matrix's record for the decode-batch kernel (byte sizes within 32 bits:
+// gemm_supported's limits).
+static DecMat dec_mat(int type, int64_t K, const void *w, int64_t n, const float *bias, float *y, int tile0) {
+  const int64_t sb_bytes = type == kQ6_K ? kQ6KBytes : type == kQ8_0 ? 8 * kQ8Bytes : kQ4KBytes;
+  DecMat d{};
+  d.w = static_cast<const uint8_t *>(w);
+  d.bias = bias;
+  d.y = y;
+  d.n = (int)n;
+  d.tile0 = tile0;
+  d.w_bytes = (uint32_t)(n * (K / 256) * sb_bytes);
+  d.bias_bytes = bias ? (uint32_t)(n * 4) : 0u;
+  return d;
+}
+
 hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
                                     void *workspace, const GemmPlan &plan, hipStream_t s) {
@@ -1593,10 +1651,7 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
   int tiles = 0;
   for (int i = 0; i < kDecMats; ++i) {
     if (i < count) {
-      mats.w[i] = static_cast<const uint8_t *>(w[i]);
-      mats.bias[i] = bias[i];
-      mats.y[i] = y[i];
-      mats.n[i] = (int)N[i];
+      mats.mat[i] = dec_mat(type, K, w[i], N[i], bias[i], y[i], tiles);
       mats.tile0[i] = tiles;
       tiles += (int)((N[i] + 15) / 16);
     } else {
@@ -1619,10 +1674,7 @@ hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, in
       return hipErrorInvalidValue;
   for (int i = 0; i < kDecMats; ++i) {
     if (i < count) {
-      mats.w[i] = static_cast<const uint8_t *>(w[i]);
-      mats.bias[i] = bias[i];
-      mats.y[i] = y[i];
-      mats.n[i] = (int)N[i];
+      mats.mat[i] = dec_mat(types[i], K, w[i], N[i], bias[i], y[i], tiles);
       mats.tile0[i] = tiles;
       tiles += (int)((N[i] + 15) / 16);
       if (types[i] == kQ4_K) nt1 = tiles;
@@ -1674,10 +1726,7 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   if (plan.bm == kDecRows) {
     if (M > kDecRows) return hipErrorInvalidValue;
     DecMats mats{};
-    mats.w[0] = W;
-    mats.bias[0] = bias;
-    mats.y[0] = y;
-    mats.n[0] = n;
+    mats.mat[0] = dec_mat(type, K, W, N, bias, y, 0);
     for (int i = 1; i < kDecMats; ++i) mats.tile0[i] = INT32_MAX;
     return launch_decode(type, type, (int)((N + 15) / 16), x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s);
   }
