@@ -786,7 +786,7 @@ struct DecQ4K {
     for (int j = 0; j < 2; ++j) {
       uint32_t sc, mv;
       q4k_scale_min_sel(2u * (uint32_t)g + (uint32_t)j, it.hd.y, it.hd.z, it.hd.w, sc, mv);
-      const _Float16 sh = (_Float16)(float)sc, oh = (_Float16)(-1024.0f * (float)sc);
+      const _Float16 sh = (_Float16)(uint16_t)sc, oh = sh * (_Float16)-1024.0f;
       scv[j] = h2{sh, sh};
       offv[j] = h2{oh, oh};
     }
@@ -795,7 +795,7 @@ struct DecQ4K {
     for (int j = 0; j < 4; ++j) {
       uint32_t sc, mv;
       q4k_scale_min_sel((4u * (uint32_t)g + (uint32_t)j) & 7u, it.hd.y, it.hd.z, it.hd.w, sc, mv);
-      const _Float16 mh = g < 2 ? (_Float16)(float)mv : (_Float16)0.0f;
+      const _Float16 mh = g < 2 ? (_Float16)(uint16_t)mv : (_Float16)0.0f;
       mb[2 * j] = mh;
       mb[2 * j + 1] = mh;
     }
@@ -831,7 +831,7 @@ struct DecQ4K {
       const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
       const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
 #pragma unroll
-      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(dm * s4[v], mins[v], fmaf(dv * s4[v], accs[q][v], acc[q][v]));
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(s4[v], fmaf(dm, mins[v], dv * accs[q][v]), acc[q][v]);
     }
   }
 };
@@ -1055,8 +1055,10 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   float *Rsb = Bs + kDecMaxTiles * 256;  // [nsbs][kDecRows]: the 2^s of each (super-block, row)
 
   // 1. this wave's items.  The kDecWaves waves form T = kDecWaves / kw tile
-  //    slots of kw waves each: slot ts's tile of round ti is column tile
-  //    (ti * groups + grp) * T + ts, and wave kp of the slot takes the slice's
+  //    slots of kw waves each.  Column group grp owns a contiguous block of
+  //    the tiles, the blocks balanced to within one tile (so no CU holds a
+  //    round more than another); slot ts's tile of round ti is tile
+  //    ti * T + ts of the block, and wave kp of the slot takes the slice's
   //    super-blocks kp, kp + kw, ... (kw > 1 only with unsplit K: the slot's
   //    waves then sum their partial tiles through LDS at the end).  Item
   //    (ti, jj) is round ti's super-block kp + kw jj, jj < cnt.  Tile numbers
@@ -1065,12 +1067,15 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // (all wave-uniform: readfirstlane keeps them, and the matrix selects and
   // weight descriptors built from them, in scalar registers -- a descriptor
   // the compiler takes for divergent costs a waterfall loop per load)
+  static_assert(kDecWaves == 16, "T = 16 >> kw_shift");
   const int T = kDecWaves >> kw_shift, ts = wave >> kw_shift, kp = wave & (kw - 1);
-  const int stride = __builtin_amdgcn_readfirstlane(groups * T);
-  const int first = __builtin_amdgcn_readfirstlane(grp * T + ts);
+  const int qg = __builtin_amdgcn_readfirstlane(ntl / groups), rg = ntl - qg * groups;
+  const int t0g = grp * qg + (grp < rg ? grp : rg), ntg = qg + (grp < rg ? 1 : 0);  // the group's block
   const int cnt = __builtin_amdgcn_readfirstlane(nsbs > kp ? (nsbs - kp + kw - 1) >> kw_shift : 0);  // items per tile
   const int mytiles =
-      __builtin_amdgcn_readfirstlane(first < ntl && cnt > 0 ? (ntl - first + stride - 1) / stride : 0);
+      __builtin_amdgcn_readfirstlane(ts < ntg && cnt > 0 ? (ntg - ts + T - 1) >> (4 - kw_shift) : 0);
+  // the local tile of round ti (wave-uniform)
+  auto ltile = [&](int ti) { return __builtin_amdgcn_readfirstlane(t0g + ti * T + ts); };
   // a local tile's launch tile (tiles past the end: the format's last one)
   auto gtile = [&](int t) { return tbase + (t < ntl ? t : ntl - 1); };
   const int nitems = mytiles * cnt;
@@ -1098,19 +1103,19 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   };
   // The weights of the wave's tile of round ti: the matrix's descriptor and
   // this lane's byte offset of its column's first super-block of the slice.
-  // Rows past the matrix (and tiles past the end) read past the tensor:
+  // Rows past the matrix (and rounds past the wave's tiles) read past the tensor:
   // zeros.  Set once per tile, so an item's load costs one address add.
   struct WTile {
     Rsrc rs;
     uint32_t base;
   };
   auto wtile = [&](int ti) {
-    const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
+    const int lt = ltile(ti), tile = gtile(lt), m = mat_of(tile);
     const DecMat &mt = mats.mat[m];
     const uint32_t n = (uint32_t)((tile - mt.tile0) * 16 + cn);
     WTile wt;
     wt.rs = make_rsrc(mt.w, mt.w_bytes);
-    wt.base = lt < ntl ? n * row_bytes + (uint32_t)sb0 * F::kBlk : mt.w_bytes;
+    wt.base = ti < mytiles ? n * row_bytes + (uint32_t)sb0 * F::kBlk : mt.w_bytes;
     return wt;
   };
   WTile lw = wtile(0);
@@ -1165,12 +1170,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   if (ksplit == 1) {
 #pragma unroll
     for (int ti = 0; ti < kDecMaxTiles; ++ti) {
-      const int lt = __builtin_amdgcn_readfirstlane(ti * stride + first), tile = gtile(lt), m = mat_of(tile);
+      const int lt = ltile(ti), tile = gtile(lt), m = mat_of(tile);
       const DecMat &mt = mats.mat[m];
       // columns past the matrix fall past bias_bytes: the range check reads 0
       const uint32_t col = (uint32_t)((tile - mt.tile0) * 16 + lane);
       bbits[ti] = __builtin_amdgcn_raw_buffer_load_b32(make_rsrc(mt.bias, mt.bias_bytes),
-                                                       lane < 16 && lt < ntl ? col * 4u : mt.bias_bytes, 0, 0);
+                                                       lane < 16 && ti < mytiles ? col * 4u : mt.bias_bytes, 0, 0);
     }
   }
   // A CU returns vector loads in issue order: this bare barrier (no memory
@@ -1296,7 +1301,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // a finished tile (round ti of this wave's slot): scaled back by the rows'
   // 2^s, plus the bias (unsplit K), or the raw partial of slice z
   auto store = [&](int ti, const f4 *vals) {
-    const int tile = gtile(__builtin_amdgcn_readfirstlane(ti * stride + first)), m = mat_of(tile);
+    const int tile = gtile(ltile(ti)), m = mat_of(tile);
     const DecMat &mt = mats.mat[m];
     const int nm = mt.n, col = (tile - mt.tile0) * 16 + cn;
     const float bv = ksplit == 1 ? Bs[(ti < kDecMaxTiles ? ti : 0) * 256 + wave * 16 + cn] : 0.0f;
