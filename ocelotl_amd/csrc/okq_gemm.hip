@@ -1182,11 +1182,15 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // fence) puts every activation load of the workgroup ahead of every weight
   // load, so no wave's activations queue behind another wave's weights.
   __builtin_amdgcn_s_barrier();
-  // With one 16-row group the weights go out once the wave's first
-  // activations have arrived (after its first piece below), so that the rest
-  // of the conversion overlaps their latency; issued before that, they delay
-  // the activations themselves.  The staging's closing barrier waits for LDS
-  // only, not for these loads.
+  // The weights go out once the wave's first activations have arrived (after
+  // its first piece below), so that the rest of the conversion overlaps their
+  // latency; issued before that, they delay the activations themselves.  With
+  // two 16-row groups only waves with more than D items do so (measured: the
+  // 1-2 item waves of the small projections lose more to the weights
+  // competing with their staging than they gain); theirs go out after the
+  // staging.  The staging's closing barrier waits for LDS only, not for
+  // these loads.
+  const bool early = RG == 1 || nitems > D;
   Item S[D];
   if (ksplit == 1 && lane < 16) {
 #pragma unroll
@@ -1276,7 +1280,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
       }
       if ((c & 31) == 0) Rsb[(c >> 5) * kDecRows + r] = ldexpf(1.0f, sx);
     }
-    if (RG == 1 && i == 0) {  // (two 16-row groups: registers allow the items only after the staging)
+    if (early && i == 0) {
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < D; ++j) load_next(S[j]);
@@ -1284,7 +1288,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     }
   }
   lds_barrier();
-  if constexpr (RG != 1) {
+  if (!early) {
 #pragma unroll
     for (int j = 0; j < D; ++j) load_next(S[j]);
   }
