@@ -1008,14 +1008,17 @@ struct DecQ80 {
 // (exact), so split-K partials leave the kernel unscaled and
 // splitk_reduce_kernel only sums them in slice order and adds the bias.
 // (Reducing in the kernel instead -- the last workgroup of a column group to
-// count its arrival sums the partials -- needs a device-scope release per
-// workgroup, an L2 write-back that serialises per XCD: measured 1.5-2x
-// slower at the C5 shapes than the separate reduction launch.)
+// count its arrival sums the partials -- measured 1.5-2x slower at the C5
+// shapes than the separate reduction launch: with plain stores the
+// device-scope release is an L2 write-back per workgroup; with write-through
+// partials the last workgroup still reads every slice of its group alone, at
+// one CU's bandwidth.)
 //
 // One launch may serve up to kDecMats matrices of one format and K that read
 // the same activations (gate/up): their 16-column tiles are numbered
-// consecutively (`DecMats`), and each tile finds its matrix, weights, bias and
-// output through wave-uniform scalar selects.  Split-K partials are laid out
+// consecutively (`DecMats`), and each tile finds its matrix from the tile
+// boundaries and reads the matrix's record (weights, bias, output, sizes)
+// with a wave-uniform scalar load.  Split-K partials are laid out
 // over the concatenated tile columns, [ksplit][M][ntiles * 16].
 // Index arithmetic stays off the scalar ALU, which one CU's 16 waves share:
 // the grid is (column group, K slice), the host passes the slice partition
@@ -1064,7 +1067,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   //    (ti, jj) is round ti's super-block kp + kw jj, jj < cnt.  Tile numbers
   //    are local to the workgroup's format (tiles [tbase, tbase + ntl) of the
   //    launch); gtile() gives the launch's tile number (matrix, partials).
-  // (all wave-uniform: readfirstlane keeps them, and the matrix selects and
+  // (all wave-uniform: readfirstlane keeps them, and the matrix records and
   // weight descriptors built from them, in scalar registers -- a descriptor
   // the compiler takes for divergent costs a waterfall loop per load)
   static_assert(kDecWaves == 16, "T = 16 >> kw_shift");
