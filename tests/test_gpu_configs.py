@@ -132,9 +132,10 @@ def c5_layer(orc):
 @pytest.mark.parametrize("rows", [1, 8, 32])
 def test_c5_layer_through_the_grouped_calls(torch, okq, orc, c5_layer, rows):
     """C5: one Llama-3-8B layer in the Q4_K_M mix, issued as the bench's
-    `grouped` step issues it -- q+k and gate+up through okq_gemv_multi (shared
-    GEMV launch at batch 1, one decode-batch launch at 8 and 32), v, o and
-    down through okq_linear_out_by_in_q -- every output against the reference."""
+    `grouped` step issues it -- q+k+v through okq_linear_multi_q (Q4_K q/k and
+    Q6_K v: GEMV launches at batch 1, one mixed-format decode-batch launch at 8
+    and 32), gate+up through okq_gemv_multi, o and down through
+    okq_linear_out_by_in_q -- every output against the reference."""
     s = _stream(torch)
     x4 = orc.normal(8100 + rows, rows * 4096, 1.0)
     x14 = orc.normal(8101 + rows, rows * 14336, 1.0)
@@ -152,6 +153,15 @@ def test_c5_layer_through_the_grouped_calls(torch, okq, orc, c5_layer, rows):
                  (ctypes.c_int64 * c)(*[c5_layer[m][1] for m in names]), None,
                  (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), s)
 
+    def multi(names):
+        c = len(names)
+        okq.call("okq_linear_multi_q", xd4.data_ptr(), rows, 4096, c,
+                 (ctypes.c_uint32 * c)(*[c5_layer[m][0] for m in names]),
+                 (ctypes.c_void_p * c)(*[wd[m].data_ptr() for m in names]),
+                 (ctypes.c_uint64 * c)(*[c5_layer[m][3].size for m in names]),
+                 (ctypes.c_int64 * c)(*[c5_layer[m][1] for m in names]), None,
+                 (ctypes.c_void_p * c)(*[outs[m].data_ptr() for m in names]), s)
+
     def one(name):
         t, n, k, wq = c5_layer[name]
         xd = xd14 if k == 14336 else xd4
@@ -159,8 +169,7 @@ def test_c5_layer_through_the_grouped_calls(torch, okq, orc, c5_layer, rows):
                  outs[name].data_ptr(), s)
 
     print(f"[gpu] C5 layer rows={rows}", flush=True)
-    group(["q", "k"])
-    one("v")
+    multi(["q", "k", "v"])
     one("o")
     group(["gate", "up"])
     one("down")
