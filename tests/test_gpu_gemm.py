@@ -152,6 +152,11 @@ DEC_CASES = [
     # column groups x the LDS-bound K split exceed one round of 256 CUs: the
     # plan takes fewer column groups and waves take several tiles (ragged)
     ("okq_gemm", 32, 28672, 4096), ("okq_gemm_bf16", 32, 30000, 4096),
+    # one real row in the second 16-row group, a single column, a few columns
+    # at 32 rows, one super-block per row with more tiles than the staged
+    # biases, and column blocks that do not divide evenly among the groups
+    ("okq_gemm", 17, 1, 256), ("okq_gemm", 32, 5, 512), ("okq_gemm_bf16", 32, 70000, 256),
+    ("okq_gemm", 29, 33000, 1024),
 ]
 
 
