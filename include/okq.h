@@ -251,7 +251,8 @@ okq_status okq_rmsnorm_linear_q_multi(const float *x, int64_t rows, int64_t hidd
  * when they share a format.  A single row folds silu(gate) * up into the down
  * GEMV's prologue whenever the down weight takes the streaming GEMV (gate_buf
  * then holds gate(x)); otherwise silu(gate(x)) * up(x) is left in gate_buf,
- * as the reference does.  up_buf always holds up(x).  Treat both as scratch.  Zero rows, hidden or
+ * as the reference does (when gate and up share one decode-batch launch that
+ * splits K, by its reduction: no separate pass over the intermediate).  up_buf always holds up(x).  Treat both as scratch.  Zero rows, hidden or
  * intermediate are errors (mlp.rs:151-165). */
 okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, int64_t intermediate,
                                 uint32_t gate_type, const void *gate_w, uint64_t gate_bytes, uint32_t up_type,

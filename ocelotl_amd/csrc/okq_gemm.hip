@@ -1478,6 +1478,43 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   ym[(size_t)row * nm + col] = acc + (bm ? bm[col] : 0.0f);
 }
 
+// The gate/up pair of a gated-SiLU MLP in one decode-batch launch (matrix 0
+// gate, matrix 1 up, the same rows): each thread reduces one output of both,
+// in slice order from -0.0 as splitk_reduce_mats_kernel does, and leaves the
+// reference MLP's buffers (crates/kernels/src/mlp.rs:77-88, :233-238): up(x)
+// in up's output and silu(gate(x)) * up(x) in gate's, with the standalone
+// swiglu kernel's operations in its order (both files build with the same
+// flags), one launch and one round trip fewer.
+__global__ __launch_bounds__(256) void splitk_reduce_swiglu_kernel(const float *__restrict__ part, int ksplit, int M,
+                                                                   int ntiles, DecMats mats) {
+  const int n = sarg(mats.mat[0].n);
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= (int64_t)M * n) return;
+  const int row = (int)(i / n), col = (int)(i - (int64_t)row * n);
+  const int64_t ncat = (int64_t)ntiles * 16, total = (int64_t)M * ncat;
+  const int64_t ig = (int64_t)row * ncat + col, iu = ig + (int64_t)sarg(mats.tile0[1]) * 16;
+  constexpr int kBatch = 16;
+  float g = -0.0f, u = -0.0f;
+  for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
+    float vg[kBatch], vu[kBatch];
+#pragma unroll
+    for (int d = 0; d < kBatch; ++d) {
+      vg[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + ig] : 0.0f;
+      vu[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + iu] : 0.0f;
+    }
+#pragma unroll
+    for (int d = 0; d < kBatch; ++d)
+      if (z0 + d < ksplit) g += vg[d], u += vu[d];
+  }
+  const float *const bg = sarg(mats.mat[0].bias), *const bu = sarg(mats.mat[1].bias);
+  g = g + (bg ? bg[col] : 0.0f);
+  u = u + (bu ? bu[col] : 0.0f);
+  float *const yg = sarg(mats.mat[0].y), *const yu = sarg(mats.mat[1].y);
+  yu[(size_t)row * n + col] = u;
+  const float sig = 1.0f / (1.0f + expf(-g));
+  yg[(size_t)row * n + col] = (g * sig) * u;
+}
+
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
@@ -1578,15 +1615,15 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
 }
 
 // The decode-batch kernel (it converts the activations itself: no pre-pass)
-// and, when K is split, the reduction of its partials.
-// The decode-batch kernel (it converts the activations itself: no pre-pass)
-// and, when K is split, the reduction of its partials.  type2 != type: the
+// and, when K is split, the reduction of its partials (swiglu: the gate/up
+// pair's reduction with the gated SiLU).  type2 != type: the
 // first nt1 tiles (matrices) are of format `type`, the rest of type2 (Q4_K
 // then Q6_K); the plan's column groups are shared out in proportion to the
 // two formats' tiles, each format's group keeping at most the plan's tiles
 // per wave.
 static hipError_t launch_decode(int type, int type2, int nt1, const void *x, bool x_is_bf16, int64_t M, int64_t K,
-                                const DecMats &mats, int ntiles, char *ws, const GemmPlan &plan, hipStream_t s) {
+                                const DecMats &mats, int ntiles, char *ws, const GemmPlan &plan, hipStream_t s,
+                                bool swiglu) {
   const int m = (int)M, k = (int)K, ks = plan.ksplit;
   float *part = ks > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
   const int nsb = (int)(K / 256), sl_base = nsb / ks, sl_rem = nsb % ks;  // slice z: sl_base + (z < sl_rem)
@@ -1632,6 +1669,12 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
 #undef OKQ_DEC
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
+  if (swiglu) {
+    const int64_t pairs = M * (int64_t)mats.mat[0].n;
+    hipLaunchKernelGGL(splitk_reduce_swiglu_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, part, ks,
+                       m, ntiles, mats);
+    return hipGetLastError();
+  }
   const int64_t total = M * (int64_t)ntiles * 16;
   hipLaunchKernelGGL(splitk_reduce_mats_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m,
                      ntiles, mats);
@@ -1655,9 +1698,9 @@ static DecMat dec_mat(int type, int64_t K, const void *w, int64_t n, const float
 
 hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
-                                    void *workspace, const GemmPlan &plan, hipStream_t s) {
+                                    void *workspace, const GemmPlan &plan, hipStream_t s, bool swiglu) {
   if ((type != kQ4_K && type != kQ6_K && type != kQ8_0) || plan.bm != kDecRows || M > kDecRows || count < 1 ||
-      count > kDecMats)
+      count > kDecMats || (swiglu && (count != 2 || N[0] != N[1])))
     return hipErrorInvalidValue;
   DecMats mats{};
   int tiles = 0;
@@ -1670,7 +1713,8 @@ hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int
       mats.tile0[i] = INT32_MAX;
     }
   }
-  return launch_decode(type, type, tiles, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
+  return launch_decode(type, type, tiles, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s,
+                       swiglu);
 }
 
 hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, int64_t K, int count, const int *types,
@@ -1694,7 +1738,8 @@ hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, in
       mats.tile0[i] = INT32_MAX;
     }
   }
-  return launch_decode(kQ4_K, kQ6_K, nt1, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s);
+  return launch_decode(kQ4_K, kQ6_K, nt1, x, x_is_bf16, M, K, mats, tiles, static_cast<char *>(workspace), plan, s,
+                       false);
 }
 
 // The tiled kernel over the pre-pass's planes (every format; f32 or bf16).
@@ -1740,7 +1785,8 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     DecMats mats{};
     mats.mat[0] = dec_mat(type, K, W, N, bias, y, 0);
     for (int i = 1; i < kDecMats; ++i) mats.tile0[i] = INT32_MAX;
-    return launch_decode(type, type, (int)((N + 15) / 16), x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s);
+    return launch_decode(type, type, (int)((N + 15) / 16), x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s,
+                         false);
   }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);

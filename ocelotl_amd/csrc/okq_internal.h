@@ -94,11 +94,13 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
 // Up to kDecMats matrices of one format and K that read the same activations
 // in one decode-batch launch (plan: gemm_plan with N = sum of the matrices'
 // rows rounded up to 16 each, which must pick the decode-batch kernel).
+// swiglu (two matrices of equal rows, gate then up): when the plan splits K,
+// the reduction leaves up in y[1] and silu(gate) * up in y[0].
 constexpr int kDecMats = 4;
 constexpr int kGemmDecodeRows = 32;  // batches up to this many rows take the decode-batch kernel
 hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
-                                    void *workspace, const GemmPlan &plan, hipStream_t s);
+                                    void *workspace, const GemmPlan &plan, hipStream_t s, bool swiglu = false);
 
 // Q4_K and Q6_K matrices that read the same activations in one decode-batch
 // launch: types[] lists the Q4_K matrices first, then the Q6_K ones (at least

@@ -578,9 +578,14 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
 // combined columns, so those outputs match each matrix's own call within
 // the reference rule rather than bit for bit.  A single MFMA matrix, or
 // larger batches, run through okq_linear_out_by_in_q's own dispatch.
+// swiglu_pair (count 2: gate then up of a gated-SiLU MLP): when both take one
+// decode-batch launch that splits K, its reduction also applies the SiLU
+// (out[0] = silu(gate) * up, out[1] = up) and *swiglu_done says so.
 okq_status grouped_linear(const float *x, int64_t rows, int64_t in_features, uint32_t w_type, int count,
                           const void *const *w, const uint64_t *w_bytes, const int64_t *out_features,
-                          const float *const *b, float *const *out, void *stream, int dev, const DevInfo &info) {
+                          const float *const *b, float *const *out, void *stream, int dev, const DevInfo &info,
+                          bool swiglu_pair = false, bool *swiglu_done = nullptr) {
+  if (swiglu_done) *swiglu_done = false;
   hipStream_t s = static_cast<hipStream_t>(stream);
   std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   okq_status st = OKQ_OK;
@@ -615,10 +620,12 @@ okq_status grouped_linear(const float *x, int64_t rows, int64_t in_features, uin
     void *ws = nullptr;
     st = get_workspace(dev, s, plan.workspace, &ws);
     if (st != OKQ_OK) return st;
+    const bool swiglu = swiglu_pair && count == 2 && mfma == 2 && plan.ksplit > 1;
     st = hip_status(okq::launch_gemm_decode_multi((int)w_type, x, false, rows, in_features, mfma, mw, mn, mb, mo, ws,
-                                                  plan, s),
+                                                  plan, s, swiglu),
                     "gemv_multi decode-batch launch");
     if (st != OKQ_OK) return st;
+    if (swiglu_done) *swiglu_done = swiglu;
     grouped = true;
   }
   for (int i = 0; i < mfma && !grouped; ++i) {
@@ -853,14 +860,17 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
   hipStream_t s = static_cast<hipStream_t>(stream);
   std::lock_guard<std::recursive_mutex> enqueue(stream_lock(dev, s));
   // gate and up: grouped like okq_gemv_multi when they share a format (one
-  // GEMV pass over both weights, or one decode-batch launch)
+  // GEMV pass over both weights, or one decode-batch launch, whose split-K
+  // reduction then applies the SiLU too)
+  bool swiglu_done = false;
   if (gate_type == up_type) {
     const void *ws[2] = {gate_w, up_w};
     const uint64_t wb[2] = {gate_bytes, up_bytes};
     const int64_t ns[2] = {intermediate, intermediate};
     const float *bs[2] = {nullptr, nullptr};
     float *const os[2] = {gate_buf, up_buf};
-    st = grouped_linear(x, rows, hidden, gate_type, 2, ws, wb, ns, bs, os, stream, dev, info);
+    st = grouped_linear(x, rows, hidden, gate_type, 2, ws, wb, ns, bs, os, stream, dev, info, rows > 1,
+                        &swiglu_done);
     if (st != OKQ_OK) return st;
   } else {
     st = linear_impl(x, false, rows, hidden, gate_type, gate_w, gate_bytes, intermediate, nullptr, gate_buf, stream,
@@ -871,7 +881,8 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
     if (st != OKQ_OK) return st;
   }
   // down: silu(gate) * up folded into the GEMV prologue, or materialised in
-  // gate_buf (the reference's final content of gate_buf) for the other paths
+  // gate_buf (the reference's final content of gate_buf) for the other paths:
+  // by gate/up's split-K reduction, else by its own pass
   if (rows == 1 && okq::gemv_streams((int)down_type, intermediate, down_w, hidden)) {
     const okq::GemvPro base{okq::kProSwiGLU, nullptr, 0.0f};
     const float *nob = nullptr;
@@ -886,8 +897,10 @@ okq_status okq_mlp_gated_silu_q(const float *x, int64_t rows, int64_t hidden, in
     }
     return ok();
   }
-  hipError_t e = okq::launch_swiglu(gate_buf, up_buf, rows * intermediate, gate_buf, s);
-  if (e != hipSuccess) return hip_status(e, "swiglu launch");
+  if (!swiglu_done) {
+    hipError_t e = okq::launch_swiglu(gate_buf, up_buf, rows * intermediate, gate_buf, s);
+    if (e != hipSuccess) return hip_status(e, "swiglu launch");
+  }
   return linear_impl(gate_buf, false, rows, intermediate, down_type, down_w, down_bytes, hidden, nullptr, out, stream,
                      Path::Auto);
 }

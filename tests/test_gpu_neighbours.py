@@ -221,6 +221,8 @@ MLP_CASES = [
     (O.Q4_K, O.Q4_K, O.Q6_K, 7, 1024, 2816),   # batch: GEMM gate/up, materialised SiLU, per-row Q6_K down
     (O.Q8_0, O.Q8_0, O.Q8_0, 3, 512, 1024),
     (O.Q4_K, O.Q4_K, O.Q6_K, 8, 4096, 14336),   # Llama-3-8B batch of 8: gate+up in one decode-batch launch
+    (O.Q4_K, O.Q4_K, O.Q6_K, 24, 1024, 256),    # few tiles: gate+up split K, the SiLU in their reduction
+    (O.Q6_K, O.Q6_K, O.Q4_K, 20, 1024, 512),    # the same with Q6_K gate/up
 ]
 
 
@@ -260,6 +262,58 @@ def test_mlp_gated_silu_q_matches_reference_order(torch, okq, orc, tg, tu, td, r
     # the single-projection rule.
     want = orc.linear_q(td, orc.swiglu(gate, up), rows, inter, dq, hidden).reshape(-1)
     assert np.abs(got - want).max() <= 1e-3 * np.abs(want).max()
+
+
+MLP_SPLIT_CASES = [
+    # (gate/up type, down type, rows, hidden, intermediate): gate and up share
+    # one decode-batch launch that splits K over workgroups: above 16 rows
+    # (up to 16 rows keep K inside the workgroup when it fits), for the LDS
+    # (4 super-blocks of 32 rows) or to fill the CUs with few tiles
+    (O.Q4_K, O.Q6_K, 32, 4096, 14336),   # Llama-3-8B batch of 32
+    (O.Q4_K, O.Q4_K, 24, 1024, 256),
+    (O.Q6_K, O.Q4_K, 20, 1024, 512),
+    (O.Q8_0, O.Q8_0, 17, 1024, 224),     # down on the GEMV (K = 224 is not whole super-blocks)
+]
+
+
+@pytest.mark.parametrize("tgu,td,rows,hidden,inter", MLP_SPLIT_CASES)
+def test_mlp_gated_silu_q_split_reduction_applies_silu(torch, okq, orc, tgu, td, rows, hidden, inter):
+    """Where gate+up split K, their reduction leaves up(x) and silu(gate(x)) *
+    up(x) itself: up_buf equals okq_gemv_multi's up output bit for bit (the
+    same launch plan and slice-order sums), gate_buf equals silu(g) * u of
+    okq_gemv_multi's outputs up to the rounding of exp (so each output pairs
+    the right gate and up columns), and out is the down projection of
+    gate_buf (bit for bit against okq_linear_out_by_in_q on it)."""
+    print(f"[gpu] mlp split reduction types={tgu},{td} rows={rows} hidden={hidden} inter={inter}", flush=True)
+    x = orc.normal(7500 + rows, rows * hidden, 1.0)
+    gq = orc.quantize(tgu, orc.normal(7501, inter * hidden, 0.02))
+    uq = orc.quantize(tgu, orc.normal(7502, inter * hidden, 0.02))
+    dq = orc.quantize(td, orc.normal(7503, hidden * inter, 0.02))
+    gd, ud, dd, xd = _dev(torch, gq), _dev(torch, uq), _dev(torch, dq), _dev(torch, x)
+    gb = torch.full((rows * inter,), float("nan"), device="cuda")
+    ub = torch.full((rows * inter,), float("nan"), device="cuda")
+    out = torch.full((rows * hidden,), float("nan"), device="cuda")
+    okq.call("okq_mlp_gated_silu_q", xd.data_ptr(), rows, hidden, inter, tgu, gd.data_ptr(), gq.size,
+             tgu, ud.data_ptr(), uq.size, td, dd.data_ptr(), dq.size, gb.data_ptr(), ub.data_ptr(), out.data_ptr(),
+             _stream(torch))
+    g2 = torch.full((rows * inter,), float("nan"), device="cuda")
+    u2 = torch.full((rows * inter,), float("nan"), device="cuda")
+    okq.call("okq_gemv_multi", xd.data_ptr(), rows, hidden, tgu, 2, (ctypes.c_void_p * 2)(gd.data_ptr(), ud.data_ptr()),
+             (ctypes.c_uint64 * 2)(gq.size, uq.size), (ctypes.c_int64 * 2)(inter, inter), None,
+             (ctypes.c_void_p * 2)(g2.data_ptr(), u2.data_ptr()), _stream(torch))
+    torch.cuda.synchronize()
+    u_buf, g_buf = ub.cpu().numpy(), gb.cpu().numpy()
+    g, u = g2.cpu().numpy(), u2.cpu().numpy()
+    assert (u_buf.view(np.uint32) == u.view(np.uint32)).all()
+    want = (g * (np.float32(1.0) / (np.float32(1.0) + np.exp(-g)))) * u
+    assert np.all(np.isfinite(g_buf))
+    assert np.abs(g_buf - want).max() <= 4e-7 * np.abs(want).max() + 1e-30
+    assert np.all(np.abs(g_buf - want) <= 8 * np.spacing(np.abs(want)))
+    out2 = torch.full((rows * hidden,), float("nan"), device="cuda")
+    okq.call("okq_linear_out_by_in_q", gb.data_ptr(), rows, inter, td, dd.data_ptr(), dq.size, hidden, None,
+             out2.data_ptr(), _stream(torch))
+    torch.cuda.synchronize()
+    assert (out.cpu().numpy().view(np.uint32) == out2.cpu().numpy().view(np.uint32)).all()
 
 
 def test_mlp_gated_silu_q_validates_before_launch(torch, okq, orc):
