@@ -1191,8 +1191,10 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // two 16-row groups only waves with more than D items do so (measured: the
   // 1-2 item waves of the small projections lose more to the weights
   // competing with their staging than they gain); theirs go out after the
-  // staging.  The staging's closing barrier waits for LDS only, not for
-  // these loads.
+  // staging.  The closing barrier itself waits for LDS only, but with the
+  // issue a per-wave choice the compiler's wait counts after it hold on
+  // both paths: an early wave's last piece waits for its weights too (exact
+  // counts, from issuing on every wave, measured no faster).
   const bool early = RG == 1 || nitems > D;
   Item S[D];
   if (ksplit == 1 && lane < 16) {
@@ -1349,8 +1351,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   };
 
   // 3. the ring: consume slot j, refill it D items ahead; loads stay
-  //    unconditional (items past the end read past the tensor: zeros).  The
-  //    staging barrier above waits for LDS only, not for these loads.
+  //    unconditional (items past the end read past the tensor: zeros).
   int c_ti = 0, c_jj = 0;  // the next item to consume
   int u0 = 0;
   for (; u0 + D < nitems; u0 += D) {
