@@ -35,7 +35,8 @@ The JSON line also carries:
                 C4 per call, C5)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate_up|copy|gemm_gate512   (bare workloads for counter passes)
+     python bench.py --probe gate_up|copy|gemm_gate512|decode_gate_up32
+                                                        (bare workloads for counter passes)
 """
 from __future__ import annotations
 
@@ -713,6 +714,22 @@ def run_probe(ctx: Ctx, what: str):
         for i in range(20):
             launch_group(ctx, names, {m: pools[m][0].narrow(0, (i % copies) * b, b) for m in names}, x, outs)
         log(f"probe gate_up: 20 launches, {2 * b} weight bytes each")
+    elif what == "decode_gate_up32":
+        names = ["gate", "up"]
+        ws = {m: ctx.quantized(Q4K, *C2_SHAPE[m], seed=10_004 + i) for i, m in enumerate(names)}
+        pools = {m: ctx.replicas(ws[m]) for m in names}
+        copies = min(cp for _, cp in pools.values())
+        rows, (n, k) = 32, C2_SHAPE["gate"]
+        x = ctx.normal(rows * k, 32)
+        outs = [torch.empty(rows * n, dtype=torch.float32, device="cuda") for _ in names]
+        b = wbytes(Q4K, n, k)
+        for i in range(20):
+            w = [pools[m][0].narrow(0, (i % copies) * b, b) for m in names]
+            ctx.okq.call("okq_gemv_multi", x.data_ptr(), rows, k, Q4K, 2, (ctypes.c_void_p * 2)(*[t.data_ptr() for t in w]),
+                         (ctypes.c_uint64 * 2)(b, b), (ctypes.c_int64 * 2)(n, n), None,
+                         (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs]), ctx.stream)
+        log(f"probe decode_gate_up32: 20 calls of 32 rows over gate+up ({2 * b} weight bytes each): "
+            f"one decode-batch launch and its split-K reduction per call")
     elif what == "gemm_gate512":
         n, k, m = 14336, 4096, 512
         ws = [ctx.quantized(Q4K, n, k, seed=10_004 + c) for c in range(4)]
@@ -750,10 +767,10 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
     ap.add_argument("--only", default="c1,c3,c4,c5", help="secondary configs to run (comma list of c1,c3,c4,c5)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
-    ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512"], default=None,
+    ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "decode_gate_up32"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
-                         "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), or 20 Q4_K "
-                         "GEMM calls at M=512 on the gate shape")
+                         "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), 20 Q4_K "
+                         "GEMM calls at M=512 on the gate shape, or 20 gate+up calls at 32 rows (decode-batch kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
