@@ -1317,16 +1317,22 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     // unsplit: the matrix's own output; split: the concatenated partials
     const uint32_t out_end = ksplit > 1 ? part_end : (uint32_t)((size_t)M * nm * 4);
     const Rsrc rs_out = ksplit > 1 ? rs_part : make_rsrc(mt.y, out_end);
+    // element offsets in 32 bits (both ranges are below 4 GiB), selected
+    // rather than branched on: row 4g + v of row group q is base + (16q + v)
+    // * pitch; lanes past the matrix's rows or columns store to out_end
+    const uint32_t pitch = ksplit > 1 ? (uint32_t)ncat : (uint32_t)nm;
+    const uint32_t base = ksplit > 1 ? ((uint32_t)z * (uint32_t)M + 4u * (uint32_t)g) * (uint32_t)ncat +
+                                           (uint32_t)tile * 16u + (uint32_t)cn
+                                     : 4u * (uint32_t)g * (uint32_t)nm + (uint32_t)col;
+    const bool col_ok = col < nm;
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
 #pragma unroll
       for (int v = 0; v < 4; ++v) {
         const int row = 16 * q + 4 * g + v;
         const float val = vals[q][v] + bv;  // rows >= M: the range check drops their stores
-        const uint32_t off =
-            (row < M && col < nm)
-                ? (uint32_t)(ksplit > 1 ? ((size_t)z * M + row) * ncat + (size_t)tile * 16 + cn : (size_t)row * nm + col) * 4u
-                : out_end;
+        const uint32_t e = base + (uint32_t)(16 * q + v) * pitch;
+        const uint32_t off = col_ok && row < M ? e * 4u : out_end;
         __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(val), rs_out, off, 0, 0);
       }
     }
