@@ -402,14 +402,20 @@ __device__ __forceinline__ unsigned quant_group(u32x4a4 raw, int f, int nf, XRec
 // ---------------------------------------------------------------------------
 // the streaming kernel
 // ---------------------------------------------------------------------------
-// Matrices 1..3 of a multi-matrix launch (matrix 0 travels in the kernel's
-// own arguments): rows [start[i], start[i+1]) belong to matrix i + 1;
-// start[i] = INT_MAX for unused entries.
+// The matrices of a multi-matrix launch, matrix 0 included: its blocks
+// (bytes: the tensor's size, within 32 bits), bias and output, its first row
+// among the launch's concatenated rows and its row count (the output's row
+// stride).  Rows [start[i], start[i+1]) belong to matrix i + 1; start[i] =
+// INT_MAX and an empty record for unused entries.
+struct GemvMat {
+  const uint8_t *w;
+  const float *bias;
+  float *y;
+  uint32_t bytes;
+  int first, rows, pad;
+};
 struct GemvMore {
-  const uint8_t *w[kGemvMaxProblems - 1];
-  const float *bias[kGemvMaxProblems - 1];
-  float *y[kGemvMaxProblems - 1];
-  uint32_t bytes[kGemvMaxProblems - 1];
+  GemvMat mat[kGemvMaxProblems];
   int start[kGemvMaxProblems - 1];
 };
 
@@ -485,33 +491,30 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   const int end = N;
   float inv_rms = 0.0f;  // kProRms: 1 / rms of the row (the IEEE path reapplies it)
   auto row_of = [&](int step) { return step * window + (int)blockIdx.x * G + g; };
-  // Matrix selection: single-matrix launches (kMulti = false) never touch M,
-  // so their argument fetch is one small block; multi-matrix launches read
-  // every field of M once with constant indices (runtime indexing would make
-  // each row's lookup a dependent kernel-argument load ahead of the weight
-  // loads) and rows pick their matrix with scalar selects.
+  // Matrix selection: single-matrix launches (kMulti = false) never touch M;
+  // in multi-matrix launches a row finds its matrix from the three row
+  // boundaries and reads that matrix's record with scalar loads at a
+  // wave-uniform index.  (Selecting each field from four candidates instead
+  // compiled into chains of scalar compares and branches -- ~170 scalar
+  // instructions per row, with every wave of the CU sharing one scalar unit;
+  // the records halve that and took q+k+v from 7.07 to 6.72 us.)
   const int st1 = kMulti ? M.start[0] : INT32_MAX, st2 = kMulti ? M.start[1] : INT32_MAX;
   const int st3 = kMulti ? M.start[2] : INT32_MAX;
-  const Rsrc rs0 = make_rsrc(W, w_bytes);
-  const Rsrc rs1 = make_rsrc(kMulti ? M.w[0] : nullptr, kMulti ? M.bytes[0] : 0u);
-  const Rsrc rs2 = make_rsrc(kMulti ? M.w[1] : nullptr, kMulti ? M.bytes[1] : 0u);
-  const Rsrc rs3 = make_rsrc(kMulti ? M.w[2] : nullptr, kMulti ? M.bytes[2] : 0u);
+  auto rec = [&](int p) -> GemvMat {
+    if constexpr (kMulti) return M.mat[__builtin_amdgcn_readfirstlane(p)];
+    else return GemvMat{W, bias, y, w_bytes, 0, N, 0};
+  };
   // the matrix of a row (rows past the end map to the last one)
   auto prob = [&](int row) {
     return kMulti ? (int)(row >= st1) + (int)(row >= st2) + (int)(row >= st3) : 0;
   };
-  auto first_row = [&](int p) { return p == 0 ? 0 : p == 1 ? st1 : p == 2 ? st2 : st3; };
-  auto rsrc = [&](int p) { return p == 0 ? rs0 : p == 1 ? rs1 : p == 2 ? rs2 : rs3; };
-  auto bytes_of = [&](int p) {
-    return p == 0 ? w_bytes : p == 1 ? M.bytes[0] : p == 2 ? M.bytes[1] : M.bytes[2];
-  };
-  auto bias_of = [&](int p) { return p == 0 ? bias : p == 1 ? M.bias[0] : p == 2 ? M.bias[1] : M.bias[2]; };
-  auto y_of = [&](int p) { return p == 0 ? y : p == 1 ? M.y[0] : p == 2 ? M.y[1] : M.y[2]; };
+  auto first_row = [&](int p) { return rec(p).first; };
+  auto rsrc = [&](int p) { const GemvMat m = rec(p); return make_rsrc(m.w, m.bytes); };
+  auto bytes_of = [&](int p) { return rec(p).bytes; };
+  auto bias_of = [&](int p) { return rec(p).bias; };
+  auto y_of = [&](int p) { return rec(p).y; };
   // rows of matrix p (the row stride of its output)
-  auto rows_of = [&](int p) {
-    if (!kMulti) return N;
-    return p == 0 ? st1 : p == 1 ? min(st2, N) - st1 : p == 2 ? min(st3, N) - st2 : N - st3;
-  };
+  auto rows_of = [&](int p) { return rec(p).rows; };
   // Byte offset of this lane's unit in `row`; rows past the end (and idle
   // lanes) point at the end of their tensor, where buffer loads return zeros
   // without touching memory, so every load is unconditional.
@@ -542,7 +545,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     const int p = prob(row);
     y_of(p)[(size_t)r * rows_of(p) + (row - first_row(p))] = v;
   };
-  auto wbase_of = [&](int p) { return p == 0 ? W : p == 1 ? M.w[0] : p == 2 ? M.w[1] : M.w[2]; };
+  auto wbase_of = [&](int p) { return rec(p).w; };
   // The IEEE path, taken by the whole launch when some activation row holds
   // an infinity or a NaN (bit r of `slow`).  Team g's rows are shared out
   // step by step among its T waves, and each wave computes whole rows, 64
@@ -1061,15 +1064,19 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, 
   P.bytes = (uint32_t)((size_t)N[0] * row_bytes_of(type, K));
   P.bias = bias[0];
   P.multi = count > 1;
-  int64_t start = N[0];
-  for (int i = 1; i < kGemvMaxProblems; ++i) {
+  int64_t start = 0;
+  for (int i = 0; i < kGemvMaxProblems; ++i) {
+    GemvMat &m = P.M.mat[i];
     if (i < count) {
-      P.M.w[i - 1] = static_cast<const uint8_t *>(w[i]);
-      P.M.bytes[i - 1] = (uint32_t)((size_t)N[i] * row_bytes_of(type, K));
-      P.M.bias[i - 1] = bias[i];
-      P.M.start[i - 1] = (int)start;
+      m.w = static_cast<const uint8_t *>(w[i]);
+      m.bytes = (uint32_t)((size_t)N[i] * row_bytes_of(type, K));
+      m.bias = bias[i];
+      m.first = (int)start;
+      m.rows = (int)N[i];
+      if (i > 0) P.M.start[i - 1] = (int)start;
       start += N[i];
     } else {
+      m = GemvMat{nullptr, nullptr, nullptr, 0u, INT32_MAX, 0, 0};
       P.M.start[i - 1] = INT32_MAX;
     }
   }
@@ -1086,7 +1093,7 @@ hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, 
     const int nr = (int)std::min<int64_t>(per_launch, rows - r0);
     P.nrows = nr;
     P.y = y[0] + r0 * N[0];
-    for (int i = 1; i < count; ++i) P.M.y[i - 1] = y[i] + r0 * N[i];
+    for (int i = 0; i < count; ++i) P.M.mat[i].y = y[i] + r0 * N[i];
     const int R = nr == 1 ? 1 : nr == 2 ? 2 : 4;
     hipError_t e = launch_stream(type, x + r0 * K, K, P, R, cu_count, s);
     if (e != hipSuccess) return e;
