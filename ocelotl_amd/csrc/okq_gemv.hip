@@ -546,6 +546,16 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     y_of(p)[(size_t)r * rows_of(p) + (row - first_row(p))] = v;
   };
   auto wbase_of = [&](int p) { return rec(p).w; };
+  // The output of (row, activation row r) from lane 0 of a wave: a
+  // range-checked buffer store whose other lanes (and rows that store
+  // nothing) address past the end, where the hardware drops them, so no
+  // branch on the lane surrounds it.
+  auto store_l0 = [&](int row, int r, float v, bool ok) {
+    const GemvMat m = rec(prob(row));
+    const uint32_t yb = (uint32_t)nrows * (uint32_t)m.rows * 4u;
+    const uint32_t off = lane == 0 && ok ? ((uint32_t)r * (uint32_t)m.rows + (uint32_t)(row - m.first)) * 4u : yb;
+    __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), make_rsrc(m.y, yb), off, 0, 0);
+  };
   // The IEEE path, taken by the whole launch when some activation row holds
   // an infinity or a NaN (bit r of `slow`).  Team g's rows are shared out
   // step by step among its T waves, and each wave computes whole rows, 64
@@ -711,22 +721,17 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
     };
     auto finish = [&](const typename F::Regs &Q, float b, int step) {
       const int row = row_of(step);
+      // idle lanes and rows past the end hold zero activations or read zero
+      // weights, so the compute needs no branch around it
       float acc[R];
   #pragma unroll
-      for (int r = 0; r < R; ++r) acc[r] = 0.0f;
-      if (active && row < end) {
-  #pragma unroll
-        for (int r = 0; r < R; ++r) acc[r] = F::compute(Q, xreg[r], xlo[r], (wide_rows >> r) & 1u, lane);  // the weight unpack is shared
-      }
+      for (int r = 0; r < R; ++r) acc[r] = F::compute(Q, xreg[r], xlo[r], (wide_rows >> r) & 1u, lane);  // the weight unpack is shared
       float sum[R];
   #pragma unroll
       for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
       if (T == 1) {
-        if (lane == 0 && row < end) {
   #pragma unroll
-          for (int r = 0; r < R; ++r)
-            if (r < nrows) store(row, r, sum[r] + b);
-        }
+        for (int r = 0; r < R; ++r) store_l0(row, r, sum[r] + b, row < end && r < nrows);
       } else {
         if (lane == 0) {
   #pragma unroll
@@ -754,11 +759,8 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
         float sum[R];
   #pragma unroll
         for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
-        if (lane == 0 && row < end) {
   #pragma unroll
-          for (int r = 0; r < R; ++r)
-            if (r < nrows) store(row, r, sum[r] + bs[j]);
-        }
+        for (int r = 0; r < R; ++r) store_l0(row, r, sum[r] + bs[j], row < end && r < nrows);
       };
       const int nb = (int)gridDim.x, bi = (int)blockIdx.x;
       while (ring_row[D - 1] < end) {
