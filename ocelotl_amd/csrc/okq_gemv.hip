@@ -759,8 +759,14 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
         float sum[R];
   #pragma unroll
         for (int r = 0; r < R; ++r) sum[r] = wave_sum(acc[r]);
+        // lane 0 alone stores here: a store by every lane (the others
+        // dropped past the end) made the one-row ring of the Q6_K head 8%
+        // slower
+        if (lane == 0 && row < end) {
   #pragma unroll
-        for (int r = 0; r < R; ++r) store_l0(row, r, sum[r] + bs[j], row < end && r < nrows);
+          for (int r = 0; r < R; ++r)
+            if (r < nrows) store(row, r, sum[r] + bs[j]);
+        }
       };
       const int nb = (int)gridDim.x, bi = (int)blockIdx.x;
       while (ring_row[D - 1] < end) {
