@@ -1450,13 +1450,15 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 // The decode-batch kernel's partials [ksplit][M][ntiles * 16] over the
 // concatenated tiles of its matrices: the same slice-order sum, scattered to
 // each matrix's output with its bias (columns past a matrix's rows skipped).
+// Grid: 256-column blocks x rows, so no thread divides its index; the
+// partials are read through a range-checked buffer resource with 32-bit
+// offsets (the decode-batch kernel addresses them so too), slices past
+// ksplit pointed at its end, where they read zeros without a branch.
 __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__restrict__ part, int ksplit, int M,
                                                                  int ntiles, DecMats mats) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int ncat = ntiles * 16;
-  const int64_t total = (int64_t)M * ncat;
-  if (i >= total) return;
-  const int row = (int)(i / ncat), cc = (int)(i - (int64_t)row * ncat), tile = cc >> 4;
+  const int cc = (int)blockIdx.x * 256 + (int)threadIdx.x, row = (int)blockIdx.y, tile = cc >> 4;
+  if (cc >= ncat) return;
   const int st1 = sarg(mats.tile0[1]), st2 = sarg(mats.tile0[2]), st3 = sarg(mats.tile0[3]);
   const int mn0 = sarg(mats.mat[0].n), mn1 = sarg(mats.mat[1].n), mn2 = sarg(mats.mat[2].n), mn3 = sarg(mats.mat[3].n);
   const int m = (int)(tile >= st1) + (int)(tile >= st2) + (int)(tile >= st3);
@@ -1466,15 +1468,22 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   if (col >= nm) return;
   // every slice's load in flight at once (one memory round trip for up to
   // 16 slices), then the sum in slice order from -0.0, as splitk_reduce_kernel
+  // (the zeros past ksplit change no sum but an exact -0, which the bias
+  // term below turns into +0 either way)
+  const uint32_t slice = (uint32_t)M * (uint32_t)ncat, end = (uint32_t)ksplit * slice * 4u;
+  const Rsrc rs = make_rsrc(part, end);
+  const uint32_t i = (uint32_t)row * (uint32_t)ncat + (uint32_t)cc;
   constexpr int kBatch = 16;
   float acc = -0.0f;
   for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
     float v[kBatch];
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
+    for (int d = 0; d < kBatch; ++d) {
+      const uint32_t off = z0 + d < ksplit ? ((uint32_t)(z0 + d) * slice + i) * 4u : end;
+      v[d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+    }
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d)
-      if (z0 + d < ksplit) acc += v[d];
+    for (int d = 0; d < kBatch; ++d) acc += v[d];
   }
   float *const y0 = sarg(mats.mat[0].y), *const y1 = sarg(mats.mat[1].y), *const y2 = sarg(mats.mat[2].y),
               *const y3 = sarg(mats.mat[3].y);
@@ -1682,8 +1691,7 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
                        m, ntiles, mats);
     return hipGetLastError();
   }
-  const int64_t total = M * (int64_t)ntiles * 16;
-  hipLaunchKernelGGL(splitk_reduce_mats_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m,
+  hipLaunchKernelGGL(splitk_reduce_mats_kernel, dim3((unsigned)((ntiles * 16 + 255) / 256), (unsigned)M), dim3(256), 0, s, part, ks, m,
                      ntiles, mats);
   return hipGetLastError();
 }
