@@ -1429,22 +1429,28 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int ksplit, int M, int N,
                                                             const float *__restrict__ rscale,
                                                             const float *__restrict__ bias, float *__restrict__ Y) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = (int64_t)M * N;
-  if (i >= total) return;
-  // the slices' loads go out eight at a time (not one round trip per slice);
-  // the sum runs in slice order from -0.0 (x + -0.0 == x, so p0 + p1 + ...)
-  float acc = -0.0f;
-  for (int z0 = 0; z0 < ksplit; z0 += 8) {
-    float v[8];
+  // grid: 256-column blocks x rows (a row stride of gridDim.y beyond 65535
+  // rows), so no thread divides its index
+  const int n = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (n >= N) return;
+  const size_t total = (size_t)M * (size_t)N;
+  const float bn = bias ? bias[n] : 0.0f;
+  for (int m = (int)blockIdx.y; m < M; m += (int)gridDim.y) {
+    const size_t i = (size_t)m * (size_t)N + (size_t)n;
+    // the slices' loads go out eight at a time (not one round trip per
+    // slice); the sum runs in slice order from -0.0 (x + -0.0 == x, so
+    // p0 + p1 + ...)
+    float acc = -0.0f;
+    for (int z0 = 0; z0 < ksplit; z0 += 8) {
+      float v[8];
 #pragma unroll
-    for (int d = 0; d < 8; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
+      for (int d = 0; d < 8; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
 #pragma unroll
-    for (int d = 0; d < 8; ++d)
-      if (z0 + d < ksplit) acc += v[d];
+      for (int d = 0; d < 8; ++d)
+        if (z0 + d < ksplit) acc += v[d];
+    }
+    Y[i] = (rscale ? acc * rscale[m] : acc) + bn;
   }
-  const int m = (int)(i / N), n = (int)(i % N);
-  Y[i] = (rscale ? acc * rscale[m] : acc) + (bias ? bias[n] : 0.0f);
 }
 
 // The decode-batch kernel's partials [ksplit][M][ntiles * 16] over the
@@ -1833,9 +1839,8 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);
   }
   if (e != hipSuccess || ks == 1) return e;
-  const int64_t total = M * N;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s, part, ks, m, n,
-                     rscale, bias, y);
+  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(M, 65535)),
+                     dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
   return hipGetLastError();
 }
 
