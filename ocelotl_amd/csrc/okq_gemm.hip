@@ -1459,7 +1459,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 // Grid: 256-column blocks x rows, so no thread divides its index; the
 // partials are read through a range-checked buffer resource with 32-bit
 // offsets (the decode-batch kernel addresses them so too), slices past
-// ksplit pointed at its end, where they read zeros without a branch.
+// ksplit pointed at its end, where they read zeros without a branch.  KB:
+// the slices loaded per batch, the split rounded up to 4, 8 or 16.
+template <int KB>
 __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__restrict__ part, int ksplit, int M,
                                                                  int ntiles, DecMats mats) {
   const int ncat = ntiles * 16;
@@ -1479,17 +1481,16 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
   const uint32_t slice = (uint32_t)M * (uint32_t)ncat, end = (uint32_t)ksplit * slice * 4u;
   const Rsrc rs = make_rsrc(part, end);
   const uint32_t i = (uint32_t)row * (uint32_t)ncat + (uint32_t)cc;
-  constexpr int kBatch = 16;
   float acc = -0.0f;
-  for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
-    float v[kBatch];
+  for (int z0 = 0; z0 < ksplit; z0 += KB) {
+    float v[KB];
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d) {
+    for (int d = 0; d < KB; ++d) {
       const uint32_t off = z0 + d < ksplit ? ((uint32_t)(z0 + d) * slice + i) * 4u : end;
       v[d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
     }
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d) acc += v[d];
+    for (int d = 0; d < KB; ++d) acc += v[d];
   }
   float *const y0 = sarg(mats.mat[0].y), *const y1 = sarg(mats.mat[1].y), *const y2 = sarg(mats.mat[2].y),
               *const y3 = sarg(mats.mat[3].y);
@@ -1697,8 +1698,10 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
                        m, ntiles, mats);
     return hipGetLastError();
   }
-  hipLaunchKernelGGL(splitk_reduce_mats_kernel, dim3((unsigned)((ntiles * 16 + 255) / 256), (unsigned)M), dim3(256), 0, s, part, ks, m,
-                     ntiles, mats);
+  const dim3 rgrid((unsigned)((ntiles * 16 + 255) / 256), (unsigned)M);
+  if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_mats_kernel<4>, rgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
+  else if (ks <= 8) hipLaunchKernelGGL(splitk_reduce_mats_kernel<8>, rgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
+  else hipLaunchKernelGGL(splitk_reduce_mats_kernel<16>, rgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
   return hipGetLastError();
 }
 
