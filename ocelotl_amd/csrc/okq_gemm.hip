@@ -1507,27 +1507,29 @@ __global__ __launch_bounds__(256) void splitk_reduce_mats_kernel(const float *__
 // reference MLP's buffers (crates/kernels/src/mlp.rs:77-88, :233-238): up(x)
 // in up's output and silu(gate(x)) * up(x) in gate's, with the standalone
 // swiglu kernel's operations in its order (both files build with the same
-// flags), one launch and one round trip fewer.
+// flags), one launch and one round trip fewer.  Grid, offsets and batches
+// as splitk_reduce_mats_kernel.
+template <int KB>
 __global__ __launch_bounds__(256) void splitk_reduce_swiglu_kernel(const float *__restrict__ part, int ksplit, int M,
                                                                    int ntiles, DecMats mats) {
   const int n = sarg(mats.mat[0].n);
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= (int64_t)M * n) return;
-  const int row = (int)(i / n), col = (int)(i - (int64_t)row * n);
-  const int64_t ncat = (int64_t)ntiles * 16, total = (int64_t)M * ncat;
-  const int64_t ig = (int64_t)row * ncat + col, iu = ig + (int64_t)sarg(mats.tile0[1]) * 16;
-  constexpr int kBatch = 16;
+  const int col = (int)blockIdx.x * 256 + (int)threadIdx.x, row = (int)blockIdx.y;
+  if (col >= n) return;
+  const uint32_t ncat = (uint32_t)ntiles * 16u, slice = (uint32_t)M * ncat, end = (uint32_t)ksplit * slice * 4u;
+  const Rsrc rs = make_rsrc(part, end);
+  const uint32_t ig = (uint32_t)row * ncat + (uint32_t)col, iu = ig + (uint32_t)sarg(mats.tile0[1]) * 16u;
   float g = -0.0f, u = -0.0f;
-  for (int z0 = 0; z0 < ksplit; z0 += kBatch) {
-    float vg[kBatch], vu[kBatch];
+  for (int z0 = 0; z0 < ksplit; z0 += KB) {
+    float vg[KB], vu[KB];
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d) {
-      vg[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + ig] : 0.0f;
-      vu[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + iu] : 0.0f;
+    for (int d = 0; d < KB; ++d) {
+      const bool in = z0 + d < ksplit;
+      const uint32_t zo = (uint32_t)(z0 + d) * slice;
+      vg[d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, in ? (zo + ig) * 4u : end, 0, 0));
+      vu[d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, in ? (zo + iu) * 4u : end, 0, 0));
     }
 #pragma unroll
-    for (int d = 0; d < kBatch; ++d)
-      if (z0 + d < ksplit) g += vg[d], u += vu[d];
+    for (int d = 0; d < KB; ++d) g += vg[d], u += vu[d];  // zeros past the split: see splitk_reduce_mats_kernel
   }
   const float *const bg = sarg(mats.mat[0].bias), *const bu = sarg(mats.mat[1].bias);
   g = g + (bg ? bg[col] : 0.0f);
@@ -1693,9 +1695,10 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
   hipError_t e = hipGetLastError();
   if (e != hipSuccess || ks == 1) return e;
   if (swiglu) {
-    const int64_t pairs = M * (int64_t)mats.mat[0].n;
-    hipLaunchKernelGGL(splitk_reduce_swiglu_kernel, dim3((unsigned)((pairs + 255) / 256)), dim3(256), 0, s, part, ks,
-                       m, ntiles, mats);
+    const dim3 sgrid((unsigned)((mats.mat[0].n + 255) / 256), (unsigned)M);
+    if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<4>, sgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
+    else if (ks <= 8) hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<8>, sgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
+    else hipLaunchKernelGGL(splitk_reduce_swiglu_kernel<16>, sgrid, dim3(256), 0, s, part, ks, m, ntiles, mats);
     return hipGetLastError();
   }
   const dim3 rgrid((unsigned)((ntiles * 16 + 255) / 256), (unsigned)M);
