@@ -1426,30 +1426,39 @@ __global__ __launch_bounds__(kDecWaves * 64) void gemm_decode_kernel(const void 
 // Sum of the split-K partials in slice order (deterministic), then the row
 // scale (tiled kernel; the decode-batch kernel's partials are unscaled:
 // rscale == nullptr) and the bias: Y[m, n] = (sum_z P[z][m, n]) * rscale[m] + bias[n].
+// Grid: 256-column blocks x rows (a row stride of gridDim.y beyond 65535
+// rows), so no thread divides its index.  The partials are read through a
+// range-checked buffer resource with 32-bit offsets (K is split only for
+// output grids under 3/4 of the CUs' tiles: at most 8 slices of a few
+// million floats), KB slices per batch, the split rounded up to 2, 4 or 8,
+// slices past it pointed at the end, where they read zeros without a branch.
+template <int KB>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restrict__ part, int ksplit, int M, int N,
                                                             const float *__restrict__ rscale,
                                                             const float *__restrict__ bias, float *__restrict__ Y) {
-  // grid: 256-column blocks x rows (a row stride of gridDim.y beyond 65535
-  // rows), so no thread divides its index
   const int n = (int)blockIdx.x * 256 + (int)threadIdx.x;
   if (n >= N) return;
-  const size_t total = (size_t)M * (size_t)N;
+  const uint32_t total = (uint32_t)M * (uint32_t)N, end = (uint32_t)ksplit * total * 4u;
+  const Rsrc rs = make_rsrc(part, end);
   const float bn = bias ? bias[n] : 0.0f;
   for (int m = (int)blockIdx.y; m < M; m += (int)gridDim.y) {
-    const size_t i = (size_t)m * (size_t)N + (size_t)n;
-    // the slices' loads go out eight at a time (not one round trip per
-    // slice); the sum runs in slice order from -0.0 (x + -0.0 == x, so
-    // p0 + p1 + ...)
+    const uint32_t i = (uint32_t)m * (uint32_t)N + (uint32_t)n;
+    // every slice's load of a batch in flight at once; the sum runs in slice
+    // order from -0.0 (x + -0.0 == x, so p0 + p1 + ...; the zeros past the
+    // split change no sum but an exact -0, which the bias term below turns
+    // into +0 either way)
     float acc = -0.0f;
-    for (int z0 = 0; z0 < ksplit; z0 += 8) {
-      float v[8];
+    for (int z0 = 0; z0 < ksplit; z0 += KB) {
+      float v[KB];
 #pragma unroll
-      for (int d = 0; d < 8; ++d) v[d] = z0 + d < ksplit ? part[(size_t)(z0 + d) * total + i] : 0.0f;
+      for (int d = 0; d < KB; ++d) {
+        const uint32_t off = z0 + d < ksplit ? ((uint32_t)(z0 + d) * total + i) * 4u : end;
+        v[d] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rs, off, 0, 0));
+      }
 #pragma unroll
-      for (int d = 0; d < 8; ++d)
-        if (z0 + d < ksplit) acc += v[d];
+      for (int d = 0; d < KB; ++d) acc += v[d];
     }
-    Y[i] = (rscale ? acc * rscale[m] : acc) + bn;
+    Y[(size_t)i] = (rscale ? acc * rscale[m] : acc) + bn;
   }
 }
 
@@ -1845,8 +1854,11 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);
   }
   if (e != hipSuccess || ks == 1) return e;
-  hipLaunchKernelGGL(splitk_reduce_kernel, dim3((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(M, 65535)),
-                     dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+  if ((int64_t)ks * M * N * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // excluded by gemm_plan
+  const dim3 rgrid((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(M, 65535));
+  if (ks <= 2) hipLaunchKernelGGL(splitk_reduce_kernel<2>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+  else if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_kernel<4>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+  else hipLaunchKernelGGL(splitk_reduce_kernel<8>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
   return hipGetLastError();
 }
 
