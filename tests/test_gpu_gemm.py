@@ -157,6 +157,9 @@ DEC_CASES = [
     # biases, and column blocks that do not divide evenly among the groups
     ("okq_gemm", 17, 1, 256), ("okq_gemm", 32, 5, 512), ("okq_gemm_bf16", 32, 70000, 256),
     ("okq_gemm", 29, 33000, 1024),
+    # more than 16 K slices (32 rows stage 4 super-blocks a slice: 32 and 64
+    # slices): the split-K reduction loads its slices in several batches of 16
+    ("okq_gemm", 32, 300, 32768), ("okq_gemm_bf16", 32, 300, 65536),
 ]
 
 
