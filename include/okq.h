@@ -152,15 +152,16 @@ okq_status okq_linear_out_by_in_q_bf16(const uint16_t *x, int64_t rows, int64_t 
 
 /* okq_linear_out_by_in_q without any device allocation: the same contract,
  * dispatch and kernels (bit-identical outputs), with the MFMA kernels'
- * scratch (activation planes, split-K partials) taken from a static 32 MiB
+ * scratch (activation planes, split-K partials) taken from a static 64 MiB
  * device array instead of the per-stream workspace, so no call allocates or
  * frees memory (hipMalloc, hipFree, or any library routine that allocates).
  * No counterpart in the reference: it serves callers that cannot allocate --
  * code under HIP graph capture, tight serving loops, harnesses that forbid
- * allocation.  Limits: a problem whose scratch exceeds 32 MiB fails with
- * OKQ_E_SHAPE before anything launches (f32 activations: for example up to
- * 32 rows at any Llama-3-8B shape, and the tiled GEMM while 2 x rows x
- * in_features x 2 bytes plus its partials fit); every call on one device
+ * allocation.  Limits: a problem whose scratch exceeds 64 MiB fails with
+ * OKQ_E_SHAPE before anything launches (f32 activations: every Llama-3-8B
+ * shape up to 32 rows, the 128256 x 4096 output head included, whose 32-row
+ * split-K partials take 62.6 MiB; the tiled GEMM while 2 x rows x
+ * in_features x 2 bytes plus its sums and partials fit); every call on one device
  * shares the array and keeps the last call's contents, so calls that overlap
  * on one device (several streams or threads at once) race.  The array's
  * device address is resolved once per device by okq_init (or by the first

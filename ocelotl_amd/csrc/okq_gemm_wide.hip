@@ -61,6 +61,9 @@ __shared__ __attribute__((aligned(16))) _Float16 wA0[kWM * 256];
 __shared__ __attribute__((aligned(16))) _Float16 wA1[kWM * 256];
 __shared__ __attribute__((aligned(16))) _Float16 wX0[kWM * 16];
 __shared__ __attribute__((aligned(16))) _Float16 wX1[kWM * 16];
+// The tile's row scales, read by the epilogue (four consecutive rows per
+// 16-byte read) instead of one dependent global load per output value.
+__shared__ __attribute__((aligned(16))) float wR[kWM];
 
 // 0x6400 | q is the fp16 1024 + q; (1024 + q) * sc - 1024 * sc = sc * q is one
 // fused fp16 FMA with an exact integer result (<= 945).
@@ -107,22 +110,24 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // instruction; lane L of instruction t writes chunk L & 31 of row
   // 16w + 2t + L/32, which holds the row's logical 16-byte chunk
   // (L & 31) ^ (row & 15), so that the fragment reads of 16 consecutive rows
-  // hit distinct banks.  The sums (4 KB): waves 0-3, one instruction each,
-  // lane L takes half L & 1 (four (hi, lo) pairs) of row 32w + L/2.
+  // hit distinct banks.  The sums (4 KB): one instruction per wave, lane L
+  // of wave w takes half L & 1 (four (hi, lo) pairs) of row 32 (w & 3) + L/2.
   uint32_t a_off[8];
 #pragma unroll
   for (int t = 0; t < 8; ++t)
     a_off[t] = (uint32_t)(m0 + 16 * wave + (lane >> 5)) * K32 * 2u +
                16u * ((uint32_t)cl ^ ((uint32_t)(2 * t + (lane >> 5)) & 15u));
+  // (Waves 4-7 repeat the sums of waves 0-3 -- the same bytes to the same
+  // place -- so that every wave issues the same nine loads per stage and the
+  // compiler's vector-load counts stay exact on every path.)
   const uint32_t s_off = ((uint32_t)(m0 + 32 * (wave & 3) + (lane >> 1)) * (K32 / 32u) + 4u * (uint32_t)(lane & 1)) * 4u;
   auto copy_stage = [&](int sb, _Float16 *bufA, _Float16 *bufX) {
 #pragma unroll
     for (int t = 0; t < 8; ++t)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (LdsPtr)(bufA + (16 * wave + 2 * t) * 256), 16, a_off[t],
                                                (int)((uint32_t)t * 4u * K32 + (uint32_t)sb * 512u), 0, 0);
-    if (wave < 4)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_s, (LdsPtr)(bufX + 32 * wave * 16), 16, s_off,
-                                               (int)((uint32_t)sb * 32u), 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_s, (LdsPtr)(bufX + 32 * (wave & 3) * 16), 16, s_off,
+                                             (int)((uint32_t)sb * 32u), 0, 0);
   };
 
   // This lane's weight column n0 + 32w + cl: the 16-byte header of each
@@ -130,13 +135,14 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // the tensor: zeros).  q[t] holds qs bytes 64g + 16t ..; q[0..1] are last
   // used at MFMA step 7 and q[2..3] at step 15, so each pair is reloaded for
   // the next super-block right after its last use (half a super-block
-  // ahead); the header is double buffered.
+  // ahead); the header is double buffered in two register sets that the two
+  // halves of the main loop use alternately (no copy between them).
   const uint32_t w_hd = (uint32_t)(n0 + 32 * wave + cl) * row_bytes;
   const uint32_t w_q = w_hd + 16u + 64u * (uint32_t)g;
   auto ldw = [&](uint32_t voff, int sb) {
     return __builtin_amdgcn_raw_buffer_load_b128(rs_w, voff, (int)((uint32_t)sb * kQ4KBytes), 0);
   };
-  u32x4 q[4], hd, hdn;
+  u32x4 q[4], hdA, hdB;
 
   f16x acc[4], accs[4];
   const f16x zero = {};
@@ -158,7 +164,7 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // (sc, -1024 sc) on 0x6400 | q = 1024 + q; high planes (u odd) take the
   // byte masked in place, 0x6400 | 16 q = 1024 + 16 q, with (sc / 16, -64 sc):
   // the fused product 64 sc + sc q is exact and so is the result sc q.
-  auto scales = [&](int u, h2 &sc2, h2 &off2) {
+  auto scales = [&](const u32x4 &hd, int u, h2 &sc2, h2 &off2) {
     uint32_t sc, mv;
     q4k_scale_min_sel(4u * (uint32_t)g + (uint32_t)u, hd.y, hd.z, hd.w, sc, mv);
     const float f = (float)sc;
@@ -178,17 +184,18 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
     return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   };
 
-  // One super-block sb from (bufA, bufX): 16 MFMA steps of 4 MFMAs, then the
-  // min term into acc and acc += d * accs.  Step s's MFMAs issue while the
-  // A fragments and the B fragment of step s + 1 are read and dequantised.
-  // When `more`, the weights of super-block sb + 1 are reloaded as their
-  // registers free up.
-  auto contract = [&](const _Float16 *bufA, const _Float16 *bufX, int sb, bool more) {
+  // One super-block from (bufA, bufX) with header hd: 16 MFMA steps of 4
+  // MFMAs, then the min term into acc and acc += d * accs.  Step s's MFMAs
+  // issue while the A fragments and the B fragment of step s + 1 are read and
+  // dequantised.  The qs bytes of super-block sb_next are reloaded as their
+  // registers free up (unconditionally: the last super-block reloads itself,
+  // so every path issues the same loads).
+  auto contract = [&](const _Float16 *bufA, const _Float16 *bufX, const u32x4 &hd, int sb_next) {
     h8 a[4], an[4], bv;
     h2 sc2, off2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = a_at(bufA, a_addr(0), i);
-    scales(0, sc2, off2);
+    scales(hd, 0, sc2, off2);
     bv = dequant(0, sc2, off2);
 #pragma unroll
     for (int s = 0; s < 16; ++s) {
@@ -201,9 +208,9 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
 #pragma unroll
         for (int i = 0; i < 4; ++i) an[i] = a_at(bufA, ad, i);
       }
-      if (more && s == 8) {  // q[0..1] last used at step 7
-        q[0] = ldw(w_q, sb + 1);
-        q[1] = ldw(w_q + 16u, sb + 1);
+      if (s == 8) {  // q[0..1] last used at step 7
+        q[0] = ldw(w_q, sb_next);
+        q[1] = ldw(w_q + 16u, sb_next);
       }
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
@@ -211,16 +218,15 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
         accs[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv, s == 0 ? zero : accs[i], 0, 0, 0);
       __builtin_amdgcn_s_setprio(0);
       if (s < 15) {
-        if (((s + 1) & 3) == 0) scales((s + 1) >> 2, sc2, off2);
+        if (((s + 1) & 3) == 0) scales(hd, (s + 1) >> 2, sc2, off2);
         bv = dequant(s + 1, sc2, off2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) a[i] = an[i];
       }
     }
-    if (more) {  // q[2..3] last used at step 15
-      q[2] = ldw(w_q + 32u, sb + 1);
-      q[3] = ldw(w_q + 48u, sb + 1);
-    }
+    // q[2..3] last used at step 15
+    q[2] = ldw(w_q + 32u, sb_next);
+    q[3] = ldw(w_q + 48u, sb_next);
     // min term: lane group g holds the (hi, lo) sums of sub-blocks 4g .. 4g+3
     // of its row, B the matching -dmin * m planes (each value twice)
     h8 xa[4];
@@ -247,66 +253,96 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
 #pragma unroll
       for (int e = 0; e < 16; ++e) acc[i][e] = __builtin_fmaf(dv, accs[i][e], acc[i][e]);
     }
-    hd = hdn;
   };
 
-  // Pipeline: super-block i reads activation buffer i & 1 while the next
-  // super-block's activations are copied into the other (issued first at the
-  // start of i, ahead of its header and the qs reloads, so waiting for all
-  // but the last four vector loads -- the reloads -- at the end of i waits
-  // for the copy and the header), one barrier per super-block.
+  // Pipeline: super-block i reads activation buffer i & 1 and header set
+  // (hdA, hdB)[i & 1] while the next super-block's activations are copied
+  // into the other buffer and its header into the other set (issued first
+  // at the start of i, ahead of the qs reloads, so waiting for all but the
+  // last four vector loads -- the reloads -- at the end of i waits for the
+  // copy and the header), one barrier per super-block.  Every stage issues
+  // the same loads (the last one reloads its own super-block into the idle
+  // buffer), so no path leaves the compiler an inexact load count and no
+  // wait covers the reloads in flight.
+  const int last = nsb - 1;
+  auto nxt = [&](int i) { return sb0 + (i + 1 < last ? i + 1 : last); };
   copy_stage(sb0, wA0, wX0);
-  hd = ldw(w_hd, sb0);
+  if (tid < kWM) wR[tid] = m0 + tid < M ? rscale[m0 + tid] : 0.0f;
+  hdA = ldw(w_hd, sb0);
 #pragma unroll
   for (int t = 0; t < 4; ++t) q[t] = ldw(w_q + 16u * t, sb0);
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   __syncthreads();
   constexpr int kWaitCopy = 0x0074;  // vmcnt(4) expcnt(7) lgkmcnt(0), gfx9 encoding
-  for (int i = 0; i < nsb; i += 2) {
-    const bool more1 = i + 1 < nsb;
-    if (more1) {
-      copy_stage(sb0 + i + 1, wA1, wX1);
-      hdn = ldw(w_hd, sb0 + i + 1);
-    }
-    contract(wA0, wX0, sb0 + i, more1);
-    if (more1) {
-      __builtin_amdgcn_s_waitcnt(kWaitCopy);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
+  for (int i = 0;; i += 2) {
+    copy_stage(nxt(i), wA1, wX1);
+    hdB = ldw(w_hd, nxt(i));
+    contract(wA0, wX0, hdA, nxt(i));
+    __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
-    if (!more1) break;
-    const bool more2 = i + 2 < nsb;
-    if (more2) {
-      copy_stage(sb0 + i + 2, wA0, wX0);
-      hdn = ldw(w_hd, sb0 + i + 2);
-    }
-    contract(wA1, wX1, sb0 + i + 1, more2);
-    if (more2) {
-      __builtin_amdgcn_s_waitcnt(kWaitCopy);
-    } else {
-      __builtin_amdgcn_s_waitcnt(0);
-    }
+    if (i + 1 >= nsb) break;
+    copy_stage(nxt(i + 1), wA0, wX0);
+    hdA = ldw(w_hd, nxt(i + 1));
+    contract(wA1, wX1, hdB, nxt(i + 1));
+    __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
+    if (i + 2 >= nsb) break;
   }
+  // The last stage's copy into the idle buffer and its reloads must land
+  // before the workgroup's LDS is released.  The empty asm reads the
+  // prefetched registers on the way out, so that the loads a stage issues
+  // for the next one are live on both sides of the exit test between the
+  // two halves of the loop: the compiler cannot sink them past the test to
+  // just before their first use, where each would wait out its latency.
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::"v"(hdA), "v"(hdB), "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]));
 
   // epilogue: lane (cl, g) holds rows 8 (e / 4) + 4 g + e % 4 of column cl
-  // of each 32 x 32 block
+  // of each 32 x 32 block; split K stores the raw partial sums, otherwise the
+  // row scale (from LDS) and the bias are applied
+  // A whole tile stores without per-value row tests: branches there would
+  // leave loads pending at every join and cost a wait per store.
   const int col = n0 + 32 * wave + cl;
+  const int rows = M - m0 < kWM ? M - m0 : kWM;
   if (col < N) {
-    const float bv = (ksplit == 1 && bias) ? bias[col] : 0.0f;
+    if (ksplit > 1) {
+      float *dst = part + ((size_t)z * M + m0) * N + col;
+      auto store = [&](bool guard) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+        for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = m0 + 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
-        if (row >= M) continue;
-        if (ksplit > 1) {
-          part[((size_t)z * M + row) * N + col] = acc[i][e];
-        } else {
-          Y[(size_t)row * N + col] = acc[i][e] * rscale[row] + bv;
-        }
+          for (int e = 0; e < 16; ++e) {
+            const int r = 32 * i + 8 * (e >> 2) + 4 * g + (e & 3);
+            if (!guard || r < rows) dst[(size_t)r * N] = acc[i][e];
+          }
+      };
+      if (rows == kWM) {
+        store(false);
+      } else {
+        store(true);
       }
+    } else {
+      const float bv = bias ? bias[col] : 0.0f;
+      float *dst = Y + (size_t)m0 * N + col;
+      auto store = [&](bool guard) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r0 = 32 * i + 8 * j + 4 * g;
+            const float4 rs = *reinterpret_cast<const float4 *>(wR + r0);
+            const float rv[4] = {rs.x, rs.y, rs.z, rs.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (!guard || r0 + q < rows) dst[(size_t)(r0 + q) * N] = acc[i][4 * j + q] * rv[q] + bv;
+          }
+      };
+      if (rows == kWM) {
+        store(false);
+      } else {
+        store(true);
+      }
+    }
   }
 }
 

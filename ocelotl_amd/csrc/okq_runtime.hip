@@ -207,9 +207,12 @@ okq_status validate_rmsnorm(const float *x, int64_t rows, int64_t hidden, const 
 // A buffer is never freed once handed out.  A graph captured earlier keeps
 // the pointer it recorded, and another host thread may have looked up the
 // buffer and not yet enqueued its kernel, so a grown slot moves to a new
-// buffer and the old one stays allocated until the process ends.  Growth is
-// by half again of the request, so the buffers of one slot stay within about
-// three times its largest request.
+// buffer and the old one stays allocated until the process ends.  Each growth
+// allocates half again of its request, and a request that grows the slot
+// exceeds the previous allocation (itself 1.5x an earlier request), so a
+// slot's buffers sum to at most about 4.5 times its largest request
+// (1.5 R (1 + 2/3 + 4/9 + ...)), kept per (device, stream, slot) until the
+// process ends, also after the stream is destroyed.
 struct Workspace {
   void *ptr = nullptr;
   size_t bytes = 0;
@@ -296,7 +299,7 @@ bool gemv_serves(uint32_t, int64_t rows, int64_t K, uint64_t w_bytes) {
 // host-side stand-in).  Calls on one device share the array: overlapping calls
 // (several streams or threads at once) race.  Nothing in it needs clearing:
 // every kernel writes the scratch it later reads.
-constexpr size_t kScratchBytes = 32u << 20;
+constexpr size_t kScratchBytes = 64u << 20;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 
 std::mutex g_scratch_mutex;
@@ -462,8 +465,12 @@ okq_status okq_init(int ordinal) {
   DevInfo info;
   okq_status st = current_device(dev, info);
   if (st != OKQ_OK) return st;
+  // Resolve the allocation-free entry point's scratch address on this device
+  // now, best effort: a failure concerns only that entry point, which looks
+  // the address up again (and reports the failure) on its first call.
   void *p = nullptr;
-  return scratch_for(dev, &p);  // the allocation-free entry point's scratch address on this device
+  if (scratch_for(dev, &p) != OKQ_OK) g_last_error.clear();
+  return ok();
 }
 
 okq_status okq_alloc(void **ptr, size_t bytes) {
