@@ -29,7 +29,8 @@ COMMON = [
 EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=off"],
          # MFMA accumulators in VGPRs where they fit: the per-super-block sums
          # then feed the f32 scaling without AGPR round trips
-         "okq_gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+         "okq_gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "okq_gemm_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

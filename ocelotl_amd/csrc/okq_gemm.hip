@@ -1622,14 +1622,35 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     if (ks == 1 && mytiles > kDecMaxTiles)
       p.groups = (int)((ntiles + (int64_t)kDecWaves * kDecMaxTiles - 1) / ((int64_t)kDecWaves * kDecMaxTiles));
   } else {
-    // Q4_K with bf16 activations: the kernel that dequantises the weights in
-    // registers (128 x 256 tiles); everything else: the tiled kernel
-    p.wide = x_is_bf16 && gemm_wide_supported(type, M, K, N) ? 1 : 0;
-    p.bm = p.wide ? 128 : (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
-    const int64_t tiles = p.wide ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
-    // Split K when the tiles alone leave CUs idle: enough slices for about
-    // one workgroup per CU, at least two super-blocks per slice, at most 8.
-    if (tiles * 4 < (int64_t)cu_count * 3) ks = std::min<int64_t>({(cu_count + tiles - 1) / tiles, nsb / 2, 8});
+    // Q4_K with bf16 activations: a kernel that dequantises the weights in
+    // registers; everything else: the tiled kernel.  Split K when the tiles
+    // alone leave CUs idle: enough slices for about one workgroup per CU, at
+    // least two super-blocks per slice, at most 8.
+    const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
+    p.bm = reg_dequant ? 128 : (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
+    const int64_t cus = cu_count;
+    const int64_t tiles = reg_dequant ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
+    if (tiles * 4 < cus * 3) ks = std::min<int64_t>({(cus + tiles - 1) / tiles, nsb / 2, 8});
+    if (reg_dequant) {
+      // gemm_wide_q4k_kernel (128 x 256 tiles, one 8-wave workgroup per CU)
+      // while its workgroups fill at least 3/4 of their rounds of CUs (C4,
+      // us per call: M=512 gate 76.9 vs 86.7 for the other kernel, down 85.5
+      // vs 91.2, q 40.0 vs 41.1; M=2048 gate 292 vs 296, down 268 vs 301);
+      // otherwise gemm_pair_q4k_kernel (128 x 128 tiles, two 4-wave
+      // workgroups per CU), whose finer tiles and slices occupy every CU
+      // where the wide ones cannot (M=128 gate 39.5 vs 56.3, down 36.6 vs
+      // 42.8, q 24.2 vs 26.3; M=512 v 25.3 vs 27.8), with as many slices as
+      // fit one round of two workgroups per CU.
+      const int64_t jobs = tiles * std::max<int64_t>(1, ks);
+      const int64_t rounds = (jobs + cus - 1) / cus;
+      if (jobs * 4 >= rounds * cus * 3) {
+        p.wide = 1;
+      } else {
+        p.wide = 2;
+        const int64_t ptiles = gemm_pair_tiles(M, N), slots = 2 * cus;
+        ks = ptiles * 4 < slots * 3 ? std::max<int64_t>(1, std::min<int64_t>({slots / ptiles, nsb / 2, 8})) : 1;
+      }
+    }
   }
   p.ksplit = (int)std::max<int64_t>(1, ks);
   auto up = [](size_t v) { return (v + 255) & ~(size_t)255; };
@@ -1848,7 +1869,9 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
 #undef OKQ_PREP
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (plan.wide) {
+  if (plan.wide == 2) {
+    e = launch_gemm_pair(xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
+  } else if (plan.wide) {
     e = launch_gemm_wide(xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
   } else {
     e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);

@@ -121,11 +121,11 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // place -- so that every wave issues the same nine loads per stage and the
   // compiler's vector-load counts stay exact on every path.)
   const uint32_t s_off = ((uint32_t)(m0 + 32 * (wave & 3) + (lane >> 1)) * (K32 / 32u) + 4u * (uint32_t)(lane & 1)) * 4u;
-  auto copy_stage = [&](int sb, _Float16 *bufA, _Float16 *bufX) {
-#pragma unroll
-    for (int t = 0; t < 8; ++t)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (LdsPtr)(bufA + (16 * wave + 2 * t) * 256), 16, a_off[t],
-                                               (int)((uint32_t)t * 4u * K32 + (uint32_t)sb * 512u), 0, 0);
+  auto copy_piece = [&](int t, int sb, _Float16 *bufA) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (LdsPtr)(bufA + (16 * wave + 2 * t) * 256), 16, a_off[t],
+                                             (int)((uint32_t)t * 4u * K32 + (uint32_t)sb * 512u), 0, 0);
+  };
+  auto copy_sums = [&](int sb, _Float16 *bufX) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_s, (LdsPtr)(bufX + 32 * (wave & 3) * 16), 16, s_off,
                                              (int)((uint32_t)sb * 32u), 0, 0);
   };
@@ -187,10 +187,15 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // One super-block from (bufA, bufX) with header hd: 16 MFMA steps of 4
   // MFMAs, then the min term into acc and acc += d * accs.  Step s's MFMAs
   // issue while the A fragments and the B fragment of step s + 1 are read and
-  // dequantised.  The qs bytes of super-block sb_next are reloaded as their
-  // registers free up (unconditionally: the last super-block reloads itself,
-  // so every path issues the same loads).
-  auto contract = [&](const _Float16 *bufA, const _Float16 *bufX, const u32x4 &hd, int sb_next) {
+  // dequantised.  Super-block sb_next is prefetched meanwhile
+  // (unconditionally: the last super-block reloads itself, so every path
+  // issues the same loads): its activations into (nbufA, nbufX), one copy
+  // instruction per step over steps 0-8 -- issued all at once, the eight
+  // waves' 72 copy instructions queue at the vector memory unit and hold
+  // every wave's MFMAs back at the start of each super-block --, its qs
+  // bytes as their registers free up.
+  auto contract = [&](const _Float16 *bufA, const _Float16 *bufX, const u32x4 &hd, int sb_next, _Float16 *nbufA,
+                      _Float16 *nbufX) {
     h8 a[4], an[4], bv;
     h2 sc2, off2;
 #pragma unroll
@@ -208,7 +213,9 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
 #pragma unroll
         for (int i = 0; i < 4; ++i) an[i] = a_at(bufA, ad, i);
       }
-      if (s == 8) {  // q[0..1] last used at step 7
+      if (s < 8) copy_piece(s, sb_next, nbufA);
+      if (s == 8) {  // the sums, then q[0..1] (last used at step 7)
+        copy_sums(sb_next, nbufX);
         q[0] = ldw(w_q, sb_next);
         q[1] = ldw(w_q + 16u, sb_next);
       }
@@ -256,17 +263,18 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   };
 
   // Pipeline: super-block i reads activation buffer i & 1 and header set
-  // (hdA, hdB)[i & 1] while the next super-block's activations are copied
-  // into the other buffer and its header into the other set (issued first
-  // at the start of i, ahead of the qs reloads, so waiting for all but the
-  // last four vector loads -- the reloads -- at the end of i waits for the
-  // copy and the header), one barrier per super-block.  Every stage issues
-  // the same loads (the last one reloads its own super-block into the idle
-  // buffer), so no path leaves the compiler an inexact load count and no
-  // wait covers the reloads in flight.
+  // (hdA, hdB)[i & 1] while the next super-block's header (first) and
+  // activations (steps 0-8) go into the other set and buffer, ahead of the
+  // qs reloads, so waiting for all but the last four vector loads -- the
+  // reloads -- at the end of i waits for the copy and the header; one barrier
+  // per super-block.  Every stage issues the same loads (the last one reloads
+  // its own super-block into the idle buffer), so no path leaves the compiler
+  // an inexact load count and no wait covers the reloads in flight.
   const int last = nsb - 1;
   auto nxt = [&](int i) { return sb0 + (i + 1 < last ? i + 1 : last); };
-  copy_stage(sb0, wA0, wX0);
+#pragma unroll
+  for (int t = 0; t < 8; ++t) copy_piece(t, sb0, wA0);
+  copy_sums(sb0, wX0);
   if (tid < kWM) wR[tid] = m0 + tid < M ? rscale[m0 + tid] : 0.0f;
   hdA = ldw(w_hd, sb0);
 #pragma unroll
@@ -275,15 +283,13 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   __syncthreads();
   constexpr int kWaitCopy = 0x0074;  // vmcnt(4) expcnt(7) lgkmcnt(0), gfx9 encoding
   for (int i = 0;; i += 2) {
-    copy_stage(nxt(i), wA1, wX1);
     hdB = ldw(w_hd, nxt(i));
-    contract(wA0, wX0, hdA, nxt(i));
+    contract(wA0, wX0, hdA, nxt(i), wA1, wX1);
     __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
     if (i + 1 >= nsb) break;
-    copy_stage(nxt(i + 1), wA0, wX0);
     hdA = ldw(w_hd, nxt(i + 1));
-    contract(wA1, wX1, hdB, nxt(i + 1));
+    contract(wA1, wX1, hdB, nxt(i + 1), wA0, wX0);
     __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
     if (i + 2 >= nsb) break;
