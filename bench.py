@@ -24,6 +24,12 @@ The JSON line also carries:
                 weight replicas per matrix, vs 8 TB/s; `traffic` is the HBM
                 bytes per launch from rocprofv3 FETCH_SIZE and WRITE_SIZE passes
                 (profiles/gemv_q4k_gate_up_traffic.md)
+  roofline_gemm the prefill half of the metric: the Q4_K GEMM kernel of the
+                C4 M=512 gate call (14336x4096, bf16 activations), 2*M*N*K
+                flops / its average dispatch duration (stream events around
+                each launch) vs the 2.5 PFLOP/s dense fp16/bf16 MFMA peak;
+                `traffic` from rocprofv3 FETCH_SIZE / WRITE_SIZE passes
+                (profiles/gemm_q4k_m512_gate_counters.md)
   cpu_baseline  the reference CPU path (oracle restatement of
                 linear_out_by_in, scalar mode, 1 core since rows < 32) on one
                 layer copy, dequantized once outside the timing, with a check
@@ -35,7 +41,7 @@ The JSON line also carries:
                 C4 per call, C5)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate_up|copy|gemm_gate512|decode_gate_up32
+     python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|decode_gate_up32
                                                         (bare workloads for counter passes)
 """
 from __future__ import annotations
@@ -315,14 +321,15 @@ def run_c2(ctx: Ctx, args):
 
 
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemv_q4k_gate_up_traffic.md")
+GEMM_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_q4k_m512_gate_counters.md")
 
 
-def measured_traffic():
-    """HBM bytes per launch of the roofline kernel from the committed
-    rocprofv3 FETCH_SIZE / WRITE_SIZE summary (line `traffic_bytes_per_launch:
-    N`), or None when no such measurement is committed."""
+def measured_traffic(path=TRAFFIC_FILE):
+    """HBM bytes per launch of a roofline kernel from a committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (line `traffic_bytes_per_launch: N`), or
+    None when no such measurement is committed."""
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             for line in f:
                 if line.strip().startswith("traffic_bytes_per_launch:"):
                     return int(line.split(":", 1)[1].strip().split()[0])
@@ -342,6 +349,23 @@ def roofline_from(launches):
             "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": measured_traffic(),
             "algorithmic_bytes_per_launch": s["weight_bytes"], "launch_us_mean": s["us_mean"]}
+
+
+def roofline_gemm_from(c4):
+    """The prefill half of the metric: the Q4_K GEMM kernel of the C4 M=512
+    gate call (the dominant prefill shape), algorithmic flops 2*M*N*K per
+    launch over the kernel's average dispatch duration."""
+    r = c4.get("M512_gate")
+    if r is None:
+        return None
+    flops = 2 * r["m"] * r["n"] * r["k"]
+    achieved = flops / r["us_kernel"] / 1e6
+    return {"bound": "mfma", "kernel": r.get("kernel", "okq::gemm_wide_q4k_kernel"),
+            "shape": "M=512 x N=14336 x K=4096 (C4 gate, bf16 activations)",
+            "achieved": round(achieved, 1), "peak": BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / BF16_PEAK_TFLOPS, 4), "traffic": measured_traffic(GEMM_TRAFFIC_FILE),
+            "algorithmic_flops_per_launch": flops, "launch_us_mean": r["us_kernel"],
+            "per_call_frac": r["frac_bf16_peak"], "per_call_us": r["us_call"]}
 
 
 # ---------------------------------------------------------------------------
@@ -446,6 +470,9 @@ def run_c4(ctx: Ctx, args, c2):
             t_k = sum(us) / len(us)
             flops = 2.0 * m * n * k
             key = f"M{m}_{name}" if t == Q4K else f"M{m}_q8_0_4096"
+            kernel = None
+            if key == "M512_gate":  # the plan's choice at 256 CUs (gemm_plan, okq_gemm.hip)
+                kernel = "okq::gemm_wide_q4k_kernel (128x256 tiles, 8 waves, weights dequantised in registers)"
             res[key] = {"type": "Q4_K" if t == Q4K else "Q8_0", "m": m, "n": n, "k": k,
                         "us_call": round(t_call, 2), "us_call_p10": round(pct(per, 10), 2),
                         "us_call_median": round(median(per), 2), "us_call_p90": round(pct(per, 90), 2),
@@ -453,6 +480,8 @@ def run_c4(ctx: Ctx, args, c2):
                         "frac_bf16_peak": round(flops / t_call / 1e6 / BF16_PEAK_TFLOPS, 4),
                         "us_kernel": round(t_k, 2), "tflops_kernel": round(flops / t_k / 1e6, 1),
                         "frac_bf16_peak_kernel": round(flops / t_k / 1e6 / BF16_PEAK_TFLOPS, 4)}
+            if kernel:
+                res[key]["kernel"] = kernel
     del q8
     return res
 
@@ -628,12 +657,24 @@ def run_cpu_baseline(ctx: Ctx, c2, args):
         launch_group(ctx, names, lay, c2["x14336"] if C2_SHAPE[names[0]][1] == 14336 else c2["x4096"], gpu_out)
     ctx.torch.cuda.synchronize()
     parity = all(O.allclose_ref_rule(gpu_out[name].cpu().numpy(), cpu_out[name], 1e-3)[0] for name, _, _ in C2_PROJ)
+    # the timed step's error against the reference CPU path: largest absolute
+    # difference, and largest relative one over outputs with |want| >= 1e-3
+    abs_err, rel_err = 0.0, 0.0
+    for name, _, _ in C2_PROJ:
+        got = gpu_out[name].cpu().numpy().astype(np.float64)
+        want = cpu_out[name].astype(np.float64)
+        d = np.abs(got - want)
+        abs_err = max(abs_err, float(d.max()))
+        big = np.abs(want) >= 1e-3
+        if big.any():
+            rel_err = max(rel_err, float((d[big] / np.abs(want[big])).max()))
     head = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"C2 layer copy 0 (7 Q4_K projections, {c2['step_bytes']} quantized bytes) dequantized to f32 "
                       f"once (untimed); reference scalar linear_out_by_in, batch 1, serial (rows < 32); "
                       f"{passes} passes in {sec_pass * passes:.2f} s on {model}",
             "ms_per_step": round(1000.0 * sec_pass, 2),
-            "gpu_outputs_match_cpu_within_rule": bool(parity)}
+            "gpu_outputs_match_cpu_within_rule": bool(parity),
+            "gpu_vs_cpu_max_abs_err": float(f"{abs_err:.3g}"), "gpu_vs_cpu_max_rel_err": float(f"{rel_err:.3g}")}
     if args.cpu_configs:
         head["configs"] = run_cpu_configs(ctx, orc, O, args)
     return head
@@ -666,20 +707,32 @@ def run_cpu_configs(ctx: Ctx, orc, O, args):
         res["c3_q6_k_head_scalar"] = {"us_per_call": round(1e6 * t, 1), "gbs": round(wq.size / t / 1e9, 3), "cores": 1,
                                       "calls": calls}
         del wf
-    # C4: Q4_K prefill at M = 128 and 512 on q (4096 x 4096), rows chunked over the host cores
-    wq = ctx.quantized(Q4K, 4096, 4096, seed=10_000).cpu().numpy()
-    wf = orc.dequantize(O.Q4_K, wq, 4096 * 4096).reshape(4096, 4096)
-    for m in (128, 512):
-        xb = orc.f32_to_bf16(orc.normal(50 + m, m * 4096, 1.0))
+    # C4: Q4_K prefill at M = 128, 512, 2048 on the q (4096 x 4096), gate
+    # (14336 x 4096) and down (4096 x 14336) shapes, rows chunked over the
+    # host cores as the reference does at rows >= 32 (each sample at least
+    # one whole call)
+    c4_cases = [(m, name, n, k, n) for m in (128, 512, 2048)
+                for name, n, k in (("q", 4096, 4096), ("gate", 14336, 4096), ("down", 4096, 14336))]
+    wcache = {}
+    for m, name, n, k, n_s in c4_cases:
+        if (name, n_s) not in wcache:
+            seed = {"q": 10_000, "gate": 10_004, "down": 10_006}[name]
+            rb = (k // 256) * 144
+            wq = ctx.quantized(Q4K, n, k, seed=seed).cpu().numpy()[: n_s * rb]
+            wcache[(name, n_s)] = orc.dequantize(O.Q4_K, wq, n_s * k).reshape(n_s, k)
+        wf = wcache[(name, n_s)]
+        xb = orc.f32_to_bf16(orc.normal(50 + m, m * k, 1.0))
         x = orc.bf16_to_f32(xb)
         for mode, label in ((O.MODE_SCALAR, "scalar"), (O.MODE_AVX2, "avx2")):
             if mode == O.MODE_AVX2 and not orc.has_avx2():
                 continue
-            t, calls = cpu_time(lambda: orc.linear(x, m, 4096, wf, 4096, None, mode, thr), sec)
-            res[f"c4_M{m}_q_{label}"] = {"us_per_call": round(1e6 * t, 1),
-                                          "tflops": round(2.0 * m * 4096 * 4096 / t / 1e12, 4), "cores": thr,
-                                          "calls": calls}
-    del wf
+            t, calls = cpu_time(lambda: orc.linear(x, m, k, wf, n_s, None, mode, thr), sec)
+            rec = {"us_per_call": round(1e6 * t * n / n_s, 1), "tflops": round(2.0 * m * n_s * k / t / 1e12, 4),
+                   "cores": thr, "calls": calls}
+            if n_s < n:
+                rec["sample"] = f"{n_s} of {n} output features per call, time scaled by {n / n_s:g}"
+            res[f"c4_M{m}_{name}_{label}"] = rec
+    del wcache
     # C5: one Q4_K_M layer (Q6_K v and down) at batch 1, 8 (serial) and 32 (all cores)
     lay = {name: ctx.quantized(t, n, k, seed=50_000 + i).cpu().numpy() for i, (name, t, n, k) in enumerate(C5_PROJ)}
     wl = {name: orc.dequantize(t, lay[name], n * k).reshape(n, k) for name, t, n, k in C5_PROJ}
@@ -730,8 +783,9 @@ def run_probe(ctx: Ctx, what: str):
                          (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs]), ctx.stream)
         log(f"probe decode_gate_up32: 20 calls of 32 rows over gate+up ({2 * b} weight bytes each): "
             f"one decode-batch launch and its split-K reduction per call")
-    elif what == "gemm_gate512":
-        n, k, m = 14336, 4096, 512
+    elif what.startswith("gemm_"):
+        m, n, k = {"gemm_gate512": (512, 14336, 4096), "gemm_down512": (512, 4096, 14336),
+                   "gemm_gate128": (128, 14336, 4096)}[what]
         ws = [ctx.quantized(Q4K, n, k, seed=10_004 + c) for c in range(4)]
         xf = ctx.normal(m * k, 562)
         xb = torch.empty(m * k, dtype=torch.int16, device="cuda")
@@ -739,7 +793,7 @@ def run_probe(ctx: Ctx, what: str):
         y = torch.empty(m * n, dtype=torch.float32, device="cuda")
         for i in range(20):
             ctx.gemv(Q4K, xb, k, ws[i % len(ws)], n, y, entry="okq_gemm_bf16", rows=m)
-        log(f"probe gemm_gate512: 20 Q4_K GEMM calls M={m} N={n} K={k} (bf16), {2 * m * n * k} flops each")
+        log(f"probe {what}: 20 Q4_K GEMM calls M={m} N={n} K={k} (bf16), {2 * m * n * k} flops each")
     else:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
         dst = torch.empty_like(src)
@@ -767,10 +821,12 @@ def main():
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
     ap.add_argument("--only", default="c1,c3,c4,c5", help="secondary configs to run (comma list of c1,c3,c4,c5)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
-    ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "decode_gate_up32"], default=None,
+    ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "gemm_down512", "gemm_gate128",
+                                        "decode_gate_up32"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
                          "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), 20 Q4_K "
-                         "GEMM calls at M=512 on the gate shape, or 20 gate+up calls at 32 rows (decode-batch kernel)")
+                         "GEMM calls (M=512 gate or down, M=128 gate), or 20 gate+up calls at 32 rows "
+                         "(decode-batch kernel)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
@@ -815,7 +871,9 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "q4_k weights x f32 activations (int8 dot4 -> i32, f32 scale/accumulate)",
+        "dtype": "q4_k weights (4-bit ints, 6-bit scales/mins, f16 d/dmin) x f32 activations encoded per 32-run as "
+                 "16-bit block integers (two int8 limbs; a third limb, 24 bits, only on outlier runs) with a power-of-2 "
+                 "run scale; v_dot4_i32_i8 -> exact i32 sums; f32 scale and accumulate",
         "data": "synthetic: seeded N(0,0.02) weights quantized to Q4_K on the GPU, N(0,1) f32 activations",
         "config": {"workload": "C2: Q4_K decode GEMV, one Llama-3-8B layer per step (q 4096x4096, k/v 1024x4096, "
                                "o 4096x4096, gate/up 14336x4096, down 4096x14336), batch 1, as 4 launches: "
@@ -824,6 +882,7 @@ def main():
                    "weight_bytes_per_step": c2["step_bytes"],
                    "frac_hbm_peak": round(c2["gbs"] / HBM_PEAK_GBS, 4)},
         "roofline": roofline_from(c2["launches"]),
+        "roofline_gemm": roofline_gemm_from(extra["c4_q4_k_gemm_bf16"]) if "c4_q4_k_gemm_bf16" in extra else None,
         "cpu_baseline": cpu,
         "extra": extra,
     }

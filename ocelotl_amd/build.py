@@ -46,7 +46,8 @@ def _compile(src: str) -> str:
     return obj
 
 
-HOST_SRC = [os.path.join(HERE, "host", f) for f in ("kernel_backend.cpp", "gguf.cpp", "dequant_policy.cpp")]
+HOST_SRC = [os.path.join(HERE, "host", f)
+            for f in ("kernel_backend.cpp", "gguf.cpp", "dequant_policy.cpp", "dequant_host.cpp")]
 HOST_LIB = os.path.join(HERE, "libocelotl_hip.so")
 CXX = os.environ.get("CXX", "g++")
 
@@ -56,7 +57,9 @@ def build_host(verbose: bool = False) -> str:
     boundary; host/gguf.*: the GGUF loader), a plain C++17 library over okq.h
     linked against libokq.so."""
     tmp = HOST_LIB + ".tmp"
-    cmd = [CXX, "-std=c++17", "-O2", "-Wall", "-Wextra", "-fPIC", "-shared", "-I", os.path.join(HERE, "..", "include"),
+    # no FMA contraction: the host decoders round every product on its own
+    cmd = [CXX, "-std=c++17", "-O2", "-ffp-contract=off", "-Wall", "-Wextra", "-fPIC", "-shared",
+           "-I", os.path.join(HERE, "..", "include"),
            "-I", os.path.join(HERE, "host"), *HOST_SRC, "-o", tmp, "-L", HERE, "-lokq", "-Wl,-rpath,$ORIGIN"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

@@ -4,11 +4,13 @@
 #include "kernel_backend.hpp"
 
 #include <cstdint>
+#include <optional>
 #include <cstdio>
 #include <cstring>
 #include <limits>
 #include <mutex>
 
+#include "dequant_host.hpp"
 #include "okq.h"
 
 namespace ocelotl {
@@ -227,7 +229,107 @@ Result<void> DeviceTensor::write_from_host_slice(const float *src, size_t len) c
   return check(okq_sync(stream_));  // the host slice may be reused on return
 }
 
-const void *QuantizedWeight::device_ptr() const { return buf_->ptr; }
+Result<QuantizedWeight> QuantizedWeight::from_host(GgmlTensorType type, size_t ne0, size_t ne1,
+                                                   std::vector<uint8_t> blocks) {
+  auto want = tensor_byte_len(type, {(int64_t)ne0, (int64_t)ne1});
+  if (want.is_err()) return want.error();
+  if (blocks.size() != want.value()) {
+    return kernel_err("quantized weight has " + std::to_string(blocks.size()) + " bytes, shape [" +
+                      std::to_string(ne0) + ", " + std::to_string(ne1) + "] needs " + std::to_string(want.value()));
+  }
+  QuantizedWeight w(type, ne0, ne1, blocks.size(), nullptr);
+  w.host_ = std::make_shared<const std::vector<uint8_t>>(std::move(blocks));
+  return w;
+}
+
+Residency QuantizedWeight::residency() const {
+  if (host_) return Residency{Residency::Kind::Host, nullptr};
+  return Residency{Residency::Kind::Device, kBackend};
+}
+
+const void *QuantizedWeight::device_ptr() const { return buf_ ? buf_->ptr : nullptr; }
+
+Result<std::vector<uint8_t>> QuantizedWeight::to_host_bytes() const {
+  if (host_) return *host_;
+  std::vector<uint8_t> v((size_t)bytes_);
+  if (v.empty()) return v;
+  Result<void> r = check(okq_memcpy_d2h(v.data(), buf_->ptr, v.size(), nullptr));
+  if (r.is_err()) return r.error();
+  r = check(okq_sync(nullptr));
+  if (r.is_err()) return r.error();
+  return v;
+}
+
+// ---- trait defaults ------------------------------------------------------------
+
+namespace {
+// The checks of validate_linear_out_by_in (lib.rs:2443-2497) for a quantized
+// weight, in order: weight shape against the features, then x, bias and out
+// lengths.
+Result<void> validate_quantized_linear(const char *backend, size_t x_len, size_t rows, size_t in_features,
+                                       const QuantizedWeight &weight, size_t out_features, bool has_bias,
+                                       size_t bias_len, size_t out_len) {
+  auto err = [&](const std::string &m) { return OcelotlError::kernel(backend, m); };
+  if (weight.ne0() != in_features || weight.ne1() != out_features) {
+    return err("linear_out_by_in weight shape [" + std::to_string(weight.ne0()) + ", " + std::to_string(weight.ne1()) +
+               "] does not match in_features=" + std::to_string(in_features) +
+               " out_features=" + std::to_string(out_features));
+  }
+  if (rows != 0 && in_features > SIZE_MAX / rows) return err("linear_out_by_in rows*in_features overflows");
+  if (x_len != rows * in_features) return err(len_mismatch("x.len()", x_len, "rows*in_features", rows, in_features));
+  if (has_bias && bias_len != out_features) {
+    return err("linear_out_by_in bias.len()=" + std::to_string(bias_len) +
+               " does not match out_features=" + std::to_string(out_features));
+  }
+  if (rows != 0 && out_features > SIZE_MAX / rows) return err("linear_out_by_in rows*out_features overflows");
+  if (out_len != rows * out_features)
+    return err(len_mismatch("out.len()", out_len, "rows*out_features", rows, out_features));
+  return {};
+}
+}  // namespace
+
+Result<void> KernelBackend::dequantize(GgmlTensorType type, const uint8_t *src, size_t src_len, size_t n,
+                                       float *out) const {
+  return dequantize_host(type, src, src_len, n, out);
+}
+
+// The weight's blocks on the host, dequantized, then this backend's f32
+// linear_out_by_in.
+Result<void> KernelBackend::linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
+                                             const QuantizedWeight &weight, size_t out_features, const float *bias,
+                                             size_t bias_len, float *out, size_t out_len) const {
+  Result<void> v = validate_quantized_linear(name(), x_len, rows, in_features, weight, out_features, bias != nullptr,
+                                             bias_len, out_len);
+  if (v.is_err()) return v;
+  auto blocks = weight.to_host_bytes();
+  if (blocks.is_err()) return blocks.error();
+  const size_t n = in_features * out_features;
+  std::vector<float> wf(n);
+  Result<void> r = dequantize(weight.tensor_type(), blocks.value().data(), blocks.value().size(), n, wf.data());
+  if (r.is_err()) return r;
+  return linear_out_by_in(x, x_len, rows, in_features, wf.data(), wf.size(), out_features, bias, bias_len, out,
+                          out_len);
+}
+
+// lib.rs:193-217: x and bias read back, linear_out_by_in on the slices, out
+// written from the host.
+Result<void> KernelBackend::linear_d(const DeviceTensor &x, size_t rows, size_t in_features,
+                                     const QuantizedWeight &weight, size_t out_features, const DeviceTensor *bias,
+                                     const DeviceTensor &out) const {
+  auto xh = x.to_host_owned();
+  if (xh.is_err()) return xh.error();
+  std::vector<float> bh;
+  if (bias) {
+    auto b = bias->to_host_owned();
+    if (b.is_err()) return b.error();
+    bh = std::move(b.value());
+  }
+  std::vector<float> oh(out.len(), 0.0f);
+  Result<void> r = linear_out_by_in(xh.value().data(), xh.value().size(), rows, in_features, weight, out_features,
+                                    bias ? bh.data() : nullptr, bh.size(), oh.data(), oh.size());
+  if (r.is_err()) return r;
+  return out.write_from_host_slice(oh.data(), oh.size());
+}
 
 // ---- backend -------------------------------------------------------------------
 
@@ -281,7 +383,47 @@ Result<QuantizedWeight> HipKernelBackend::upload_quantized(GgmlTensorType type, 
   return QuantizedWeight(type, ne0, ne1, len, a.value());
 }
 
+Result<void> HipKernelBackend::linear_out_by_in(const float *, size_t, size_t, size_t, const float *, size_t,
+                                                size_t, const float *, size_t, float *, size_t) const {
+  return OcelotlError::unsupported("f32_linear_out_by_in", std::string(kBackend),
+                                   {"quantized weights: Q8_0", "Q4K", "Q6K"});
+}
+
+Result<void> HipKernelBackend::dequantize(GgmlTensorType type, const uint8_t *src, size_t src_len, size_t n,
+                                          float *out) const {
+  if (!is_block_format(type))
+    return OcelotlError::unsupported("quantized_tensor_type", std::to_string((uint32_t)type), block_format_names());
+  auto info = block_info(type);
+  if (info.is_err()) return info.error();
+  const size_t elems = (size_t)info.value().first, bytes = (size_t)info.value().second;
+  if (n % elems != 0 || src_len < n / elems * bytes) {
+    return kernel_err("dequantize: " + std::to_string(n) + " elements need whole " + std::to_string(elems) +
+                      "-element blocks within the " + std::to_string(src_len) + " source bytes");
+  }
+  if (n == 0) return {};
+  auto a = device_alloc(n / elems * bytes);
+  if (a.is_err()) return a.error();
+  auto o = device_alloc(n * sizeof(float));
+  if (o.is_err()) return o.error();
+  Result<void> r = check(okq_memcpy_h2d(a.value()->ptr, src, n / elems * bytes, stream_));
+  if (r.is_err()) return r;
+  r = check(okq_dequantize((uint32_t)type, a.value()->ptr, (int64_t)n, static_cast<float *>(o.value()->ptr), stream_),
+            (uint32_t)type);
+  if (r.is_err()) return r;
+  r = check(okq_memcpy_d2h(out, o.value()->ptr, n * sizeof(float), stream_));
+  if (r.is_err()) return r;
+  return check(okq_sync(stream_));
+}
+
 Result<DeviceTensor> HipKernelBackend::dequantize(const QuantizedWeight &weight) const {
+  if (weight.device_ptr() == nullptr && weight.byte_len() > 0) {
+    auto blocks = weight.to_host_bytes();
+    if (blocks.is_err()) return blocks.error();
+    auto dw = upload_quantized(weight.tensor_type(), weight.ne0(), weight.ne1(), blocks.value().data(),
+                               blocks.value().size());
+    if (dw.is_err()) return dw.error();
+    return dequantize(dw.value());
+  }
   const size_t n = weight.ne0() * weight.ne1();
   auto a = device_alloc(n * sizeof(float));
   if (a.is_err()) return a.error();
@@ -389,6 +531,15 @@ Result<DeviceTensor> HipKernelBackend::embedding_rows(const QuantizedWeight &tab
 Result<void> HipKernelBackend::linear_d(const DeviceTensor &x, size_t rows, size_t in_features,
                                         const QuantizedWeight &weight, size_t out_features, const DeviceTensor *bias,
                                         const DeviceTensor &out) const {
+  if (weight.device_ptr() == nullptr && weight.byte_len() > 0) {
+    // a host-resident weight: a device copy for this call
+    auto blocks = weight.to_host_bytes();
+    if (blocks.is_err()) return blocks.error();
+    auto dw = upload_quantized(weight.tensor_type(), weight.ne0(), weight.ne1(), blocks.value().data(),
+                               blocks.value().size());
+    if (dw.is_err()) return dw.error();
+    return linear_d(x, rows, in_features, dw.value(), out_features, bias, out);
+  }
   if (weight.ne0() != in_features || weight.ne1() != out_features) {
     return kernel_err("linear_d weight shape [" + std::to_string(weight.ne0()) + ", " + std::to_string(weight.ne1()) +
                       "] does not match in_features=" + std::to_string(in_features) +

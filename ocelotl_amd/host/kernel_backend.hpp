@@ -204,18 +204,28 @@ class DeviceTensor {
   void *stream_ = nullptr;                          // Device
 };
 
-// A GGUF weight tensor resident on the device in its file layout:
-// [ne0 = in_features, ne1 = out_features], rows of consecutive blocks
-// (gguf_inspect.rs:118-130).
+// A GGUF weight tensor in its file layout: [ne0 = in_features, ne1 =
+// out_features], rows of consecutive blocks (gguf_inspect.rs:118-130).
+// Device-resident (HipKernelBackend::upload_quantized) or host-resident
+// (from_host: blocks as read from a file, for a backend without a device or
+// the trait defaults below).
 class QuantizedWeight {
  public:
+  // Host blocks; the byte length is checked against the shape.
+  static Result<QuantizedWeight> from_host(GgmlTensorType type, size_t ne0, size_t ne1, std::vector<uint8_t> blocks);
+
   GgmlTensorType tensor_type() const { return type_; }
   size_t ne0() const { return ne0_; }
   size_t ne1() const { return ne1_; }
   size_t in_features() const { return ne0_; }
   size_t out_features() const { return ne1_; }
   uint64_t byte_len() const { return bytes_; }
+  Residency residency() const;
+  // The device blocks (null for a host weight).
   const void *device_ptr() const;
+  // The blocks in host memory: a host weight's own bytes, or a device
+  // weight's read back.
+  Result<std::vector<uint8_t>> to_host_bytes() const;
 
  private:
   friend class HipKernelBackend;
@@ -224,12 +234,22 @@ class QuantizedWeight {
   GgmlTensorType type_;
   size_t ne0_, ne1_;
   uint64_t bytes_;
-  std::shared_ptr<DeviceAllocation> buf_;
+  std::shared_ptr<DeviceAllocation> buf_;              // device
+  std::shared_ptr<const std::vector<uint8_t>> host_;  // host
 };
 
 // ---- the backend (crates/kernels/src/lib.rs:84-495) ------------------------
 
-// The slice of KernelBackend the quantized linear touches.
+// The slice of KernelBackend the quantized linear touches.  A backend
+// implements the f32 linear_out_by_in (lib.rs:106-116, required as in the
+// reference); the quantized entry points have defaults in the reference's
+// style (lib.rs:186-217: correct on any backend, slow), which a backend with
+// a native path overrides:
+//   * dequantize: the host decoders (dequant_host.hpp, bit-exact);
+//   * linear_out_by_in with a QuantizedWeight: the weight's blocks on the
+//     host, dequantize, then the f32 linear_out_by_in;
+//   * linear_d: the host bounce -- read x and bias back, linear_out_by_in on
+//     the slices, write out.
 class KernelBackend {
  public:
   virtual ~KernelBackend() = default;
@@ -238,18 +258,24 @@ class KernelBackend {
   // lib.rs:171-181
   virtual Result<DeviceTensor> upload(const float *host, size_t len) const = 0;
   virtual Result<DeviceTensor> alloc(size_t len) const = 0;
-  // linear_out_by_in over host slices (lib.rs:106-116) with a quantized
-  // weight: out[r, o] = bias[o] + sum_k x[r, k] * W[o, k].  `bias` may be
-  // null (bias_len 0).
+  // linear_out_by_in over host slices with f32 weights W[out, in]
+  // (lib.rs:106-116): out[r, o] = bias[o] + sum_k x[r, k] * W[o, k].  `bias`
+  // may be null (bias_len 0).
+  virtual Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
+                                        const float *weight, size_t weight_len, size_t out_features,
+                                        const float *bias, size_t bias_len, float *out, size_t out_len) const = 0;
+  // The same contract with a quantized weight.
   virtual Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
                                         const QuantizedWeight &weight, size_t out_features, const float *bias,
-                                        size_t bias_len, float *out, size_t out_len) const = 0;
-  // linear_d (lib.rs:186-217); `out` is caller-supplied and written in
-  // place.  Device-resident x, bias and out run on the device directly; any
-  // other residency (host tensors, views) takes the trait default's bounce:
-  // read x and bias back, run linear_out_by_in on the slices, write out.
+                                        size_t bias_len, float *out, size_t out_len) const;
+  // n elements of raw GGUF blocks (src_len bytes) decoded into out, host
+  // slices (no reference counterpart: the reference has no dequantization;
+  // the signature follows its slice style).
+  virtual Result<void> dequantize(GgmlTensorType type, const uint8_t *src, size_t src_len, size_t n,
+                                  float *out) const;
+  // linear_d (lib.rs:186-217); `out` is caller-supplied and written in place.
   virtual Result<void> linear_d(const DeviceTensor &x, size_t rows, size_t in_features, const QuantizedWeight &weight,
-                                size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const = 0;
+                                size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const;
 };
 
 // The gfx950 backend: name() == "hip-gfx950" (the backend_id convention of
@@ -264,18 +290,30 @@ class HipKernelBackend final : public KernelBackend {
   const KernelContext &context() const override { return ctx_; }
   Result<DeviceTensor> upload(const float *host, size_t len) const override;
   Result<DeviceTensor> alloc(size_t len) const override;
+  // f32 weights are not offloaded by this backend: Unsupported{feature:
+  // "f32_linear_out_by_in"} (the path it serves is the quantized one).
+  Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features, const float *weight,
+                                size_t weight_len, size_t out_features, const float *bias, size_t bias_len, float *out,
+                                size_t out_len) const override;
+  // Quantized weights on the GPU (a host-resident weight is uploaded first).
   Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features,
                                 const QuantizedWeight &weight, size_t out_features, const float *bias, size_t bias_len,
                                 float *out, size_t out_len) const override;
+  // Device-resident x, bias and out run on the device directly; any other
+  // residency (host tensors, views) takes the trait default's bounce.
   Result<void> linear_d(const DeviceTensor &x, size_t rows, size_t in_features, const QuantizedWeight &weight,
                         size_t out_features, const DeviceTensor *bias, const DeviceTensor &out) const override;
+  // Host slices decoded on the GPU (okq_dequantize; every block format).
+  Result<void> dequantize(GgmlTensorType type, const uint8_t *src, size_t src_len, size_t n,
+                          float *out) const override;
 
   // Uploads raw GGUF blocks after checking their byte length against the
   // shape; any block format is accepted (Unsupported otherwise).  linear_d
   // takes Q8_0 / Q4K / Q6K weights, dequantize and embedding_rows all of them.
   Result<QuantizedWeight> upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1, const uint8_t *blocks,
                                            size_t len) const;
-  // The weight dequantized to f32 (bit-exact with the CPU definition).
+  // The weight dequantized to f32 on the device (bit-exact with the CPU
+  // definition).
   Result<DeviceTensor> dequantize(const QuantizedWeight &weight) const;
 
   // KernelBackend::rmsnorm over host slices (lib.rs:139-147,

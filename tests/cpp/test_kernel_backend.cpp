@@ -28,6 +28,8 @@ int64_t okr_block_elems(int type);
 int64_t okr_block_bytes(int type);
 void okr_rmsnorm(const float *x, int64_t rows, int64_t hidden, const float *weight, float eps, float *out);
 void okr_swiglu(const float *gate, const float *up, int64_t n, float *out);
+int okr_linear_out_by_in(int mode, int threads, const float *x, int64_t rows, int64_t in_f, const float *w,
+                         int64_t out_f, const float *bias, float *out);
 }
 
 using namespace ocelotl;
@@ -96,7 +98,146 @@ bool same_bits(const std::vector<float> &a, const std::vector<float> &b) {
 
 const GgmlTensorType kTypes[] = {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q6K};
 
+// A backend with only the required f32 linear_out_by_in -- the reference CPU
+// path (the oracle) -- so every quantized entry point runs the trait's
+// defaults: host dequantization (product code), then this f32 linear.
+class F32OnlyBackend final : public KernelBackend {
+ public:
+  const char *name() const override { return "cpu"; }
+  const KernelContext &context() const override { return ctx_; }
+  Result<DeviceTensor> upload(const float *host, size_t len) const override {
+    return DeviceTensor::from_host(std::vector<float>(host, host + len));
+  }
+  Result<DeviceTensor> alloc(size_t len) const override { return DeviceTensor::host_zeros(len); }
+  using KernelBackend::linear_out_by_in;
+  Result<void> linear_out_by_in(const float *x, size_t x_len, size_t rows, size_t in_features, const float *weight,
+                                size_t weight_len, size_t out_features, const float *bias, size_t bias_len, float *out,
+                                size_t out_len) const override {
+    if (x_len != rows * in_features || weight_len != out_features * in_features ||
+        (bias && bias_len != out_features) || out_len != rows * out_features)
+      return OcelotlError::kernel("cpu", "length mismatch");
+    if (okr_linear_out_by_in(kScalarMode, 1, x, (int64_t)rows, (int64_t)in_features, weight, (int64_t)out_features,
+                             bias, out) != 0)
+      return OcelotlError::kernel("cpu", "oracle linear failed");
+    ++f32_calls;
+    return {};
+  }
+  mutable int f32_calls = 0;
+
+ private:
+  KernelContext ctx_{Device{Device::Kind::Cpu, 0}};
+};
+
+// Random blocks whose f16 scales are finite (the low byte random, the high
+// byte kept in the normal range), so the decoders see every quant pattern.
+std::vector<uint8_t> random_blocks(GgmlTensorType t, size_t blocks, uint64_t seed) {
+  const auto info = ok(block_info(t), "block_info");
+  std::vector<uint8_t> b(blocks * (size_t)info.second);
+  uint64_t z = seed;
+  for (auto &v : b) {
+    z += 0x9E3779B97F4A7C15ull;
+    uint64_t r = z;
+    r = (r ^ (r >> 30)) * 0xBF58476D1CE4E5B9ull;
+    r = (r ^ (r >> 27)) * 0x94D049BB133111EBull;
+    v = (uint8_t)(r ^ (r >> 31));
+  }
+  auto fix_half = [&](size_t off) { b[off + 1] = (uint8_t)(0x18 + (b[off + 1] & 0x0F)); };  // |h| in [2^-9, 2^-1)
+  for (size_t i = 0; i < blocks; ++i) {
+    const size_t o = i * (size_t)info.second;
+    if (t == GgmlTensorType::Q6K) {
+      fix_half(o + 208);
+    } else {
+      fix_half(o);
+      if (t == GgmlTensorType::Q4K || t == GgmlTensorType::Q5K) fix_half(o + 2);
+    }
+  }
+  return b;
+}
+
+bool same_bits_nan_equal(const std::vector<float> &a, const std::vector<float> &b) {
+  if (a.size() != b.size()) return false;
+  for (size_t i = 0; i < a.size(); ++i) {
+    if (std::isnan(a[i]) && std::isnan(b[i])) continue;
+    if (std::memcmp(&a[i], &b[i], sizeof(float)) != 0) return false;
+  }
+  return true;
+}
+
 // ---- tests that need no GPU ---------------------------------------------------
+
+void trait_default_dequantize_matches_the_cpu_definition() {
+  F32OnlyBackend be;
+  for (GgmlTensorType t : {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q5K, GgmlTensorType::Q6K}) {
+    const auto info = ok(block_info(t), "block_info");
+    const size_t blocks = 97, n = blocks * (size_t)info.first;
+    const auto q = random_blocks(t, blocks, 4100 + (uint64_t)t);
+    std::vector<float> got(n), want(n);
+    ok(be.dequantize(t, q.data(), q.size(), n, got.data()), "default dequantize");
+    CHECK(okr_dequantize((int)t, q.data(), (int64_t)n, want.data()) == 0, "oracle dequant");
+    CHECK(same_bits_nan_equal(got, want), "host dequant must be bit-exact with the CPU definition");
+    // special halves: zero, subnormal, infinity as the scale
+    if (t == GgmlTensorType::Q8_0) {
+      auto q2 = q;
+      const uint16_t halves[] = {0x0000, 0x0001, 0x03ff, 0x7c00, 0xfc00};
+      for (size_t i = 0; i < 5; ++i) {
+        q2[i * 34] = (uint8_t)(halves[i] & 0xff);
+        q2[i * 34 + 1] = (uint8_t)(halves[i] >> 8);
+      }
+      ok(be.dequantize(t, q2.data(), q2.size(), n, got.data()), "default dequantize (special scales)");
+      CHECK(okr_dequantize((int)t, q2.data(), (int64_t)n, want.data()) == 0, "oracle dequant");
+      CHECK(same_bits_nan_equal(got, want), "special f16 scales");
+    }
+  }
+  // a format the host decoders do not cover is Unsupported; a short input a KernelError
+  std::vector<float> y(32);
+  std::vector<uint8_t> q40(18);
+  auto e = be.dequantize(GgmlTensorType::Q4_0, q40.data(), q40.size(), 32, y.data());
+  CHECK(e.is_err() && e.error().kind() == OcelotlError::Kind::Unsupported, "Q4_0 host dequant is unsupported");
+  std::vector<uint8_t> shortq(33);
+  e = be.dequantize(GgmlTensorType::Q8_0, shortq.data(), shortq.size(), 32, y.data());
+  CHECK(e.is_err() && e.error().kind() == OcelotlError::Kind::Kernel, "short input");
+}
+
+void trait_default_quantized_linear_is_host_dequant_then_f32_linear() {
+  // rows 5 x in 512 x out 37 (tails of the 4x4 tile), with and without bias:
+  // the default must give the reference CPU path's bits (same dequant, same
+  // f32 linear_out_by_in)
+  F32OnlyBackend be;
+  const size_t rows = 5, in = 512, out_f = 37;
+  const auto x = normal(4200, rows * in, 1.0f);
+  const auto bias = normal(4201, out_f, 0.1f);
+  for (GgmlTensorType t : {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q5K, GgmlTensorType::Q6K}) {
+    const auto info = ok(block_info(t), "block_info");
+    const auto q = t == GgmlTensorType::Q5K ? random_blocks(t, out_f * in / (size_t)info.first, 4202)
+                                           : quantize(t, normal(4203 + (uint64_t)t, out_f * in, 0.02f));
+    auto w = ok(QuantizedWeight::from_host(t, in, out_f, q), "from_host");
+    CHECK(w.residency().kind == Residency::Kind::Host && w.device_ptr() == nullptr, "host residency");
+    for (const float *b : {(const float *)nullptr, bias.data()}) {
+      std::vector<float> got(rows * out_f, -1.0f);
+      const int calls = be.f32_calls;
+      ok(be.linear_out_by_in(x.data(), x.size(), rows, in, w, out_f, b, b ? out_f : 0, got.data(), got.size()),
+         "default quantized linear");
+      CHECK(be.f32_calls == calls + 1, "the default runs the backend's f32 linear_out_by_in once");
+      CHECK(same_bits(got, reference(t, x, rows, in, q, out_f, b)), "default quantized linear vs reference path");
+    }
+    // linear_d over host tensors: the default bounce, same bits
+    auto xd = DeviceTensor::from_host(x);
+    auto od = DeviceTensor::host_zeros(rows * out_f);
+    ok(be.linear_d(xd, rows, in, w, out_f, nullptr, od), "default linear_d");
+    CHECK(same_bits(ok(od.to_host_owned(), "read out"), reference(t, x, rows, in, q, out_f, nullptr)),
+          "default linear_d vs reference path");
+  }
+  // validation before any work: a weight whose shape disagrees with the features
+  const auto q = quantize(GgmlTensorType::Q8_0, normal(4204, 64 * 32, 0.02f));
+  auto w = ok(QuantizedWeight::from_host(GgmlTensorType::Q8_0, 64, 32, q), "from_host");
+  std::vector<float> xs(2 * 64), ys(2 * 31);
+  const int calls = be.f32_calls;
+  auto e = be.linear_out_by_in(xs.data(), xs.size(), 2, 64, w, 31, nullptr, 0, ys.data(), ys.size());
+  CHECK(e.is_err() && e.error().kind() == OcelotlError::Kind::Kernel && be.f32_calls == calls,
+        "shape mismatch is a KernelError before any compute");
+  auto bad = QuantizedWeight::from_host(GgmlTensorType::Q8_0, 64, 32, std::vector<uint8_t>(q.size() - 1));
+  CHECK(bad.is_err(), "from_host checks the byte length");
+}
 
 void block_info_matches_gguf_block_sizes() {
   struct Case { GgmlTensorType t; int64_t e, b; };
@@ -259,6 +400,32 @@ void linear_out_by_in_host_slices_match_linear_d_bit_for_bit() {
     ok(be.linear_d(xd, rows, in, w, out_f, nullptr, od), "linear_d");
     CHECK(same_bits(host_out, ok(od.to_host_owned(), "readback")), "host-slice and device paths agree");
   }
+}
+
+// A host-resident weight (QuantizedWeight::from_host) is uploaded for the
+// call and gives the device weight's bits; the f32 linear is Unsupported on
+// this backend; dequantize over host slices runs on the GPU, bit-exact.
+void host_weights_and_slices_on_the_hip_backend() {
+  HipKernelBackend be = backend();
+  const size_t rows = 3, in = 1024, out_f = 70;
+  for (GgmlTensorType t : kTypes) {
+    const auto wq = quantize(t, normal(450 + (int)t, out_f * in, 0.02f));
+    const auto x = normal(451, rows * in, 1.0f);
+    QuantizedWeight wd = ok(be.upload_quantized(t, in, out_f, wq.data(), wq.size()), "upload_quantized");
+    QuantizedWeight wh = ok(QuantizedWeight::from_host(t, in, out_f, wq), "from_host");
+    std::vector<float> a(rows * out_f, NAN), b(rows * out_f, NAN);
+    ok(be.linear_out_by_in(x.data(), x.size(), rows, in, wd, out_f, nullptr, 0, a.data(), a.size()), "device weight");
+    ok(be.linear_out_by_in(x.data(), x.size(), rows, in, wh, out_f, nullptr, 0, b.data(), b.size()), "host weight");
+    CHECK(same_bits(a, b), "a host weight gives the device weight's bits");
+    CHECK(ok(wd.to_host_bytes(), "read back blocks") == wq, "device blocks read back");
+    std::vector<float> deq(out_f * in), want(out_f * in);
+    ok(be.dequantize(t, wq.data(), wq.size(), deq.size(), deq.data()), "dequantize host slices");
+    CHECK(okr_dequantize((int)t, wq.data(), (int64_t)want.size(), want.data()) == 0, "oracle dequant");
+    CHECK(same_bits(deq, want), "GPU dequantize of host slices is bit-exact");
+  }
+  std::vector<float> x(4), w(4), y(1);
+  auto e = be.linear_out_by_in(x.data(), 4, 1, 4, w.data(), 4, 1, nullptr, 0, y.data(), 1);
+  CHECK(e.is_err() && e.error().kind() == OcelotlError::Kind::Unsupported, "f32 weights are not offloaded");
 }
 
 // Wrong residency stays correct: host-resident x, bias and out, and views of
@@ -471,7 +638,11 @@ int main(int argc, char **argv) {
              {"create_without_a_gfx950_device_is_unsupported", create_without_a_gfx950_device_is_unsupported},
              {"host_tensors_and_views_follow_the_reference_semantics",
               host_tensors_and_views_follow_the_reference_semantics},
-             {"dequant_policy_gate_flips_for_executable_types", dequant_policy_gate_flips_for_executable_types}};
+             {"dequant_policy_gate_flips_for_executable_types", dequant_policy_gate_flips_for_executable_types},
+             {"trait_default_dequantize_matches_the_cpu_definition",
+              trait_default_dequantize_matches_the_cpu_definition},
+             {"trait_default_quantized_linear_is_host_dequant_then_f32_linear",
+              trait_default_quantized_linear_is_host_dequant_then_f32_linear}};
   } else if (suite == "gpu") {
     tests = {{"backend_identity", backend_identity},
              {"linear_d_matches_reference_cpu_path", linear_d_matches_reference_cpu_path},
@@ -485,7 +656,8 @@ int main(int argc, char **argv) {
              {"linear_d_one_hot_column_is_exact", linear_d_one_hot_column_is_exact},
              {"rmsnorm_matches_the_reference_and_its_kats", rmsnorm_matches_the_reference_and_its_kats},
              {"mlp_gated_silu_q_matches_the_reference_chain", mlp_gated_silu_q_matches_the_reference_chain},
-             {"embedding_rows_are_the_dequantized_rows", embedding_rows_are_the_dequantized_rows}};
+             {"embedding_rows_are_the_dequantized_rows", embedding_rows_are_the_dequantized_rows},
+             {"host_weights_and_slices_on_the_hip_backend", host_weights_and_slices_on_the_hip_backend}};
   } else {
     std::fprintf(stderr, "usage: %s cpu|gpu\n", argv[0]);
     return 2;
