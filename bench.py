@@ -657,24 +657,29 @@ def run_cpu_baseline(ctx: Ctx, c2, args):
         launch_group(ctx, names, lay, c2["x14336"] if C2_SHAPE[names[0]][1] == 14336 else c2["x4096"], gpu_out)
     ctx.torch.cuda.synchronize()
     parity = all(O.allclose_ref_rule(gpu_out[name].cpu().numpy(), cpu_out[name], 1e-3)[0] for name, _, _ in C2_PROJ)
-    # the timed step's error against the reference CPU path: largest absolute
-    # difference, and largest relative one over outputs with |want| >= 1e-3
-    abs_err, rel_err = 0.0, 0.0
+    # the timed step's error against the reference CPU path: the largest
+    # absolute difference, the largest relative one over outputs with
+    # |want| >= 0.1, and the largest min(abs, rel) -- the quantity the
+    # reference rule bounds by 1e-3 (outputs are ~N(0, 1.3))
+    abs_err, rel_err, rule = 0.0, 0.0, 0.0
     for name, _, _ in C2_PROJ:
         got = gpu_out[name].cpu().numpy().astype(np.float64)
         want = cpu_out[name].astype(np.float64)
         d = np.abs(got - want)
         abs_err = max(abs_err, float(d.max()))
-        big = np.abs(want) >= 1e-3
+        big = np.abs(want) >= 0.1
         if big.any():
             rel_err = max(rel_err, float((d[big] / np.abs(want[big])).max()))
+        rule = max(rule, float(np.minimum(d, d / np.maximum(np.abs(want), 1e-30)).max()))
     head = {"value": round(gbs, 4), "unit": "GB/s", "cores": 1, "kind": "port",
             "sample": f"C2 layer copy 0 (7 Q4_K projections, {c2['step_bytes']} quantized bytes) dequantized to f32 "
                       f"once (untimed); reference scalar linear_out_by_in, batch 1, serial (rows < 32); "
                       f"{passes} passes in {sec_pass * passes:.2f} s on {model}",
             "ms_per_step": round(1000.0 * sec_pass, 2),
             "gpu_outputs_match_cpu_within_rule": bool(parity),
-            "gpu_vs_cpu_max_abs_err": float(f"{abs_err:.3g}"), "gpu_vs_cpu_max_rel_err": float(f"{rel_err:.3g}")}
+            "gpu_vs_cpu_max_abs_err": float(f"{abs_err:.3g}"),
+            "gpu_vs_cpu_max_rel_err_where_abs_want_ge_0.1": float(f"{rel_err:.3g}"),
+            "gpu_vs_cpu_max_min_abs_rel": float(f"{rule:.3g}")}
     if args.cpu_configs:
         head["configs"] = run_cpu_configs(ctx, orc, O, args)
     return head

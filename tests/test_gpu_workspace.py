@@ -117,3 +117,43 @@ def test_two_threads_on_one_stream_growing_its_workspace(torch, okq, orc):
     assert not errors, errors
     for (i, r), o in outs.items():
         assert (o.cpu().numpy().view(np.uint32) == want[i].view(np.uint32)).all(), (i, r)
+
+
+def test_graph_replayed_on_another_stream_after_its_capture_stream_is_idle(torch, okq, orc):
+    """A graph records its capture stream's workspace pointer.  The rule for
+    replays (graph capture): a replay on another stream must
+    be serialised with the capture stream's own work -- here the capture
+    stream's eager calls finish (an event the replay stream waits for) before
+    the replay starts, and the next eager call on the capture stream waits
+    for the replay.  Each replay equals the eager result bit for bit, and so
+    do the eager calls in between."""
+    cap, other = torch.cuda.Stream(), torch.cuda.Stream()
+    prob = _problem(torch, orc, 9200, O.Q4_K, 16, 4096, 14336)  # split-K partials in the workspace
+    busy = _problem(torch, orc, 9210, O.Q4_K, 24, 14336, 4096)
+    ref = torch.empty(16 * 4096, dtype=torch.float32, device="cuda")
+    out = torch.empty_like(ref)
+    bo = torch.empty(24 * 14336, dtype=torch.float32, device="cuda")
+    with torch.cuda.stream(cap):
+        _launch(okq, prob, ref, cap.cuda_stream)
+        _launch(okq, busy, bo, cap.cuda_stream)
+    torch.cuda.synchronize()
+    want_busy = bo.cpu().numpy().copy()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cap):
+        _launch(okq, prob, out, cap.cuda_stream)
+    for rep in range(3):
+        out.fill_(float("nan"))
+        with torch.cuda.stream(cap):
+            _launch(okq, busy, bo, cap.cuda_stream)  # eager work on the capture stream's workspace
+        done = torch.cuda.Event()
+        done.record(cap)
+        other.wait_event(done)  # serialised: the replay waits for it
+        with torch.cuda.stream(other):
+            g.replay()
+        replayed = torch.cuda.Event()
+        replayed.record(other)
+        cap.wait_event(replayed)  # and the capture stream waits for the replay
+        torch.cuda.synchronize()
+        assert (out.cpu().numpy().view(np.uint32) == ref.cpu().numpy().view(np.uint32)).all(), rep
+        assert (bo.cpu().numpy().view(np.uint32) == want_busy.view(np.uint32)).all(), rep
+    del g
