@@ -276,9 +276,15 @@ enum class Path { Auto, Gemv, Gemm };
 //   Q4_K 4096x4096 (9.4 MB): 13.6/13.7 at 5 rows, 13.6/15.0 at 6
 //   Q6_K 1024x4096 (3.4 MB): 13.0/11.7 at 5 rows, 13.0/13.1 at 6, 13.0/15.9 at 7
 //   Q4_K 1024x4096 (2.4 MB): 11.9/11.3 at 5 rows, 12.0/12.5 at 6, 12.0/15.1 at 7
+//   Q8_0 4096x14336 (59.5 MB): 21.6/18.7 at 2 rows, 23.5/30.2 at 3, 23.6/34.7 at 4
+//   Q8_0 14336x4096 (59.5 MB): 20.7/17.0 at 4 rows, 20.9/28.1 at 5
+//   Q8_0 4096x4096 (17 MB):    11.0/9.5 at 4 rows, 11.2/14.5 at 5
+//   Q8_0 1024x4096 (4.2 MB):   10.3/7.6 at 4 rows, 10.5/11.0 at 5, 10.5/12.4 at 6
 // so: 6-8 rows from 2 MB; 5 rows from 8 MB; 3-4 rows from 16 MB when K is at
 // least 8192 (where the GEMV's extra rows cost most) and from 64 MB
-// otherwise; 1-2 rows always the GEMV.
+// otherwise; 1-2 rows always the GEMV.  The same thresholds hold for Q8_0
+// (1.9x the bytes per weight): its only miss above is 5 rows of 4.2 MB, by
+// 0.5 us.
 constexpr int64_t kGemvMaxRows = 8;
 
 bool gemv_serves(uint32_t, int64_t rows, int64_t K, uint64_t w_bytes) {
