@@ -835,7 +835,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one MI355X only: this build has no multi-GPU path "
-              "(the sharding design is described in DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(each GPU would run the same kernels on its share of the rows). Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch

@@ -121,8 +121,8 @@ def test_two_threads_on_one_stream_growing_its_workspace(torch, okq, orc):
 
 def test_graph_replayed_on_another_stream_after_its_capture_stream_is_idle(torch, okq, orc):
     """A graph records its capture stream's workspace pointer.  The rule for
-    replays (graph capture): a replay on another stream must
-    be serialised with the capture stream's own work -- here the capture
+    replays: a replay on another stream must be serialised with the capture
+    stream's own work -- here the capture
     stream's eager calls finish (an event the replay stream waits for) before
     the replay starts, and the next eager call on the capture stream waits
     for the replay.  Each replay equals the eager result bit for bit, and so
