@@ -2,7 +2,7 @@
  * okq.h -- C-ABI of libokq.so, the MI355X (gfx950) k-quant linear path.
  *
  * The library implements Ocelotl's quantized linear projection for the GGUF
- * block formats Q8_0 (type id 8), Q4_K (12) and Q6_K (14) with hand-written
+ * block formats Q8_0 (type id 8), Q4_K (12), Q5_K (13) and Q6_K (14) with hand-written
  * HIP kernels: dequantize, a fused dequant-GEMV for decode and an MFMA
  * dequant-GEMM for prefill.  Weights stay in the GGUF layout: tensor shape
  * [ne0 = in_features, ne1 = out_features], each row one output feature made of
@@ -58,7 +58,7 @@ enum {
     OKQ_TYPE_Q2_K = 10, /* dequantize / get_rows only */
     OKQ_TYPE_Q3_K = 11, /* dequantize / get_rows only */
     OKQ_TYPE_Q4_K = 12,
-    OKQ_TYPE_Q5_K = 13, /* dequantize / get_rows only */
+    OKQ_TYPE_Q5_K = 13,
     OKQ_TYPE_Q6_K = 14,
     OKQ_TYPE_BF16 = 30
 };
@@ -79,7 +79,7 @@ size_t okq_last_error(char *buf, size_t len);
 /* Elements and bytes per block: Q8_0 32/34, Q4_K 256/144, Q6_K 256/210;
  * Q4_0 32/18, Q4_1 32/20, Q5_0 32/22, Q5_1 32/24, Q2_K 256/84, Q3_K 256/110,
  * Q5_K 256/176; and 1/4, 1/2, 1/2 for F32, F16, BF16.  OKQ_E_TYPE for
- * anything else.  The linear entry points take Q8_0, Q4_K and Q6_K weights;
+ * anything else.  The linear entry points take Q8_0, Q4_K, Q5_K and Q6_K weights;
  * okq_dequantize and okq_get_rows_q take every block format listed here. */
 okq_status okq_type_info(uint32_t ggml_type, int64_t *block_elems, int64_t *block_bytes);
 
@@ -137,7 +137,7 @@ okq_status okq_get_rows_q(uint32_t w_type, const void *w, uint64_t w_bytes, int6
  * weights large enough for the MFMA kernel to repay its fixed cost: from 2 MB
  * at 6-8 rows, from 8 MB at 5 rows, and at 3-4 rows from 16 MB when
  * in_features >= 8192 or from 64 MB otherwise; more rows run the MFMA
- * dequant-GEMM (Q4_K, Q6_K, and Q8_0 when in_features is a multiple of 256),
+ * dequant-GEMM (Q4_K, Q5_K, Q6_K, and Q8_0 when in_features is a multiple of 256),
  * which for up to 32 rows streams the weights once with the rows in one or
  * two MFMA tiles. */
 okq_status okq_linear_out_by_in_q(const float *x, int64_t rows, int64_t in_features, uint32_t w_type,

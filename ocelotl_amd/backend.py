@@ -94,7 +94,7 @@ class GgmlTensorType(enum.IntEnum):
 
 
 # Weight formats the linear kernels execute.
-QUANTIZED = (GgmlTensorType.Q8_0, GgmlTensorType.Q4K, GgmlTensorType.Q6K)
+QUANTIZED = (GgmlTensorType.Q8_0, GgmlTensorType.Q4K, GgmlTensorType.Q5K, GgmlTensorType.Q6K)
 # Every block format dequantize and the row gather accept.
 BLOCK_FORMATS = (GgmlTensorType.Q4_0, GgmlTensorType.Q4_1, GgmlTensorType.Q5_0, GgmlTensorType.Q5_1,
                  GgmlTensorType.Q8_0, GgmlTensorType.Q2K, GgmlTensorType.Q3K, GgmlTensorType.Q4K,

@@ -21,10 +21,15 @@ namespace okq {
 
 constexpr int kQ8_0 = 8, kQ4_K = 12, kQ6_K = 14;
 constexpr int kQ8Bytes = 34, kQ4KBytes = 144, kQ6KBytes = 210;
-// Formats served by dequantize / row gather only (gguf_inspect.rs:170-206 ids).
+// Q5_K (linear kernels too) and the formats served by dequantize / row
+// gather only (gguf_inspect.rs:170-206 ids).
 constexpr int kQ4_0 = 2, kQ4_1 = 3, kQ5_0 = 6, kQ5_1 = 7, kQ2_K = 10, kQ3_K = 11, kQ5_K = 13;
 constexpr int kQ40Bytes = 18, kQ41Bytes = 20, kQ50Bytes = 22, kQ51Bytes = 24, kQ2KBytes = 84, kQ3KBytes = 110,
               kQ5KBytes = 176;
+// Bytes per 256 weights of a row in a linear-kernel format.
+__host__ __device__ constexpr int sb_bytes_of(int type) {
+  return type == kQ6_K ? kQ6KBytes : type == kQ8_0 ? 8 * kQ8Bytes : type == kQ5_K ? kQ5KBytes : kQ4KBytes;
+}
 
 __device__ __forceinline__ float as_f32(uint32_t u) { return __uint_as_float(u); }
 __device__ __forceinline__ uint32_t as_u32(float f) { return __float_as_uint(f); }

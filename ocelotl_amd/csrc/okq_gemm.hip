@@ -210,7 +210,7 @@ constexpr int kLDB = kKB + 8;   // LDS row pitch in halves (spreads rows over ba
 
 template <int BM, bool kLo, int kFmt>
 struct alignas(16) GemmSmem {
-  static constexpr bool kMins = kFmt == kQ4_K;
+  static constexpr bool kMins = kFmt == kQ4_K || kFmt == kQ5_K;
   _Float16 A[2][BM][kLDB];
   _Float16 Alo[2][kLo ? BM : 1][kLDB];
   _Float16 B[2][kBN][kLDB];
@@ -227,6 +227,7 @@ struct StepRegs {
   u32x4 xs;                     // 4 (hi, lo) xsum pairs (first chunk of a super-block)
   u32x4 hd;                     // Q4_K header of the weight row's super-block
   u32x4 q;                      // 16 (BM=128) or 8 (BM=256, in .x/.y) qs bytes
+  u32x4 qh;                     // Q5_K: the qh bytes of the same l (fifth bits)
   // Q6_K (BM = 128): dword windows (5 dwords for 16 bytes) of the ql bytes of
   // k < 32, of k >= 32 and of the qh bytes; 3 dwords around the half's 8
   // scales; d (2-byte load, first chunk of a super-block)
@@ -283,11 +284,11 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
   constexpr int NT = BM * 2;       // threads
   constexpr int TPR = NT / kBN;    // B-staging threads per weight row (2 or 4)
   constexpr int QB = 32 / TPR;     // qs bytes per thread per step (16 or 8)
-  constexpr bool kQ6 = kFmt == kQ6_K, kQ8 = kFmt == kQ8_0;
+  constexpr bool kQ6 = kFmt == kQ6_K, kQ8 = kFmt == kQ8_0, kQ5 = kFmt == kQ5_K;
   static_assert(!kQ6 || QB == 16, "Q6_K staging takes 16-byte windows (BM = 128)");
   static_assert(!kQ8 || TPR == 2, "Q8_0 staging takes one 34-byte block per thread (BM = 128)");
   // bytes per 256 weights of a row: one super-block, or eight Q8_0 blocks
-  constexpr uint32_t kBlk = kQ6 ? kQ6KBytes : kQ8 ? 8 * kQ8Bytes : kQ4KBytes;
+  constexpr uint32_t kBlk = kQ6 ? kQ6KBytes : kQ8 ? 8 * kQ8Bytes : kQ5 ? kQ5KBytes : kQ4KBytes;
   __shared__ GemmSmem<BM, kLo, kFmt> sm;
   // XCD-aware tile order: workgroup b runs on XCD b % 8; give each XCD a
   // contiguous range of tiles (consecutive tiles share an N-tile).
@@ -372,14 +373,21 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
       return;
     }
     if constexpr (c == 0) r.xs = bload4(rs_xs, s_row + 32u * (uint32_t)sb);
-    const uint32_t blk = w_row + (uint32_t)sb * kQ4KBytes;
+    // Q4_K / Q5_K: the header, this thread's QB qs bytes of chunk c and
+    // (Q5_K) the qh bytes of the same positions l
+    const uint32_t blk = w_row + (uint32_t)sb * kBlk;
     r.hd = bload4(rs_w, blk);
-    const uint32_t qo = blk + 16u + 32u * (uint32_t)c + (uint32_t)(QB * bq);
+    const uint32_t qo = blk + (kQ5 ? 48u : 16u) + 32u * (uint32_t)c + (uint32_t)(QB * bq);
     if (QB == 16) {
       r.q = bload4(rs_w, qo);
+      if (kQ5) r.qh = bload4(rs_w, blk + 16u + (uint32_t)(QB * bq));
     } else {
       const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(rs_w, qo, 0, 0);
       r.q = u32x4{v.x, v.y, 0u, 0u};
+      if (kQ5) {
+        const u32x2 h = __builtin_amdgcn_raw_buffer_load_b64(rs_w, blk + 16u + (uint32_t)(QB * bq), 0, 0);
+        r.qh = u32x4{h.x, h.y, 0u, 0u};
+      }
     }
   };
 
@@ -476,11 +484,16 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
     const h2 sc0v = {s0, s0}, sc1v = {s1, s1}, off0 = {o0, o0}, off1 = {o1, o1};
     constexpr int NW = QB / 4;
     const uint32_t q[4] = {r.q.x, r.q.y, r.q.z, r.q.w};
+    const uint32_t qh[4] = {r.qh.x, r.qh.y, r.qh.z, r.qh.w};
     h2 lo[2 * NW], hi[2 * NW];
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      nib4(q[w] & 0x0F0F0F0Fu, sc0v, off0, lo[2 * w], lo[2 * w + 1]);
-      nib4((q[w] >> 4) & 0x0F0F0F0Fu, sc1v, off1, hi[2 * w], hi[2 * w + 1]);
+      // Q5_K: bit 2c of qh[l] is bit 4 of the low nibble's value, bit 2c + 1
+      // of the high one's (sc * q <= 63 * 31 stays an exact fp16 integer)
+      const uint32_t f0 = kQ5 ? ((qh[w] >> (2 * c)) & 0x01010101u) << 4 : 0u;
+      const uint32_t f1 = kQ5 ? ((qh[w] >> (2 * c + 1)) & 0x01010101u) << 4 : 0u;
+      nib4((q[w] & 0x0F0F0F0Fu) | f0, sc0v, off0, lo[2 * w], lo[2 * w + 1]);
+      nib4(((q[w] >> 4) & 0x0F0F0F0Fu) | f1, sc1v, off1, hi[2 * w], hi[2 * w + 1]);
     }
     u32x4 *dlo = reinterpret_cast<u32x4 *>(&sm.B[buf][br][QB * bq]);
     u32x4 *dhi = reinterpret_cast<u32x4 *>(&sm.B[buf][br][32 + QB * bq]);
@@ -830,6 +843,88 @@ struct DecQ4K {
       const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(xs[q] + 8 * g) : h8{};
       const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
       const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(s4[v], fmaf(dm, mins[v], dv * accs[q][v]), acc[q][v]);
+    }
+  }
+};
+
+// Q5_K: DecQ4K with the fifth bit of every weight from qh (bit 2g + nibble
+// plane of qh[l] for byte l of qs chunk g); sc * q <= 63 * 31 stays an exact
+// fp16 integer.  A lane group reads the header, all 32 qh bytes and its qs
+// chunk: 20 registers per item, so the ring is one item shorter.
+struct DecQ5K {
+  static constexpr uint32_t kBlk = kQ5KBytes;
+  static constexpr bool kSums = true;
+  static constexpr int kDepth = 2, kDepth1 = 3;
+  struct Item {
+    u32x4 hd, h0, h1, q0, q1;
+  };
+  __device__ static void load(Item &it, Rsrc rs, uint32_t blk, int g) {
+    it.hd = bload4(rs, blk);
+    it.h0 = bload4(rs, blk + 16u);
+    it.h1 = bload4(rs, blk + 32u);
+    it.q0 = bload4(rs, blk + 48u + 32u * (uint32_t)g);
+    it.q1 = bload4(rs, blk + 64u + 32u * (uint32_t)g);
+  }
+  template <bool kLo, int RG>
+  __device__ static void contract(const Item &it, const _Float16 *const *ar, const _Float16 *const *arl,
+                                  const _Float16 *const *xs, const float *rsc, int g, f4 *acc) {
+    const f4 zero4 = {0.0f, 0.0f, 0.0f, 0.0f};
+    h2 scv[2], offv[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel(2u * (uint32_t)g + (uint32_t)j, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 sh = (_Float16)(uint16_t)sc, oh = sh * (_Float16)-1024.0f;
+      scv[j] = h2{sh, sh};
+      offv[j] = h2{oh, oh};
+    }
+    h8 mb;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      uint32_t sc, mv;
+      q4k_scale_min_sel((4u * (uint32_t)g + (uint32_t)j) & 7u, it.hd.y, it.hd.z, it.hd.w, sc, mv);
+      const _Float16 mh = g < 2 ? (_Float16)(uint16_t)mv : (_Float16)0.0f;
+      mb[2 * j] = mh;
+      mb[2 * j + 1] = mh;
+    }
+    f4 accs[RG];
+#pragma unroll
+    for (int q = 0; q < RG; ++q) accs[q] = zero4;
+    const uint32_t hsh = 2u * (uint32_t)g;
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int nib = t & 1, p8 = t >> 1;
+      const u32x4 pc = (p8 >> 1) ? it.q1 : it.q0;
+      const u32x4 hc = (p8 >> 1) ? it.h1 : it.h0;
+      const uint32_t d0 = (p8 & 1) ? pc.z : pc.x, d1 = (p8 & 1) ? pc.w : pc.y;
+      const uint32_t e0 = (p8 & 1) ? hc.z : hc.x, e1 = (p8 & 1) ? hc.w : hc.y;
+      const uint32_t f0 = ((e0 >> (hsh + (uint32_t)nib)) & 0x01010101u) << 4;
+      const uint32_t f1 = ((e1 >> (hsh + (uint32_t)nib)) & 0x01010101u) << 4;
+      const uint32_t n0v = (nib ? (d0 >> 4) & 0x0F0F0F0Fu : d0 & 0x0F0F0F0Fu) | f0;
+      const uint32_t n1v = (nib ? (d1 >> 4) & 0x0F0F0F0Fu : d1 & 0x0F0F0F0Fu) | f1;
+      h2 p0, p1, p2, p3;
+      nib4(n0v, scv[nib], offv[nib], p0, p1);
+      nib4(n1v, scv[nib], offv[nib], p2, p3);
+      const h8 bv = {p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
+      const int ka = 64 * g + 32 * nib + 8 * p8;
+#pragma unroll
+      for (int q = 0; q < RG; ++q) {
+        const h8 ah = *reinterpret_cast<const h8 *>(ar[q] + ka);
+        accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ah, bv, accs[q], 0, 0, 0);
+        if (kLo) {
+          const h8 al = *reinterpret_cast<const h8 *>(arl[q] + ka);
+          accs[q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(al, bv, accs[q], 0, 0, 0);
+        }
+      }
+    }
+    const float dv = f16_bits_hw(it.hd.x & 0xffffu), dm = -f16_bits_hw(it.hd.x >> 16);
+#pragma unroll
+    for (int q = 0; q < RG; ++q) {
+      const h8 xa = g < 2 ? *reinterpret_cast<const h8 *>(xs[q] + 8 * g) : h8{};
+      const f4 mins = __builtin_amdgcn_mfma_f32_16x16x32_f16(xa, mb, zero4, 0, 0, 0);
+      const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);
 #pragma unroll
       for (int v = 0; v < 4; ++v) acc[q][v] = fmaf(s4[v], fmaf(dm, mins[v], dv * accs[q][v]), acc[q][v]);
     }
@@ -1555,9 +1650,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_swiglu_kernel(const float *
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
   // 32-bit buffer offsets: activations (with a tile of padding rows) and weights
   const int64_t a_bytes = (M + 256) * K * 2;
-  const int64_t sb_bytes = type == kQ6_K ? kQ6KBytes : type == kQ8_0 ? 8 * kQ8Bytes : kQ4KBytes;
+  const int64_t sb_bytes = sb_bytes_of(type);
   const int64_t w_bytes = (N + kBN) * (K / 256) * sb_bytes + 1024;
-  return (type == kQ4_K || type == kQ6_K || type == kQ8_0) && K % 256 == 0 && N >= 1 && M >= 1 &&
+  return (type == kQ4_K || type == kQ5_K || type == kQ6_K || type == kQ8_0) && K % 256 == 0 && N >= 1 && M >= 1 &&
          a_bytes < (int64_t)UINT32_MAX && w_bytes < (int64_t)UINT32_MAX;
 }
 
@@ -1627,7 +1722,7 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // alone leave CUs idle: enough slices for about one workgroup per CU, at
     // least two super-blocks per slice, at most 8.
     const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
-    p.bm = reg_dequant ? 128 : (type == kQ4_K && x_is_bf16 && M > 128) ? 256 : 128;
+    p.bm = reg_dequant ? 128 : ((type == kQ4_K || type == kQ5_K) && x_is_bf16 && M > 128) ? 256 : 128;
     const int64_t cus = cu_count;
     const int64_t tiles = reg_dequant ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
     if (tiles * 4 < cus * 3) ks = std::min<int64_t>({(cus + tiles - 1) / tiles, nsb / 2, 8});
@@ -1716,6 +1811,9 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
   } else if (type == kQ8_0) {
     if (x_is_bf16) OKQ_DEC_RG(DecQ80, DecQ80, false);
     else OKQ_DEC_RG(DecQ80, DecQ80, true);
+  } else if (type == kQ5_K) {
+    if (x_is_bf16) OKQ_DEC_RG(DecQ5K, DecQ5K, false);
+    else OKQ_DEC_RG(DecQ5K, DecQ5K, true);
   } else {
     if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ4K, false);
     else OKQ_DEC_RG(DecQ4K, DecQ4K, true);
@@ -1741,7 +1839,7 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
 // A matrix's record for the decode-batch kernel (byte sizes within 32 bits:
 // gemm_supported's limits).
 static DecMat dec_mat(int type, int64_t K, const void *w, int64_t n, const float *bias, float *y, int tile0) {
-  const int64_t sb_bytes = type == kQ6_K ? kQ6KBytes : type == kQ8_0 ? 8 * kQ8Bytes : kQ4KBytes;
+  const int64_t sb_bytes = sb_bytes_of(type);
   DecMat d{};
   d.w = static_cast<const uint8_t *>(w);
   d.bias = bias;
@@ -1756,7 +1854,7 @@ static DecMat dec_mat(int type, int64_t K, const void *w, int64_t n, const float
 hipError_t launch_gemm_decode_multi(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, int count,
                                     const void *const *w, const int64_t *N, const float *const *bias, float *const *y,
                                     void *workspace, const GemmPlan &plan, hipStream_t s, bool swiglu) {
-  if ((type != kQ4_K && type != kQ6_K && type != kQ8_0) || plan.bm != kDecRows || M > kDecRows || count < 1 ||
+  if ((type != kQ4_K && type != kQ5_K && type != kQ6_K && type != kQ8_0) || plan.bm != kDecRows || M > kDecRows || count < 1 ||
       count > kDecMats || (swiglu && (count != 2 || N[0] != N[1])))
     return hipErrorInvalidValue;
   DecMats mats{};
@@ -1818,6 +1916,10 @@ static hipError_t launch_gemm_tiled(int type, bool x_is_bf16, _Float16 *xhi, _Fl
   } else if (type == kQ8_0) {
     if (x_is_bf16) OKQ_GEMM(128, false, kQ8_0);
     else OKQ_GEMM(128, true, kQ8_0);
+  } else if (type == kQ5_K) {
+    if (plan.bm == 256) OKQ_GEMM(256, false, kQ5_K);
+    else if (x_is_bf16) OKQ_GEMM(128, false, kQ5_K);
+    else OKQ_GEMM(128, true, kQ5_K);
   } else if (plan.bm == 256) {
     OKQ_GEMM(256, false, kQ4_K);
   } else if (x_is_bf16) {
@@ -1832,8 +1934,8 @@ static hipError_t launch_gemm_tiled(int type, bool x_is_bf16, _Float16 *xhi, _Fl
 
 hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64_t K, const void *w, int64_t N,
                        const float *bias, float *y, void *workspace, const GemmPlan &plan, hipStream_t s) {
-  if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
-  if (type != kQ4_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
+  if (type != kQ4_K && type != kQ5_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
+  if (type != kQ4_K && type != kQ5_K && plan.bm != 128 && plan.bm != kDecRows) return hipErrorInvalidValue;
   char *ws = static_cast<char *>(workspace);
   const uint8_t *W = static_cast<const uint8_t *>(w);
   const int m = (int)M, n = (int)N, ks = plan.ksplit;

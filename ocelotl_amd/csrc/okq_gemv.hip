@@ -183,6 +183,84 @@ struct FQ4K {
 };
 
 // ---------------------------------------------------------------------------
+// Q5_K: Q4_K with a fifth bit per weight.  Unit = (super-block, 64-weight
+// chunk c): the 16-byte header, the 32 qh bytes (bit 2c of qh[l] tops the
+// low nibble of qs byte l of the chunk, bit 2c + 1 the high one) and the
+// chunk's 32 qs bytes.  The four lanes of a super-block read the same qh
+// bytes in one instruction.
+// ---------------------------------------------------------------------------
+struct FQ5K {
+  static constexpr int kRun = 32;
+  static constexpr int kType = kQ5_K;
+  __device__ static int kidx(int u, int e) { return 64 * u + e; }
+  static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 256) * kQ5KBytes; }
+  struct Regs {
+    u32x4a4 hd, ha, hb, qa, qb;
+  };
+  static constexpr int kMaxDepth = 2;
+  __device__ static uint32_t unit_off(int u) { return (uint32_t)(u >> 2) * kQ5KBytes; }
+  __device__ static void load(Regs &r, Rsrc rs, uint32_t blk, uint32_t lane) {
+    const uint32_t c = lane & 3;
+    r.hd = ld4(rs, blk);
+    r.ha = ld4(rs, blk + 16);
+    r.hb = ld4(rs, blk + 32);
+    r.qa = ld4(rs, blk + 48 + 32 * c);
+    r.qb = ld4(rs, blk + 64 + 32 * c);
+  }
+  __device__ static void xslot(int run, int &rec, int &word, int &slot) { FQ4K::xslot(run, rec, word, slot); }
+  __device__ static float compute(const Regs &r, const XRec &x, const LdsU32 *xlo, bool lo3, uint32_t lane) {
+    const uint32_t c = lane & 3;
+    const uint32_t q[8] = {r.qa.x, r.qa.y, r.qa.z, r.qa.w, r.qb.x, r.qb.y, r.qb.z, r.qb.w};
+    const uint32_t h[8] = {r.ha.x, r.ha.y, r.ha.z, r.ha.w, r.hb.x, r.hb.y, r.hb.z, r.hb.w};
+    uint32_t lo5[8], hi5[8];
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const uint32_t hs = h[w] >> (2 * c);
+      lo5[w] = (q[w] & 0x0F0F0F0Fu) | ((hs << 4) & 0x10101010u);
+      hi5[w] = ((q[w] >> 4) & 0x0F0F0F0Fu) | ((hs << 3) & 0x10101010u);
+    }
+    int ah = 0, am = 0, al = 0, bh = 0, bm = 0, bl = 0;
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      ah = sdot4(lo5[w], x.hi[w], ah);
+      am = sdot4(lo5[w], x.mi[w], am);
+      bh = sdot4(hi5[w], x.hi[8 + w], bh);
+      bm = sdot4(hi5[w], x.mi[8 + w], bm);
+    }
+    if (lo3) {  // wave-uniform
+#pragma unroll
+      for (int w = 0; w < 8; ++w) {
+        al = sdot4(lo5[w], xlo[w], al);
+        bl = sdot4(hi5[w], xlo[8 + w], bl);
+      }
+    }
+    // the scale/min fields are Q4_K's (see FQ4K::compute)
+    const bool lowj = c < 2;
+    const uint32_t width = lowj ? 6u : 4u;
+    const uint32_t himask = lowj ? 0u : 0x30u;
+    const uint32_t srcs = lowj ? r.hd.y : r.hd.w;
+    const uint32_t srcm = lowj ? r.hd.z : r.hd.w;
+    const uint32_t j0 = (2 * c) & 3, j1 = (2 * c + 1) & 3;
+    const uint32_t mo = lowj ? 0u : 4u;
+    const uint32_t scA =
+        __builtin_amdgcn_ubfe(srcs, 8 * j0, width) | ((__builtin_amdgcn_ubfe(r.hd.y, 8 * j0 + 6, 2) << 4) & himask);
+    const uint32_t scB =
+        __builtin_amdgcn_ubfe(srcs, 8 * j1, width) | ((__builtin_amdgcn_ubfe(r.hd.y, 8 * j1 + 6, 2) << 4) & himask);
+    const uint32_t mA =
+        __builtin_amdgcn_ubfe(srcm, 8 * j0 + mo, width) | ((__builtin_amdgcn_ubfe(r.hd.z, 8 * j0 + 6, 2) << 4) & himask);
+    const uint32_t mB =
+        __builtin_amdgcn_ubfe(srcm, 8 * j1 + mo, width) | ((__builtin_amdgcn_ubfe(r.hd.z, 8 * j1 + 6, 2) << 4) & himask);
+    const float d = f16_bits_hw(r.hd.x & 0xffffu);
+    const float dmin = f16_bits_hw(r.hd.x >> 16);
+    const float pa = x.s[0] * limb_sum(ah, am, al);
+    const float pb = x.s[1] * limb_sum(bh, bm, bl);
+    const float a = fmaf(d * (float)scA, pa, -((dmin * (float)mA) * x.t[0]));
+    const float b = fmaf(d * (float)scB, pb, -((dmin * (float)mB) * x.t[1]));
+    return a + b;
+  }
+};
+
+// ---------------------------------------------------------------------------
 // Q6_K
 // ---------------------------------------------------------------------------
 struct FQ6K {
@@ -327,14 +405,16 @@ __device__ __forceinline__ float deq_elem(int type, const uint8_t *row, uint32_t
     const uint8_t *blk = row + (size_t)(k >> 5) * kQ8Bytes;
     const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk));
     return (float)(int8_t)blk[2 + (k & 31)] * d;
-  } else if (type == kQ4_K) {
-    const uint8_t *blk = row + (size_t)(k >> 8) * kQ4KBytes;
+  } else if (type == kQ4_K || type == kQ5_K) {
+    const bool q5 = type == kQ5_K;
+    const uint8_t *blk = row + (size_t)(k >> 8) * (q5 ? kQ5KBytes : kQ4KBytes);
     const uint32_t rr = k & 255u, c = rr >> 6, hi = (rr >> 5) & 1u, l = rr & 31u;
     const uint32_t *wd = reinterpret_cast<const uint32_t *>(blk);
     uint32_t sc, m;
     q4k_scale_min(2 * c + hi, wd[1], wd[2], wd[3], sc, m);
     const float d = f16_bits_hw(wd[0] & 0xffffu), dmin = f16_bits_hw(wd[0] >> 16);
-    const uint32_t q = (blk[16 + 32 * c + l] >> (4 * hi)) & 15u;
+    uint32_t q = (blk[(q5 ? 48 : 16) + 32 * c + l] >> (4 * hi)) & 15u;
+    if (q5) q |= ((blk[16 + l] >> (2 * c + hi)) & 1u) << 4;
     return (d * (float)sc) * (float)q - dmin * (float)m;
   } else {
     const uint8_t *blk = row + (size_t)(k >> 8) * kQ6KBytes;
@@ -970,7 +1050,8 @@ void launch_rows(int R, int xv, int64_t steps, dim3 grid, dim3 block, size_t lds
 namespace {
 
 size_t row_bytes_of(int type, int64_t K) {
-  return (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes : (K / 256) * (type == kQ4_K ? kQ4KBytes : kQ6KBytes));
+  return (size_t)(type == kQ8_0 ? (K / 32) * kQ8Bytes
+                                : (K / 256) * (type == kQ4_K ? kQ4KBytes : type == kQ5_K ? kQ5KBytes : kQ6KBytes));
 }
 
 // Conditions of the streaming kernel for one matrix: aligned base, a 32-bit
@@ -979,7 +1060,7 @@ bool fast_ok(int type, int64_t K, const void *w, int64_t N) {
   const uintptr_t wa = reinterpret_cast<uintptr_t>(w);
   const size_t bytes = (size_t)N * row_bytes_of(type, K);
   bool fast = (K % 64 == 0) && K <= 4 * kMaxXV * 1024 && bytes < 0xFFFFFFFFull;
-  if (type == kQ4_K) fast = fast && (wa & 15u) == 0;
+  if (type == kQ4_K || type == kQ5_K) fast = fast && (wa & 15u) == 0;
   else if (type == kQ6_K) fast = fast && (wa & 3u) == 0;
   else fast = fast && (wa & 3u) == 0 && ((K / 32) % 2 == 0);
   return fast;
@@ -1029,6 +1110,7 @@ hipError_t launch_stream(int type, const float *x, int64_t K, const GemvLaunch &
   const int64_t steps = (N + blocks * G - 1) / (blocks * G);  // the kernel's own count
   L.dyn = T == 1 && steps > kDynSteps;
   if (type == kQ4_K) launch_rows<FQ4K>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
+  else if (type == kQ5_K) launch_rows<FQ5K>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
   else if (type == kQ6_K) launch_rows<FQ6K>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
   else launch_rows<FQ80>(R, xv, steps0, grid, block, lds, s, L, x, k, T, gg);
   return hipGetLastError();
@@ -1041,7 +1123,7 @@ bool gemv_streams(int type, int64_t K, const void *w, int64_t N) { return fast_o
 hipError_t launch_gemv_multi(int type, const float *x, int64_t K, int64_t rows, int count, const void *const *w,
                              const int64_t *N, const float *const *bias, float *const *y, int cu_count,
                              hipStream_t s, const GemvPro &pro) {
-  if (type != kQ4_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
+  if (type != kQ4_K && type != kQ5_K && type != kQ6_K && type != kQ8_0) return hipErrorInvalidValue;
   if (count < 1 || count > kGemvMaxProblems) return hipErrorInvalidValue;
   if (pro.kind != kProNone && rows != 1) return hipErrorNotSupported;  // prologues run one row at a time
   GemvLaunch P{};

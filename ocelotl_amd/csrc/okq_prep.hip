@@ -208,12 +208,16 @@ __global__ __launch_bounds__(64) void quantize_q8_0_kernel(const float *__restri
   }
 }
 
-__global__ __launch_bounds__(64) void quantize_q4_k_kernel(const float *__restrict__ x, int64_t nblocks,
-                                                            uint8_t *__restrict__ dst) {
-  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (b >= nblocks) return;
-  const float *xb = x + b * 256;
-  uint8_t *blk = dst + b * kQ4KBytes;
+// Q4_K and Q5_K (kQ5): per 32-sub-block mn = min(0, min x), mx = max x,
+// scale = (mx - mn) / L (L = 15 or 31 levels), mmin = -mn; d = max scale /
+// 63, dmin = max mmin / 63 (fp16); 6-bit ls, lm = rint(63 * v / max);
+// q = clamp(rint((x + dmin16 * lm) / (d16 * ls)), 0, L).  Q5_K keeps the
+// low four bits in qs and bit 4 of element l of chunk c in bit 2c (low
+// nibbles) or 2c + 1 (high nibbles) of qh[l].
+template <bool kQ5>
+__device__ __forceinline__ void quantize_q45_k(const float *__restrict__ xb, uint8_t *__restrict__ blk) {
+  constexpr float kLevels = kQ5 ? 31.0f : 15.0f;
+  constexpr int kMaxQ = kQ5 ? 31 : 15;
   float scale[8], mmin[8];
   float max_scale = 0.0f, max_min = 0.0f;
   for (int s = 0; s < 8; ++s) {
@@ -223,7 +227,7 @@ __global__ __launch_bounds__(64) void quantize_q4_k_kernel(const float *__restri
       mx = maxf_(mx, xb[32 * s + j]);
     }
     mn = minf_(mn, 0.0f);
-    scale[s] = __fdiv_rn(__fsub_rn(mx, mn), 15.0f);
+    scale[s] = __fdiv_rn(__fsub_rn(mx, mn), kLevels);
     mmin[s] = -mn;
     max_scale = maxf_(max_scale, scale[s]);
     max_min = maxf_(max_min, mmin[s]);
@@ -247,18 +251,39 @@ __global__ __launch_bounds__(64) void quantize_q4_k_kernel(const float *__restri
   }
   for (int j = 0; j < 12; ++j) blk[4 + j] = (uint8_t)sc[j];
   float d16 = f16_bits_exact(dh), dmin16 = f16_bits_exact(dminh);
-  uint8_t *qs = blk + 16;
+  uint8_t *qh = blk + 16;
+  uint8_t *qs = blk + (kQ5 ? 48 : 16);
+  uint32_t hbits[32];
+  for (int l = 0; l < 32; ++l) hbits[l] = 0u;
   for (int c = 0; c < 4; ++c) {
     float de0 = __fmul_rn(d16, (float)ls[2 * c]), me0 = __fmul_rn(dmin16, (float)lm[2 * c]);
     float de1 = __fmul_rn(d16, (float)ls[2 * c + 1]), me1 = __fmul_rn(dmin16, (float)lm[2 * c + 1]);
     for (int l = 0; l < 32; ++l) {
       int q0 = 0, q1 = 0;
-      if (de0 != 0.0f) q0 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + l], me0), de0)), 0, 15);
+      if (de0 != 0.0f)
+        q0 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + l], me0), de0)), 0, kMaxQ);
       if (de1 != 0.0f)
-        q1 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + 32 + l], me1), de1)), 0, 15);
-      qs[32 * c + l] = (uint8_t)(q0 | (q1 << 4));
+        q1 = clampi_((int)__builtin_rintf(__fdiv_rn(__fadd_rn(xb[64 * c + 32 + l], me1), de1)), 0, kMaxQ);
+      qs[32 * c + l] = (uint8_t)((q0 & 15) | ((q1 & 15) << 4));
+      if (kQ5) hbits[l] |= ((uint32_t)(q0 >> 4) << (2 * c)) | ((uint32_t)(q1 >> 4) << (2 * c + 1));
     }
   }
+  if (kQ5)
+    for (int l = 0; l < 32; ++l) qh[l] = (uint8_t)hbits[l];
+}
+
+__global__ __launch_bounds__(64) void quantize_q4_k_kernel(const float *__restrict__ x, int64_t nblocks,
+                                                            uint8_t *__restrict__ dst) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  quantize_q45_k<false>(x + b * 256, dst + b * kQ4KBytes);
+}
+
+__global__ __launch_bounds__(64) void quantize_q5_k_kernel(const float *__restrict__ x, int64_t nblocks,
+                                                            uint8_t *__restrict__ dst) {
+  int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (b >= nblocks) return;
+  quantize_q45_k<true>(x + b * 256, dst + b * kQ5KBytes);
 }
 
 __global__ __launch_bounds__(64) void quantize_q6_k_kernel(const float *__restrict__ x, int64_t nblocks,
@@ -404,6 +429,11 @@ hipError_t launch_quantize(int type, const float *src, int64_t n, void *dst, hip
   case kQ4_K: {
     int64_t nb = n / 256;
     hipLaunchKernelGGL(quantize_q4_k_kernel, dim3(grid_for(nb, 64)), dim3(64), 0, s, src, nb, p);
+    break;
+  }
+  case kQ5_K: {
+    int64_t nb = n / 256;
+    hipLaunchKernelGGL(quantize_q5_k_kernel, dim3(grid_for(nb, 64)), dim3(64), 0, s, src, nb, p);
     break;
   }
   case kQ6_K: {

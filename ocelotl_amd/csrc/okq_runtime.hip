@@ -38,7 +38,7 @@ okq_status ok() { return OKQ_OK; }
 struct TypeInfo {
   int64_t elems, bytes;
   bool quantized;  // block-encoded: dequantize and row gather serve it
-  bool linear;     // the linear kernels serve it (Q8_0, Q4_K, Q6_K)
+  bool linear;     // the linear kernels serve it (Q8_0, Q4_K, Q5_K, Q6_K)
 };
 
 bool type_info(uint32_t t, TypeInfo &ti) {
@@ -52,7 +52,7 @@ bool type_info(uint32_t t, TypeInfo &ti) {
   case OKQ_TYPE_Q5_1: ti = {32, 24, true, false}; return true;
   case OKQ_TYPE_Q2_K: ti = {256, 84, true, false}; return true;
   case OKQ_TYPE_Q3_K: ti = {256, 110, true, false}; return true;
-  case OKQ_TYPE_Q5_K: ti = {256, 176, true, false}; return true;
+  case OKQ_TYPE_Q5_K: ti = {256, 176, true, true}; return true;
   case OKQ_TYPE_F32: ti = {1, 4, false, false}; return true;
   case OKQ_TYPE_F16: ti = {1, 2, false, false}; return true;
   case OKQ_TYPE_BF16: ti = {1, 2, false, false}; return true;
@@ -81,7 +81,7 @@ const char *type_name(uint32_t t) {
 }
 
 okq_status unsupported_type(uint32_t t, const char *what) {
-  return fail(OKQ_E_TYPE, "unsupported %s: tensor type %s (%u); supported: Q8_0, Q4K, Q6K", what, type_name(t),
+  return fail(OKQ_E_TYPE, "unsupported %s: tensor type %s (%u); supported: Q8_0, Q4K, Q5K, Q6K", what, type_name(t),
               t);
 }
 

@@ -16,8 +16,8 @@
 
 namespace ocelotl {
 
-// The block formats decoded on the host: the three the linear path executes
-// (Q8_0, Q4K, Q6K) and Q5K.
+// The block formats decoded on the host: the four the linear path executes
+// (Q8_0, Q4K, Q5K, Q6K).
 bool host_dequant_supports(GgmlTensorType type);
 
 // Decodes n elements (a multiple of the format's block) of `src` (src_len

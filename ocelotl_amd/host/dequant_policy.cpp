@@ -38,10 +38,11 @@ TensorExecution tensor_execution(uint32_t raw_type) {
   switch (raw_type) {
   case 8:   // Q8_0
   case 12:  // Q4K
+  case 13:  // Q5K
   case 14:  // Q6K
     return TensorExecution::QuantizedLinear;
   case 2: case 3: case 6: case 7:  // Q4_0, Q4_1, Q5_0, Q5_1
-  case 10: case 11: case 13:       // Q2K, Q3K, Q5K
+  case 10: case 11:                // Q2K, Q3K
     return TensorExecution::DequantizeToF32;
   default:
     return TensorExecution::None;
@@ -62,9 +63,9 @@ Result<void> ensure_supported_for_execution(const std::vector<uint32_t> &tensor_
   std::string requested;
   for (size_t i = 0; i < refused.size(); ++i) requested += (i ? "," : "") + ggml_type_name(refused[i]);
   return OcelotlError::unsupported("quantized_tensor_types", requested,
-                                   {"Q8_0", "Q4K", "Q6K", "Q4_0 (dequantized)", "Q4_1 (dequantized)",
+                                   {"Q8_0", "Q4K", "Q5K", "Q6K", "Q4_0 (dequantized)", "Q4_1 (dequantized)",
                                     "Q5_0 (dequantized)", "Q5_1 (dequantized)", "Q2K (dequantized)",
-                                    "Q3K (dequantized)", "Q5K (dequantized)"});
+                                    "Q3K (dequantized)"});
 }
 
 Result<void> ensure_supported_for_execution(const GgufManifest &manifest) {

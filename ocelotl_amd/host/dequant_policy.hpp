@@ -32,10 +32,10 @@ std::string ggml_type_name(uint32_t raw_type);
 
 // How this backend executes a tensor of a GGML type:
 //   Float           -- not quantized: the reference's own f32 path
-//   QuantizedLinear -- Q8_0, Q4K, Q6K: linear_d / linear_out_by_in on the GGUF
+//   QuantizedLinear -- Q8_0, Q4K, Q5K, Q6K: linear_d / linear_out_by_in on the GGUF
 //                      blocks (decode GEMV, MFMA GEMM), dequantize and
 //                      embedding_rows
-//   DequantizeToF32 -- Q4_0, Q4_1, Q5_0, Q5_1, Q2K, Q3K, Q5K: dequantize /
+//   DequantizeToF32 -- Q4_0, Q4_1, Q5_0, Q5_1, Q2K, Q3K: dequantize /
 //                      embedding_rows on the GPU, then the f32 path
 //   None            -- every other block format (Q8_1, Q8K, the IQ and TQ
 //                      formats, MXFP4, unknown ids)

@@ -20,7 +20,7 @@ namespace {
 constexpr const char *kBackend = "hip-gfx950";
 
 const std::vector<std::string> &quantized_names() {
-  static const std::vector<std::string> v = {"Q8_0", "Q4K", "Q6K"};
+  static const std::vector<std::string> v = {"Q8_0", "Q4K", "Q5K", "Q6K"};
   return v;
 }
 
@@ -386,7 +386,7 @@ Result<QuantizedWeight> HipKernelBackend::upload_quantized(GgmlTensorType type, 
 Result<void> HipKernelBackend::linear_out_by_in(const float *, size_t, size_t, size_t, const float *, size_t,
                                                 size_t, const float *, size_t, float *, size_t) const {
   return OcelotlError::unsupported("f32_linear_out_by_in", std::string(kBackend),
-                                   {"quantized weights: Q8_0", "Q4K", "Q6K"});
+                                   {"quantized weights: Q8_0", "Q4K", "Q5K", "Q6K"});
 }
 
 Result<void> HipKernelBackend::dequantize(GgmlTensorType type, const uint8_t *src, size_t src_len, size_t n,

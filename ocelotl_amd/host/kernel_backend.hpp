@@ -130,7 +130,7 @@ struct KernelContext {
 
 // Raw GGML tensor type ids (crates/loader/src/gguf_inspect.rs:170-206): the
 // block formats this path dequantizes and gathers (the linear kernels execute
-// Q8_0, Q4K and Q6K) plus the unquantized float types.
+// Q8_0, Q4K, Q5K and Q6K) plus the unquantized float types.
 enum class GgmlTensorType : uint32_t {
   F32 = 0,
   F16 = 1,
@@ -309,7 +309,7 @@ class HipKernelBackend final : public KernelBackend {
 
   // Uploads raw GGUF blocks after checking their byte length against the
   // shape; any block format is accepted (Unsupported otherwise).  linear_d
-  // takes Q8_0 / Q4K / Q6K weights, dequantize and embedding_rows all of them.
+  // takes Q8_0 / Q4K / Q5K / Q6K weights, dequantize and embedding_rows all of them.
   Result<QuantizedWeight> upload_quantized(GgmlTensorType type, size_t ne0, size_t ne1, const uint8_t *blocks,
                                            size_t len) const;
   // The weight dequantized to f32 on the device (bit-exact with the CPU

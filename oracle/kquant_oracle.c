@@ -19,9 +19,10 @@
  *     (gguf_inspect.rs:208-219 leaves quantized byte_len = None); the layouts
  *     are the public GGUF/ggml block spec.  Pinned by an independent numpy
  *     bit-field decoder, closed forms and element-order probes.
- *   - Quantizers for the three formats.  The reference has none; this is the
- *     build's own algorithm (ggml-like, not bit-identical to ggml), defined
- *     exactly here so that the GPU quantizer can be checked byte-for-byte.
+ *   - Quantizers for the linear path's formats (Q8_0, Q4_K, Q5_K, Q6_K).
+ *     The reference has none; this is the build's own algorithm (ggml-like,
+ *     not bit-identical to ggml), defined exactly here so that the GPU
+ *     quantizer can be checked byte-for-byte.
  *   - Seeded N(0, sigma) generator (SplitMix64 + Irwin-Hall(12) in integer
  *     arithmetic, so CPU and GPU produce identical floats).
  *   - The reference CPU linear path, restated with the same accumulation
@@ -464,15 +465,21 @@ OKR_API int okr_quantize_q8_0(const float *x, int64_t n, uint8_t *dst) {
     return 0;
 }
 
-/* Q4_K: per 32-sub-block  mn = min(0, min x), mx = max x,
- * scale = (mx - mn)/15, mmin = -mn; super-block d = max(scale)/63,
- * dmin = max(mmin)/63; 6-bit ls = rint(scale*63/max_scale), lm likewise;
- * q = clamp(rint((x + dmin16*lm) / (d16*ls)), 0, 15). */
-OKR_API int okr_quantize_q4_k(const float *x, int64_t n, uint8_t *dst) {
+/* Q4_K (levels 15) and Q5_K (levels 31): per 32-sub-block
+ * mn = min(0, min x), mx = max x, scale = (mx - mn)/levels, mmin = -mn;
+ * super-block d = max(scale)/63, dmin = max(mmin)/63; 6-bit
+ * ls = rint(scale*63/max_scale), lm likewise;
+ * q = clamp(rint((x + dmin16*lm) / (d16*ls)), 0, levels).  Q5_K stores the
+ * low four bits of q in qs and bit 4 of element l of chunk c in bit 2c (low
+ * nibble) or 2c+1 (high nibble) of qh[l]. */
+static int quantize_q45_k(const float *x, int64_t n, uint8_t *dst, int q5) {
     if (n % 256) return 1;
+    const float levels = q5 ? 31.0f : 15.0f;
+    const int maxq = q5 ? 31 : 15;
+    const int64_t bytes = q5 ? 176 : 144;
     for (int64_t b = 0; b < n / 256; ++b) {
         const float *xb = x + b * 256;
-        uint8_t *blk = dst + b * 144;
+        uint8_t *blk = dst + b * bytes;
         float scale[8], mmin[8];
         float max_scale = 0.0f, max_min = 0.0f;
         for (int s = 0; s < 8; ++s) {
@@ -482,7 +489,7 @@ OKR_API int okr_quantize_q4_k(const float *x, int64_t n, uint8_t *dst) {
                 mx = maxf_(mx, xb[32 * s + j]);
             }
             mn = minf_(mn, 0.0f);
-            scale[s] = (mx - mn) / 15.0f;
+            scale[s] = (mx - mn) / levels;
             mmin[s] = -mn;
             max_scale = maxf_(max_scale, scale[s]);
             max_min = maxf_(max_min, mmin[s]);
@@ -516,16 +523,29 @@ OKR_API int okr_quantize_q4_k(const float *x, int64_t n, uint8_t *dst) {
             float me = dmin16 * (float)lm[s];
             for (int j = 0; j < 32; ++j) {
                 int q = 0;
-                if (de != 0.0f) q = clampi_((int)rintf((xb[32 * s + j] + me) / de), 0, 15);
+                if (de != 0.0f) q = clampi_((int)rintf((xb[32 * s + j] + me) / de), 0, maxq);
                 L[32 * s + j] = (uint8_t)q;
             }
         }
-        uint8_t *qs = blk + 16;
+        uint8_t *qs = blk + (q5 ? 48 : 16);
         for (int c = 0; c < 4; ++c)
-            for (int l = 0; l < 32; ++l) qs[32 * c + l] = (uint8_t)(L[64 * c + l] | (L[64 * c + 32 + l] << 4));
+            for (int l = 0; l < 32; ++l)
+                qs[32 * c + l] = (uint8_t)((L[64 * c + l] & 15) | ((L[64 * c + 32 + l] & 15) << 4));
+        if (q5) {
+            uint8_t *qh = blk + 16;
+            for (int l = 0; l < 32; ++l) {
+                uint8_t h = 0;
+                for (int c = 0; c < 4; ++c)
+                    h |= (uint8_t)(((L[64 * c + l] >> 4) << (2 * c)) | ((L[64 * c + 32 + l] >> 4) << (2 * c + 1)));
+                qh[l] = h;
+            }
+        }
     }
     return 0;
 }
+
+OKR_API int okr_quantize_q4_k(const float *x, int64_t n, uint8_t *dst) { return quantize_q45_k(x, n, dst, 0); }
+OKR_API int okr_quantize_q5_k(const float *x, int64_t n, uint8_t *dst) { return quantize_q45_k(x, n, dst, 1); }
 
 /* Q6_K: per 16-sub-block the signed value of largest |x| (first on ties)
  * gives scale = -mx/32; super-block iscale = -128/max_scale (signed, largest
@@ -584,6 +604,7 @@ OKR_API int okr_quantize(int type, const float *x, int64_t n, uint8_t *dst) {
     switch (type) {
     case OKR_Q8_0: return okr_quantize_q8_0(x, n, dst);
     case OKR_Q4_K: return okr_quantize_q4_k(x, n, dst);
+    case OKR_Q5_K: return okr_quantize_q5_k(x, n, dst);
     case OKR_Q6_K: return okr_quantize_q6_k(x, n, dst);
     default: return 2;
     }

@@ -34,7 +34,7 @@ F32, F16, Q8_0, Q4_K, Q6_K, BF16 = 0, 1, 8, 12, 14, 30
 # the other block formats GgmlTensorType names (gguf_inspect.rs:132-167) that
 # the dequantize and row-gather entry points serve
 Q4_0, Q4_1, Q5_0, Q5_1, Q2_K, Q3_K, Q5_K = 2, 3, 6, 7, 10, 11, 13
-LINEAR_TYPES = (Q8_0, Q4_K, Q6_K)
+LINEAR_TYPES = (Q8_0, Q4_K, Q5_K, Q6_K)
 GATHER_TYPES = (Q4_0, Q4_1, Q5_0, Q5_1, Q8_0, Q2_K, Q3_K, Q4_K, Q5_K, Q6_K)
 BLOCK_ELEMS = {Q4_0: 32, Q4_1: 32, Q5_0: 32, Q5_1: 32, Q8_0: 32,
                Q2_K: 256, Q3_K: 256, Q4_K: 256, Q5_K: 256, Q6_K: 256}

@@ -327,9 +327,9 @@ void dequant_policy_gate_flips_for_executable_types() {
   }
   CHECK(is_quantized_tensor_type(1000), "unknown ids are quantized");
   CHECK(tensor_execution(12) == TensorExecution::QuantizedLinear && tensor_execution(8) == TensorExecution::QuantizedLinear &&
-            tensor_execution(14) == TensorExecution::QuantizedLinear,
-        "Q8_0, Q4K, Q6K run the quantized linear");
-  for (uint32_t t : {2u, 3u, 6u, 7u, 10u, 11u, 13u}) CHECK(tensor_execution(t) == TensorExecution::DequantizeToF32, "dequantized");
+            tensor_execution(13) == TensorExecution::QuantizedLinear && tensor_execution(14) == TensorExecution::QuantizedLinear,
+        "Q8_0, Q4K, Q5K, Q6K run the quantized linear");
+  for (uint32_t t : {2u, 3u, 6u, 7u, 10u, 11u}) CHECK(tensor_execution(t) == TensorExecution::DequantizeToF32, "dequantized");
   for (uint32_t t : {9u, 15u, 16u, 23u, 29u, 34u, 39u, 77u}) CHECK(tensor_execution(t) == TensorExecution::None, "refused");
   CHECK(tensor_execution(0) == TensorExecution::Float && tensor_execution(30) == TensorExecution::Float, "float");
   CHECK(ggml_type_name(16) == "Iq2Xxs" && ggml_type_name(9) == "Q8_1" && ggml_type_name(39) == "MXFP4" &&

@@ -83,9 +83,9 @@ def test_linear_validation_happens_before_launch(okqlib):
     # in_features must be block aligned
     assert _linear(okqlib, 1, 4000, 12, 0, 10) == okq.E_SHAPE
     # unsupported type -> Unsupported: the dequantize-only block formats too
-    for t in (2, 3, 6, 7, 10, 11, 13, 0, 9):
+    for t in (2, 3, 6, 7, 10, 11, 0, 9):
         assert _linear(okqlib, 1, 4096, t, 0, 10) == okq.E_TYPE
-        assert "supported: Q8_0, Q4K, Q6K" in okq.last_error()
+        assert "supported: Q8_0, Q4K, Q5K, Q6K" in okq.last_error()
     # rows == 0 is a no-op even with null pointers (reference accepts empty slices)
     assert okqlib.okq_linear_out_by_in_q(None, 0, 4096, 12, None, 2304 * 10, 10, None, None, None) == okq.OK
     # null pointers with work to do

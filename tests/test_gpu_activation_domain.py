@@ -29,7 +29,7 @@ from oracle import oracle as O
 
 pytestmark = pytest.mark.gpu
 TOL = 1e-3
-TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
+TYPES = [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
 
 
 @pytest.fixture(scope="module")
@@ -206,7 +206,7 @@ def test_rmsnorm_linear_with_an_infinity_is_nan_like_the_reference(torch, okq, o
     assert same_ieee(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("t,rows", [(O.Q4_K, 8), (O.Q6_K, 12), (O.Q4_K, 40), (O.Q6_K, 40)])
+@pytest.mark.parametrize("t,rows", [(O.Q4_K, 8), (O.Q6_K, 12), (O.Q4_K, 40), (O.Q6_K, 40), (O.Q5_K, 12), (O.Q5_K, 40)])
 def test_mfma_paths_confine_non_finite_rows(torch, okq, orc, t, rows):
     """Decode-batch and tiled MFMA kernels: a row holding an infinity or a NaN
     gets non-finite outputs (not necessarily the reference's sign pattern),

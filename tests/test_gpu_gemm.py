@@ -544,3 +544,102 @@ def test_gemm_wide_one_hot_columns_are_exact(torch, okq, orc):
     x[np.arange(cols.size), cols] = 1.0
     got = run(torch, okq, "okq_gemm_bf16", O.Q4_K, orc.f32_to_bf16(x.reshape(-1)), cols.size, k, wq, n)
     assert np.array_equal(got, w[:, cols].T)
+
+
+# ---- Q5_K ------------------------------------------------------------------------
+# Q4_K with a fifth bit per weight (qh): B = sc * q with q <= 31, so sc * q <=
+# 1953 stays an exact fp16 integer and every product is exact as for Q4_K.
+# The decode-batch kernel (DecQ5K) and the tiled kernel take it; the
+# register-dequant prefill kernels stay Q4_K-only.
+
+Q5K_CASES = [
+    # decode batches: one and two 16-row groups, split and unsplit K, ragged N
+    ("okq_gemm", 1, 96, 256), ("okq_gemm", 5, 300, 1024), ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1000, 768),
+    ("okq_gemm", 13, 4096, 14336), ("okq_gemm_bf16", 3, 14336, 4096), ("okq_gemm", 6, 8000, 4096),
+    ("okq_gemm", 17, 300, 1024), ("okq_gemm", 32, 4096, 4096), ("okq_gemm_bf16", 25, 1000, 768),
+    ("okq_gemm", 2, 70001, 256), ("okq_gemm", 32, 300, 32768),
+    # tiled GEMM: 128-row tiles (f32 with the lo plane, bf16) and 256-row tiles (bf16 above 128 rows)
+    ("okq_gemm", 33, 300, 1024), ("okq_gemm", 100, 257, 768), ("okq_gemm_bf16", 40, 1000, 512),
+    ("okq_gemm_bf16", 130, 1024, 4096), ("okq_gemm_bf16", 300, 4096, 14336), ("okq_gemm", 64, 4096, 4096),
+]
+
+
+@pytest.mark.parametrize("entry,rows,n,k", Q5K_CASES)
+def test_gemm_q5k_matches_reference(torch, okq, orc, entry, rows, n, k):
+    print(f"[gpu] gemm {entry} Q5_K M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(O.Q5_K, orc.normal(2100 + n + k, n * k, 0.02))
+    bias = orc.normal(2101 + rows, n, 0.1)
+    if entry == "okq_gemm_bf16":
+        xin, x32 = bf16_inputs(orc, 2102 + rows, rows, k)
+    else:
+        xin = x32 = orc.normal(2102 + rows, rows * k, 1.0)
+    got = run(torch, okq, entry, O.Q5_K, xin, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q5_K, got, x32, rows, k, wq, n, bias, None if n * k * rows <= 2e9 else 8)
+
+
+@pytest.mark.parametrize("rows", [128, 512, 2048])
+def test_gemm_q5k_prefill_c4_gate_sampled_rows(torch, okq, orc, rows):
+    """Q5_K prefill at M in {128, 512, 2048} on the 14336 x 4096 gate shape
+    (bf16 activations), rows from both ends of the batch."""
+    n, k = 14336, 4096
+    print(f"[gpu] gemm Q5_K prefill M={rows}", flush=True)
+    wq = orc.quantize(O.Q5_K, orc.normal(2150, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 2151 + rows, rows, k)
+    got = run(torch, okq, "okq_linear_out_by_in_q_bf16", O.Q5_K, xb, rows, k, wq, n)
+    assert np.isfinite(got).all()
+    check_rows(orc, O.Q5_K, got, x32, rows, k, wq, n, None, 8)
+
+
+def test_gemm_q5k_one_hot_columns_are_exact(torch, okq, orc):
+    """x = e_j picks column j of every weight row: every Q5_K path (GEMV, the
+    decode-batch kernel at 16 rows, the tiled kernel at 40 rows, f32 and
+    bf16) returns the dequantized value bit for bit, with the fifth bit set
+    on part of the columns."""
+    n, k = 64, 512
+    wq = orc.quantize(O.Q5_K, orc.normal(2160, n * k, 0.02))
+    w = orc.dequantize(O.Q5_K, wq, n * k).reshape(n, k)
+    assert (wq.reshape(-1, 176)[:, 16:48] != 0).any()
+    for rows in (1, 16, 40):
+        x = np.zeros((rows, k), np.float32)
+        cols = (np.arange(rows) * 37 + 5) % k
+        x[np.arange(rows), cols] = 1.0
+        entries = (("okq_gemv", x.reshape(-1)),) if rows == 1 else \
+            (("okq_gemm", x.reshape(-1)), ("okq_gemm_bf16", orc.f32_to_bf16(x.reshape(-1))))
+        for entry, xin in entries:
+            got = run(torch, okq, entry, O.Q5_K, xin, rows, k, wq, n)
+            assert np.array_equal(got, w[:, cols].T), (entry, rows)
+
+
+def test_gemm_q5k_fifth_bit_probe(torch, okq, orc):
+    """Blocks whose only non-zero quant bit is the fifth (qs = 0, one qh bit
+    set, d = 1, sc = 1, dmin = 0): the value 16 must land at exactly the
+    element the bit names, on the GEMV, the decode-batch and the tiled
+    kernels (a misplaced bit plane or chunk shift moves or drops it)."""
+    k = 256
+    blocks = []
+    for p in range(k):
+        b = np.zeros(176, np.uint8)
+        b[0], b[1] = 0x00, 0x3C                  # d = 1.0
+        b[4:8] = 1                                # sc of sub-blocks 0-3 = 1 (6-bit), mins 0
+        b[12:16] = 0x01                           # sc of sub-blocks 4-7 = 1 (low nibble), mins 0
+        c, hi, l = p // 64, (p // 32) % 2, p % 32
+        b[16 + l] = 1 << (2 * c + hi)
+        blocks.append(b)
+    wq = np.concatenate(blocks)
+    w = orc.dequantize(O.Q5_K, wq, k * k).reshape(k, k)
+    assert (w == 16.0 * np.eye(k, dtype=np.float32)).all()
+    x = np.eye(k, dtype=np.float32)[:40]
+    for entry, rows in (("okq_gemv", 1), ("okq_gemm", 16), ("okq_gemm", 40)):
+        got = run(torch, okq, entry, O.Q5_K, x[:rows].reshape(-1), rows, k, wq, k)
+        assert np.array_equal(got, w[:, :rows].T), entry
+
+
+def test_linear_dispatch_routes_q5k_like_q4k(torch, okq, orc):
+    """okq_linear_out_by_in_q on Q5_K weights: up to 8 rows the GEMV (a
+    36.7 MB 4096 x 14336 weight from 3 rows the decode-batch kernel), 9-32
+    rows the decode-batch kernel, above 32 the tiled kernel; each bit for bit
+    equal to the pinned entry point and within the rule of the reference."""
+    _dispatch_pairs(torch, okq, orc, O.Q5_K, 256, 1024, 2170,
+                    ((8, "okq_gemv"), (9, "okq_gemm"), (40, "okq_gemm")))
+    _dispatch_pairs(torch, okq, orc, O.Q5_K, 4096, 14336, 2180, ((2, "okq_gemv"), (3, "okq_gemm")))

@@ -60,6 +60,9 @@ MIXED_CASES = [
     (12, 14336, [(O.Q4_K, 1024), (O.Q6_K, 600)], True),                   # a long K
     (3, 1024, [(O.Q4_K, 256), (O.Q6_K, 256)], False),                     # small weights at 3 rows: GEMV
     (40, 1024, [(O.Q4_K, 300), (O.Q6_K, 200)], False),                    # above 32 rows: each on its GEMM
+    # a Q5_K_M layer (q/k in Q5_K, v in Q6_K): grouped per format
+    (1, 4096, [(O.Q5_K, 4096), (O.Q5_K, 1024), (O.Q6_K, 1024)], False),
+    (8, 4096, [(O.Q5_K, 4096), (O.Q5_K, 1024), (O.Q6_K, 1024)], True),
 ]
 
 

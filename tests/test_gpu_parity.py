@@ -13,7 +13,7 @@ from oracle import oracle as O
 pytestmark = pytest.mark.gpu
 
 TOL = 1e-3
-TYPES = [O.Q8_0, O.Q4_K, O.Q6_K]
+TYPES = [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K]
 
 
 @pytest.fixture(scope="module")
@@ -141,6 +141,9 @@ GEMV_SHAPES = {
              (20000, 256)],
     O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480), (5, 14336),
              (20000, 256)],
+    # Q5_K streams like Q4_K (same units, one more 32-byte qh read per unit)
+    O.Q5_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (64, 20480), (300, 14336),
+             (2, 16384), (20000, 256)],
 }
 CASES = [(t, n, k) for t in TYPES for (n, k) in GEMV_SHAPES[t]]
 
@@ -234,6 +237,7 @@ MULTIROW_CASES = [
     (O.Q4_K, 8, 512, 14336), (O.Q4_K, 4, 33, 8192),
     (O.Q6_K, 2, 1024, 4096), (O.Q6_K, 4, 4096, 14336), (O.Q6_K, 7, 300, 12288),
     (O.Q8_0, 3, 4096, 4096), (O.Q8_0, 4, 17, 16384), (O.Q8_0, 5, 300, 96),
+    (O.Q5_K, 2, 4096, 4096), (O.Q5_K, 4, 4096, 14336), (O.Q5_K, 3, 20000, 256),
     # dynamic rows in both the batched and the one-row launches
     (O.Q8_0, 2, 20000, 256), (O.Q6_K, 3, 20000, 512),
 ]
@@ -340,6 +344,8 @@ MULTI_CASES = [
     (O.Q4_K, 3, 14336, [300, 17]),           # K > 4096: teams of waves
     (O.Q6_K, 2, 1024, [33, 300, 5, 64]),
     (O.Q8_0, 1, 4096, [1024, 4096]),
+    (O.Q5_K, 1, 4096, [14336, 14336]),
+    (O.Q5_K, 2, 14336, [300, 17, 64]),
 ]
 
 
@@ -386,6 +392,8 @@ MULTI_BATCH_CASES = [
     (O.Q4_K, 32, 1024, [17, 1000, 256, 40], True),   # four matrices, ragged tiles, two 16-row groups
     (O.Q8_0, 12, 1024, [100, 64], True),             # Q8_0 above 8 rows: the MFMA kernels too
     (O.Q4_K, 40, 1024, [300, 200], False),           # above 32 rows: each on the tiled GEMM
+    (O.Q5_K, 8, 4096, [14336, 14336], True),         # a Q5_K gate/up pair at 8 rows
+    (O.Q5_K, 24, 1024, [33, 300, 17], True),         # Q5_K above 8 rows: one decode-batch launch
 ]
 
 

@@ -95,8 +95,8 @@ def test_f32_to_bf16_matches_torch(orc):
 def test_type_ids_block_sizes_and_row_bytes(kats):
     ids = kats["type_ids"]
     assert (ids["Q8_0"], ids["Q4K"], ids["Q6K"]) == (O.Q8_0, O.Q4_K, O.Q6_K)
-    assert {t: O.BLOCK_BYTES[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 34, O.Q4_K: 144, O.Q6_K: 210}
-    assert {t: O.BLOCK_ELEMS[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 32, O.Q4_K: 256, O.Q6_K: 256}
+    assert {t: O.BLOCK_BYTES[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 34, O.Q4_K: 144, O.Q5_K: 176, O.Q6_K: 210}
+    assert {t: O.BLOCK_ELEMS[t] for t in O.LINEAR_TYPES} == {O.Q8_0: 32, O.Q4_K: 256, O.Q5_K: 256, O.Q6_K: 256}
     row = lambda t, k: k // O.BLOCK_ELEMS[t] * O.BLOCK_BYTES[t]  # noqa: E731
     assert (row(O.Q8_0, 4096), row(O.Q4_K, 4096), row(O.Q6_K, 4096)) == (4352, 2304, 3360)
     assert (row(O.Q4_K, 14336), row(O.Q6_K, 14336)) == (8064, 11760)
@@ -257,7 +257,7 @@ def test_element_order_probe(orc, t):
     assert (y == np.eye(n, dtype=np.float32)).all()
 
 
-@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_K, O.Q6_K])
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K])
 def test_quantizer_invariants(orc, t):
     x = orc.normal(77 + t, 256 * 64, 0.02)
     q = orc.quantize(t, x)
@@ -280,12 +280,53 @@ def test_quantizer_invariants(orc, t):
         step = np.repeat(de, 16, axis=1).reshape(-1)
         # no clipping happens for sub-blocks whose 6-bit scale was not clamped
         assert (err <= 0.5 * step * (1 + 1e-5) + np.abs(x) * 2.0 ** -6 + 1e-9).mean() > 0.99
+    elif t in (O.Q4_K, O.Q5_K):
+        # the dequantized values of a sub-block lie on one grid k * de - me
+        # (k = 0..levels); every input lies within half a grid step of its
+        # value unless the 6-bit rounding of the scale clamped it at the top
+        # level.  The smallest gap between distinct values of a sub-block is a
+        # multiple of de, so half of it bounds the error of unclamped values.
+        ys, xs = y.reshape(-1, 32), x.reshape(-1, 32)
+        gaps = np.array([np.diff(np.unique(r)).min() if np.unique(r).size > 1 else np.inf for r in ys])
+        ok = np.abs(ys - xs) <= 0.5 * gaps[:, None] * (1 + 1e-4) + 1e-9
+        assert ok.mean() > 0.99, ok.mean()
+        # the finer grid of Q5_K: twice the levels over the same range
+        levels = 31 if t == O.Q5_K else 15
+        span = xs.max(1) - np.minimum(xs.min(1), 0)
+        assert np.median(gaps[np.isfinite(gaps)] / (span[np.isfinite(gaps)] / levels)) < 1.1
     # reconstruction error relative to the weight scale
     rel = np.sqrt(np.mean(err.astype(np.float64) ** 2)) / x.std()
-    assert rel < {O.Q8_0: 0.01, O.Q4_K: 0.12, O.Q6_K: 0.04}[t], rel
+    assert rel < {O.Q8_0: 0.01, O.Q4_K: 0.12, O.Q5_K: 0.06, O.Q6_K: 0.04}[t], rel
 
 
-@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_K, O.Q6_K])
+def test_q5_k_quantizer_is_q4_k_with_a_fifth_bit(orc):
+    """The Q5_K quantizer's fifth bit: qs holds the low four bits of each
+    index and qh bit 2c (low nibble) / 2c + 1 (high nibble) of byte l the
+    fifth; decoding the indices from the bytes and re-applying the block's
+    scales reproduces the oracle's dequantisation, and the indices use the
+    whole 0..31 range (the top half occurs, so the fifth bit is exercised)."""
+    x = orc.normal(4321, 256 * 32, 0.02)
+    q = orc.quantize(O.Q5_K, x).reshape(-1, 176)
+    qs, qh = q[:, 48:].astype(np.int64), q[:, 16:48].astype(np.int64)
+    idx = np.zeros((q.shape[0], 256), np.int64)
+    for c in range(4):
+        for l in range(32):
+            idx[:, 64 * c + l] = (qs[:, 32 * c + l] & 15) | (((qh[:, l] >> (2 * c)) & 1) << 4)
+            idx[:, 64 * c + 32 + l] = (qs[:, 32 * c + l] >> 4) | (((qh[:, l] >> (2 * c + 1)) & 1) << 4)
+    assert idx.max() == 31 and (idx >= 16).mean() > 0.2
+    # the same block with the fifth bits cleared and the nibbles kept is a
+    # valid Q4_K block (same header): Q5_K = Q4_K's value + 16 * d * sc
+    q4 = np.concatenate([q[:, :16], q[:, 48:]], axis=1).reshape(-1)
+    y5 = orc.dequantize(O.Q5_K, q.reshape(-1), x.size).reshape(-1, 256)
+    y4 = orc.dequantize(O.Q4_K, q4, x.size).reshape(-1, 256)
+    q0 = q.copy()
+    q0[:, 16:48] = 0
+    y50 = orc.dequantize(O.Q5_K, q0.reshape(-1), x.size).reshape(-1, 256)
+    assert (y50 == y4).all()
+    assert ((y5 != y4) == (idx >= 16)).all()
+
+
+@pytest.mark.parametrize("t", [O.Q8_0, O.Q4_K, O.Q5_K, O.Q6_K])
 def test_quantize_roundtrip_on_representable_values(orc, t):
     """Inputs that are exactly a block's dequantized values of a canonical
     block re-quantize to themselves (values stay representable)."""
