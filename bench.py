@@ -37,8 +37,9 @@ The JSON line also carries:
                 bounded samples of C1, C3, C4 (scalar and AVX2, rows chunked
                 over the host cores) and C5 (one layer at batch 1, 8, 32)
   extra         per-launch and per-projection times (mean, p10, median,
-                p90), the 7-launch step, and the secondary configs (C1, C3,
-                C4 per call, C5)
+                p90), the 7-launch step, the secondary configs (C1, C3,
+                C4 per call, C5), and Q5_K at the MLP shapes (gate+up at
+                batch 1 and 8, the M=512 gate prefill call)
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
      python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|decode_gate_up32
@@ -59,8 +60,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0          # MI355X datasheet HBM3E bandwidth
 BF16_PEAK_TFLOPS = 2500.0      # MI355X dense bf16/fp16 MFMA
-Q4K, Q6K, Q8_0 = 12, 14, 8
-BLOCK = {Q4K: (256, 144), Q6K: (256, 210), Q8_0: (32, 34)}
+Q4K, Q5K, Q6K, Q8_0 = 12, 13, 14, 8
+BLOCK = {Q4K: (256, 144), Q5K: (256, 176), Q6K: (256, 210), Q8_0: (32, 34)}
 C2_PROJ = [("q", 4096, 4096), ("k", 1024, 4096), ("v", 1024, 4096), ("o", 4096, 4096),
            ("gate", 14336, 4096), ("up", 14336, 4096), ("down", 4096, 14336)]
 METRIC = "Q4_K dequant-GEMV GB/s (% of HBM peak) + prefill dequant-GEMM TFLOPS"
@@ -486,6 +487,85 @@ def run_c4(ctx: Ctx, args, c2):
     return res
 
 
+def graph_call_us(ctx, call, reps: int, replays: int = 10):
+    """Per-call duration (µs) of `reps` back-to-back call(r) captured into one
+    HIP graph on a capture stream whose GEMM workspace is allocated before
+    capture; stream events around each of `replays` replays: (mean, per-replay
+    means)."""
+    torch = ctx.torch
+    cs = torch.cuda.Stream()
+    with torch.cuda.stream(cs):
+        call(0)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=cs):
+        for r in range(reps):
+            call(r)
+    g.replay()
+    torch.cuda.synchronize()
+    evs = [torch.cuda.Event(enable_timing=True) for _ in range(replays + 1)]
+    evs[0].record()
+    for r in range(replays):
+        g.replay()
+        evs[r + 1].record()
+    torch.cuda.synchronize()
+    del g
+    per = [1000.0 * evs[r].elapsed_time(evs[r + 1]) / reps for r in range(replays)]
+    return sum(per) / replays, per
+
+
+def run_q5k(ctx: Ctx, args):
+    """Q5_K, the linear path's fourth format, at the Llama-3-8B MLP shapes:
+    the gate+up pair (2 x 14336x4096) as one okq_gemv_multi call at batch 1
+    (the grouped GEMV launch) and at 8 rows (one decode-batch launch), and the
+    M=512 gate prefill call with bf16 activations (pre-pass + tiled kernel).
+    Each rotates over >= 512 MB of weight replicas inside a HIP graph."""
+    torch = ctx.torch
+    n, k = 14336, 4096
+    b = wbytes(Q5K, n, k)
+    log("Q5_K: gate+up at batch 1 and 8, M=512 gate prefill")
+    pools = [ctx.replicas(ctx.quantized(Q5K, n, k, seed=900 + i)) for i in range(2)]
+    copies = min(cp for _, cp in pools)
+    w_at = lambda i, r: pools[i][0].narrow(0, (r % copies) * b, b)
+    res = {"weight_bytes_per_matrix": b}
+    for rows in (1, 8):
+        x = ctx.normal(rows * k, 902 + rows)
+        ys = [torch.empty(rows * n, dtype=torch.float32, device="cuda") for _ in range(2)]
+
+        def call(r, rows=rows, x=x, ys=ys):
+            ctx.okq.call("okq_gemv_multi", x.data_ptr(), rows, k, Q5K, 2,
+                         (ctypes.c_void_p * 2)(w_at(0, r).data_ptr(), w_at(1, r).data_ptr()),
+                         (ctypes.c_uint64 * 2)(b, b), (ctypes.c_int64 * 2)(n, n), None,
+                         (ctypes.c_void_p * 2)(ys[0].data_ptr(), ys[1].data_ptr()), ctx.stream)
+
+        us, per = graph_call_us(ctx, call, max(64, 2 * copies))
+        res[f"gate_up_b{rows}"] = {"rows": rows, "us_mean": round(us, 3), "us_p10": round(pct(per, 10), 3),
+                                   "us_median": round(median(per), 3), "us_p90": round(pct(per, 90), 3),
+                                   "gbs": round(2 * b / us / 1e3, 1), "frac_hbm": round(2 * b / us / 1e3 / HBM_PEAK_GBS, 4)}
+    m = 512
+    xf = ctx.normal(m * k, 905)
+    xb = torch.empty(m * k, dtype=torch.int16, device="cuda")
+    ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
+    y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    reps = max(8, args.kernel_reps // 8)
+
+    def gcall(r):
+        ctx.gemv(Q5K, xb, k, w_at(0, r), n, y, entry="okq_gemm_bf16", rows=m)
+
+    gcall(0)
+    us_k = ctx.kernel_us(gcall, reps)
+    t_call, per = graph_call_us(ctx, gcall, reps)
+    t_k = sum(us_k) / len(us_k)
+    flops = 2.0 * m * n * k
+    res["M512_gate"] = {"m": m, "n": n, "k": k, "us_call": round(t_call, 2), "us_call_p10": round(pct(per, 10), 2),
+                        "us_call_median": round(median(per), 2), "us_call_p90": round(pct(per, 90), 2),
+                        "tflops_call": round(flops / t_call / 1e6, 1),
+                        "frac_bf16_peak": round(flops / t_call / 1e6 / BF16_PEAK_TFLOPS, 4),
+                        "us_kernel": round(t_k, 2), "frac_bf16_peak_kernel": round(flops / t_k / 1e6 / BF16_PEAK_TFLOPS, 4)}
+    del pools
+    return res
+
+
 # ---------------------------------------------------------------------------
 # C5: the 32-layer decoder-stack sweep (Q4_K_M mix)
 # ---------------------------------------------------------------------------
@@ -824,7 +904,8 @@ def main():
                     help="CPU baseline of the C2 headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", default="c1,c3,c4,c5", help="secondary configs to run (comma list of c1,c3,c4,c5)")
+    ap.add_argument("--only", default="c1,c3,c4,c5,q5k",
+                    help="secondary configs to run (comma list of c1,c3,c4,c5,q5k)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
     ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "gemm_down512", "gemm_gate128",
                                         "decode_gate_up32"], default=None,
@@ -861,6 +942,8 @@ def main():
         extra["c4_q4_k_gemm_bf16"] = run_c4(ctx, args, c2)
     if "c5" in only:
         extra["c5_stack_sweep"] = run_c5(ctx, args)
+    if "q5k" in only:
+        extra["q5_k"] = run_q5k(ctx, args)
     cpu = None if args.no_cpu else run_cpu_baseline(ctx, c2, args)
 
     rec = {

@@ -124,13 +124,72 @@ __device__ __forceinline__ float block_max(float amax, float *red, int tid) {
   return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
 }
 
+// Rows holding an infinity or a NaN.  The MFMA kernels cannot give them the
+// reference's IEEE results: they contract sc * q and the min term apart, so
+// an infinite activation meets a zero product of one part (inf * 0 = NaN)
+// where the reference multiplies it by the whole weight d * sc * q - dmin * m
+// (non-zero: a signed infinity).  The pre-pass computes such a row's outputs
+// itself and marks its row scale NaN; the GEMM epilogues and the split-K
+// reduction leave rows with a NaN scale alone.  Only the non-finite
+// activations decide an output here (a finite product cannot turn an
+// infinity or a NaN into anything else), so each output is the IEEE sum of
+// x_k * W[o, k] over the row's non-finite positions k, then + bias[o]:
+// NaN where a product is NaN or infinities of both signs meet, the
+// infinity otherwise -- the reference's own values.
+struct PrepIeee {
+  const uint8_t *w;
+  const float *bias;
+  float *y;
+  size_t row_bytes;
+  int type, N;
+};
+constexpr int kIeeeCap = 1024;  // non-finite positions listed in LDS; more: every column scans the row
+
+template <bool kF32>
+__device__ __forceinline__ float x_at(const void *X, int64_t i) {
+  if (kF32) return static_cast<const float *>(X)[i];
+  return as_f32((uint32_t) static_cast<const uint16_t *>(X)[i] << 16);
+}
+__device__ __forceinline__ bool non_finite(float v) { return !(fabsf(v) <= 3.4028235e38f); }
+
+template <bool kF32>
+__device__ void prep_ieee_row(const void *__restrict__ X, int m, int K, const PrepIeee &P, int tid) {
+  __shared__ int cnt;
+  __shared__ int pos[kIeeeCap];
+  if (tid == 0) cnt = 0;
+  __syncthreads();
+  const int64_t row = (int64_t)m * K;
+  for (int k = tid; k < K; k += 256)
+    if (non_finite(x_at<kF32>(X, row + k))) {
+      const int i = atomicAdd(&cnt, 1);
+      if (i < kIeeeCap) pos[i] = k;
+    }
+  __syncthreads();
+  const int n = cnt;
+  for (int o = tid; o < P.N; o += 256) {
+    const uint8_t *wrow = P.w + (size_t)o * P.row_bytes;
+    float acc = 0.0f;
+    if (n <= kIeeeCap) {
+      for (int j = 0; j < n; ++j)
+        acc = __fadd_rn(acc, __fmul_rn(x_at<kF32>(X, row + pos[j]), deq_elem(P.type, wrow, (uint32_t)pos[j])));
+    } else {
+      for (int k = 0; k < K; ++k) {
+        const float v = x_at<kF32>(X, row + k);
+        if (non_finite(v)) acc = __fadd_rn(acc, __fmul_rn(v, deq_elem(P.type, wrow, (uint32_t)k)));
+      }
+    }
+    P.y[(size_t)m * P.N + o] = __fadd_rn(acc, P.bias ? P.bias[o] : 0.0f);
+  }
+}
+
 // CH > 0: each thread holds its CH chunks of 8 activations in registers
 // (chunk c = tid + 256 i), so the row is read once; CH == 0: rows longer than
 // 8 chunks per thread are read twice (max, then convert).
 template <bool kF32, int CH>
 __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__ X, int M, int K,
                                                         _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
-                                                        h2 *__restrict__ xsum, float *__restrict__ rscale) {
+                                                        h2 *__restrict__ xsum, float *__restrict__ rscale,
+                                                        PrepIeee ieee) {
   __shared__ float red[4];
   const int m = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
@@ -139,6 +198,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
   if constexpr (CH > 0) {
     float v[CH][8];
     float amax = 0.0f;
+    int nf = 0;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;
@@ -152,26 +212,36 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
 #pragma unroll
     for (int i = 0; i < CH; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+      for (int e = 0; e < 8; ++e) {
+        amax = fmaxf(amax, fabsf(v[i][e]));
+        nf |= non_finite(v[i][e]) ? 1 : 0;
+      }
     const int s = prep_exp(block_max(amax, red, tid));
-    if (tid == 0) rscale[m] = ldexpf(1.0f, s);
+    const bool bad = __syncthreads_or(nf) != 0;
+    if (tid == 0) rscale[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, s);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;  // chunks is a multiple of 32: runs never straddle the bound
       prep_chunk<kF32>(v[i], s, c < chunks, row + 8 * (int64_t)c, m, K, c, tid, xhi, xlo, xsum);
     }
+    if (bad) prep_ieee_row<kF32>(X, m, K, ieee, tid);
     return;
   }
   // pass 1: row max |x|
   float amax = 0.0f;
+  int nf = 0;
   for (int c = tid; c < chunks; c += 256) {
     float v[8];
     load8<kF32>(X, row + 8 * (int64_t)c, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) amax = fmaxf(amax, fabsf(v[i]));
+    for (int i = 0; i < 8; ++i) {
+      amax = fmaxf(amax, fabsf(v[i]));
+      nf |= non_finite(v[i]) ? 1 : 0;
+    }
   }
   const int s = prep_exp(block_max(amax, red, tid));
-  if (tid == 0) rscale[m] = ldexpf(1.0f, s);
+  const bool bad = __syncthreads_or(nf) != 0;
+  if (tid == 0) rscale[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, s);
   // pass 2: scaled fp16 planes and per-32 sums
   for (int c0 = 0; c0 < chunks; c0 += 256) {
     const int c = c0 + tid;
@@ -185,6 +255,7 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
     }
     prep_chunk<kF32>(v, s, ok, row + 8 * (int64_t)c, m, K, c, tid, xhi, xlo, xsum);
   }
+  if (bad) prep_ieee_row<kF32>(X, m, K, ieee, tid);
 }
 
 // ---------------------------------------------------------------------------
@@ -689,7 +760,8 @@ __global__ __launch_bounds__(BM * 2) void gemm_kq_kernel(const _Float16 *__restr
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
         const int row = m0 + wm * 64 + 32 * i + 8 * (e / 4) + 4 * (lane >> 5) + (e % 4);
-        if (row < M) Y[(size_t)row * N + col] = acc[i][j][e] * rs[i][e] + bv;
+        // a NaN scale: the pre-pass wrote this row's IEEE outputs
+        if (row < M && !__builtin_isnan(rs[i][e])) Y[(size_t)row * N + col] = acc[i][j][e] * rs[i][e] + bv;
       }
     }
   }
@@ -1537,6 +1609,8 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
   const Rsrc rs = make_rsrc(part, end);
   const float bn = bias ? bias[n] : 0.0f;
   for (int m = (int)blockIdx.y; m < M; m += (int)gridDim.y) {
+    const float rs_m = rscale ? rscale[m] : 1.0f;
+    if (__builtin_isnan(rs_m)) continue;  // the pre-pass wrote this row's IEEE outputs
     const uint32_t i = (uint32_t)m * (uint32_t)N + (uint32_t)n;
     // every slice's load of a batch in flight at once; the sum runs in slice
     // order from -0.0 (x + -0.0 == x, so p0 + p1 + ...; the zeros past the
@@ -1553,7 +1627,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 #pragma unroll
       for (int d = 0; d < KB; ++d) acc += v[d];
     }
-    Y[(size_t)i] = (rscale ? acc * rscale[m] : acc) + bn;
+    Y[(size_t)i] = (rscale ? acc * rs_m : acc) + bn;
   }
 }
 
@@ -1954,9 +2028,10 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   float *part = plan.ksplit > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
   // chunks of 8 activations per thread: 2 (K <= 4096), 4, 8 held in registers, longer rows read twice
   const int64_t per_thread = (K / 8 + 255) / 256;
+  const PrepIeee ieee{W, bias, y, (size_t)(K / 256) * (size_t)sb_bytes_of(type), type, (int)N};
 #define OKQ_PREP(F32_, CH_)                                                                                       \
   hipLaunchKernelGGL((gemm_prep_kernel<F32_, CH_>), dim3((unsigned)M), dim3(256), 0, s, x, (int)M, (int)K, xhi, xlo, \
-                     xsum, rscale)
+                     xsum, rscale, ieee)
 #define OKQ_PREP_CH(F32_)                     \
   if (per_thread <= 2) OKQ_PREP(F32_, 2);     \
   else if (per_thread <= 4) OKQ_PREP(F32_, 4); \

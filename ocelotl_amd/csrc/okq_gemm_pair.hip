@@ -322,6 +322,10 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   // without per-value row tests.
   const int col = n0 + 32 * wave + cl;
   const int rows = M - m0 < kPM ? M - m0 : kPM;
+  // rows whose scale is NaN (computed by the pre-pass), tested by every lane
+  // of the wave before any lane leaves for a column past N
+  const bool flagged =
+      __builtin_amdgcn_ballot_w64(__builtin_isnan(pR[lane]) || __builtin_isnan(pR[64 + lane])) != 0;
   if (col < N) {
     if (ksplit > 1) {
       float *dst = part + ((size_t)z * M + m0) * N + col;
@@ -342,7 +346,10 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
     } else {
       const float bv = bias ? bias[col] : 0.0f;
       float *dst = Y + (size_t)m0 * N + col;
-      auto store = [&](bool guard) {
+      // skip: rows whose scale is NaN hold an infinity or a NaN; the pre-pass
+      // wrote their IEEE outputs (a wave-uniform test over the tile's scales,
+      // so whole tiles keep the branch-free stores)
+      auto store = [&](bool guard, bool skip) {
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -352,13 +359,16 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
             const float rv[4] = {rs.x, rs.y, rs.z, rs.w};
 #pragma unroll
             for (int q = 0; q < 4; ++q)
-              if (!guard || r0 + q < rows) dst[(size_t)(r0 + q) * N] = acc[i][4 * j + q] * rv[q] + bv;
+              if ((!guard || r0 + q < rows) && (!skip || !__builtin_isnan(rv[q])))
+                dst[(size_t)(r0 + q) * N] = acc[i][4 * j + q] * rv[q] + bv;
           }
       };
-      if (rows == kPM) {
-        store(false);
+      if (flagged) {
+        store(true, true);
+      } else if (rows == kPM) {
+        store(false, false);
       } else {
-        store(true);
+        store(true, false);
       }
     }
   }

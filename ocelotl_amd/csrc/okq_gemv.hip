@@ -396,40 +396,6 @@ struct FQ80 {
 };
 
 // ---------------------------------------------------------------------------
-// One weight dequantised exactly as the CPU oracle does it (every product and
-// difference rounded separately; this file is built without FMA contraction):
-// the generic fallback kernel and the IEEE path of the streaming kernel.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ float deq_elem(int type, const uint8_t *row, uint32_t k) {
-  if (type == kQ8_0) {
-    const uint8_t *blk = row + (size_t)(k >> 5) * kQ8Bytes;
-    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk));
-    return (float)(int8_t)blk[2 + (k & 31)] * d;
-  } else if (type == kQ4_K || type == kQ5_K) {
-    const bool q5 = type == kQ5_K;
-    const uint8_t *blk = row + (size_t)(k >> 8) * (q5 ? kQ5KBytes : kQ4KBytes);
-    const uint32_t rr = k & 255u, c = rr >> 6, hi = (rr >> 5) & 1u, l = rr & 31u;
-    const uint32_t *wd = reinterpret_cast<const uint32_t *>(blk);
-    uint32_t sc, m;
-    q4k_scale_min(2 * c + hi, wd[1], wd[2], wd[3], sc, m);
-    const float d = f16_bits_hw(wd[0] & 0xffffu), dmin = f16_bits_hw(wd[0] >> 16);
-    uint32_t q = (blk[(q5 ? 48 : 16) + 32 * c + l] >> (4 * hi)) & 15u;
-    if (q5) q |= ((blk[16 + l] >> (2 * c + hi)) & 1u) << 4;
-    return (d * (float)sc) * (float)q - dmin * (float)m;
-  } else {
-    const uint8_t *blk = row + (size_t)(k >> 8) * kQ6KBytes;
-    const uint32_t rr = k & 255u, hh = rr >> 7, quarter = (rr >> 5) & 3u, l = rr & 31u;
-    const uint32_t qlb = blk[64 * hh + l + ((quarter & 1u) ? 32u : 0u)];
-    const uint32_t lo4 = (qlb >> ((quarter & 2u) ? 4u : 0u)) & 15u;
-    const uint32_t hi2 = (blk[128 + 32 * hh + l] >> (2 * quarter)) & 3u;
-    const int q = (int)(lo4 | (hi2 << 4)) - 32;
-    const int sc = (int8_t)blk[192 + 8 * hh + l / 16 + 2 * quarter];
-    const float d = f16_bits_hw(*reinterpret_cast<const uint16_t *>(blk + 208));
-    return (d * (float)sc) * (float)q;
-  }
-}
-
-// ---------------------------------------------------------------------------
 // activation prologue: lanes in groups of kRun/4 each hold one float4 of a
 // run; the group shares the run's max|x| and sum through DPP (fixed order),
 // then each lane writes one dword of each limb of the run's XRec.

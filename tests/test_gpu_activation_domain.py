@@ -15,10 +15,13 @@ Two things the random N(0,1) parity tests do not reach:
   (a NaN activation, or an infinity times a zero weight) or infinities of
   both signs meet, else +-inf.  The GEMV reproduces that pattern exactly
   (its IEEE path), and leaves finite rows of the same launch bit-identical to
-  a launch without the non-finite row.  The MFMA kernels (decode batches
-  above the GEMV's rows, prefill) make a non-finite activation row's outputs
-  non-finite without the exact sign pattern, and leave every other row
-  unchanged; that is tested here and documented at the boundary.
+  a launch without the non-finite row.  Prefill (more than 32 rows) matches
+  it exactly too: the activation pre-pass finds such rows, computes their
+  outputs in IEEE f32 and marks them, and the GEMM leaves them alone.  The
+  decode-batch MFMA kernel (2-32 rows, no pre-pass) makes a non-finite
+  activation row's outputs non-finite without the exact sign pattern and
+  leaves every other row unchanged; that is tested here and documented at
+  the boundary.
 """
 import ctypes
 
@@ -56,7 +59,10 @@ def _dev(torch, a):
 
 
 def linear(torch, okq, entry, t, x, rows, k, wq, n, bias=None):
-    xd, wd = _dev(torch, np.asarray(x, np.float32).reshape(-1)), _dev(torch, wq)
+    """One call of `entry`; x is f32, or bf16 bits (uint16) for the _bf16 entry points."""
+    x = np.asarray(x)
+    xd = _dev(torch, (x if x.dtype == np.uint16 else x.astype(np.float32)).reshape(-1))
+    wd = _dev(torch, wq)
     bd = None if bias is None else _dev(torch, np.asarray(bias, np.float32))
     out = torch.full((rows * n,), 12345.0, dtype=torch.float32, device="cuda")
     okq.call(entry, xd.data_ptr(), rows, k, t, wd.data_ptr(), wq.size, n, None if bd is None else bd.data_ptr(),
@@ -206,11 +212,12 @@ def test_rmsnorm_linear_with_an_infinity_is_nan_like_the_reference(torch, okq, o
     assert same_ieee(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("t,rows", [(O.Q4_K, 8), (O.Q6_K, 12), (O.Q4_K, 40), (O.Q6_K, 40), (O.Q5_K, 12), (O.Q5_K, 40)])
-def test_mfma_paths_confine_non_finite_rows(torch, okq, orc, t, rows):
-    """Decode-batch and tiled MFMA kernels: a row holding an infinity or a NaN
-    gets non-finite outputs (not necessarily the reference's sign pattern),
-    and every other row equals the same batch without it, bit for bit."""
+@pytest.mark.parametrize("t,rows", [(O.Q4_K, 8), (O.Q6_K, 12), (O.Q5_K, 12), (O.Q8_0, 24), (O.Q4_K, 32)])
+def test_decode_batch_confines_non_finite_rows(torch, okq, orc, t, rows):
+    """Decode-batch MFMA kernel (2-32 rows): a row holding an infinity or a
+    NaN gets non-finite outputs (not necessarily the reference's sign
+    pattern), and every other row equals the same batch without it, bit for
+    bit."""
     n, k = 1000, 2048
     wq = orc.quantize(t, orc.normal(9700 + t + rows, n * k, 0.02))
     x = orc.normal(9701 + rows, rows * k, 1.0).reshape(rows, k)
@@ -222,3 +229,52 @@ def test_mfma_paths_confine_non_finite_rows(torch, okq, orc, t, rows):
     assert not np.isfinite(got[1]).any() and np.isnan(got[rows - 1]).all()
     keep = [r for r in range(rows) if r not in (1, rows - 1)]
     assert (got[keep].view(np.uint32) == ref[keep].view(np.uint32)).all()
+
+
+PREFILL_NONFINITE = [
+    # (entry, type, rows, n, k): the register-dequant kernels (bf16 Q4_K, whole
+    # tiles and split K through the reduction), the tiled kernel (f32, other
+    # formats), the pre-pass's two-pass form (K > 16384)
+    ("okq_gemm_bf16", O.Q4_K, 512, 14336, 4096),
+    ("okq_gemm_bf16", O.Q4_K, 512, 4096, 14336),
+    ("okq_gemm_bf16", O.Q4_K, 130, 14336, 4096),
+    ("okq_gemm_bf16", O.Q4_K, 40, 1000, 2048),
+    ("okq_gemm", O.Q4_K, 40, 1000, 2048),
+    ("okq_gemm", O.Q6_K, 64, 1000, 2048),
+    ("okq_gemm_bf16", O.Q8_0, 33, 300, 1024),
+    ("okq_gemm_bf16", O.Q5_K, 300, 1024, 4096),
+    ("okq_gemm_bf16", O.Q4_K, 40, 300, 20480),
+]
+
+
+@pytest.mark.parametrize("entry,t,rows,n,k", PREFILL_NONFINITE)
+def test_prefill_non_finite_rows_follow_ieee(torch, okq, orc, entry, t, rows, n, k):
+    """Prefill (more than 32 rows): rows holding +inf, -inf, both, a NaN, or
+    an infinity in every position get exactly the reference CPU path's NaNs
+    and signed infinities (the pre-pass computes them in IEEE f32), and every
+    other row equals the same batch without them, bit for bit."""
+    print(f"[gpu] non-finite prefill {entry} type={t} M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(t, orc.normal(9800 + t + k, n * k, 0.02))
+    x = orc.normal(9801 + rows, rows * k, 1.0).reshape(rows, k)
+    bias = orc.normal(9802, n, 0.1)
+    bad = {1: [(300, np.inf)], 2: [(5, -np.inf), (k - 1, -np.inf)], 3: [(17, np.inf), (k // 2, -np.inf)],
+           rows // 2: [(k - 3, np.nan)], rows - 1: [(j, np.inf) for j in range(k)]}
+    clean = x.copy()
+    for r, cells in bad.items():
+        for j, v in cells:
+            x[r, j] = v
+    if entry == "okq_gemm_bf16":
+        xin, cin = orc.f32_to_bf16(x.reshape(-1)), orc.f32_to_bf16(clean.reshape(-1))
+        x32 = orc.bf16_to_f32(xin).reshape(rows, k)
+    else:
+        xin, cin, x32 = x.reshape(-1), clean.reshape(-1), x
+    got = linear(torch, okq, entry, t, xin, rows, k, wq, n, bias)
+    ref = linear(torch, okq, entry, t, cin, rows, k, wq, n, bias)
+    rs = sorted(bad)
+    want = orc.linear_q(t, x32[rs].reshape(-1), len(rs), k, wq, n, bias)
+    for i, r in enumerate(rs):
+        assert same_ieee(got[r], want[i]), (r, np.isnan(got[r]).sum(), np.isnan(want[i]).sum(),
+                                            np.isposinf(got[r]).sum(), np.isposinf(want[i]).sum())
+    keep = [r for r in range(rows) if r not in bad]
+    assert (got[keep].view(np.uint32) == ref[keep].view(np.uint32)).all()
+
