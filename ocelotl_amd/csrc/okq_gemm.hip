@@ -846,6 +846,7 @@ __host__ __device__ constexpr size_t dec_tail_offset(int M, int P, int nsbs, int
 // first activation, `xs` at the row's xsum pairs of the super-block.
 struct DecQ4K {
   static constexpr uint32_t kBlk = kQ4KBytes;
+  static constexpr int kType = kQ4_K;
   static constexpr bool kSums = true;  // the min term contracts the per-32 activation sums
   // items in flight per wave: 4 with one 16-row group (the Llama shapes give
   // a wave 4 items, so all are issued at once), 3 with two (register budget)
@@ -927,6 +928,7 @@ struct DecQ4K {
 // chunk: 20 registers per item, so the ring is one item shorter.
 struct DecQ5K {
   static constexpr uint32_t kBlk = kQ5KBytes;
+  static constexpr int kType = kQ5_K;
   static constexpr bool kSums = true;
   static constexpr int kDepth = 2, kDepth1 = 3;
   struct Item {
@@ -1005,6 +1007,7 @@ struct DecQ5K {
 
 struct DecQ6K {
   static constexpr uint32_t kBlk = kQ6KBytes;
+  static constexpr int kType = kQ6_K;
   static constexpr bool kSums = false;
   static constexpr int kDepth = 2, kDepth1 = 2;
   // Slice t = (half hh = t >> 2, quarter qq = t & 3); lane group g covers
@@ -1102,6 +1105,7 @@ struct DecQ6K {
 // B planes (q8_4), so the item needs no scaling afterwards.
 struct DecQ80 {
   static constexpr uint32_t kBlk = 8 * kQ8Bytes;
+  static constexpr int kType = kQ8_0;
   static constexpr bool kSums = false;
   static constexpr int kDepth = 2, kDepth1 = 3;
   struct Item {
@@ -1223,6 +1227,8 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // row) of the slice
   float *Bs = reinterpret_cast<float *>(dsm + dec_tail_offset(M, P, nsbs, kLo ? 2 : 1, kW, RG));  // [kDecMaxTiles][256]
   float *Rsb = Bs + kDecMaxTiles * 256;  // [nsbs][kDecRows]: the 2^s of each (super-block, row)
+  // bit r: row r of the slice holds an infinity or a NaN
+  uint32_t *Dbad = reinterpret_cast<uint32_t *>(Rsb + nsbs * kDecRows);
 
   // 1. this wave's items.  The kDecWaves waves form T = kDecWaves / kw tile
   //    slots of kw waves each.  Column group grp owns a contiguous block of
@@ -1348,6 +1354,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
                                                        lane < 16 && ti < mytiles ? col * 4u : mt.bias_bytes, 0, 0);
     }
   }
+  // the non-finite row mask starts empty (written before the barrier below,
+  // and waited for, so that no wave's staging can set a bit ahead of it)
+  if (tid == 0) {
+    *Dbad = 0u;
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  }
   // A CU returns vector loads in issue order: this bare barrier (no memory
   // fence) puts every activation load of the workgroup ahead of every weight
   // load, so no wave's activations queue behind another wave's weights.
@@ -1384,8 +1396,9 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // super-block (pieces per row are a multiple of 32), so its max is a
   // half-wave reduction: DPP within each 16-lane row, readlane across the
   // two.  Pieces past the last row are skipped (a uniform bound).
-  auto dmax = [](float a, auto ctl) {
-    return fmaxf(a, as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(a), decltype(ctl)::value, 0xf, 0xf, false)));
+  auto umax_u32 = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
+  auto dmax = [&](uint32_t a, auto ctl) {
+    return umax_u32(a, (uint32_t)__builtin_amdgcn_mov_dpp((int)a, decltype(ctl)::value, 0xf, 0xf, false));
   };
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
@@ -1393,19 +1406,22 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     const int r = pc_r[i], c = pc_c[i];
     float v[8];
     piece(i, v);
-    float a = 0.0f;  // fmaxf drops NaNs
+    // the largest |x| as the largest magnitude bit pattern: for |x| the
+    // unsigned order is the float order, with NaN above infinity above every
+    // finite value (a float max would drop NaNs)
+    uint32_t a = 0u;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) a = fmaxf(a, fabsf(v[e]));
+    for (int e = 0; e < 8; ++e) a = umax_u32(a, as_u32(v[e]) & 0x7fffffffu);
     a = dmax(a, std::integral_constant<int, 0xB1>{});   // quad_perm 1,0,3,2
     a = dmax(a, std::integral_constant<int, 0x4E>{});   // quad_perm 2,3,0,1
     a = dmax(a, std::integral_constant<int, 0x141>{});  // row_half_mirror
     a = dmax(a, std::integral_constant<int, 0x140>{});  // row_mirror
-    const float h0 = fmaxf(as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 0)),
-                           as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 16)));
-    const float h1 = fmaxf(as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 32)),
-                           as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(a), 48)));
-    const float amax = lane < 32 ? h0 : h1;
-    const int sx = (amax > 0.0f && amax <= 3.4028235e38f) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
+    const uint32_t h0 = umax_u32((uint32_t)__builtin_amdgcn_readlane((int)a, 0), (uint32_t)__builtin_amdgcn_readlane((int)a, 16));
+    const uint32_t h1 = umax_u32((uint32_t)__builtin_amdgcn_readlane((int)a, 32), (uint32_t)__builtin_amdgcn_readlane((int)a, 48));
+    const uint32_t abits = lane < 32 ? h0 : h1;
+    const bool nonfin = abits >= 0x7f800000u;  // the block holds an infinity or a NaN
+    const float amax = as_f32(abits);
+    const int sx = (amax > 0.0f && !nonfin) ? __builtin_amdgcn_frexp_expf(amax) - 10 : 0;
     // hi = fp16 of w = x * 2^-sx rounded to nearest, lo = fp16 of the exact
     // residue w - hi (rounded to nearest once), so hi + lo = w to 2^-22
     // relative.  Sums (Q4_K): the 8 values of a piece in order, then the 4
@@ -1450,7 +1466,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
         pair[1] = (_Float16)(t - (float)sh);
         *reinterpret_cast<h2 *>(Xs + ((size_t)(c >> 5) * M + r) * 16 + 2 * ((c >> 2) & 7)) = pair;
       }
-      if ((c & 31) == 0) Rsb[(c >> 5) * kDecRows + r] = ldexpf(1.0f, sx);
+      // a NaN scale marks a block holding an infinity or a NaN: the row's
+      // outputs of this slice are recomputed in IEEE f32 at the end
+      if ((c & 31) == 0) {
+        Rsb[(c >> 5) * kDecRows + r] = nonfin ? __builtin_nanf("") : ldexpf(1.0f, sx);
+        if (nonfin) atomicOr(Dbad, 1u << r);
+      }
     }
     if (early && i == 0) {
       __builtin_amdgcn_sched_barrier(0);
@@ -1523,6 +1544,37 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
     }
   };
 
+  // Rows of this slice holding an infinity or a NaN (Dbad) get the IEEE f32
+  // value of their products over the slice instead of the MFMA result, which
+  // contracts sc * q and the min term apart (an infinity meets a zero part:
+  // NaN, where the reference multiplies it by a non-zero weight).  Only the
+  // non-finite activations decide it: the sum of x_k * W[col, k] over them,
+  // weights dequantised exactly; split K: this slice's partial (the
+  // reduction's f32 sum of slices keeps IEEE semantics), unsplit: plus the
+  // bias.  Rare inputs: one lane per (row, column), a plain loop.
+  auto ieee_fix = [&](int ti, uint32_t bad) {
+    const int tile = gtile(ltile(ti)), m = mat_of(tile);
+    const DecMat &mt = mats.mat[m];
+    const int nm = mt.n, col = (tile - mt.tile0) * 16 + cn;
+    if (col >= nm) return;
+    const uint8_t *wrow = mt.w + (size_t)col * row_bytes;
+    const int k0 = sb0 * 256, k1 = (sb0 + nsbs) * 256;
+    for (int q = 0; q < RG; ++q)
+      for (int v = 0; v < 4; ++v) {
+        const int row = 16 * q + 4 * g + v;
+        if (row >= M || !((bad >> row) & 1u)) continue;
+        float t = 0.0f;
+        for (int k = k0; k < k1; ++k) {
+          const float xv = x_at<kLo>(X, (int64_t)row * K + k);
+          if (non_finite(xv)) t = __fadd_rn(t, __fmul_rn(xv, deq_elem(F::kType, wrow, (uint32_t)k)));
+        }
+        if (ksplit > 1)
+          part[((size_t)z * M + row) * (size_t)ncat + (size_t)tile * 16 + cn] = t;
+        else
+          mt.y[(size_t)row * nm + col] = __fadd_rn(t, mt.bias ? mt.bias[col] : 0.0f);
+      }
+  };
+
   // 3. the ring: consume slot j, refill it D items ahead; loads stay
   //    unconditional (items past the end read past the tensor: zeros).
   int c_ti = 0, c_jj = 0;  // the next item to consume
@@ -1541,7 +1593,12 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
       consume(S[j], c_ti, c_jj);
       advance(c_ti, c_jj);
     }
-  if constexpr (!kW) return;
+  if constexpr (!kW) {
+    const uint32_t bad = *Dbad;  // set during the staging, before its barrier
+    if (bad != 0u)
+      for (int ti = 0; ti < mytiles; ++ti) ieee_fix(ti, bad);
+    return;
+  }
   // 4. kw > 1: the kw waves of each slot hold partial sums of its one tile
   //    over disjoint super-blocks.  Once every wave is past the activations,
   //    their LDS holds the partials [wave][RG][lane][4]; the slot's first
@@ -1559,6 +1616,8 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
 #pragma unroll
     for (int q = 0; q < RG; ++q) acc[q] += Red[((wave + k2) * RG + q) * 64 + lane];
   store(0, acc);
+  const uint32_t bad = *Dbad;
+  if (bad != 0u) ieee_fix(0, bad);
 }
 
 // One format (F1 == F2: every workgroup) or two: workgroups below g_split run
@@ -1856,7 +1915,7 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
   while ((1 << kw_shift) < plan.kwaves) ++kw_shift;
   const bool split_w = plan.kwaves > 1;
   const size_t lds = dec_tail_offset(m, 256 * nsbs_max + 8, nsbs_max, x_is_bf16 ? 1 : 2, split_w, M > 16 ? 2 : 1) +
-                     ((size_t)kDecMaxTiles * 256 + (size_t)nsbs_max * kDecRows) * sizeof(float);
+                     ((size_t)kDecMaxTiles * 256 + (size_t)nsbs_max * kDecRows) * sizeof(float) + 16;
   if (lds > 160 * 1024 || (1 << kw_shift) != plan.kwaves || kDecWaves % plan.kwaves != 0 ||
       (split_w && (ks != 1 || M > 16)))
     return hipErrorInvalidValue;

@@ -15,13 +15,11 @@ Two things the random N(0,1) parity tests do not reach:
   (a NaN activation, or an infinity times a zero weight) or infinities of
   both signs meet, else +-inf.  The GEMV reproduces that pattern exactly
   (its IEEE path), and leaves finite rows of the same launch bit-identical to
-  a launch without the non-finite row.  Prefill (more than 32 rows) matches
-  it exactly too: the activation pre-pass finds such rows, computes their
-  outputs in IEEE f32 and marks them, and the GEMM leaves them alone.  The
-  decode-batch MFMA kernel (2-32 rows, no pre-pass) makes a non-finite
-  activation row's outputs non-finite without the exact sign pattern and
-  leaves every other row unchanged; that is tested here and documented at
-  the boundary.
+  a launch without the non-finite row.  The MFMA paths match it exactly too:
+  prefill's activation pre-pass finds such rows, computes their outputs in
+  IEEE f32 and marks them (the GEMM leaves them alone); the decode-batch
+  kernel marks them while staging its slice and recomputes their outputs of
+  that slice in IEEE f32 after its ring.
 """
 import ctypes
 
@@ -212,29 +210,21 @@ def test_rmsnorm_linear_with_an_infinity_is_nan_like_the_reference(torch, okq, o
     assert same_ieee(out.cpu().numpy(), want)
 
 
-@pytest.mark.parametrize("t,rows", [(O.Q4_K, 8), (O.Q6_K, 12), (O.Q5_K, 12), (O.Q8_0, 24), (O.Q4_K, 32)])
-def test_decode_batch_confines_non_finite_rows(torch, okq, orc, t, rows):
-    """Decode-batch MFMA kernel (2-32 rows): a row holding an infinity or a
-    NaN gets non-finite outputs (not necessarily the reference's sign
-    pattern), and every other row equals the same batch without it, bit for
-    bit."""
-    n, k = 1000, 2048
-    wq = orc.quantize(t, orc.normal(9700 + t + rows, n * k, 0.02))
-    x = orc.normal(9701 + rows, rows * k, 1.0).reshape(rows, k)
-    clean = x.copy()
-    x[1, 300] = np.inf
-    x[rows - 1, 5] = np.nan
-    got = linear(torch, okq, "okq_gemm", t, x.reshape(-1), rows, k, wq, n)
-    ref = linear(torch, okq, "okq_gemm", t, clean.reshape(-1), rows, k, wq, n)
-    assert not np.isfinite(got[1]).any() and np.isnan(got[rows - 1]).all()
-    keep = [r for r in range(rows) if r not in (1, rows - 1)]
-    assert (got[keep].view(np.uint32) == ref[keep].view(np.uint32)).all()
-
-
-PREFILL_NONFINITE = [
-    # (entry, type, rows, n, k): the register-dequant kernels (bf16 Q4_K, whole
-    # tiles and split K through the reduction), the tiled kernel (f32, other
-    # formats), the pre-pass's two-pass form (K > 16384)
+NONFINITE_BATCH = [
+    # decode batches (the decode-batch MFMA kernel: split K, unsplit K with
+    # whole tiles per wave, and K split among a workgroup's waves)
+    ("okq_gemm", O.Q4_K, 8, 1000, 2048),
+    ("okq_gemm", O.Q6_K, 12, 1000, 2048),
+    ("okq_gemm", O.Q5_K, 12, 4096, 4096),
+    ("okq_gemm", O.Q8_0, 24, 1000, 2048),
+    ("okq_gemm", O.Q4_K, 32, 4096, 14336),
+    ("okq_gemm_bf16", O.Q4_K, 16, 4096, 4096),
+    ("okq_gemm", O.Q4_K, 6, 8000, 4096),
+    ("okq_gemm", O.Q4_K, 3, 70001, 256),
+    # prefill (
+    # the register-dequant kernels (bf16 Q4_K, whole tiles and split K
+    # through the reduction), the tiled kernel (f32, other formats), the
+    # pre-pass's two-pass form (K > 16384)
     ("okq_gemm_bf16", O.Q4_K, 512, 14336, 4096),
     ("okq_gemm_bf16", O.Q4_K, 512, 4096, 14336),
     ("okq_gemm_bf16", O.Q4_K, 130, 14336, 4096),
@@ -247,18 +237,21 @@ PREFILL_NONFINITE = [
 ]
 
 
-@pytest.mark.parametrize("entry,t,rows,n,k", PREFILL_NONFINITE)
-def test_prefill_non_finite_rows_follow_ieee(torch, okq, orc, entry, t, rows, n, k):
-    """Prefill (more than 32 rows): rows holding +inf, -inf, both, a NaN, or
-    an infinity in every position get exactly the reference CPU path's NaNs
-    and signed infinities (the pre-pass computes them in IEEE f32), and every
+@pytest.mark.parametrize("entry,t,rows,n,k", NONFINITE_BATCH)
+def test_mfma_non_finite_rows_follow_ieee(torch, okq, orc, entry, t, rows, n, k):
+    """The MFMA paths (decode batches and prefill): rows holding +inf, -inf,
+    both, a NaN, or an infinity in every position get exactly the reference
+    CPU path's NaNs and signed infinities (computed in IEEE f32 by the
+    prefill pre-pass, or at the end of the decode-batch kernel), and every
     other row equals the same batch without them, bit for bit."""
-    print(f"[gpu] non-finite prefill {entry} type={t} M={rows} N={n} K={k}", flush=True)
+    print(f"[gpu] non-finite mfma {entry} type={t} M={rows} N={n} K={k}", flush=True)
     wq = orc.quantize(t, orc.normal(9800 + t + k, n * k, 0.02))
     x = orc.normal(9801 + rows, rows * k, 1.0).reshape(rows, k)
     bias = orc.normal(9802, n, 0.1)
-    bad = {1: [(300, np.inf)], 2: [(5, -np.inf), (k - 1, -np.inf)], 3: [(17, np.inf), (k // 2, -np.inf)],
-           rows // 2: [(k - 3, np.nan)], rows - 1: [(j, np.inf) for j in range(k)]}
+    bad = {1: [(300 % k, np.inf)], 2: [(5, -np.inf), (k - 1, -np.inf)], 3: [(17, np.inf), (k // 2, -np.inf)],
+           rows // 2 + 1: [(k - 3, np.nan)], rows - 1: [(j, np.inf) for j in range(k)]}
+    if rows <= 4:
+        bad = {1: bad[1], rows - 1: bad[rows - 1]}
     clean = x.copy()
     for r, cells in bad.items():
         for j, v in cells:
