@@ -38,8 +38,9 @@ The JSON line also carries:
                 over the host cores) and C5 (one layer at batch 1, 8, 32)
   extra         per-launch and per-projection times (mean, p10, median,
                 p90), the 7-launch step, the secondary configs (C1, C3,
-                C4 per call, C5), and Q5_K at the MLP shapes (gate+up at
-                batch 1 and 8, the M=512 gate prefill call)
+                C4 per call, C5), Q5_K at the MLP shapes (gate+up at
+                batch 1 and 8, the M=512 gate prefill call), and the Q6_K
+                down projection's M=512 prefill call
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
      python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|decode_gate_up32
@@ -566,6 +567,39 @@ def run_q5k(ctx: Ctx, args):
     return res
 
 
+def run_q6k_prefill(ctx: Ctx, args):
+    """The Q4_K_M / Q5_K_M files' other format at prefill: the Q6_K down
+    projection (4096 x 14336, the largest matrix a Q4_K_M layer stores in
+    Q6_K) at M=512 with bf16 activations (pre-pass + tiled kernel + split-K
+    reduction), rotating over >= 512 MB of weight replicas in a HIP graph."""
+    torch = ctx.torch
+    n, k, m = 4096, 14336, 512
+    b = wbytes(Q6K, n, k)
+    log("Q6_K: M=512 down prefill")
+    pool, copies = ctx.replicas(ctx.quantized(Q6K, n, k, seed=910))
+    xf = ctx.normal(m * k, 911)
+    xb = torch.empty(m * k, dtype=torch.int16, device="cuda")
+    ctx.okq.call("okq_f32_to_bf16", xf.data_ptr(), xf.numel(), xb.data_ptr(), ctx.stream)
+    y = torch.empty(m * n, dtype=torch.float32, device="cuda")
+    reps = max(8, args.kernel_reps // 8)
+
+    def gcall(r):
+        ctx.gemv(Q6K, xb, k, pool.narrow(0, (r % copies) * b, b), n, y, entry="okq_gemm_bf16", rows=m)
+
+    gcall(0)
+    us_k = ctx.kernel_us(gcall, reps)
+    t_call, per = graph_call_us(ctx, gcall, reps)
+    t_k = sum(us_k) / len(us_k)
+    flops = 2.0 * m * n * k
+    del pool
+    return {"M512_down": {"m": m, "n": n, "k": k, "us_call": round(t_call, 2), "us_call_p10": round(pct(per, 10), 2),
+                          "us_call_median": round(median(per), 2), "us_call_p90": round(pct(per, 90), 2),
+                          "tflops_call": round(flops / t_call / 1e6, 1),
+                          "frac_bf16_peak": round(flops / t_call / 1e6 / BF16_PEAK_TFLOPS, 4),
+                          "us_kernel": round(t_k, 2),
+                          "frac_bf16_peak_kernel": round(flops / t_k / 1e6 / BF16_PEAK_TFLOPS, 4)}}
+
+
 # ---------------------------------------------------------------------------
 # C5: the 32-layer decoder-stack sweep (Q4_K_M mix)
 # ---------------------------------------------------------------------------
@@ -904,8 +938,8 @@ def main():
                     help="CPU baseline of the C2 headline only")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-extra", action="store_true", help="only the C2 headline")
-    ap.add_argument("--only", default="c1,c3,c4,c5,q5k",
-                    help="secondary configs to run (comma list of c1,c3,c4,c5,q5k)")
+    ap.add_argument("--only", default="c1,c3,c4,c5,q5k,q6k",
+                    help="secondary configs to run (comma list of c1,c3,c4,c5,q5k,q6k)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
     ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "gemm_down512", "gemm_gate128",
                                         "decode_gate_up32"], default=None,
@@ -944,6 +978,8 @@ def main():
         extra["c5_stack_sweep"] = run_c5(ctx, args)
     if "q5k" in only:
         extra["q5_k"] = run_q5k(ctx, args)
+    if "q6k" in only:
+        extra["q6_k_prefill"] = run_q6k_prefill(ctx, args)
     cpu = None if args.no_cpu else run_cpu_baseline(ctx, c2, args)
 
     rec = {

@@ -1792,8 +1792,9 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
   p.kwaves = 1;
-  // More than 32 rows: Q4_K with bf16 activations takes gemm_wide_q4k_kernel
-  // (okq_gemm_wide.hip); the tiled kernel takes the rest with 128 x 128 tiles
+  // More than 32 rows: Q4_K and Q5_K with bf16 activations take the
+  // register-dequant kernels (okq_gemm_wide.hip, okq_gemm_pair.hip); the
+  // tiled kernel takes the rest with 128 x 128 tiles
   // (f32 activations need the second fp16 plane, which only fits the LDS
   // budget at 128 rows; Q6_K stages its larger raw windows in the 4-wave
   // tile's register budget), or 256 x 128 tiles for bf16 Q4_K shapes beyond
@@ -1850,8 +1851,8 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     if (ks == 1 && mytiles > kDecMaxTiles)
       p.groups = (int)((ntiles + (int64_t)kDecWaves * kDecMaxTiles - 1) / ((int64_t)kDecWaves * kDecMaxTiles));
   } else {
-    // Q4_K with bf16 activations: a kernel that dequantises the weights in
-    // registers; everything else: the tiled kernel.  Split K when the tiles
+    // Q4_K and Q5_K with bf16 activations: a kernel that dequantises the
+    // weights in registers; everything else: the tiled kernel.  Split K when the tiles
     // alone leave CUs idle: enough slices for about one workgroup per CU, at
     // least two super-blocks per slice, at most 8.
     const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
@@ -2106,9 +2107,9 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   if (plan.wide == 2) {
-    e = launch_gemm_pair(xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
+    e = launch_gemm_pair(type, xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
   } else if (plan.wide) {
-    e = launch_gemm_wide(xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
+    e = launch_gemm_wide(type, xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
   } else {
     e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);
   }

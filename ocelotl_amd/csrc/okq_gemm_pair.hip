@@ -1,5 +1,6 @@
-// okq_gemm_pair.hip -- Q4_K prefill dequant-GEMM, weights dequantised in
-// registers, two 4-wave workgroups per CU: Y[M,N] = X[M,K] W[N,K]^T (+bias).
+// okq_gemm_pair.hip -- Q4_K (and Q5_K) prefill dequant-GEMM, weights
+// dequantised in registers, two 4-wave workgroups per CU:
+// Y[M,N] = X[M,K] W[N,K]^T (+bias).
 //
 // Operands and numerics are those of gemm_wide_q4k_kernel (okq_gemm_wide.hip):
 // A = the pre-pass's row-scaled fp16 activations, B = sc * q exact in fp16,
@@ -71,13 +72,14 @@ __device__ __forceinline__ h2 nib_pair(uint32_t spread, h2 sc2, h2 off2) {
 
 }  // namespace
 
-__global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *__restrict__ xhi,
-                                                               const h2 *__restrict__ xsum,
-                                                               const float *__restrict__ rscale,
-                                                               const uint8_t *__restrict__ W,
-                                                               const float *__restrict__ bias, float *__restrict__ Y,
-                                                               int M, int N, int K, int tiles_m, int tiles,
-                                                               int ksplit, float *__restrict__ part) {
+// The kernel body for Q4_K (kQ5 = false) and Q5_K (kQ5: the fifth bit of
+// every weight from the block's qh bytes, as in okq_gemm_wide.hip).
+template <bool kQ5>
+__device__ __forceinline__ void pair_body(const _Float16 *__restrict__ xhi, const h2 *__restrict__ xsum,
+                                          const float *__restrict__ rscale, const uint8_t *__restrict__ W,
+                                          const float *__restrict__ bias, float *__restrict__ Y, int M, int N, int K,
+                                          int tiles_m, int tiles, int ksplit, float *__restrict__ part) {
+  constexpr uint32_t kSB = kQ5 ? kQ5KBytes : kQ4KBytes;  // bytes per super-block
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a
   // contiguous range of (slice, tile) jobs, and consecutive jobs are the
   // M-tiles of one N-tile (they share its weights in that XCD's L2).
@@ -96,7 +98,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   const int nsb_all = K >> 8;
   const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
   const int nst = 2 * ((int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0);  // stages (half super-blocks)
-  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
+  const uint32_t row_bytes = (uint32_t)nsb_all * kSB;
   const uint32_t K2 = (uint32_t)K * 2u;
 
   const Rsrc rs_x = make_rsrc(xhi, (uint32_t)((size_t)M * K * 2));
@@ -131,9 +133,23 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   // tensor: zeros): the 16-byte header of each super-block and, per stage,
   // the 32 qs bytes of chunk 2h + g.
   const uint32_t w_hd = (uint32_t)(n0 + 32 * wave + cl) * row_bytes;
-  const uint32_t w_q = w_hd + 16u + 32u * (uint32_t)g;
+  const uint32_t w_q = w_hd + (kQ5 ? 48u : 16u) + 32u * (uint32_t)g;
   auto ldw = [&](uint32_t voff, int sb) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rs_w, voff, (int)((uint32_t)sb * kQ4KBytes), 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(rs_w, voff, (int)((uint32_t)sb * kSB), 0);
+  };
+  // Q5_K: the 32 qh bytes of a super-block (hr0, hr1: loaded with its header,
+  // one super-block ahead) and, for the current one, the 4 bits lane group g
+  // uses of each -- bits 2g, 2g + 1 (half 0: chunk g) and 4 + 2g, 5 + 2g
+  // (half 1: chunk 2 + g) -- packed as field bit 2h + plane, with bytes
+  // 8j .. 8j + 3 in the low nibbles of hc[j] and 8j + 4 .. 8j + 7 in the high
+  u32x4 hr0 = {}, hr1 = {};
+  uint32_t hc[4] = {0u, 0u, 0u, 0u};
+  auto compact_qh = [&]() {
+    const uint32_t sh = 2u * (uint32_t)g;
+    const uint32_t r[8] = {hr0.x, hr0.y, hr0.z, hr0.w, hr1.x, hr1.y, hr1.z, hr1.w};
+    auto field = [&](uint32_t x) { return ((x >> sh) & 0x03030303u) | ((x >> (sh + 2u)) & 0x0C0C0C0Cu); };
+#pragma unroll
+    for (int j = 0; j < 4; ++j) hc[j] = field(r[2 * j]) | (field(r[2 * j + 1]) << 4);
   };
   auto ldq = [&](int st, u32x4 &q0, u32x4 &q1) {
     const int sb = sb0 + (st >> 1);
@@ -169,15 +185,35 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
     sc2 = h2{sh, sh};
     off2 = h2{oh, oh};
   };
-  auto dequant = [&](int s, const u32x4 &q0, const u32x4 &q1, h2 sc2, h2 off2) {
+  // Q5_K's fifth bit (field bit 2h + s / 4 of byte l): bit 4 of the byte
+  // on low planes (1024 + q5), the exponent byte 0x64 | h on high planes
+  // (1024 + 256 h + 16 q4 = 1024 + 16 q5), so the scale pairs stay Q4_K's
+  auto dequant = [&](int s, int h, const u32x4 &q0, const u32x4 &q1, h2 sc2, h2 off2) {
     const u32x4 qq = ((s & 3) >> 1) ? q1 : q0;
     const uint32_t d0 = (s & 1) ? qq.z : qq.x, d1 = (s & 1) ? qq.w : qq.y;
-    const uint32_t mask = (s >> 2) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    const uint32_t n0v = d0 & mask, n1v = d1 & mask;
-    const h2 p0 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n0v, 0x04010400u), sc2, off2);
-    const h2 p1 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n0v, 0x04030402u), sc2, off2);
-    const h2 p2 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n1v, 0x04010400u), sc2, off2);
-    const h2 p3 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n1v, 0x04030402u), sc2, off2);
+    const bool hi = (s >> 2) != 0;
+    const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    uint32_t n0v = d0 & mask, n1v = d1 & mask;
+    uint32_t e0 = 0x64646464u, e1 = 0x64646464u;
+    uint32_t s00 = 0x04010400u, s01 = 0x04030402u;
+    if constexpr (kQ5) {
+      const uint32_t b = 2u * (uint32_t)h + (uint32_t)(s >> 2);
+      const uint32_t c = hc[s & 3];
+      const uint32_t h0 = (c >> b) & 0x01010101u, h1 = (c >> (b + 4u)) & 0x01010101u;
+      if (hi) {
+        e0 |= h0;
+        e1 |= h1;
+        s00 = 0x05010400u;
+        s01 = 0x07030602u;
+      } else {
+        n0v |= h0 << 4;
+        n1v |= h1 << 4;
+      }
+    }
+    const h2 p0 = nib_pair(__builtin_amdgcn_perm(e0, n0v, s00), sc2, off2);
+    const h2 p1 = nib_pair(__builtin_amdgcn_perm(e0, n0v, s01), sc2, off2);
+    const h2 p2 = nib_pair(__builtin_amdgcn_perm(e1, n1v, s00), sc2, off2);
+    const h2 p3 = nib_pair(__builtin_amdgcn_perm(e1, n1v, s01), sc2, off2);
     return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   };
 
@@ -197,7 +233,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
 #pragma unroll
     for (int i = 0; i < 4; ++i) a[i] = a_at(bufA, a_addr(0), i);
     scales(hd, j0, false, sc2, off2);
-    bv = dequant(0, q0, q1, sc2, off2);
+    bv = dequant(0, h, q0, q1, sc2, off2);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
       if (s < 7) {
@@ -218,7 +254,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
         accs[i] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a[i], bv, (h == 0 && s == 0) ? zero : accs[i], 0, 0, 0);
       if (s < 7) {
         if (s + 1 == 4) scales(hd, j0 + 1u, true, sc2, off2);
-        bv = dequant(s + 1, q0, q1, sc2, off2);
+        bv = dequant(s + 1, h, q0, q1, sc2, off2);
 #pragma unroll
         for (int i = 0; i < 4; ++i) a[i] = an[i];
       }
@@ -274,13 +310,27 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   if (tid < kPM) pR[tid] = m0 + tid < M ? rscale[m0 + tid] : 0.0f;
   hdA = ldw(w_hd, sb0);
   ldq(0, qe0, qe1);
+  if constexpr (kQ5) {
+    hr0 = ldw(w_hd + 16u, sb0);
+    hr1 = ldw(w_hd + 32u, sb0);
+  }
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   __syncthreads();
+  // Q5_K: at a super-block's first stage its qh bits are packed, then the raw
+  // registers take the next super-block's (with its header)
+  auto next_qh = [&](int sb) {
+    if constexpr (kQ5) {
+      compact_qh();
+      hr0 = ldw(w_hd + 16u, sb);
+      hr1 = ldw(w_hd + 32u, sb);
+    }
+  };
   constexpr int kWaitAll = 0x0070;  // vmcnt(0) expcnt(7) lgkmcnt(0), gfx9 encoding
   for (int st = 0;; st += 4) {
     // stage st: first half of a super-block (header hdA), buffer 0, qs qe
     ldq(cl_st(st + 1), qo0, qo1);
     hdB = ldw(w_hd, hd_sb(st + 2));
+    next_qh(hd_sb(st + 2));
     __builtin_amdgcn_sched_barrier(0);  // the prefetch issues first
     contract(pA0, pX0, hdA, qe0, qe1, 0, cl_st(st + 1), pA1, pX1);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -295,6 +345,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
     // stage st + 2: first half of the next super-block (hdB), buffer 0, qs qe
     ldq(cl_st(st + 3), qo0, qo1);
     hdA = ldw(w_hd, hd_sb(st + 4));
+    next_qh(hd_sb(st + 4));
     __builtin_amdgcn_sched_barrier(0);
     contract(pA0, pX0, hdB, qe0, qe1, 0, cl_st(st + 3), pA1, pX1);
     __builtin_amdgcn_s_waitcnt(kWaitAll);
@@ -315,6 +366,7 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   // out its latency.
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("" ::"v"(hdA), "v"(hdB), "v"(qe0), "v"(qe1), "v"(qo0), "v"(qo1));
+  if constexpr (kQ5) asm volatile("" ::"v"(hr0), "v"(hr1));
 
   // epilogue: lane (cl, g) holds rows 8 (e / 4) + 4 g + e % 4 of column cl
   // of each 32 x 32 block; split K stores the raw partial sums, otherwise the
@@ -374,17 +426,37 @@ __global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *_
   }
 }
 
+__global__ __launch_bounds__(256, 2) void gemm_pair_q4k_kernel(const _Float16 *__restrict__ xhi,
+                                                               const h2 *__restrict__ xsum,
+                                                               const float *__restrict__ rscale,
+                                                               const uint8_t *__restrict__ W,
+                                                               const float *__restrict__ bias, float *__restrict__ Y,
+                                                               int M, int N, int K, int tiles_m, int tiles,
+                                                               int ksplit, float *__restrict__ part) {
+  pair_body<false>(xhi, xsum, rscale, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
+__global__ __launch_bounds__(256, 2) void gemm_pair_q5k_kernel(const _Float16 *__restrict__ xhi,
+                                                               const h2 *__restrict__ xsum,
+                                                               const float *__restrict__ rscale,
+                                                               const uint8_t *__restrict__ W,
+                                                               const float *__restrict__ bias, float *__restrict__ Y,
+                                                               int M, int N, int K, int tiles_m, int tiles,
+                                                               int ksplit, float *__restrict__ part) {
+  pair_body<true>(xhi, xsum, rscale, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
 int gemm_pair_tiles(int64_t M, int64_t N) { return (int)(((M + kPM - 1) / kPM) * ((N + kPN - 1) / kPN)); }
 
-hipError_t launch_gemm_pair(const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
+hipError_t launch_gemm_pair(int type, const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s) {
   const int tiles_m = (int)((M + kPM - 1) / kPM);
   const int tiles = gemm_pair_tiles(M, N);
   const int per_xcd = (tiles * ksplit + 7) / 8;
-  launch_timed(gemm_pair_q4k_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256), 0u, s, xhi,
-               static_cast<const h2 *>(xsum), rscale, static_cast<const uint8_t *>(w), bias, y, (int)M, (int)N,
-               (int)K, tiles_m, tiles, ksplit, part);
+  launch_timed(type == kQ5_K ? gemm_pair_q5k_kernel : gemm_pair_q4k_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256),
+               0u, s, xhi, static_cast<const h2 *>(xsum), rscale, static_cast<const uint8_t *>(w), bias, y, (int)M,
+               (int)N, (int)K, tiles_m, tiles, ksplit, part);
   return hipGetLastError();
 }
 

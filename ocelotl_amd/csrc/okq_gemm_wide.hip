@@ -1,5 +1,7 @@
-// okq_gemm_wide.hip -- Q4_K prefill dequant-GEMM with weights dequantised
-// straight into MFMA registers: Y[M,N] = X[M,K] W[N,K]^T (+bias).
+// okq_gemm_wide.hip -- Q4_K (and Q5_K) prefill dequant-GEMM with weights
+// dequantised straight into MFMA registers: Y[M,N] = X[M,K] W[N,K]^T (+bias).
+// Q5_K is the same contraction with the fifth bit of every weight taken from
+// the block's 32 qh bytes (sc * q5 <= 1953 stays an exact fp16 integer).
 //
 // Operands and numerics are those of gemm_kq_kernel (okq_gemm.hip): A = the
 // pre-pass's row-scaled fp16 activations, B = sc * q exact in fp16, every
@@ -73,13 +75,14 @@ __device__ __forceinline__ h2 nib_pair(uint32_t spread, h2 sc2, h2 off2) {
 
 }  // namespace
 
-__global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__restrict__ xhi,
-                                                            const h2 *__restrict__ xsum,
-                                                            const float *__restrict__ rscale,
-                                                            const uint8_t *__restrict__ W,
-                                                            const float *__restrict__ bias, float *__restrict__ Y,
-                                                            int M, int N, int K, int tiles_m, int tiles, int ksplit,
-                                                            float *__restrict__ part) {
+// The kernel body for Q4_K (kQ5 = false) and Q5_K (kQ5: the same with the
+// fifth bit of every weight from the block's 32 qh bytes; see dequant below).
+template <bool kQ5>
+__device__ __forceinline__ void wide_body(const _Float16 *__restrict__ xhi, const h2 *__restrict__ xsum,
+                                          const float *__restrict__ rscale, const uint8_t *__restrict__ W,
+                                          const float *__restrict__ bias, float *__restrict__ Y, int M, int N, int K,
+                                          int tiles_m, int tiles, int ksplit, float *__restrict__ part) {
+  constexpr uint32_t kSB = kQ5 ? kQ5KBytes : kQ4KBytes;  // bytes per super-block
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a
   // contiguous range of (slice, tile) jobs, and consecutive jobs are the
   // M-tiles of one N-tile (they share its weights in that XCD's L2).
@@ -98,7 +101,7 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   const int nsb_all = K >> 8;
   const int sb0 = (int)((int64_t)z * nsb_all / ksplit);
   const int nsb = (int)((int64_t)(z + 1) * nsb_all / ksplit) - sb0;
-  const uint32_t row_bytes = (uint32_t)nsb_all * kQ4KBytes;
+  const uint32_t row_bytes = (uint32_t)nsb_all * kSB;
   const uint32_t K32 = (uint32_t)K;
 
   const Rsrc rs_x = make_rsrc(xhi, (uint32_t)((size_t)M * K * 2));
@@ -138,11 +141,25 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // ahead); the header is double buffered in two register sets that the two
   // halves of the main loop use alternately (no copy between them).
   const uint32_t w_hd = (uint32_t)(n0 + 32 * wave + cl) * row_bytes;
-  const uint32_t w_q = w_hd + 16u + 64u * (uint32_t)g;
+  const uint32_t w_q = w_hd + (kQ5 ? 48u : 16u) + 64u * (uint32_t)g;
   auto ldw = [&](uint32_t voff, int sb) {
-    return __builtin_amdgcn_raw_buffer_load_b128(rs_w, voff, (int)((uint32_t)sb * kQ4KBytes), 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(rs_w, voff, (int)((uint32_t)sb * kSB), 0);
   };
   u32x4 q[4], hdA, hdB;
+  // Q5_K: the 32 qh bytes of the super-block (hr0, hr1: loaded one
+  // super-block ahead) and, for the one being contracted, the 4 bits lane
+  // group g uses of each (bits 4g .. 4g + 3: chunks 2g and 2g + 1, both
+  // nibble planes), packed as hc[j] = those of bytes 8j .. 8j + 3 in the low
+  // nibbles and of bytes 8j + 4 .. 8j + 7 in the high ones
+  u32x4 hr0 = {}, hr1 = {};
+  uint32_t hc[4] = {0u, 0u, 0u, 0u};
+  auto compact_qh = [&]() {
+    const uint32_t sh = 4u * (uint32_t)g;
+    const uint32_t r[8] = {hr0.x, hr0.y, hr0.z, hr0.w, hr1.x, hr1.y, hr1.z, hr1.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      hc[j] = ((r[2 * j] >> sh) & 0x0F0F0F0Fu) | (((r[2 * j + 1] >> sh) & 0x0F0F0F0Fu) << 4);
+  };
 
   f16x acc[4], accs[4];
   const f16x zero = {};
@@ -172,15 +189,37 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
     sc2 = h2{sh, sh};
     off2 = h2{oh, oh};
   };
+  // Q5_K adds the fifth bit (bit b = 2 (s / 8) + (s / 4) % 2 of the lane
+  // group's field of byte l): on low planes as bit 4 of the byte (1024 + q5),
+  // on high planes, where the byte holds 16 q4, as 256 -- the exponent byte
+  // 0x64 | h, i.e. 1024 + 256 h + 16 q4 = 1024 + 16 q5 -- so (sc, -1024 sc)
+  // and (sc / 16, -64 sc) give sc * q5 (<= 1953) exactly as for Q4_K.
   auto dequant = [&](int s, h2 sc2, h2 off2) {
     const u32x4 qq = q[(s >> 3) * 2 + ((s & 3) >> 1)];
     const uint32_t d0 = (s & 1) ? qq.z : qq.x, d1 = (s & 1) ? qq.w : qq.y;
-    const uint32_t mask = ((s >> 2) & 1) ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
-    const uint32_t n0v = d0 & mask, n1v = d1 & mask;
-    const h2 p0 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n0v, 0x04010400u), sc2, off2);
-    const h2 p1 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n0v, 0x04030402u), sc2, off2);
-    const h2 p2 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n1v, 0x04010400u), sc2, off2);
-    const h2 p3 = nib_pair(__builtin_amdgcn_perm(0x64646464u, n1v, 0x04030402u), sc2, off2);
+    const bool hi = ((s >> 2) & 1) != 0;
+    const uint32_t mask = hi ? 0xF0F0F0F0u : 0x0F0F0F0Fu;
+    uint32_t n0v = d0 & mask, n1v = d1 & mask;
+    uint32_t e0 = 0x64646464u, e1 = 0x64646464u;
+    uint32_t s00 = 0x04010400u, s01 = 0x04030402u;
+    if constexpr (kQ5) {
+      const uint32_t b = 2u * (uint32_t)(s >> 3) + (uint32_t)((s >> 2) & 1);
+      const uint32_t c = hc[s & 3];
+      const uint32_t h0 = (c >> b) & 0x01010101u, h1 = (c >> (b + 4u)) & 0x01010101u;
+      if (hi) {
+        e0 |= h0;
+        e1 |= h1;
+        s00 = 0x05010400u;
+        s01 = 0x07030602u;
+      } else {
+        n0v |= h0 << 4;
+        n1v |= h1 << 4;
+      }
+    }
+    const h2 p0 = nib_pair(__builtin_amdgcn_perm(e0, n0v, s00), sc2, off2);
+    const h2 p1 = nib_pair(__builtin_amdgcn_perm(e0, n0v, s01), sc2, off2);
+    const h2 p2 = nib_pair(__builtin_amdgcn_perm(e1, n1v, s00), sc2, off2);
+    const h2 p3 = nib_pair(__builtin_amdgcn_perm(e1, n1v, s01), sc2, off2);
     return h8{p0[0], p0[1], p1[0], p1[1], p2[0], p2[1], p3[0], p3[1]};
   };
 
@@ -279,16 +318,32 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   hdA = ldw(w_hd, sb0);
 #pragma unroll
   for (int t = 0; t < 4; ++t) q[t] = ldw(w_q + 16u * t, sb0);
+  if constexpr (kQ5) {
+    hr0 = ldw(w_hd + 16u, sb0);
+    hr1 = ldw(w_hd + 32u, sb0);
+  }
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   __syncthreads();
   constexpr int kWaitCopy = 0x0074;  // vmcnt(4) expcnt(7) lgkmcnt(0), gfx9 encoding
+  // Q5_K: the current super-block's qh bits are packed before its contraction,
+  // then the raw registers take the next super-block's (ahead of the qs
+  // reloads, so the wait before each barrier covers them)
+  auto next_qh = [&](int sb) {
+    if constexpr (kQ5) {
+      compact_qh();
+      hr0 = ldw(w_hd + 16u, sb);
+      hr1 = ldw(w_hd + 32u, sb);
+    }
+  };
   for (int i = 0;; i += 2) {
     hdB = ldw(w_hd, nxt(i));
+    next_qh(nxt(i));
     contract(wA0, wX0, hdA, nxt(i), wA1, wX1);
     __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
     if (i + 1 >= nsb) break;
     hdA = ldw(w_hd, nxt(i + 1));
+    next_qh(nxt(i + 1));
     contract(wA1, wX1, hdB, nxt(i + 1), wA0, wX0);
     __builtin_amdgcn_s_waitcnt(kWaitCopy);
     __builtin_amdgcn_s_barrier();
@@ -302,6 +357,7 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   // just before their first use, where each would wait out its latency.
   __builtin_amdgcn_s_waitcnt(0);
   asm volatile("" ::"v"(hdA), "v"(hdB), "v"(q[0]), "v"(q[1]), "v"(q[2]), "v"(q[3]));
+  if constexpr (kQ5) asm volatile("" ::"v"(hr0), "v"(hr1));
 
   // epilogue: lane (cl, g) holds rows 8 (e / 4) + 4 g + e % 4 of column cl
   // of each 32 x 32 block; split K stores the raw partial sums, otherwise the
@@ -362,24 +418,44 @@ __global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__re
   }
 }
 
+__global__ __launch_bounds__(512) void gemm_wide_q4k_kernel(const _Float16 *__restrict__ xhi,
+                                                            const h2 *__restrict__ xsum,
+                                                            const float *__restrict__ rscale,
+                                                            const uint8_t *__restrict__ W,
+                                                            const float *__restrict__ bias, float *__restrict__ Y,
+                                                            int M, int N, int K, int tiles_m, int tiles, int ksplit,
+                                                            float *__restrict__ part) {
+  wide_body<false>(xhi, xsum, rscale, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
+__global__ __launch_bounds__(512) void gemm_wide_q5k_kernel(const _Float16 *__restrict__ xhi,
+                                                            const h2 *__restrict__ xsum,
+                                                            const float *__restrict__ rscale,
+                                                            const uint8_t *__restrict__ W,
+                                                            const float *__restrict__ bias, float *__restrict__ Y,
+                                                            int M, int N, int K, int tiles_m, int tiles, int ksplit,
+                                                            float *__restrict__ part) {
+  wide_body<true>(xhi, xsum, rscale, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
 bool gemm_wide_supported(int type, int64_t M, int64_t K, int64_t N) {
   const int64_t a_bytes = (M + kWM) * K * 2;
-  const int64_t w_bytes = (N + kWN) * (K / 256) * kQ4KBytes + 1024;
-  return type == kQ4_K && K % 256 == 0 && M >= 1 && N >= 1 && a_bytes < (int64_t)UINT32_MAX &&
+  const int64_t w_bytes = (N + kWN) * (K / 256) * (type == kQ5_K ? kQ5KBytes : kQ4KBytes) + 1024;
+  return (type == kQ4_K || type == kQ5_K) && K % 256 == 0 && M >= 1 && N >= 1 && a_bytes < (int64_t)UINT32_MAX &&
          w_bytes < (int64_t)UINT32_MAX;
 }
 
 int gemm_wide_tiles(int64_t M, int64_t N) { return (int)(((M + kWM - 1) / kWM) * ((N + kWN - 1) / kWN)); }
 
-hipError_t launch_gemm_wide(const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
+hipError_t launch_gemm_wide(int type, const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s) {
   const int tiles_m = (int)((M + kWM - 1) / kWM);
   const int tiles = gemm_wide_tiles(M, N);
   const int per_xcd = (tiles * ksplit + 7) / 8;
-  launch_timed(gemm_wide_q4k_kernel, dim3((unsigned)(per_xcd * 8)), dim3(512), 0u, s, xhi,
-               static_cast<const h2 *>(xsum), rscale, static_cast<const uint8_t *>(w), bias, y, (int)M, (int)N,
-               (int)K, tiles_m, tiles, ksplit, part);
+  launch_timed(type == kQ5_K ? gemm_wide_q5k_kernel : gemm_wide_q4k_kernel, dim3((unsigned)(per_xcd * 8)), dim3(512),
+               0u, s, xhi, static_cast<const h2 *>(xsum), rscale, static_cast<const uint8_t *>(w), bias, y, (int)M,
+               (int)N, (int)K, tiles_m, tiles, ksplit, part);
   return hipGetLastError();
 }
 

@@ -83,8 +83,8 @@ struct GemmPlan {
   int groups;          // decode-batch kernel: column groups per K slice
   int kwaves;          // decode-batch kernel, unsplit K: waves that split a tile's K inside the workgroup
   int ksplit;
-  int wide;            // weights dequantised in registers (Q4_K, bf16): 1 gemm_wide_q4k_kernel (128 x 256
-                       // tiles, one workgroup per CU), 2 gemm_pair_q4k_kernel (128 x 128 tiles, two per CU)
+  int wide;            // weights dequantised in registers (Q4_K / Q5_K, bf16): 1 the wide kernel (128 x 256
+                       // tiles, one workgroup per CU), 2 the pair kernel (128 x 128 tiles, two per CU)
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
@@ -115,18 +115,19 @@ hipError_t launch_gemm_decode_mixed(const void *x, bool x_is_bf16, int64_t M, in
 // with K a multiple of 256.
 bool gemm_supported(int type, int64_t M, int64_t K, int64_t N);
 
-// The Q4_K prefill kernel with register-dequantised weights (okq_gemm_wide.hip)
-// over the pre-pass's planes: its shape limits, its 128 x 256 tile count, and
-// its launch (ksplit > 1: raw partials [ksplit][M][N] for splitk_reduce_kernel).
+// The Q4_K / Q5_K prefill kernel with register-dequantised weights
+// (okq_gemm_wide.hip) over the pre-pass's planes: its shape limits, its
+// 128 x 256 tile count, and its launch (ksplit > 1: raw partials
+// [ksplit][M][N] for splitk_reduce_kernel).
 bool gemm_wide_supported(int type, int64_t M, int64_t K, int64_t N);
 int gemm_wide_tiles(int64_t M, int64_t N);
-hipError_t launch_gemm_wide(const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
+hipError_t launch_gemm_wide(int type, const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s);
 // The same contraction with 128 x 128 tiles and two 4-wave workgroups per CU
 // (okq_gemm_pair.hip): same shape limits, operands and partial layout.
 int gemm_pair_tiles(int64_t M, int64_t N);
-hipError_t launch_gemm_pair(const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
+hipError_t launch_gemm_pair(int type, const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s);
 

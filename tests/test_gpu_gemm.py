@@ -549,8 +549,8 @@ def test_gemm_wide_one_hot_columns_are_exact(torch, okq, orc):
 # ---- Q5_K ------------------------------------------------------------------------
 # Q4_K with a fifth bit per weight (qh): B = sc * q with q <= 31, so sc * q <=
 # 1953 stays an exact fp16 integer and every product is exact as for Q4_K.
-# The decode-batch kernel (DecQ5K) and the tiled kernel take it; the
-# register-dequant prefill kernels stay Q4_K-only.
+# The decode-batch kernel (DecQ5K), the tiled kernel (f32 activations) and
+# the register-dequant kernels (bf16 activations) take it.
 
 Q5K_CASES = [
     # decode batches: one and two 16-row groups, split and unsplit K, ragged N
@@ -614,8 +614,10 @@ def test_gemm_q5k_one_hot_columns_are_exact(torch, okq, orc):
 def test_gemm_q5k_fifth_bit_probe(torch, okq, orc):
     """Blocks whose only non-zero quant bit is the fifth (qs = 0, one qh bit
     set, d = 1, sc = 1, dmin = 0): the value 16 must land at exactly the
-    element the bit names, on the GEMV, the decode-batch and the tiled
-    kernels (a misplaced bit plane or chunk shift moves or drops it)."""
+    element the bit names, on the GEMV, the decode-batch kernel, the tiled
+    kernel (f32) and the register-dequant kernels (bf16: the 4-wave pair
+    kernel at 40 rows, the 8-wave wide kernel at 256), so that a misplaced
+    bit plane or chunk shift moves or drops it."""
     k = 256
     blocks = []
     for p in range(k):
@@ -629,10 +631,14 @@ def test_gemm_q5k_fifth_bit_probe(torch, okq, orc):
     wq = np.concatenate(blocks)
     w = orc.dequantize(O.Q5_K, wq, k * k).reshape(k, k)
     assert (w == 16.0 * np.eye(k, dtype=np.float32)).all()
-    x = np.eye(k, dtype=np.float32)[:40]
-    for entry, rows in (("okq_gemv", 1), ("okq_gemm", 16), ("okq_gemm", 40)):
-        got = run(torch, okq, entry, O.Q5_K, x[:rows].reshape(-1), rows, k, wq, k)
-        assert np.array_equal(got, w[:, :rows].T), entry
+    x = np.eye(k, dtype=np.float32)
+    for entry, rows in (("okq_gemv", 1), ("okq_gemm", 16), ("okq_gemm", 40), ("okq_gemm_bf16", 40),
+                        ("okq_gemm_bf16", 256)):
+        xin = x[:rows].reshape(-1)
+        if entry == "okq_gemm_bf16":
+            xin = orc.f32_to_bf16(xin)
+        got = run(torch, okq, entry, O.Q5_K, xin, rows, k, wq, k)
+        assert np.array_equal(got, w[:, :rows].T), (entry, rows)
 
 
 def test_linear_dispatch_routes_q5k_like_q4k(torch, okq, orc):
