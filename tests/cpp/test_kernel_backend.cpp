@@ -96,7 +96,7 @@ bool same_bits(const std::vector<float> &a, const std::vector<float> &b) {
   return a.size() == b.size() && std::memcmp(a.data(), b.data(), a.size() * sizeof(float)) == 0;
 }
 
-const GgmlTensorType kTypes[] = {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q6K};
+const GgmlTensorType kTypes[] = {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q5K, GgmlTensorType::Q6K};
 
 // A backend with only the required f32 linear_out_by_in -- the reference CPU
 // path (the oracle) -- so every quantized entry point runs the trait's
@@ -207,9 +207,7 @@ void trait_default_quantized_linear_is_host_dequant_then_f32_linear() {
   const auto x = normal(4200, rows * in, 1.0f);
   const auto bias = normal(4201, out_f, 0.1f);
   for (GgmlTensorType t : {GgmlTensorType::Q8_0, GgmlTensorType::Q4K, GgmlTensorType::Q5K, GgmlTensorType::Q6K}) {
-    const auto info = ok(block_info(t), "block_info");
-    const auto q = t == GgmlTensorType::Q5K ? random_blocks(t, out_f * in / (size_t)info.first, 4202)
-                                           : quantize(t, normal(4203 + (uint64_t)t, out_f * in, 0.02f));
+    const auto q = quantize(t, normal(4203 + (uint64_t)t, out_f * in, 0.02f));
     auto w = ok(QuantizedWeight::from_host(t, in, out_f, q), "from_host");
     CHECK(w.residency().kind == Residency::Kind::Host && w.device_ptr() == nullptr, "host residency");
     for (const float *b : {(const float *)nullptr, bias.data()}) {
