@@ -116,13 +116,22 @@ __device__ __forceinline__ void prep_chunk(const float v[8], int s, bool ok, int
   }
 }
 
-__device__ __forceinline__ float block_max(float amax, float *red, int tid) {
+// The row's largest |x| as the largest magnitude bit pattern (the unsigned
+// order of |x| is the float order, with NaN above infinity above every
+// finite value, so one reduction also tells whether the row holds an
+// infinity or a NaN: a result >= 0x7f800000).
+__device__ __forceinline__ uint32_t block_max_bits(uint32_t a, uint32_t *red, int tid) {
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) amax = fmaxf(amax, __shfl_xor(amax, o, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = amax;
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t b = (uint32_t)__shfl_xor((int)a, o, 64);
+    a = a > b ? a : b;
+  }
+  if ((tid & 63) == 0) red[tid >> 6] = a;
   __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const uint32_t x = red[0] > red[1] ? red[0] : red[1], y = red[2] > red[3] ? red[2] : red[3];
+  return x > y ? x : y;
 }
+__device__ __forceinline__ uint32_t abs_bits(float v) { return as_u32(v) & 0x7fffffffu; }
 
 // Rows holding an infinity or a NaN.  The MFMA kernels cannot give them the
 // reference's IEEE results: they contract sc * q and the min term apart, so
@@ -190,15 +199,14 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
                                                         _Float16 *__restrict__ xhi, _Float16 *__restrict__ xlo,
                                                         h2 *__restrict__ xsum, float *__restrict__ rscale,
                                                         PrepIeee ieee) {
-  __shared__ float red[4];
+  __shared__ uint32_t red[4];
   const int m = (int)blockIdx.x;
   const int tid = (int)threadIdx.x;
   const int chunks = K / 8;  // 8 activations per thread and pass; 4 consecutive threads = one 32-run
   const int64_t row = (int64_t)m * K;
   if constexpr (CH > 0) {
     float v[CH][8];
-    float amax = 0.0f;
-    int nf = 0;
+    uint32_t amax = 0u;
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int c = tid + 256 * i;
@@ -212,12 +220,10 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
 #pragma unroll
     for (int i = 0; i < CH; ++i)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        amax = fmaxf(amax, fabsf(v[i][e]));
-        nf |= non_finite(v[i][e]) ? 1 : 0;
-      }
-    const int s = prep_exp(block_max(amax, red, tid));
-    const bool bad = __syncthreads_or(nf) != 0;
+      for (int e = 0; e < 8; ++e) amax = amax > abs_bits(v[i][e]) ? amax : abs_bits(v[i][e]);
+    const uint32_t rb = block_max_bits(amax, red, tid);
+    const bool bad = rb >= 0x7f800000u;
+    const int s = bad ? 0 : prep_exp(as_f32(rb));
     if (tid == 0) rscale[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, s);
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
@@ -228,19 +234,16 @@ __global__ __launch_bounds__(256) void gemm_prep_kernel(const void *__restrict__
     return;
   }
   // pass 1: row max |x|
-  float amax = 0.0f;
-  int nf = 0;
+  uint32_t amax = 0u;
   for (int c = tid; c < chunks; c += 256) {
     float v[8];
     load8<kF32>(X, row + 8 * (int64_t)c, v);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      amax = fmaxf(amax, fabsf(v[i]));
-      nf |= non_finite(v[i]) ? 1 : 0;
-    }
+    for (int i = 0; i < 8; ++i) amax = amax > abs_bits(v[i]) ? amax : abs_bits(v[i]);
   }
-  const int s = prep_exp(block_max(amax, red, tid));
-  const bool bad = __syncthreads_or(nf) != 0;
+  const uint32_t rb = block_max_bits(amax, red, tid);
+  const bool bad = rb >= 0x7f800000u;
+  const int s = bad ? 0 : prep_exp(as_f32(rb));
   if (tid == 0) rscale[m] = bad ? __builtin_nanf("") : ldexpf(1.0f, s);
   // pass 2: scaled fp16 planes and per-32 sums
   for (int c0 = 0; c0 < chunks; c0 += 256) {
