@@ -31,7 +31,8 @@ EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=
          # MFMA accumulators in VGPRs where they fit: the per-super-block sums
          # then feed the f32 scaling without AGPR round trips
          "okq_gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-         "okq_gemm_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+         "okq_gemm_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "okq_gemm_q8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

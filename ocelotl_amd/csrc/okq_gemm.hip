@@ -1795,9 +1795,9 @@ bool gemm_supported(int type, int64_t M, int64_t K, int64_t N) {
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count) {
   GemmPlan p{};
   p.kwaves = 1;
-  // More than 32 rows: Q4_K and Q5_K with bf16 activations take the
-  // register-dequant kernels (okq_gemm_wide.hip, okq_gemm_pair.hip); the
-  // tiled kernel takes the rest with 128 x 128 tiles
+  // More than 32 rows: Q4_K, Q5_K and Q8_0 with bf16 activations take the
+  // register-dequant kernels (okq_gemm_wide.hip, okq_gemm_pair.hip,
+  // okq_gemm_q8.hip); the tiled kernel takes the rest with 128 x 128 tiles
   // (f32 activations need the second fp16 plane, which only fits the LDS
   // budget at 128 rows; Q6_K stages its larger raw windows in the 4-wave
   // tile's register budget), or 256 x 128 tiles for bf16 Q4_K shapes beyond
@@ -1854,33 +1854,47 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     if (ks == 1 && mytiles > kDecMaxTiles)
       p.groups = (int)((ntiles + (int64_t)kDecWaves * kDecMaxTiles - 1) / ((int64_t)kDecWaves * kDecMaxTiles));
   } else {
-    // Q4_K and Q5_K with bf16 activations: a kernel that dequantises the
-    // weights in registers; everything else: the tiled kernel.  Split K when the tiles
-    // alone leave CUs idle: enough slices for about one workgroup per CU, at
-    // least two super-blocks per slice, at most 8.
+    // Q4_K, Q5_K and Q8_0 with bf16 activations: a kernel that dequantises
+    // the weights in registers; everything else: the tiled kernel.  Split K
+    // when the tiles alone leave CUs idle: enough slices for about one
+    // workgroup per CU, at least two super-blocks per slice, at most 8.
     const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
-    p.bm = reg_dequant ? 128 : ((type == kQ4_K || type == kQ5_K) && x_is_bf16 && M > 128) ? 256 : 128;
-    const int64_t cus = cu_count;
-    const int64_t tiles = reg_dequant ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
-    if (tiles * 4 < cus * 3) ks = std::min<int64_t>({(cus + tiles - 1) / tiles, nsb / 2, 8});
-    if (reg_dequant) {
-      // gemm_wide_q4k_kernel (128 x 256 tiles, one 8-wave workgroup per CU)
-      // while its workgroups fill at least 3/4 of their rounds of CUs (C4,
-      // us per call: M=512 gate 76.9 vs 86.7 for the other kernel, down 85.5
-      // vs 91.2, q 40.0 vs 41.1; M=2048 gate 292 vs 296, down 268 vs 301);
-      // otherwise gemm_pair_q4k_kernel (128 x 128 tiles, two 4-wave
-      // workgroups per CU), whose finer tiles and slices occupy every CU
-      // where the wide ones cannot (M=128 gate 39.5 vs 56.3, down 36.6 vs
-      // 42.8, q 24.2 vs 26.3; M=512 v 25.3 vs 27.8), with as many slices as
-      // fit one round of two workgroups per CU.
-      const int64_t jobs = tiles * std::max<int64_t>(1, ks);
-      const int64_t rounds = (jobs + cus - 1) / cus;
-      if (jobs * 4 >= rounds * cus * 3) {
-        p.wide = 1;
-      } else {
-        p.wide = 2;
-        const int64_t ptiles = gemm_pair_tiles(M, N), slots = 2 * cus;
-        ks = ptiles * 4 < slots * 3 ? std::max<int64_t>(1, std::min<int64_t>({slots / ptiles, nsb / 2, 8})) : 1;
+    if (x_is_bf16 && type == kQ8_0) {
+      // gemm_q8_kernel (128 x 128 tiles, two 4-wave workgroups per CU, bf16
+      // activations straight from x: no pre-pass).  K split in 128-K stages
+      // while the tiles leave CUs idle: about one workgroup per CU, at least
+      // four stages per slice, at most 8 slices (Q8_0 4096 x 4096, us per
+      // call: M=512 37.9 at 2 slices vs 39.0 at 4, whose partials cost more
+      // than the second workgroup per CU gains; M=128 22.7 at 8 slices;
+      // M=2048 96.6 unsplit vs 120.3 at 2)
+      p.bm = 128;
+      p.wide = 3;
+      const int64_t qtiles = gemm_q8_tiles(M, N), cus = cu_count;
+      ks = qtiles * 4 < cus * 3 ? std::max<int64_t>(1, std::min<int64_t>({cus / qtiles, K / 512, 8})) : 1;
+    } else {
+      p.bm = reg_dequant ? 128 : ((type == kQ4_K || type == kQ5_K) && x_is_bf16 && M > 128) ? 256 : 128;
+      const int64_t cus = cu_count;
+      const int64_t tiles = reg_dequant ? gemm_wide_tiles(M, N) : ((M + p.bm - 1) / p.bm) * ((N + kBN - 1) / kBN);
+      if (tiles * 4 < cus * 3) ks = std::min<int64_t>({(cus + tiles - 1) / tiles, nsb / 2, 8});
+      if (reg_dequant) {
+        // gemm_wide_q4k_kernel (128 x 256 tiles, one 8-wave workgroup per CU)
+        // while its workgroups fill at least 3/4 of their rounds of CUs (C4,
+        // us per call: M=512 gate 76.9 vs 86.7 for the other kernel, down 85.5
+        // vs 91.2, q 40.0 vs 41.1; M=2048 gate 292 vs 296, down 268 vs 301);
+        // otherwise gemm_pair_q4k_kernel (128 x 128 tiles, two 4-wave
+        // workgroups per CU), whose finer tiles and slices occupy every CU
+        // where the wide ones cannot (M=128 gate 39.5 vs 56.3, down 36.6 vs
+        // 42.8, q 24.2 vs 26.3; M=512 v 25.3 vs 27.8), with as many slices as
+        // fit one round of two workgroups per CU.
+        const int64_t jobs = tiles * std::max<int64_t>(1, ks);
+        const int64_t rounds = (jobs + cus - 1) / cus;
+        if (jobs * 4 >= rounds * cus * 3) {
+          p.wide = 1;
+        } else {
+          p.wide = 2;
+          const int64_t ptiles = gemm_pair_tiles(M, N), slots = 2 * cus;
+          ks = ptiles * 4 < slots * 3 ? std::max<int64_t>(1, std::min<int64_t>({slots / ptiles, nsb / 2, 8})) : 1;
+        }
       }
     }
   }
@@ -1889,6 +1903,11 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
   if (p.bm == kDecRows) {  // the decode-batch kernel needs only the split-K partials (whole 16-column tiles)
     p.off_lo = p.off_sums = p.off_rscale = p.off_part = 0;
     p.workspace = p.ksplit > 1 ? up((size_t)p.ksplit * M * ((N + 15) / 16 * 16) * sizeof(float)) : 0;
+    return p;
+  }
+  if (p.wide == 3) {  // the Q8_0 bf16 kernel reads x itself: only the split-K partials
+    p.off_lo = p.off_sums = p.off_rscale = p.off_part = 0;
+    p.workspace = p.ksplit > 1 ? up((size_t)p.ksplit * M * N * sizeof(float)) : 0;
     return p;
   }
   const size_t plane = (size_t)M * (size_t)K * sizeof(_Float16);
@@ -2084,11 +2103,25 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
     return launch_decode(type, type, (int)((N + 15) / 16), x, x_is_bf16, M, K, mats, (int)((N + 15) / 16), ws, plan, s,
                          false);
   }
+  float *part = plan.ksplit > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
+  const dim3 rgrid((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(M, 65535));
+  if (ks > 1 && (int64_t)ks * M * N * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // excluded by gemm_plan
+  // the split-K reduction of the partials (rscale: the pre-pass's row scales, or none)
+  auto reduce = [&](const float *rscale) {
+    if (ks <= 2) hipLaunchKernelGGL(splitk_reduce_kernel<2>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+    else if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_kernel<4>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+    else hipLaunchKernelGGL(splitk_reduce_kernel<8>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+    return hipGetLastError();
+  };
+  if (plan.wide == 3) {
+    if (!x_is_bf16 || type != kQ8_0) return hipErrorInvalidValue;
+    hipError_t e = launch_gemm_q8(x, W, bias, y, M, N, K, ks, part, s);
+    return e != hipSuccess || ks == 1 ? e : reduce(nullptr);
+  }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);
   _Float16 *xlo = x_is_bf16 ? nullptr : reinterpret_cast<_Float16 *>(ws + plan.off_lo);
   h2 *xsum = reinterpret_cast<h2 *>(ws + plan.off_sums);
   float *rscale = reinterpret_cast<float *>(ws + plan.off_rscale);
-  float *part = plan.ksplit > 1 ? reinterpret_cast<float *>(ws + plan.off_part) : nullptr;
   // chunks of 8 activations per thread: 2 (K <= 4096), 4, 8 held in registers, longer rows read twice
   const int64_t per_thread = (K / 8 + 255) / 256;
   const PrepIeee ieee{W, bias, y, (size_t)(K / 256) * (size_t)sb_bytes_of(type), type, (int)N};
@@ -2116,13 +2149,7 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   } else {
     e = launch_gemm_tiled(type, x_is_bf16, xhi, xlo, xsum, rscale, W, bias, y, M, N, K, plan, part, s);
   }
-  if (e != hipSuccess || ks == 1) return e;
-  if ((int64_t)ks * M * N * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // excluded by gemm_plan
-  const dim3 rgrid((unsigned)((N + 255) / 256), (unsigned)std::min<int64_t>(M, 65535));
-  if (ks <= 2) hipLaunchKernelGGL(splitk_reduce_kernel<2>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
-  else if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_kernel<4>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
-  else hipLaunchKernelGGL(splitk_reduce_kernel<8>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
-  return hipGetLastError();
+  return e != hipSuccess || ks == 1 ? e : reduce(rscale);
 }
 
 }  // namespace okq

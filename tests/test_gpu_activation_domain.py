@@ -223,8 +223,9 @@ NONFINITE_BATCH = [
     ("okq_gemm", O.Q4_K, 3, 70001, 256),
     # prefill (
     # the register-dequant kernels (bf16 Q4_K, whole tiles and split K
-    # through the reduction), the tiled kernel (f32, other formats), the
-    # pre-pass's two-pass form (K > 16384)
+    # through the reduction; bf16 Q8_0, whose bf16 MFMAs and f32 fold carry
+    # the infinities themselves, split and unsplit), the tiled kernel (f32,
+    # other formats), the pre-pass's two-pass form (K > 16384)
     ("okq_gemm_bf16", O.Q4_K, 512, 14336, 4096),
     ("okq_gemm_bf16", O.Q4_K, 512, 4096, 14336),
     ("okq_gemm_bf16", O.Q4_K, 130, 14336, 4096),
@@ -232,6 +233,9 @@ NONFINITE_BATCH = [
     ("okq_gemm", O.Q4_K, 40, 1000, 2048),
     ("okq_gemm", O.Q6_K, 64, 1000, 2048),
     ("okq_gemm_bf16", O.Q8_0, 33, 300, 1024),
+    ("okq_gemm_bf16", O.Q8_0, 512, 4096, 4096),
+    ("okq_gemm_bf16", O.Q8_0, 2048, 4096, 4096),
+    ("okq_gemm", O.Q8_0, 200, 1000, 1024),
     ("okq_gemm_bf16", O.Q5_K, 300, 1024, 4096),
     ("okq_gemm_bf16", O.Q4_K, 40, 300, 20480),
 ]
@@ -242,8 +246,9 @@ def test_mfma_non_finite_rows_follow_ieee(torch, okq, orc, entry, t, rows, n, k)
     """The MFMA paths (decode batches and prefill): rows holding +inf, -inf,
     both, a NaN, or an infinity in every position get exactly the reference
     CPU path's NaNs and signed infinities (computed in IEEE f32 by the
-    prefill pre-pass, or at the end of the decode-batch kernel), and every
-    other row equals the same batch without them, bit for bit."""
+    prefill pre-pass, at the end of the decode-batch kernel, or, for bf16
+    Q8_0, by the kernel's own bf16 MFMAs and f32 fold), and every other row
+    equals the same batch without them, bit for bit."""
     print(f"[gpu] non-finite mfma {entry} type={t} M={rows} N={n} K={k}", flush=True)
     wq = orc.quantize(t, orc.normal(9800 + t + k, n * k, 0.02))
     x = orc.normal(9801 + rows, rows * k, 1.0).reshape(rows, k)

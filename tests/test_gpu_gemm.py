@@ -427,9 +427,12 @@ def test_linear_dispatch_takes_the_q6k_gemm_above_eight_rows(torch, okq, orc):
 
 
 # ---- Q8_0 -----------------------------------------------------------------------
-# B = d * q (d the block's fp16 scale, q its int8 quant) enters as two exact
-# fp16 planes, fp16(d * q) and the remainder d * q - fp16(d * q): the products
-# are exact as for the K-quants, and no per-block scaling follows.
+# f32 activations (tiled kernel): B = d * q (d the block's fp16 scale, q its
+# int8 quant) enters as two exact fp16 planes, fp16(d * q) and the remainder
+# d * q - fp16(d * q): the products are exact as for the K-quants, and no
+# per-block scaling follows.  bf16 activations above 32 rows (gemm_q8_kernel):
+# x and q enter bf16 MFMAs as they are (exact products), each block's f32 sum
+# is scaled by d; ragged tiles, split and unsplit K, K of one stage pair.
 
 Q80_CASES = [
     # decode batches (one or two 16-row MFMA groups, split and unsplit K)
@@ -439,6 +442,8 @@ Q80_CASES = [
     # tiled GEMM (odd block counts per tile row: 2-byte aligned block starts alternate)
     ("okq_gemm_bf16", 33, 300, 1024), ("okq_gemm_bf16", 130, 1024, 4096), ("okq_gemm_bf16", 128, 4096, 14336),
     ("okq_gemm", 100, 257, 768), ("okq_gemm", 64, 4096, 4096), ("okq_gemm_bf16", 200, 1001, 256),
+    ("okq_gemm_bf16", 200, 4096, 4096), ("okq_gemm_bf16", 130, 1000, 2048), ("okq_gemm_bf16", 64, 300, 256),
+    ("okq_gemm_bf16", 384, 4352, 512), ("okq_gemm_bf16", 1000, 1000, 512),
 ]
 
 
