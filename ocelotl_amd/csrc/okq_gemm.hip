@@ -1860,17 +1860,24 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // workgroup per CU, at least two super-blocks per slice, at most 8.
     const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
     if (x_is_bf16 && type == kQ8_0) {
-      // gemm_q8_kernel (128 x 128 tiles, two 4-wave workgroups per CU, bf16
-      // activations straight from x: no pre-pass).  K split in 128-K stages
-      // while the tiles leave CUs idle: about one workgroup per CU, at least
-      // four stages per slice, at most 8 slices (Q8_0 4096 x 4096, us per
-      // call: M=512 37.9 at 2 slices vs 39.0 at 4, whose partials cost more
-      // than the second workgroup per CU gains; M=128 22.7 at 8 slices;
-      // M=2048 96.6 unsplit vs 120.3 at 2)
+      // gemm_q8_kernel (bf16 activations straight from x: no pre-pass).  The
+      // 8-wave 128 x 256 tiles (one workgroup per CU) while they fill at
+      // least 3/4 of their rounds of CUs (M=2048 4096 x 4096: 1 round);
+      // otherwise 4-wave 128 x 128 tiles, two workgroups per CU, K split in
+      // 128-K stages while the tiles leave CUs idle: about one workgroup per
+      // CU, at least four stages per slice, at most 8 slices (4096 x 4096, us
+      // per call: M=512 37.9 at 2 slices vs 39.0 at 4, whose partials cost
+      // more than the second workgroup per CU gains; M=128 22.7 at 8 slices)
       p.bm = 128;
       p.wide = 3;
-      const int64_t qtiles = gemm_q8_tiles(M, N), cus = cu_count;
-      ks = qtiles * 4 < cus * 3 ? std::max<int64_t>(1, std::min<int64_t>({cus / qtiles, K / 512, 8})) : 1;
+      const int64_t cus = cu_count, t8 = gemm_q8_tiles(M, N, 8);
+      if (t8 * 4 >= (t8 + cus - 1) / cus * cus * 3) {
+        p.kwaves = 8;
+      } else {
+        p.kwaves = 4;
+        const int64_t qtiles = gemm_q8_tiles(M, N, 4);
+        ks = qtiles * 4 < cus * 3 ? std::max<int64_t>(1, std::min<int64_t>({cus / qtiles, K / 512, 8})) : 1;
+      }
     } else {
       p.bm = reg_dequant ? 128 : ((type == kQ4_K || type == kQ5_K) && x_is_bf16 && M > 128) ? 256 : 128;
       const int64_t cus = cu_count;
@@ -2115,7 +2122,7 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   };
   if (plan.wide == 3) {
     if (!x_is_bf16 || type != kQ8_0) return hipErrorInvalidValue;
-    hipError_t e = launch_gemm_q8(x, W, bias, y, M, N, K, ks, part, s);
+    hipError_t e = launch_gemm_q8(x, W, bias, y, M, N, K, ks, plan.kwaves, part, s);
     return e != hipSuccess || ks == 1 ? e : reduce(nullptr);
   }
   _Float16 *xhi = reinterpret_cast<_Float16 *>(ws);

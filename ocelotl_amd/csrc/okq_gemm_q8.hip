@@ -60,8 +60,7 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 typedef __attribute__((address_space(3))) void *LdsPtr;
 
-constexpr int kQM = 128;                          // tile rows
-constexpr int kQN = 128;                          // tile columns (4 waves x 32)
+constexpr int kQM = 128;                          // tile rows (the tile has 32 columns per wave)
 constexpr uint32_t kStageBytes = 4u * kQ8Bytes;   // one stage of a column: 4 blocks, 128 K
 
 __device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
@@ -95,11 +94,16 @@ struct Q8Ready {
 
 }  // namespace
 
-__global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restrict__ X,
-                                                         const uint8_t *__restrict__ W,
-                                                         const float *__restrict__ bias, float *__restrict__ Y, int M,
-                                                         int N, int K, int tiles_m, int tiles, int ksplit,
-                                                         float *__restrict__ part) {
+// kW waves per workgroup on a 128 x 32 kW tile: 4 (two workgroups per CU)
+// or 8 (one per CU: half the activation copies per MFMA, for grids that fill
+// the CUs with the wider tiles).
+template <int kW>
+__device__ __forceinline__ void q8_body(const uint16_t *__restrict__ X, const uint8_t *__restrict__ W,
+                                        const float *__restrict__ bias, float *__restrict__ Y, int M, int N, int K,
+                                        int tiles_m, int tiles, int ksplit, float *__restrict__ part) {
+  constexpr int kQN = 32 * kW;    // tile columns
+  constexpr int kRW = kQM / kW;   // rows each wave copies
+  constexpr int kCP = kRW / 4;    // its copy instructions per stage (4 rows each)
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a
   // contiguous range of (slice, tile) jobs, and consecutive jobs are the
   // M-tiles of one N-tile (they share its weights in that XCD's L2).
@@ -109,8 +113,14 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restr
   const int job = (b % 8) * per_xcd + b / 8;
   if (job >= jobs) return;
   const int z = job / tiles, tile = job % tiles;
-  const int m0 = (tile % tiles_m) * kQM;
-  const int n0 = (tile / tiles_m) * kQN;
+  // groups of up to 8 M-tiles: consecutive jobs walk a group's M-tiles, then
+  // its N-tiles, so an XCD's jobs share both activation and weight tiles in
+  // its L2 (M=2048: 8 x 8 tiles per XCD rather than 16 x 4, 2-3% faster)
+  const int tiles_n = tiles / tiles_m;
+  const int grp = tile / (8 * tiles_n), rg = tile % (8 * tiles_n);
+  const int gm = tiles_m - 8 * grp < 8 ? tiles_m - 8 * grp : 8;
+  const int m0 = (8 * grp + rg % gm) * kQM;
+  const int n0 = (rg / gm) * kQN;
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -125,17 +135,17 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restr
   const Rsrc rs_w = make_rsrc(W, (uint32_t)((size_t)N * row_bytes));
 
   // Activation copy of stage st (slice-relative): wave w moves rows
-  // 32w .. 32w+31, four rows (1 KB) per instruction; lane L of instruction t
-  // writes chunk L & 15 of row 32w + 4t + L/16, which holds the row's logical
-  // chunk (L & 15) ^ (row & 15).
+  // kRW w .. kRW w + kRW - 1, four rows (1 KB) per instruction; lane L of
+  // instruction t writes chunk L & 15 of row kRW w + 4t + L/16, which holds
+  // the row's logical chunk (L & 15) ^ (row & 15).
   uint32_t a_off[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t)
-    a_off[t] = (uint32_t)(m0 + 32 * wave + (lane >> 4)) * K2 +
+    a_off[t] = (uint32_t)(m0 + kRW * wave + (lane >> 4)) * K2 +
                16u * ((uint32_t)(lane & 15) ^ (uint32_t)(4 * t + (lane >> 4)));
   auto copy_piece = [&](int t, int st, uint16_t *bufA) {
     const uint32_t kb = (uint32_t)(st0 + st) * 128u;  // first K of the stage
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (LdsPtr)(bufA + (32 * wave + 4 * t) * 128), 16, a_off[t & 3],
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs_x, (LdsPtr)(bufA + (kRW * wave + 4 * t) * 128), 16, a_off[t & 3],
                                              (int)((uint32_t)t * 4u * K2 + kb * 2u), 0, 0);
   };
 
@@ -227,8 +237,8 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restr
         for (int i = 0; i < 4; ++i) an[i] = a_at(bufA, ad, i);
       }
       if (s < 4) {
-        copy_piece(2 * s, st_next, nbufA);
-        copy_piece(2 * s + 1, st_next, nbufA);
+#pragma unroll
+        for (int c = 0; c < kCP / 4; ++c) copy_piece(kCP / 4 * s + c, st_next, nbufA);
       }
       // the next step's fragment reads issue ahead of this step's MFMAs
       __builtin_amdgcn_sched_barrier(0);
@@ -270,7 +280,7 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restr
   const int last = nst - 1;
   auto cl_st = [&](int st) { return st < last ? st : last; };
 #pragma unroll
-  for (int t = 0; t < 8; ++t) copy_piece(t, 0, qA0);
+  for (int t = 0; t < kCP; ++t) copy_piece(t, 0, qA0);
   ld_raw(0, raw);
   __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
   prepare(raw, S);
@@ -324,16 +334,35 @@ __global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restr
   }
 }
 
-int gemm_q8_tiles(int64_t M, int64_t N) { return (int)(((M + kQM - 1) / kQM) * ((N + kQN - 1) / kQN)); }
+__global__ __launch_bounds__(256, 2) void gemm_q8_kernel(const uint16_t *__restrict__ X,
+                                                         const uint8_t *__restrict__ W,
+                                                         const float *__restrict__ bias, float *__restrict__ Y, int M,
+                                                         int N, int K, int tiles_m, int tiles, int ksplit,
+                                                         float *__restrict__ part) {
+  q8_body<4>(X, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
+__global__ __launch_bounds__(512, 1) void gemm_q8_wide_kernel(const uint16_t *__restrict__ X,
+                                                              const uint8_t *__restrict__ W,
+                                                              const float *__restrict__ bias, float *__restrict__ Y,
+                                                              int M, int N, int K, int tiles_m, int tiles, int ksplit,
+                                                              float *__restrict__ part) {
+  q8_body<8>(X, W, bias, Y, M, N, K, tiles_m, tiles, ksplit, part);
+}
+
+int gemm_q8_tiles(int64_t M, int64_t N, int waves) {
+  return (int)(((M + kQM - 1) / kQM) * ((N + 32 * waves - 1) / (32 * waves)));
+}
 
 hipError_t launch_gemm_q8(const void *x, const void *w, const float *bias, float *y, int64_t M, int64_t N, int64_t K,
-                          int ksplit, float *part, hipStream_t s) {
-  if (K % 256 != 0 || ksplit < 1 || ksplit > K / 128) return hipErrorInvalidValue;
+                          int ksplit, int waves, float *part, hipStream_t s) {
+  if (K % 256 != 0 || ksplit < 1 || ksplit > K / 128 || (waves != 4 && waves != 8)) return hipErrorInvalidValue;
   const int tiles_m = (int)((M + kQM - 1) / kQM);
-  const int tiles = gemm_q8_tiles(M, N);
+  const int tiles = gemm_q8_tiles(M, N, waves);
   const int per_xcd = (tiles * ksplit + 7) / 8;
-  launch_timed(gemm_q8_kernel, dim3((unsigned)(per_xcd * 8)), dim3(256), 0u, s, static_cast<const uint16_t *>(x),
-               static_cast<const uint8_t *>(w), bias, y, (int)M, (int)N, (int)K, tiles_m, tiles, ksplit, part);
+  launch_timed(waves == 8 ? gemm_q8_wide_kernel : gemm_q8_kernel, dim3((unsigned)(per_xcd * 8)), dim3(64 * waves), 0u,
+               s, static_cast<const uint16_t *>(x), static_cast<const uint8_t *>(w), bias, y, (int)M, (int)N, (int)K,
+               tiles_m, tiles, ksplit, part);
   return hipGetLastError();
 }
 

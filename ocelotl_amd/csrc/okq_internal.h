@@ -81,11 +81,12 @@ hipError_t launch_swiglu(const float *gate, const float *up, int64_t n, float *o
 struct GemmPlan {
   int bm;              // 32: the decode-batch kernel (M <= 32), else the tile height
   int groups;          // decode-batch kernel: column groups per K slice
-  int kwaves;          // decode-batch kernel, unsplit K: waves that split a tile's K inside the workgroup
+  int kwaves;          // decode-batch kernel, unsplit K: waves that split a tile's K inside the workgroup;
+                       // Q8_0 kernel: waves per workgroup (4 or 8)
   int ksplit;
   int wide;            // weights dequantised in registers (bf16 activations): 1 the wide kernel (Q4_K / Q5_K,
                        // 128 x 256 tiles, one workgroup per CU), 2 the pair kernel (Q4_K / Q5_K, 128 x 128
-                       // tiles, two per CU), 3 the Q8_0 kernel (128 x 128 tiles, two per CU)
+                       // tiles, two per CU), 3 the Q8_0 kernel (128 x 128 or 128 x 256 tiles)
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
@@ -132,11 +133,12 @@ hipError_t launch_gemm_pair(int type, const _Float16 *xhi, const void *xsum, con
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s);
 // Q8_0 with bf16 activations (okq_gemm_q8.hip): x [M, K] bf16 straight into
-// bf16 MFMAs (no pre-pass), 128 x 128 tiles, two 4-wave workgroups per CU, K
-// split in stages of 128 (ksplit <= K / 128; K a multiple of 256); ksplit > 1
-// writes unscaled partials [ksplit][M][N] for splitk_reduce_kernel.
-int gemm_q8_tiles(int64_t M, int64_t N);
+// bf16 MFMAs (no pre-pass), 128 x 32 waves tiles (waves = 4: two workgroups
+// per CU; 8: one), K split in stages of 128 (ksplit <= K / 128; K a multiple
+// of 256); ksplit > 1 writes unscaled partials [ksplit][M][N] for
+// splitk_reduce_kernel.
+int gemm_q8_tiles(int64_t M, int64_t N, int waves);
 hipError_t launch_gemm_q8(const void *x, const void *w, const float *bias, float *y, int64_t M, int64_t N, int64_t K,
-                          int ksplit, float *part, hipStream_t s);
+                          int ksplit, int waves, float *part, hipStream_t s);
 
 }  // namespace okq

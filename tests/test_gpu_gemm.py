@@ -473,6 +473,24 @@ def test_gemm_q8_0_prefill_4096_sampled_rows(torch, okq, orc, rows):
     check_rows(orc, O.Q8_0, got, x32, rows, k, wq, n, None, 16)
 
 
+@pytest.mark.parametrize("rows,n,k", [(2048, 4096, 4096), (2000, 4000, 512), (1100, 7000, 1024)])
+def test_gemm_q8_0_bf16_rows_of_every_m_tile(torch, okq, orc, rows, n, k):
+    """bf16 Q8_0 prefill on grids that take the 8-wave 128 x 256 tiles (and
+    ragged M and N tiles): two rows of every 128-row tile and the last row
+    checked against the reference CPU path."""
+    print(f"[gpu] gemm Q8_0 bf16 M={rows} N={n} K={k} (rows of every tile)", flush=True)
+    wq = orc.quantize(O.Q8_0, orc.normal(1880 + n + k, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 1881 + rows, rows, k)
+    bias = orc.normal(1882, n, 0.1)
+    got = run(torch, okq, "okq_gemm_bf16", O.Q8_0, xb, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    idx = np.unique(np.r_[np.arange(0, rows, 128) + 3, np.arange(0, rows, 128) + 126, rows - 1])
+    idx = idx[idx < rows]
+    want = orc.linear_q(O.Q8_0, x32.reshape(rows, k)[idx].reshape(-1), idx.size, k, wq, n, bias, O.MODE_SCALAR, 16)
+    ok, i, dmax, _ = O.allclose_ref_rule(got.reshape(rows, n)[idx].reshape(-1), want, TOL)
+    assert ok, f"row {idx[i // n]} col {i % n}: max_abs {dmax}"
+
+
 def test_gemm_q8_0_one_hot_columns_are_exact(torch, okq, orc):
     """x = e_j returns d * q of every weight row bit for bit (hi + lo = d * q
     exactly), on the decode-batch (16 rows) and tiled (40 rows) kernels, with
