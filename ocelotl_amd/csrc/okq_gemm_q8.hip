@@ -105,8 +105,7 @@ __device__ __forceinline__ void q8_body(const uint16_t *__restrict__ X, const ui
   constexpr int kRW = kQM / kW;   // rows each wave copies
   constexpr int kCP = kRW / 4;    // its copy instructions per stage (4 rows each)
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a
-  // contiguous range of (slice, tile) jobs, and consecutive jobs are the
-  // M-tiles of one N-tile (they share its weights in that XCD's L2).
+  // contiguous range of (slice, tile) jobs.
   const int b = (int)blockIdx.x;
   const int jobs = tiles * ksplit;
   const int per_xcd = (jobs + 7) / 8;

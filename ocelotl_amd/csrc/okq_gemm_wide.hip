@@ -84,16 +84,22 @@ __device__ __forceinline__ void wide_body(const _Float16 *__restrict__ xhi, cons
                                           int tiles_m, int tiles, int ksplit, float *__restrict__ part) {
   constexpr uint32_t kSB = kQ5 ? kQ5KBytes : kQ4KBytes;  // bytes per super-block
   // XCD-aware order: workgroup b runs on XCD b % 8; each XCD takes a
-  // contiguous range of (slice, tile) jobs, and consecutive jobs are the
-  // M-tiles of one N-tile (they share its weights in that XCD's L2).
+  // contiguous range of (slice, tile) jobs.  Tiles go in groups of up to 8
+  // M-tiles: consecutive jobs walk a group's M-tiles (they share an N-tile's
+  // weights in that XCD's L2), then its N-tiles, so an XCD's activation
+  // tiles also stay few (M=2048 gate: 8 x 14 tiles per XCD rather than
+  // 16 x 7, kernel 289.7 -> 281.7 us).
   const int b = (int)blockIdx.x;
   const int jobs = tiles * ksplit;
   const int per_xcd = (jobs + 7) / 8;
   const int job = (b % 8) * per_xcd + b / 8;
   if (job >= jobs) return;
   const int z = job / tiles, tile = job % tiles;
-  const int m0 = (tile % tiles_m) * kWM;
-  const int n0 = (tile / tiles_m) * kWN;
+  const int tiles_n = tiles / tiles_m;
+  const int grp = tile / (8 * tiles_n), rg = tile % (8 * tiles_n);
+  const int gm = tiles_m - 8 * grp < 8 ? tiles_m - 8 * grp : 8;
+  const int m0 = (8 * grp + rg % gm) * kWM;
+  const int n0 = (rg / gm) * kWN;
 
   const int tid = (int)threadIdx.x;
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);

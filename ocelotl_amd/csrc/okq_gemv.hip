@@ -930,9 +930,6 @@ __global__ __launch_bounds__(256) void gemv_generic_kernel(int type, const uint8
 // ---------------------------------------------------------------------------
 // launcher
 // ---------------------------------------------------------------------------
-// Ring depth: the format's maximum when every wave has that many rows to
-// stream, else 1 (a deeper ring than the row count would only issue loads
-// past the range).
 // The matrices of one launch: matrix 0 in the kernel arguments, the rest in M.
 struct GemvLaunch {
   const uint8_t *w;
@@ -983,15 +980,17 @@ void launch_multi(dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLa
 }
 
 // Ring depth: the format's maximum when every wave has that many rows to
-// stream, else 1 (a deeper ring than the row count would only issue loads
-// past the range).  Multi-row launches always use the maximum.
+// stream and more than two, else 1 (a deeper ring than the row count would
+// only issue loads past the range; at two rows per wave the one-row ring
+// measured faster: C2 q+k+v 6.60 -> 6.23 us).  Multi-row launches always use
+// the maximum.
 template <class F, int XV, int R>
 void launch_depth(int64_t steps, dim3 grid, dim3 block, size_t lds, hipStream_t s, const GemvLaunch &L,
                   const float *x, int k, int T, int G) {
   if constexpr (R > 1) {
     launch_multi<F, F::kMaxDepth, XV, R>(grid, block, lds, s, L, x, k, T, G);
   } else {
-    if (steps >= F::kMaxDepth) launch_multi<F, F::kMaxDepth, XV, 1>(grid, block, lds, s, L, x, k, T, G);
+    if (steps >= F::kMaxDepth && steps > 2) launch_multi<F, F::kMaxDepth, XV, 1>(grid, block, lds, s, L, x, k, T, G);
     else launch_multi<F, 1, XV, 1>(grid, block, lds, s, L, x, k, T, G);
   }
 }
