@@ -1,6 +1,5 @@
 // okq_gemm_q8.hip -- Q8_0 prefill dequant-GEMM on bf16 activations, the
-// weights dequantised in registers, two 4-wave workgroups per CU:
-// Y[M,N] = X[M,K] W[N,K]^T (+bias).
+// weights dequantised in registers: Y[M,N] = X[M,K] W[N,K]^T (+bias).
 //
 // Numerics.  A = the bf16 activations themselves, B = q itself (an int8, exact
 // in bf16): every product x * q is exact in f32 (8 x 8 significant bits) and
@@ -16,14 +15,17 @@
 // (up to 19 significant bits) and would need two planes, two MFMAs per
 // product.
 //
-// Layout, as okq_gemm_pair.hip: a workgroup is four waves, one per SIMD, on a
-// 128 x 128 tile (wave w: columns 32w .. 32w+31, all 128 rows, four 32x32x16
-// MFMA blocks per B fragment); two workgroups share a CU, so the two waves of
-// a SIMD belong to different tiles and one's MFMAs run while the other folds
-// and dequantises.  A stage is 128 K = four Q8_0 blocks (136 bytes per
-// column); activations are double-buffered in LDS (2 x 32 KB), copied one
-// stage ahead by buffer-to-LDS loads with 16-byte chunk c of row r at chunk
-// c ^ (r & 15) (conflict-free fragment reads).
+// Layout: wave w owns columns 32w .. 32w+31 of the tile for all 128 rows
+// (four 32x32x16 MFMA blocks per B fragment).  gemm_q8_kernel: four waves on
+// a 128 x 128 tile, two workgroups per CU (okq_gemm_pair.hip's layout), so
+// the two waves of a SIMD belong to different tiles and one's MFMAs run while
+// the other folds and dequantises; gemm_q8_wide_kernel: eight waves on a
+// 128 x 256 tile, one workgroup per CU (each activation stage serves twice
+// the columns), for grids whose wide tiles fill the CUs.  A stage is 128 K =
+// four Q8_0 blocks (136 bytes per column); activations are double-buffered
+// in LDS (2 x 32 KB), copied one stage ahead by buffer-to-LDS loads with
+// 16-byte chunk c of row r at chunk c ^ (r & 15) (conflict-free fragment
+// reads).
 //
 //   * K order: MFMA step s (0..7) of a stage covers block j = s / 2, lane
 //     group g = lane / 32 its elements 16 g + 8 (s & 1) + [0, 8), so every
