@@ -475,6 +475,10 @@ def run_c4(ctx: Ctx, args, c2):
             kernel = None
             if key == "M512_gate":  # the plan's choice at 256 CUs (gemm_plan, okq_gemm.hip)
                 kernel = "okq::gemm_wide_q4k_kernel (128x256 tiles, 8 waves, weights dequantised in registers)"
+            elif t == Q8_0:  # bf16 Q8_0: no pre-pass; 8-wave tiles where they fill the CUs (gemm_plan)
+                kernel = ("okq::gemm_q8_wide_kernel (128x256 tiles, 8 waves)" if m >= 2048 else
+                          "okq::gemm_q8_kernel (128x128 tiles, 4 waves, K split)") + \
+                    ": bf16 MFMAs on x and q, per-block f32 fold with d, no activation pre-pass"
             res[key] = {"type": "Q4_K" if t == Q4K else "Q8_0", "m": m, "n": n, "k": k,
                         "us_call": round(t_call, 2), "us_call_p10": round(pct(per, 10), 2),
                         "us_call_median": round(median(per), 2), "us_call_p90": round(pct(per, 90), 2),
