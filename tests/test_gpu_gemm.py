@@ -444,6 +444,9 @@ Q80_CASES = [
     ("okq_gemm", 100, 257, 768), ("okq_gemm", 64, 4096, 4096), ("okq_gemm_bf16", 200, 1001, 256),
     ("okq_gemm_bf16", 200, 4096, 4096), ("okq_gemm_bf16", 130, 1000, 2048), ("okq_gemm_bf16", 64, 300, 256),
     ("okq_gemm_bf16", 384, 4352, 512), ("okq_gemm_bf16", 1000, 1000, 512),
+    # an odd number of super-blocks, and slices of unequal stage counts (26
+    # stages over 6 slices)
+    ("okq_gemm_bf16", 130, 520, 768), ("okq_gemm_bf16", 40, 200, 3328),
 ]
 
 
