@@ -32,7 +32,8 @@ EXTRA = {"okq_prep.hip": ["-ffp-contract=off"], "okq_gemv.hip": ["-ffp-contract=
          # then feed the f32 scaling without AGPR round trips
          "okq_gemm_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
          "okq_gemm_pair.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
-         "okq_gemm_q8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+         "okq_gemm_q8.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+         "okq_gemm_q6.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
 def sources():

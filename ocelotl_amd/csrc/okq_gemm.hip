@@ -1859,6 +1859,17 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
     // when the tiles alone leave CUs idle: enough slices for about one
     // workgroup per CU, at least two super-blocks per slice, at most 8.
     const bool reg_dequant = x_is_bf16 && gemm_wide_supported(type, M, K, N);
+    // Q6_K with bf16 activations: gemm_wide_q6k_kernel (128 x 256 tiles, one
+    // 8-wave workgroup per CU) while its (tile, K-slice) jobs fill at least
+    // 3/4 of their rounds of CUs; otherwise the tiled kernel
+    bool q6_wide = false;
+    int64_t q6_ks = 1;
+    if (x_is_bf16 && type == kQ6_K) {
+      const int64_t cus = cu_count, t6 = gemm_q6_tiles(M, N);
+      if (t6 * 4 < cus * 3) q6_ks = std::max<int64_t>(1, std::min<int64_t>({(cus + t6 - 1) / t6, nsb / 2, 8}));
+      const int64_t jobs = t6 * q6_ks, rounds = (jobs + cus - 1) / cus;
+      q6_wide = jobs * 4 >= rounds * cus * 3;
+    }
     if (x_is_bf16 && type == kQ8_0) {
       // gemm_q8_kernel (bf16 activations straight from x: no pre-pass).  The
       // 8-wave 128 x 256 tiles (one workgroup per CU) while they fill at
@@ -1878,6 +1889,10 @@ GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, in
         const int64_t qtiles = gemm_q8_tiles(M, N, 4);
         ks = qtiles * 4 < cus * 3 ? std::max<int64_t>(1, std::min<int64_t>({cus / qtiles, K / 512, 8})) : 1;
       }
+    } else if (q6_wide) {
+      p.bm = 128;
+      p.wide = 4;
+      ks = q6_ks;
     } else {
       p.bm = reg_dequant ? 128 : ((type == kQ4_K || type == kQ5_K) && x_is_bf16 && M > 128) ? 256 : 128;
       const int64_t cus = cu_count;
@@ -2149,7 +2164,9 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
 #undef OKQ_PREP
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  if (plan.wide == 2) {
+  if (plan.wide == 4) {
+    e = launch_gemm_q6(xhi, rscale, W, bias, y, M, N, K, ks, part, s);
+  } else if (plan.wide == 2) {
     e = launch_gemm_pair(type, xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);
   } else if (plan.wide) {
     e = launch_gemm_wide(type, xhi, xsum, rscale, W, bias, y, M, N, K, ks, part, s);

@@ -86,7 +86,8 @@ struct GemmPlan {
   int ksplit;
   int wide;            // weights dequantised in registers (bf16 activations): 1 the wide kernel (Q4_K / Q5_K,
                        // 128 x 256 tiles, one workgroup per CU), 2 the pair kernel (Q4_K / Q5_K, 128 x 128
-                       // tiles, two per CU), 3 the Q8_0 kernel (128 x 128 or 128 x 256 tiles)
+                       // tiles, two per CU), 3 the Q8_0 kernel (128 x 128 or 128 x 256 tiles),
+                       // 4 the Q6_K kernel (128 x 256 tiles)
   size_t off_lo, off_sums, off_rscale, off_part, workspace;
 };
 GemmPlan gemm_plan(int type, int64_t M, int64_t N, int64_t K, bool x_is_bf16, int cu_count);
@@ -132,6 +133,13 @@ int gemm_pair_tiles(int64_t M, int64_t N);
 hipError_t launch_gemm_pair(int type, const _Float16 *xhi, const void *xsum, const float *rscale, const void *w,
                             const float *bias, float *y, int64_t M, int64_t N, int64_t K, int ksplit, float *part,
                             hipStream_t s);
+// Q6_K with bf16 activations (okq_gemm_q6.hip): the pre-pass's fp16 plane and
+// row scales, 128 x 256 tiles, one 8-wave workgroup per CU, the weights as
+// two exact fp16 planes dequantised in registers; K a multiple of 256 split
+// into ksplit <= K / 256 slices of whole super-blocks, the same partial layout.
+int gemm_q6_tiles(int64_t M, int64_t N);
+hipError_t launch_gemm_q6(const _Float16 *xhi, const float *rscale, const void *w, const float *bias, float *y,
+                          int64_t M, int64_t N, int64_t K, int ksplit, float *part, hipStream_t s);
 // Q8_0 with bf16 activations (okq_gemm_q8.hip): x [M, K] bf16 straight into
 // bf16 MFMAs (no pre-pass), 128 x 32 waves tiles (waves = 4: two workgroups
 // per CU; 8: one), K split in stages of 128 (ksplit <= K / 128; K a multiple

@@ -237,6 +237,7 @@ NONFINITE_BATCH = [
     ("okq_gemm_bf16", O.Q8_0, 2048, 4096, 4096),
     ("okq_gemm", O.Q8_0, 200, 1000, 1024),
     ("okq_gemm_bf16", O.Q5_K, 300, 1024, 4096),
+    ("okq_gemm_bf16", O.Q6_K, 512, 4096, 14336),
     ("okq_gemm_bf16", O.Q4_K, 40, 300, 20480),
 ]
 

@@ -373,6 +373,44 @@ def test_gemm_q6k_one_hot_columns_are_exact(torch, okq, orc):
         assert np.array_equal(got, w[:, cols].T), entry
 
 
+# bf16 grids whose 128 x 256 tiles fill the CUs take gemm_wide_q6k_kernel (the
+# weights as the same two exact planes, dequantised in registers): the C4
+# down shape, ragged M and N split and unsplit, and rows of 630 / 1050 bytes
+# (2-byte aligned super-blocks).
+Q6K_WIDE_CASES = [(512, 4096, 14336), (500, 3900, 4096), (2048, 3000, 768), (1000, 3900, 1280)]
+
+
+@pytest.mark.parametrize("rows,n,k", Q6K_WIDE_CASES)
+def test_gemm_q6k_bf16_wide_rows_of_every_m_tile(torch, okq, orc, rows, n, k):
+    print(f"[gpu] gemm Q6_K bf16 M={rows} N={n} K={k} (rows of every tile)", flush=True)
+    wq = orc.quantize(O.Q6_K, orc.normal(960 + n + k, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 961 + rows, rows, k)
+    bias = orc.normal(962, n, 0.1)
+    got = run(torch, okq, "okq_gemm_bf16", O.Q6_K, xb, rows, k, wq, n, bias)
+    assert np.isfinite(got).all()
+    idx = np.unique(np.r_[np.arange(0, rows, 128) + 3, np.arange(0, rows, 128) + 126, rows - 1])
+    idx = idx[idx < rows]
+    want = orc.linear_q(O.Q6_K, x32.reshape(rows, k)[idx].reshape(-1), idx.size, k, wq, n, bias, O.MODE_SCALAR, 16)
+    ok, i, dmax, _ = O.allclose_ref_rule(got[idx].reshape(-1), want, TOL)
+    assert ok, f"row {idx[i // n]} col {i % n}: max_abs {dmax}"
+
+
+def test_gemm_q6k_bf16_wide_one_hot_columns_are_exact(torch, okq, orc):
+    """The wide Q6_K kernel on one-hot rows returns d * sc * (q - 32), the
+    dequantized weights, for every weight row (scales beyond |sc| = 64, whose
+    products exceed 2048, included); rows of 630 bytes."""
+    rows, n, k = 2048, 3000, 768
+    wq = orc.quantize(O.Q6_K, orc.normal(970, n * k, 0.02))
+    w = orc.dequantize(O.Q6_K, wq, n * k).reshape(n, k)
+    blocks = np.frombuffer(wq.tobytes(), np.uint8).reshape(n, k // 256, 210)
+    assert np.abs(blocks[:, :, 192:208].view(np.int8).astype(int)).max() > 64
+    x = np.zeros((rows, k), np.float32)
+    cols = np.arange(rows) * 37 % k
+    x[np.arange(rows), cols] = 1.0
+    got = run(torch, okq, "okq_gemm_bf16", O.Q6_K, orc.f32_to_bf16(x.reshape(-1)), rows, k, wq, n)
+    assert np.array_equal(got, w[:, cols].T)
+
+
 def _dispatch_pairs(torch, okq, orc, t, n, k, seed, pairs):
     """okq_linear_out_by_in_q at each (rows, pinned entry): bit-identical to the
     pinned path (okq_gemv: the GEMV; okq_gemm: the MFMA kernels), and within
