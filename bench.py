@@ -574,8 +574,9 @@ def run_q5k(ctx: Ctx, args):
 def run_q6k_prefill(ctx: Ctx, args):
     """The Q4_K_M / Q5_K_M files' other format at prefill: the Q6_K down
     projection (4096 x 14336, the largest matrix a Q4_K_M layer stores in
-    Q6_K) at M=512 with bf16 activations (pre-pass + tiled kernel + split-K
-    reduction), rotating over >= 512 MB of weight replicas in a HIP graph."""
+    Q6_K) at M=512 with bf16 activations (pre-pass + gemm_wide_q6k_kernel +
+    split-K reduction), rotating over >= 512 MB of weight replicas in a HIP
+    graph."""
     torch = ctx.torch
     n, k, m = 4096, 14336, 512
     b = wbytes(Q6K, n, k)
