@@ -43,7 +43,7 @@ The JSON line also carries:
                 down projection's M=512 prefill call
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|gemm_q8_512|gemm_q8_2048|decode_gate_up32
+     python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|gemm_q8_512|gemm_q8_2048|gemm_q6_512|decode_gate_up32
                                                         (bare workloads for counter passes)
 """
 from __future__ import annotations
@@ -910,7 +910,7 @@ def run_probe(ctx: Ctx, what: str):
     elif what.startswith("gemm_"):
         t, m, n, k = {"gemm_gate512": (Q4K, 512, 14336, 4096), "gemm_down512": (Q4K, 512, 4096, 14336),
                       "gemm_gate128": (Q4K, 128, 14336, 4096), "gemm_q8_512": (Q8_0, 512, 4096, 4096),
-                      "gemm_q8_2048": (Q8_0, 2048, 4096, 4096)}[what]
+                      "gemm_q8_2048": (Q8_0, 2048, 4096, 4096), "gemm_q6_512": (Q6K, 512, 4096, 14336)}[what]
         ws = [ctx.quantized(t, n, k, seed=10_004 + c) for c in range(4)]
         xf = ctx.normal(m * k, 562)
         xb = torch.empty(m * k, dtype=torch.int16, device="cuda")
@@ -918,7 +918,7 @@ def run_probe(ctx: Ctx, what: str):
         y = torch.empty(m * n, dtype=torch.float32, device="cuda")
         for i in range(20):
             ctx.gemv(t, xb, k, ws[i % len(ws)], n, y, entry="okq_gemm_bf16", rows=m)
-        log(f"probe {what}: 20 {'Q8_0' if t == Q8_0 else 'Q4_K'} GEMM calls M={m} N={n} K={k} (bf16), "
+        log(f"probe {what}: 20 {dict([(Q8_0, 'Q8_0'), (Q6K, 'Q6_K')]).get(t, 'Q4_K')} GEMM calls M={m} N={n} K={k} (bf16), "
             f"{2 * m * n * k} flops each")
     else:
         src = torch.ones(64 << 20, dtype=torch.float32, device="cuda")
@@ -949,7 +949,7 @@ def main():
                     help="secondary configs to run (comma list of c1,c3,c4,c5,q5k,q6k)")
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
     ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "gemm_down512", "gemm_gate128",
-                                        "gemm_q8_512", "gemm_q8_2048",
+                                        "gemm_q8_512", "gemm_q8_2048", "gemm_q6_512",
                                         "decode_gate_up32"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
                          "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), 20 Q4_K "
