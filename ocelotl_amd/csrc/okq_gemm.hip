@@ -1689,7 +1689,65 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float *__restr
 #pragma unroll
       for (int d = 0; d < KB; ++d) acc += v[d];
     }
-    Y[(size_t)i] = (rscale ? acc * rs_m : acc) + bn;
+    Y[(size_t)i] = __builtin_fmaf(acc, rs_m, bn);  // rs_m a power of two: the product is exact
+  }
+}
+
+// The same sums, four consecutive outputs and RR rows per thread (N a
+// multiple of 4, Y 16-byte aligned: every partial and output row holds whole
+// 16-byte pieces): each slice's 16-byte loads of all RR rows in flight at
+// once, a quarter of the threads and an RR-th of the workgroups of
+// splitk_reduce_kernel.  Per output the same operations in the same order:
+// the slice-order sum from -0.0, then acc * rscale + bias as one FMA (the
+// power-of-two scale makes the product exact, so this is the rounding of
+// the separate multiply and add).  Grid: 1024-column blocks x RR-row blocks.
+constexpr int kReduceRows = 2;  // rows per thread of splitk_reduce4_kernel
+template <int KB, int RR>
+__global__ __launch_bounds__(256) void splitk_reduce4_kernel(const float *__restrict__ part, int ksplit, int M, int N,
+                                                             const float *__restrict__ rscale,
+                                                             const float *__restrict__ bias, float *__restrict__ Y) {
+  const int n = ((int)blockIdx.x * 256 + (int)threadIdx.x) * 4;
+  if (n >= N) return;
+  const uint32_t total = (uint32_t)M * (uint32_t)N, end = (uint32_t)ksplit * total * 4u;
+  const Rsrc rs = make_rsrc(part, end);
+  const int m0 = (int)blockIdx.y * RR;
+  f4 acc[RR];
+#pragma unroll
+  for (int r = 0; r < RR; ++r) acc[r] = f4{-0.0f, -0.0f, -0.0f, -0.0f};
+  for (int z0 = 0; z0 < ksplit; z0 += KB) {
+    u32x4 v[RR][KB];
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int d = 0; d < KB; ++d) {
+        const uint32_t i = (uint32_t)(m0 + r) * (uint32_t)N + (uint32_t)n;
+        const bool in = z0 + d < ksplit && m0 + r < M;
+        v[r][d] = bload4(rs, in ? ((uint32_t)(z0 + d) * total + i) * 4u : end);
+      }
+#pragma unroll
+    for (int r = 0; r < RR; ++r)
+#pragma unroll
+      for (int d = 0; d < KB; ++d) {
+        acc[r].x += __uint_as_float(v[r][d].x);
+        acc[r].y += __uint_as_float(v[r][d].y);
+        acc[r].z += __uint_as_float(v[r][d].z);
+        acc[r].w += __uint_as_float(v[r][d].w);
+      }
+  }
+  const float b0 = bias ? bias[n] : 0.0f, b1 = bias ? bias[n + 1] : 0.0f;
+  const float b2 = bias ? bias[n + 2] : 0.0f, b3 = bias ? bias[n + 3] : 0.0f;
+#pragma unroll
+  for (int r = 0; r < RR; ++r) {
+    const int m = m0 + r;
+    if (m >= M) break;
+    const float s = rscale ? rscale[m] : 1.0f;
+    if (__builtin_isnan(s)) continue;  // the pre-pass wrote this row's IEEE outputs
+    f4 o;
+    o.x = __builtin_fmaf(acc[r].x, s, b0);
+    o.y = __builtin_fmaf(acc[r].y, s, b1);
+    o.z = __builtin_fmaf(acc[r].z, s, b2);
+    o.w = __builtin_fmaf(acc[r].w, s, b3);
+    *reinterpret_cast<f4 *>(Y + (size_t)m * N + n) = o;
   }
 }
 
@@ -2130,6 +2188,14 @@ hipError_t launch_gemm(int type, const void *x, bool x_is_bf16, int64_t M, int64
   if (ks > 1 && (int64_t)ks * M * N * 4 > (int64_t)UINT32_MAX) return hipErrorInvalidValue;  // excluded by gemm_plan
   // the split-K reduction of the partials (rscale: the pre-pass's row scales, or none)
   auto reduce = [&](const float *rscale) {
+    constexpr int RR = kReduceRows;
+    if (N % 4 == 0 && (reinterpret_cast<uintptr_t>(y) & 15u) == 0 && (M + RR - 1) / RR <= 65535) {
+      const dim3 g4((unsigned)((N + 1023) / 1024), (unsigned)((M + RR - 1) / RR));
+      if (ks <= 2) hipLaunchKernelGGL((splitk_reduce4_kernel<2, RR>), g4, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+      else if (ks <= 4) hipLaunchKernelGGL((splitk_reduce4_kernel<4, RR>), g4, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+      else hipLaunchKernelGGL((splitk_reduce4_kernel<8, RR>), g4, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
+      return hipGetLastError();
+    }
     if (ks <= 2) hipLaunchKernelGGL(splitk_reduce_kernel<2>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
     else if (ks <= 4) hipLaunchKernelGGL(splitk_reduce_kernel<4>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
     else hipLaunchKernelGGL(splitk_reduce_kernel<8>, rgrid, dim3(256), 0, s, part, ks, m, n, rscale, bias, y);
