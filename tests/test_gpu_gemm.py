@@ -593,6 +593,36 @@ def test_gemm_wide_q4k_bf16_matches_reference(torch, okq, orc, rows, n, k):
     check_rows(orc, O.Q4_K, got, x32, rows, k, wq, n, bias, None if rows * n * k <= 4e8 else 16)
 
 
+@pytest.mark.parametrize("t,rows,n,k", [(O.Q4_K, 129, 300, 1024), (O.Q4_K, 511, 4096, 4096),
+                                         (O.Q8_0, 127, 4096, 4096), (O.Q6_K, 511, 4096, 14336)])
+def test_splitk_reduction_paths_agree_bit_for_bit(torch, okq, orc, t, rows, n, k):
+    """Split-K shapes with N a multiple of 4 and an odd row count: a 16-byte
+    aligned output takes the reduction with four outputs and two rows per
+    thread (the last row pair half empty), an output 4 bytes into its buffer
+    the one-output-per-thread reduction.  Both sum the slices in the same
+    order and scale and add the bias as one exact FMA: the same bits, and the
+    reference rule on sampled rows."""
+    print(f"[gpu] split-K reduction paths type {t} M={rows} N={n} K={k}", flush=True)
+    wq = orc.quantize(t, orc.normal(2300 + n + k, n * k, 0.02))
+    xb, x32 = bf16_inputs(orc, 2301 + rows, rows, k)
+    bias = orc.normal(2302, n, 0.1)
+    xd = torch.from_numpy(np.ascontiguousarray(xb)).cuda()
+    wd = torch.from_numpy(wq).cuda()
+    bd = torch.from_numpy(np.asarray(bias, np.float32)).cuda()
+    buf = torch.full((rows * n + 4,), float("nan"), dtype=torch.float32, device="cuda")
+    outs = []
+    for off in (0, 1):  # element offset 0: 16-byte aligned; 1: 4 bytes in
+        okq.call("okq_gemm_bf16", xd.data_ptr(), rows, k, t, wd.data_ptr(), wq.size, n, bd.data_ptr(),
+                 buf.data_ptr() + 4 * off, torch.cuda.current_stream().cuda_stream)
+        torch.cuda.synchronize()
+        outs.append(buf[off:off + rows * n].cpu().numpy().reshape(rows, n).copy())
+        buf.fill_(float("nan"))
+    assert buf.data_ptr() % 16 == 0
+    assert np.isfinite(outs[0]).all()
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    check_rows(orc, t, outs[0], x32, rows, k, wq, n, bias, 3)
+
+
 def test_gemm_wide_one_hot_columns_are_exact(torch, okq, orc):
     """x = e_j (40 rows, bf16) returns the dequantised weights bit for bit:
     d * (sc * q) + (-(dmin * m))_hi + (-(dmin * m))_lo is the reference's
