@@ -675,19 +675,19 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   }
   __builtin_amdgcn_s_barrier();
 
-  // 2. the first D rows of weights.  Long (kDyn) launches issue them after
-  //    the activations are quantised instead, so no wave stalls at issue
-  //    behind a full vector-memory queue while the workgroup waits for its x
-  //    (measured: C2 step +2%, gate+up within run-to-run noise of 15.4-15.8
-  //    us); short launches lose 0.5-1 us that way and keep the early start.
+  // 2. the first rows of weights: short launches issue all D, long (kDyn)
+  //    launches only their first and the rest once the activations are
+  //    quantised.  With all 16 waves' full rings in flight the CU's
+  //    vector-memory queue is full and a wave that still has loads to issue
+  //    stalls, holding up the quantisation barrier (the whole ring late: C2
+  //    step +2% against the early start; the first row early, the second
+  //    late: gate+up 15.5 -> 14.9 us, the one-row Q6_K head unchanged).
   typename F::Regs S[D];
   float bs[D];
-  if constexpr (!kDyn) {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
-      wload(S[j], row_of(j));
-      bs[j] = bload(row_of(j));
-    }
+  for (int j = 0; j < (kDyn ? 1 : D); ++j) {
+    wload(S[j], row_of(j));
+    bs[j] = bload(row_of(j));
   }
 
   // 3. (optional neighbour transform, then) quantise x into LDS while the
@@ -880,7 +880,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
   if constexpr (kDyn) {
 #pragma unroll
-    for (int j = 0; j < D; ++j) {
+    for (int j = 1; j < D; ++j) {
       wload(S[j], row_of(j));
       bs[j] = bload(row_of(j));
     }
