@@ -675,17 +675,18 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   }
   __builtin_amdgcn_s_barrier();
 
-  // 2. the first rows of weights: short launches issue all D, long (kDyn)
-  //    launches only their first and the rest once the activations are
-  //    quantised.  With all 16 waves' full rings in flight the CU's
+  // 2. the first row of weights; the rest of the ring once the activations
+  //    are quantised.  With all 16 waves' full rings in flight the CU's
   //    vector-memory queue is full and a wave that still has loads to issue
-  //    stalls, holding up the quantisation barrier (the whole ring late: C2
-  //    step +2% against the early start; the first row early, the second
-  //    late: gate+up 15.5 -> 14.9 us, the one-row Q6_K head unchanged).
+  //    stalls, holding up the quantisation barrier (measured against the
+  //    whole ring early: gate+up 15.5 -> 14.9 us, down 10.5 -> 9.9 us; the
+  //    whole ring late: C2 step +2%).  (The loop form matters: written as a
+  //    single statement, the one-row launches compiled to code 0.2-0.6 us
+  //    slower.)
   typename F::Regs S[D];
   float bs[D];
 #pragma unroll
-  for (int j = 0; j < (kDyn ? 1 : D); ++j) {
+  for (int j = 0; j < 1; ++j) {
     wload(S[j], row_of(j));
     bs[j] = bload(row_of(j));
   }
@@ -878,7 +879,7 @@ __global__ __launch_bounds__(gemv_max_threads<R>()) void gemv_kernel(
   if (kDyn && tid == 0) next_row = (unsigned)(D * G);
   __syncthreads();
   if (g >= G) return;  // helper wave (T == 1: no barriers follow)
-  if constexpr (kDyn) {
+  {
 #pragma unroll
     for (int j = 1; j < D; ++j) {
       wload(S[j], row_of(j));
