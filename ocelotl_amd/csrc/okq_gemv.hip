@@ -59,6 +59,7 @@ namespace okq {
 
 typedef uint32_t u32x4a4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2a4 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x3a4 __attribute__((ext_vector_type(3)));
 typedef __amdgpu_buffer_rsrc_t Rsrc;
 
 // Buffer descriptor over [base, base + bytes), bytes < 2^32 (gfx9 dword 3).
@@ -68,6 +69,7 @@ __device__ __forceinline__ Rsrc make_rsrc(const void *base, uint32_t bytes) {
 // Dword-aligned byte offsets into the descriptor's range.
 __device__ __forceinline__ u32x4a4 ld4(Rsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0); }
 __device__ __forceinline__ u32x2a4 ld2(Rsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0); }
+__device__ __forceinline__ u32x3a4 ld3(Rsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b96(r, off, 0, 0); }
 __device__ __forceinline__ uint32_t ld1(Rsrc r, uint32_t off) { return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0); }
 __device__ __forceinline__ uint32_t ld16(Rsrc r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
@@ -274,8 +276,7 @@ struct FQ6K {
   static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 256) * kQ6KBytes; }
   struct Regs {
     Win16 L, Lh, H;
-    u32x2a4 sv;
-    uint32_t se;
+    u32x3a4 sw;
     uint32_t d;
     uint32_t r;
   };
@@ -288,9 +289,10 @@ struct FQ6K {
     g.L = ldwin16(rs, B + 64 * h + 16 * u2, r);
     g.Lh = ldwin16(rs, B + 64 * h + 32 + 16 * u2, r);
     g.H = ldwin16(rs, B + 128 + 32 * h + 16 * u2, r);
-    const uint32_t S = B + 192 + 8 * h;  // 8 scale bytes: [S - r, S - r + 8) and [S + 4 + r, S + 8 + r)
-    g.sv = ld2(rs, S - r);
-    g.se = ld1(rs, S + 4 + r);
+    // the half's 8 scale bytes [S, S + 8) in one 12-byte window that stays
+    // inside the block: [S - 4, S + 8) (r = 0) or [S - 2, S + 10) (r = 2)
+    const uint32_t S = B + 192 + 8 * h;
+    g.sw = ld3(rs, S - 4 + r);
     g.d = ld16(rs, B + 208);
   }
   // run j = [16j, 16j+16): super-block j/16; within it 16*(j%16) = 128h + 32qq + 16u2
@@ -306,8 +308,8 @@ struct FQ6K {
     realign16(g.L, g.r, L);
     realign16(g.Lh, g.r, Lh);
     realign16(g.H, g.r, H);
-    const uint32_t S0 = realign(g.sv.y, g.sv.x, g.r);
-    const uint32_t S1 = realign(g.se, g.sv.y, g.r);
+    const uint32_t S0 = g.r ? realign(g.sw.y, g.sw.x, 2u) : g.sw.y;
+    const uint32_t S1 = g.r ? realign(g.sw.z, g.sw.y, 2u) : g.sw.z;
     int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
     uint32_t qv[4][4];  // [w][quarter]
 #pragma unroll
