@@ -275,7 +275,9 @@ struct FQ6K {
   }
   static __host__ __device__ size_t row_bytes(int K) { return (size_t)(K / 256) * kQ6KBytes; }
   struct Regs {
-    Win16 L, Lh, H;
+    u32x4a4 qa, qb;  // a 36-byte window of this lane's 32 ql bytes [64 h + 32 u2, + 32)
+    uint32_t qe;
+    Win16 H;
     u32x3a4 sw;
     uint32_t d;
     uint32_t r;
@@ -286,8 +288,13 @@ struct FQ6K {
     const uint32_t r = B & 3u;  // the tensor base is dword aligned
     const uint32_t h = (lane >> 1) & 1u, u2 = lane & 1u;
     g.r = r;
-    g.L = ldwin16(rs, B + 64 * h + 16 * u2, r);
-    g.Lh = ldwin16(rs, B + 64 * h + 32 + 16 * u2, r);
+    // the half's 64 ql bytes are shared out by the lane pair (u2 = 0, 1):
+    // each loads 32 contiguous bytes, and compute() trades the 16-byte
+    // pieces each needs with its partner lane
+    const uint32_t a = B + 64 * h + 32 * u2;
+    g.qa = ld4(rs, a - r);
+    g.qb = ld4(rs, a - r + 16);
+    g.qe = ld1(rs, a - r + 32);
     g.H = ldwin16(rs, B + 128 + 32 * h + 16 * u2, r);
     // the half's 8 scale bytes [S, S + 8) in one 12-byte window that stays
     // inside the block: [S - 4, S + 8) (r = 0) or [S - 2, S + 10) (r = 2)
@@ -304,9 +311,23 @@ struct FQ6K {
     slot = qq;
   }
   __device__ static float compute(const Regs &g, const XRec &x, const LdsU32 *xlo, bool lo3, uint32_t lane) {
+    // this lane's ql pieces 2 u2 and 2 u2 + 1 (16 bytes each) of its half;
+    // it needs pieces u2 (L) and u2 + 2 (Lh): lane u2 = 0 keeps piece 0 and
+    // takes piece 2 from its partner (lane ^ 1), lane u2 = 1 keeps piece 3
+    // and takes piece 1 (DPP quad_perm 1,0,3,2 swaps the pair's values)
+    const uint32_t w9[9] = {g.qa.x, g.qa.y, g.qa.z, g.qa.w, g.qb.x, g.qb.y, g.qb.z, g.qb.w, g.qe};
+    uint32_t Mq[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) Mq[i] = realign(w9[i + 1], w9[i], g.r);
+    const bool odd = (lane & 1u) != 0u;
     uint32_t L[4], Lh[4], H[4];
-    realign16(g.L, g.r, L);
-    realign16(g.Lh, g.r, Lh);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t send = odd ? Mq[i] : Mq[4 + i];
+      const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xf, 0xf, false);
+      L[i] = odd ? recv : Mq[i];
+      Lh[i] = odd ? Mq[4 + i] : recv;
+    }
     realign16(g.H, g.r, H);
     const uint32_t S0 = g.r ? realign(g.sw.y, g.sw.x, 2u) : g.sw.y;
     const uint32_t S1 = g.r ? realign(g.sw.z, g.sw.y, 2u) : g.sw.z;
