@@ -278,8 +278,7 @@ struct FQ6K {
     u32x4a4 qa, qb;  // a 36-byte window of this lane's 32 ql bytes [64 h + 32 u2, + 32)
     uint32_t qe;
     Win16 H;
-    u32x3a4 sw;
-    uint32_t d;
+    u32x4a4 sw;  // the half's scales (and, h = 1, d)
     uint32_t r;
   };
   static constexpr int kMaxDepth = 1;  // measured: deeper rings slow the long Q6_K streams
@@ -296,11 +295,14 @@ struct FQ6K {
     g.qb = ld4(rs, a - r + 16);
     g.qe = ld1(rs, a - r + 32);
     g.H = ldwin16(rs, B + 128 + 32 * h + 16 * u2, r);
-    // the half's 8 scale bytes [S, S + 8) in one 12-byte window that stays
-    // inside the block: [S - 4, S + 8) (r = 0) or [S - 2, S + 10) (r = 2)
+    // one 16-byte window: h = 0 the half's 8 scale bytes [S, S + 8) inside
+    // the block ([S - 4, S + 12) or [S - 2, S + 14)); h = 1 its scales and
+    // d, [B + 196, B + 212) (r = 0: 2 bytes into the next block) or
+    // [B + 194, B + 210) (r = 2).  The tensor's last block starts 2 bytes
+    // off a dword (its size is a multiple of 4: checked by the launcher), so
+    // no window leaves the tensor.
     const uint32_t S = B + 192 + 8 * h;
-    g.sw = ld3(rs, S - 4 + r);
-    g.d = ld16(rs, B + 208);
+    g.sw = ld4(rs, S - 4 + r - ((h & (r >> 1)) << 2));
   }
   // run j = [16j, 16j+16): super-block j/16; within it 16*(j%16) = 128h + 32qq + 16u2
   __device__ static void xslot(int run, int &rec, int &word, int &slot) {
@@ -329,8 +331,15 @@ struct FQ6K {
       Lh[i] = odd ? Mq[4 + i] : recv;
     }
     realign16(g.H, g.r, H);
-    const uint32_t S0 = g.r ? realign(g.sw.y, g.sw.x, 2u) : g.sw.y;
-    const uint32_t S1 = g.r ? realign(g.sw.z, g.sw.y, 2u) : g.sw.z;
+    // scales at window byte 4 - r (h = 0) or 4 + r (h = 1); d at 12 + r
+    // (h = 1), taken by the h = 0 lanes from their h = 1 partner (lane ^ 2)
+    const uint32_t hh = (lane >> 1) & 1u;
+    const bool hi1 = hh != 0u || g.r == 0u;  // the scales start in dword 1
+    const uint32_t S0 = hi1 ? realign(g.sw.z, g.sw.y, g.r) : realign(g.sw.y, g.sw.x, g.r);
+    const uint32_t S1 = hi1 ? realign(g.sw.w, g.sw.z, g.r) : realign(g.sw.z, g.sw.y, g.r);
+    const uint32_t dh = (g.sw.w >> (8u * g.r)) & 0xffffu;
+    const uint32_t dq = (uint32_t)__builtin_amdgcn_mov_dpp((int)dh, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+    const uint32_t dbits = hh ? dh : dq;
     int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
     uint32_t qv[4][4];  // [w][quarter]
 #pragma unroll
@@ -354,7 +363,7 @@ struct FQ6K {
     const uint32_t u2 = lane & 1u;
     const int sc[4] = {(int)__builtin_amdgcn_sbfe((int)S0, 8 * u2, 8u), (int)__builtin_amdgcn_sbfe((int)S0, 8 * u2 + 16, 8u),
                        (int)__builtin_amdgcn_sbfe((int)S1, 8 * u2, 8u), (int)__builtin_amdgcn_sbfe((int)S1, 8 * u2 + 16, 8u)};
-    const float d = f16_bits_hw(g.d);
+    const float d = f16_bits_hw(dbits);
     float acc = 0.0f;
 #pragma unroll
     for (int qq = 0; qq < 4; ++qq) {
@@ -1050,7 +1059,7 @@ bool fast_ok(int type, int64_t K, const void *w, int64_t N) {
   const size_t bytes = (size_t)N * row_bytes_of(type, K);
   bool fast = (K % 64 == 0) && K <= 4 * kMaxXV * 1024 && bytes < 0xFFFFFFFFull;
   if (type == kQ4_K || type == kQ5_K) fast = fast && (wa & 15u) == 0;
-  else if (type == kQ6_K) fast = fast && (wa & 3u) == 0;
+  else if (type == kQ6_K) fast = fast && (wa & 3u) == 0 && bytes % 4 == 0;  // the last block 2 bytes off a dword
   else fast = fast && (wa & 3u) == 0 && ((K / 32) % 2 == 0);
   return fast;
 }

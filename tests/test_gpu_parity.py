@@ -137,8 +137,13 @@ GEMV_SHAPES = {
     # wave's first ones come from the workgroup's counter
     O.Q4_K: [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (17, 256), (3, 768), (64, 20480),
              (300, 14336), (17, 8192), (2, 16384), (20000, 256)],
-    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (64, 20480), (33, 12288),
-             (20000, 256)],
+    # Q6_K: a unit's scales (and d) come in one 16-byte window that may reach
+    # 2 bytes into the next block, so the streaming kernel takes tensors whose
+    # last block starts 2 bytes off a dword (size a multiple of 4): odd
+    # super-block counts with an even row count (34 x 768) stream, with an
+    # odd one (33 x 768, 35 x 1280) they take the generic kernel
+    O.Q6_K: [(4096, 4096), (1024, 4096), (4096, 14336), (5, 512), (33, 768), (34, 768), (35, 1280), (64, 20480),
+             (33, 12288), (20000, 256)],
     O.Q8_0: [(4096, 4096), (1024, 4096), (4096, 14336), (7, 64), (9, 800), (64, 20480), (5, 14336),
              (20000, 256)],
     # Q5_K streams like Q4_K (same units, one more 32-byte qh read per unit)
