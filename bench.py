@@ -43,7 +43,7 @@ The JSON line also carries:
                 down projection's M=512 prefill call
 
 Run: python bench.py [--steps K] [--warmup W] [--copies C] [--no-cpu] ...
-     python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|gemm_q8_512|gemm_q8_2048|gemm_q6_512|decode_gate_up32
+     python bench.py --probe gate_up|copy|gemm_gate512|gemm_down512|gemm_gate128|gemm_q8_512|gemm_q8_2048|gemm_q6_512|decode_gate_up32|decode_head8
                                                         (bare workloads for counter passes)
 """
 from __future__ import annotations
@@ -907,6 +907,19 @@ def run_probe(ctx: Ctx, what: str):
                          (ctypes.c_void_p * 2)(*[o.data_ptr() for o in outs]), ctx.stream)
         log(f"probe decode_gate_up32: 20 calls of 32 rows over gate+up ({2 * b} weight bytes each): "
             f"one decode-batch launch and its split-K reduction per call")
+    elif what == "decode_head8":
+        t, n, k = C5_HEAD
+        rows = 8
+        w = ctx.quantized(t, n, k, seed=59_999)
+        pool, copies = ctx.replicas(w)
+        x = ctx.normal(rows * k, 8)
+        y = torch.empty(rows * n, dtype=torch.float32, device="cuda")
+        b = wbytes(t, n, k)
+        for i in range(20):
+            ctx.okq.call("okq_linear_out_by_in_q", x.data_ptr(), rows, k, t, pool.narrow(0, (i % copies) * b, b).data_ptr(),
+                         b, n, None, y.data_ptr(), ctx.stream)
+        log(f"probe decode_head8: 20 calls of 8 rows over the Q6_K head ({b} weight bytes each): "
+            f"one decode-batch launch per call")
     elif what.startswith("gemm_"):
         t, m, n, k = {"gemm_gate512": (Q4K, 512, 14336, 4096), "gemm_down512": (Q4K, 512, 4096, 14336),
                       "gemm_gate128": (Q4K, 128, 14336, 4096), "gemm_q8_512": (Q8_0, 512, 4096, 4096),
@@ -950,7 +963,7 @@ def main():
     ap.add_argument("--c5-steps", type=int, default=10, help="timed steps per C5 batch size")
     ap.add_argument("--probe", choices=["gate_up", "copy", "gemm_gate512", "gemm_down512", "gemm_gate128",
                                         "gemm_q8_512", "gemm_q8_2048", "gemm_q6_512",
-                                        "decode_gate_up32"], default=None,
+                                        "decode_gate_up32", "decode_head8"], default=None,
                     help="run a bare workload for rocprofv3 counter passes and exit: 20 gate+up GEMV launches over "
                          "weight replicas, 20 launches of a 256 MiB f32 elementwise copy (calibration), 20 Q4_K "
                          "GEMM calls (M=512 gate or down, M=128 gate), or 20 gate+up calls at 32 rows "
