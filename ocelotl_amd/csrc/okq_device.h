@@ -86,13 +86,30 @@ __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
+// A lane's DPP neighbour under a full-row control: a quad_perm (0x00-0xFF),
+// row_mirror (0x140) or row_half_mirror (0x141).  Every lane then reads a
+// lane of its own 16-lane row, so neither the old value nor bound_ctrl takes
+// effect and the result is a plain DPP move's.  Written as an update with
+// bound_ctrl set, the compiler folds the move into the add, max or select
+// that consumes it (v_add_f32_dpp, v_max_u32_dpp): one instruction instead
+// of a v_mov_b32_dpp and the operation.
+template <int kCtl>
+__device__ __forceinline__ uint32_t dpp_row_u(uint32_t v) {
+  static_assert(kCtl <= 0xFF || kCtl == 0x140 || kCtl == 0x141, "full-row DPP controls only");
+  return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, kCtl, 0xf, 0xf, true);
+}
+template <int kCtl>
+__device__ __forceinline__ float dpp_row_f(float v) {
+  return as_f32(dpp_row_u<kCtl>(as_u32(v)));
+}
+
 // Wave-wide sum (64 lanes) with a fixed order: DPP within rows of 16, then
 // the four row sums combined with readlane.  Result is uniform.
 __device__ __forceinline__ float wave_sum(float v) {
-  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0xB1, 0xf, 0xf, false));   // quad_perm 1,0,3,2
-  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x4E, 0xf, 0xf, false));   // quad_perm 2,3,0,1
-  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x141, 0xf, 0xf, false));  // row_half_mirror
-  v += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), 0x140, 0xf, 0xf, false));  // row_mirror
+  v += dpp_row_f<0xB1>(v);   // quad_perm 1,0,3,2
+  v += dpp_row_f<0x4E>(v);   // quad_perm 2,3,0,1
+  v += dpp_row_f<0x141>(v);  // row_half_mirror
+  v += dpp_row_f<0x140>(v);  // row_mirror
   float r0 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 0));
   float r1 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 16));
   float r2 = as_f32((uint32_t)__builtin_amdgcn_readlane((int)as_u32(v), 32));

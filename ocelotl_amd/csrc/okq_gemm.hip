@@ -101,8 +101,8 @@ __device__ __forceinline__ void prep_chunk(const float v[8], int s, bool ok, int
     hv[i] = h;
     lv[i] = (_Float16)(w - (float)h);
   }
-  t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-  t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+  t += dpp_row_f<0xB1>(t);  // quad_perm 1,0,3,2
+  t += dpp_row_f<0x4E>(t);  // quad_perm 2,3,0,1
   if (ok) {
     *reinterpret_cast<h8 *>(xhi + base) = hv;
     if (kF32) *reinterpret_cast<h8 *>(xlo + base) = lv;
@@ -125,7 +125,7 @@ __device__ __forceinline__ void prep_chunk(const float v[8], int s, bool ok, int
 // 0.3-0.6 us slower).
 template <int kCtl>
 __device__ __forceinline__ uint32_t dpp_umax(uint32_t a) {
-  const uint32_t b = (uint32_t)__builtin_amdgcn_mov_dpp((int)a, kCtl, 0xf, 0xf, false);
+  const uint32_t b = dpp_row_u<kCtl>(a);
   return a > b ? a : b;
 }
 __device__ __forceinline__ uint32_t block_max_bits(uint32_t a, uint32_t *red, int tid) {
@@ -1414,7 +1414,7 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
   // two.  Pieces past the last row are skipped (a uniform bound).
   auto umax_u32 = [](uint32_t x, uint32_t y) { return x > y ? x : y; };
   auto dmax = [&](uint32_t a, auto ctl) {
-    return umax_u32(a, (uint32_t)__builtin_amdgcn_mov_dpp((int)a, decltype(ctl)::value, 0xf, 0xf, false));
+    return umax_u32(a, dpp_row_u<decltype(ctl)::value>(a));
   };
 #pragma unroll
   for (int i = 0; i < kDecStage; ++i) {
@@ -1469,8 +1469,8 @@ __device__ __forceinline__ void dec_run(const void *__restrict__ X, const DecMat
       }
     }
     if (F::kSums) {
-      t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0xB1, 0xf, 0xf, false));  // quad_perm 1,0,3,2
-      t += as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(t), 0x4E, 0xf, 0xf, false));  // quad_perm 2,3,0,1
+      t += dpp_row_f<0xB1>(t);  // quad_perm 1,0,3,2
+      t += dpp_row_f<0x4E>(t);  // quad_perm 2,3,0,1
     }
     if (r < M) {
       *reinterpret_cast<h8 *>(Ah + dec_row(r, P) + 8 * c) = hv;

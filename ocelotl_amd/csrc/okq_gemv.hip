@@ -326,7 +326,7 @@ struct FQ6K {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t send = odd ? Mq[i] : Mq[4 + i];
-      const uint32_t recv = (uint32_t)__builtin_amdgcn_mov_dpp((int)send, 0xB1, 0xf, 0xf, false);
+      const uint32_t recv = dpp_row_u<0xB1>(send);
       L[i] = odd ? recv : Mq[i];
       Lh[i] = odd ? Mq[4 + i] : recv;
     }
@@ -338,7 +338,7 @@ struct FQ6K {
     const uint32_t S0 = hi1 ? realign(g.sw.z, g.sw.y, g.r) : realign(g.sw.y, g.sw.x, g.r);
     const uint32_t S1 = hi1 ? realign(g.sw.w, g.sw.z, g.r) : realign(g.sw.z, g.sw.y, g.r);
     const uint32_t dh = (g.sw.w >> (8u * g.r)) & 0xffffu;
-    const uint32_t dq = (uint32_t)__builtin_amdgcn_mov_dpp((int)dh, 0x4E, 0xf, 0xf, false);  // quad_perm 2,3,0,1
+    const uint32_t dq = dpp_row_u<0x4E>(dh);  // quad_perm 2,3,0,1
     const uint32_t dbits = hh ? dh : dq;
     int ah[4] = {0, 0, 0, 0}, am[4] = {0, 0, 0, 0}, al[4] = {0, 0, 0, 0};
     uint32_t qv[4][4];  // [w][quarter]
@@ -432,10 +432,6 @@ struct FQ80 {
 // run; the group shares the run's max|x| and sum through DPP (fixed order),
 // then each lane writes one dword of each limb of the run's XRec.
 // ---------------------------------------------------------------------------
-template <int kCtl>
-__device__ __forceinline__ float dpp_f(float v) {
-  return as_f32((uint32_t)__builtin_amdgcn_mov_dpp((int)as_u32(v), kCtl, 0xf, 0xf, false));
-}
 
 // Returns the run's status: bit 0 when the run is wide (its largest |x|
 // exceeds 8 times its mean |x|, so the launch contracts all three limbs),
@@ -444,20 +440,27 @@ template <class F>
 __device__ __forceinline__ unsigned quant_group(u32x4a4 raw, int f, int nf, XRec *xr) {
   constexpr int GL = F::kRun / 4;  // lanes per run: 8 (runs of 32) or 4 (runs of 16)
   const float v0 = as_f32(raw.x), v1 = as_f32(raw.y), v2 = as_f32(raw.z), v3 = as_f32(raw.w);
-  float a = fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3)));
+  // The lanes' max|x| meet as bit patterns: for |x| the unsigned order is
+  // the float order, and an unsigned max takes its DPP operand in the same
+  // instruction, where a float max first quiets it (v_max_f32 x, x).  A NaN
+  // then wins where the float max would drop it; such a run has a NaN sum,
+  // so its activation row takes the f32 path and its record goes unused.
+  auto umax = [](uint32_t p, uint32_t q) { return p > q ? p : q; };
+  uint32_t ab = as_u32(fmaxf(fmaxf(fabsf(v0), fabsf(v1)), fmaxf(fabsf(v2), fabsf(v3))));
   float t = (v0 + v1) + (v2 + v3);
   float m = (fabsf(v0) + fabsf(v1)) + (fabsf(v2) + fabsf(v3));
-  a = fmaxf(a, dpp_f<0xB1>(a));  // quad_perm 1,0,3,2
-  t += dpp_f<0xB1>(t);
-  m += dpp_f<0xB1>(m);
-  a = fmaxf(a, dpp_f<0x4E>(a));  // quad_perm 2,3,0,1
-  t += dpp_f<0x4E>(t);
-  m += dpp_f<0x4E>(m);
+  ab = umax(ab, dpp_row_u<0xB1>(ab));  // quad_perm 1,0,3,2
+  t += dpp_row_f<0xB1>(t);
+  m += dpp_row_f<0xB1>(m);
+  ab = umax(ab, dpp_row_u<0x4E>(ab));  // quad_perm 2,3,0,1
+  t += dpp_row_f<0x4E>(t);
+  m += dpp_row_f<0x4E>(m);
   if (GL == 8) {
-    a = fmaxf(a, dpp_f<0x141>(a));  // row_half_mirror: lane i <-> 7 - i within 8
-    t += dpp_f<0x141>(t);
-    m += dpp_f<0x141>(m);
+    ab = umax(ab, dpp_row_u<0x141>(ab));  // row_half_mirror: lane i <-> 7 - i within 8
+    t += dpp_row_f<0x141>(t);
+    m += dpp_row_f<0x141>(m);
   }
+  const float a = as_f32(ab);
   if (f >= nf) return 0u;
   const int e = x_exp(a);
   uint32_t hi, mi, lo;
