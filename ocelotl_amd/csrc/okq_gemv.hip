@@ -460,24 +460,30 @@ __device__ __forceinline__ unsigned quant_group(u32x4a4 raw, int f, int nf, XRec
     t += dpp_row_f<0x141>(t);
     m += dpp_row_f<0x141>(m);
   }
+  // Pinned here, with every lane on: otherwise the compiler sinks the last
+  // step's add and max into the branch below and keeps its DPP moves apart
+  // (a DPP operand must be read with all lanes on).
+  asm volatile("" : : "v"(ab), "v"(t), "v"(m));
   const float a = as_f32(ab);
-  if (f >= nf) return 0u;
-  const int e = x_exp(a);
-  uint32_t hi, mi, lo;
-  limbs4(x_digits(v0, e), x_digits(v1, e), x_digits(v2, e), x_digits(v3, e), hi, mi, lo);
-  const int run = f / GL, i = f % GL;
-  int rec, word, slot;
-  F::xslot(run, rec, word, slot);
-  xr[rec].hi[word + i] = hi;
-  xr[rec].mi[word + i] = mi;
-  xr[rec].lo[word + i] = lo;
-  if (i == 0) {
-    xr[rec].s[slot] = ldexpf(1.0f, e);
-    xr[rec].t[slot] = t;
-  }
   // max <= 8 * mean: a <= m * 8 / kRun (m is the run's sum of |x|)
   const unsigned wide = (a <= m * (8.0f / (float)F::kRun)) ? 0u : 1u;
-  return __builtin_isfinite(t) ? wide : 2u;
+  const unsigned status = f < nf ? (__builtin_isfinite(t) ? wide : 2u) : 0u;
+  if (f < nf) {
+    const int e = x_exp(a);
+    uint32_t hi, mi, lo;
+    limbs4(x_digits(v0, e), x_digits(v1, e), x_digits(v2, e), x_digits(v3, e), hi, mi, lo);
+    const int run = f / GL, i = f % GL;
+    int rec, word, slot;
+    F::xslot(run, rec, word, slot);
+    xr[rec].hi[word + i] = hi;
+    xr[rec].mi[word + i] = mi;
+    xr[rec].lo[word + i] = lo;
+    if (i == 0) {
+      xr[rec].s[slot] = ldexpf(1.0f, e);
+      xr[rec].t[slot] = t;
+    }
+  }
+  return status;
 }
 
 // ---------------------------------------------------------------------------
