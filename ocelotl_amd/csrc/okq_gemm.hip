@@ -1021,7 +1021,15 @@ struct DecQ5K {
   }
 };
 
-struct DecQ6K {
+// kDw: d is taken from the scales' last dword (bytes 208-211 of the block
+// from the dword below it: d sits at its byte r), one load fewer per item.
+// That dword reaches 2 bytes into the next block when the block starts on a
+// dword, so the launcher takes this form only for tensors whose last block
+// starts 2 bytes off one (a size that is a multiple of 4: an even number of
+// blocks); otherwise d comes with a 2-byte load of its own (a dword around
+// it could end past the tensor, where the range check zeroes it).
+template <bool kDw>
+struct DecQ6KT {
   static constexpr uint32_t kBlk = kQ6KBytes;
   static constexpr int kType = kQ6_K;
   static constexpr bool kSums = false;
@@ -1031,8 +1039,7 @@ struct DecQ6K {
   // 64hh + 32(qq & 1) + 8g .. (nibble qq >> 1), qh bytes 128 + 32hh + 8g ..
   // (bits 2qq), scale byte 8hh + 2qq + (g >> 1).  Blocks are 2-byte aligned:
   // each 8-byte field is read as a 3-dword window from the dword below it
-  // and realigned by r = block & 3; d with a 2-byte load (a dword around it
-  // could end past the tensor, where the range check zeroes it).
+  // and realigned by r = block & 3.
   struct Item {
     u32x3 ql[4], qh[2];  // ql: (hh, qq & 1) = (0,0) (0,1) (1,0) (1,1)
     u32x4 sc4;
@@ -1048,7 +1055,7 @@ struct DecQ6K {
       it.qh[h] = __builtin_amdgcn_raw_buffer_load_b96(rs, a + 128u + 32u * (uint32_t)h + 8u * (uint32_t)g, 0, 0);
     it.sc4 = bload4(rs, a + 192u);
     it.sc1 = __builtin_amdgcn_raw_buffer_load_b32(rs, a + 208u, 0, 0);
-    it.dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, blk + 208u, 0, 0);
+    if constexpr (!kDw) it.dw = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(rs, blk + 208u, 0, 0);
     it.r = r;
   }
   template <bool kLo, int RG>
@@ -1103,7 +1110,7 @@ struct DecQ6K {
         }
       }
     }
-    const float dv = f16_bits_hw(it.dw & 0xffffu);
+    const float dv = f16_bits_hw(kDw ? (it.sc1 >> (8u * r)) & 0xffffu : it.dw & 0xffffu);
 #pragma unroll
     for (int q = 0; q < RG; ++q) {
       const f4 s4 = *reinterpret_cast<const f4 *>(rsc + 16 * q);  // the rows' 2^s (exact products)
@@ -1112,6 +1119,9 @@ struct DecQ6K {
     }
   }
 };
+
+using DecQ6K = DecQ6KT<false>;
+using DecQ6KW = DecQ6KT<true>;
 
 // Q8_0: an item is 256 weights of a column, eight 34-byte blocks (272 bytes,
 // 2-byte aligned).  Lane group g covers blocks 2g and 2g + 1 (k = 64g ..
@@ -2051,12 +2061,26 @@ static hipError_t launch_decode(int type, int type2, int nt1, const void *x, boo
   if (M > 16) OKQ_DEC(F1_, F2_, LO_, 2, false);   \
   else if (split_w) OKQ_DEC(F1_, F2_, LO_, 1, true); \
   else OKQ_DEC(F1_, F2_, LO_, 1, false)
+  // Q6_K items take d from their scale window when every tensor of the
+  // launch has a size that is a multiple of 4 (Q4_K sizes always are)
+  bool dw = true;
+  for (int i = 0; i < kDecMats; ++i) dw = dw && mats.mat[i].w_bytes % 4u == 0;
   if (mixed) {
-    if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ6K, false);
-    else OKQ_DEC_RG(DecQ4K, DecQ6K, true);
+    if (dw) {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ6KW, false);
+      else OKQ_DEC_RG(DecQ4K, DecQ6KW, true);
+    } else {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ4K, DecQ6K, false);
+      else OKQ_DEC_RG(DecQ4K, DecQ6K, true);
+    }
   } else if (type == kQ6_K) {
-    if (x_is_bf16) OKQ_DEC_RG(DecQ6K, DecQ6K, false);
-    else OKQ_DEC_RG(DecQ6K, DecQ6K, true);
+    if (dw) {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ6KW, DecQ6KW, false);
+      else OKQ_DEC_RG(DecQ6KW, DecQ6KW, true);
+    } else {
+      if (x_is_bf16) OKQ_DEC_RG(DecQ6K, DecQ6K, false);
+      else OKQ_DEC_RG(DecQ6K, DecQ6K, true);
+    }
   } else if (type == kQ8_0) {
     if (x_is_bf16) OKQ_DEC_RG(DecQ80, DecQ80, false);
     else OKQ_DEC_RG(DecQ80, DecQ80, true);

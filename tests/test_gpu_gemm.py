@@ -166,7 +166,9 @@ DEC_CASES = [
 DEC_Q6K_CASES = [
     ("okq_gemm", 1, 96, 256), ("okq_gemm", 4, 257, 768), ("okq_gemm", 8, 4096, 4096), ("okq_gemm", 16, 1024, 4096),
     ("okq_gemm", 11, 4096, 14336), ("okq_gemm_bf16", 6, 300, 1024), ("okq_gemm_bf16", 16, 4095, 512),
-    # an odd super-block count per row: block starts alternate between the two 2-byte alignments
+    # an odd super-block count per row: block starts alternate between the two 2-byte alignments.
+    # Tensors of an odd block count (257 x 3, 333 x 5, 70003, 257 x 3 at 31 rows) end on a block
+    # that starts on a dword and read d with a 2-byte load; the rest take it from the scale window.
     ("okq_gemm", 5, 333, 1280), ("okq_gemm", 2, 70003, 256),
     ("okq_gemm", 20, 1024, 4096), ("okq_gemm", 32, 4096, 14336), ("okq_gemm_bf16", 31, 257, 768),
     # more column groups x K slices than one round of CUs (waves take 1-2 tiles)
