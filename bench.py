@@ -888,9 +888,10 @@ def run_probe(ctx: Ctx, what: str):
         x = ctx.normal(4096, 1)
         outs = {m: torch.empty(C2_SHAPE[m][0], dtype=torch.float32, device="cuda") for m in names}
         b = wbytes(Q4K, *C2_SHAPE["gate"])
-        for i in range(20):
+        # 100 launches, so that the first (cold) one weighs little in a trace's average
+        for i in range(100):
             launch_group(ctx, names, {m: pools[m][0].narrow(0, (i % copies) * b, b) for m in names}, x, outs)
-        log(f"probe gate_up: 20 launches, {2 * b} weight bytes each")
+        log(f"probe gate_up: 100 launches, {2 * b} weight bytes each")
     elif what == "decode_gate_up32":
         names = ["gate", "up"]
         ws = {m: ctx.quantized(Q4K, *C2_SHAPE[m], seed=10_004 + i) for i, m in enumerate(names)}
