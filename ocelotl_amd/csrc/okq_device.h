@@ -81,8 +81,13 @@ __device__ __forceinline__ uint32_t realign(uint32_t w1, uint32_t w0, uint32_t r
   return __builtin_amdgcn_alignbyte(w1, w0, r);
 }
 
-// Signed 4 x int8 dot product accumulated into c (v_dot4_i32_i8).
+// Signed 4 x int8 dot product accumulated into c (v_dot4_i32_i8).  The
+// first product of a chain (c a constant 0) is written with clamp set: the
+// compiler then keeps the three-operand form with an inline zero, where the
+// accumulating two-operand form (v_dot4c) needs a move of 0 first.  Four
+// int8 x int8 products cannot reach the int32 clamp, so the value is the same.
 __device__ __forceinline__ int sdot4(uint32_t a, uint32_t b, int c) {
+  if (__builtin_constant_p(c) && c == 0) return __builtin_amdgcn_sdot4((int)a, (int)b, 0, true);
   return __builtin_amdgcn_sdot4((int)a, (int)b, c, false);
 }
 
