@@ -227,7 +227,7 @@ class HipKernelBackend:
 
     def upload_quantized(self, tensor_type: int, ne0: int, ne1: int, blocks) -> QuantizedWeight:
         """Upload raw GGUF blocks of any block format (dequantize serves all of
-        them; linear_d takes Q8_0 / Q4K / Q6K); validates the byte length first."""
+        them; linear_d takes Q8_0 / Q4K / Q5K / Q6K); validates the byte length first."""
         torch = _torch()
         tt = int(tensor_type)
         if tt not in [int(t) for t in BLOCK_FORMATS]:
